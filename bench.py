@@ -1,0 +1,294 @@
+"""Benchmark of the MI355X attention path (one GPU).
+
+Default workload (the BASELINE.json metric's configuration): one hd512 global
+decode step at 32K context — q [1,8,512], K/V [32768,1,512] f32, unit-RMS
+Gaussian q/k, N(0,1) v, seed 4, scale 1.0 — the global layer of configs[4].
+A step is one Backend::attention call (split-K decode + LSE combine) with
+inputs resident in HBM. K/V are rotated over 4 copies (537 MB > the 256 MB
+MALL) so every step streams from HBM.
+
+Also reported (extra keys of the same JSON line): configs[0..2] decode,
+configs[3] prefill TFLOP/s, the configs[4] 35-layer schedule in us/token, and
+the CPU oracle (oracle/attn_oracle.c, the restatement of
+rust/src/backend_cpu.rs:270-336) timed on the host cores on a bounded sample.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "gemma-4-webgpu-kernels_amd"))
+
+import g4a  # noqa: E402
+import g4a.synth as synth  # noqa: E402
+
+METRIC = "decode attn µs/step + HBM GB/s (hd512, 32K ctx); prefill attn TFLOP/s"
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+FP32_MFMA_PEAK_TFLOPS = 157.3
+HQ = 8
+BUST_COPIES = 4
+
+
+def decode_bytes(S_vis: int, Dh: int, Hq: int = HQ) -> int:
+    """Algorithmic bytes of one decode step: K + V over the visible keys, plus q and out."""
+    return 4 * (2 * S_vis * Dh + 2 * Hq * Dh)
+
+
+def prefill_flops(T: int, window: int, Dh: int, Hq: int = HQ) -> int:
+    """4*Dh flops per visible (query, head, key); query i sees min(i+1, window) keys."""
+    i = np.arange(T, dtype=np.int64)
+    vis = np.minimum(i + 1, window) if window else i + 1
+    return int(4 * Dh * Hq * vis.sum())
+
+
+class Decode:
+    """A decode configuration resident on the GPU, with cache-busting copies of K/V."""
+
+    def __init__(self, ctx, S, Dh, seed, window=0, copies=BUST_COPIES, ring_cap=0):
+        self.ctx, self.S, self.Dh, self.window, self.ring_cap = ctx, S, Dh, window, ring_cap
+        ins = synth.gemma_inputs(T=1, S=S, Dh=Dh, seed=seed)
+        self.inputs = ins
+        self.q = ctx.upload(ins.q)
+        self.kv = [(ctx.upload(ins.k), ctx.upload(ins.v)) for _ in range(copies)]
+        self.out = ctx.empty((1, HQ * Dh))
+        self.i = 0
+
+    def kw(self, splits=0):
+        return dict(T=1, S=self.S, Hq=HQ, Hkv=1, Dh=self.Dh, Dv=self.Dh, q_pos0=self.S - 1, k_pos0=0,
+                    window=self.window, ring_cap=self.ring_cap, splits=splits)
+
+    def step(self, splits=0):
+        k, v = self.kv[self.i % len(self.kv)]
+        self.i += 1
+        self.ctx.attention(self.q.ptr, k.ptr, v.ptr, self.out.ptr, **self.kw(splits))
+
+    def visible(self):
+        return min(self.S, self.window) if self.window else self.S
+
+    def free(self):
+        for a in [self.q, self.out] + [x for kv in self.kv for x in kv]:
+            a.free()
+
+
+def time_steps(ctx, fn, steps, warmup):
+    """Event-timed region of `steps` calls after `warmup` untimed ones; also the
+    main kernel's own event-timed duration. Returns (ms/step, kernel ms/launch)."""
+    for _ in range(warmup):
+        fn()
+    ctx.sync()
+    ctx.kernel_timing(True)
+    ctx.timer_start()
+    for _ in range(steps):
+        fn()
+    total = ctx.timer_stop()
+    kms, n = ctx.kernel_timing_read()
+    ctx.kernel_timing(False)
+    return total / steps, (kms / n if n else float("nan"))
+
+
+def cpu_baseline(budget_s: float = 10.0):
+    """The CPU oracle on the headline decode step, on this host's cores (GEMMA_CPU_THREADS rules)."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle
+    ins = synth.gemma_inputs(T=1, S=32768, Dh=512, seed=4)
+    threads = oracle.thread_count(HQ)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or not times:
+        t0 = time.perf_counter()
+        oracle.attention(ins.q, ins.k, ins.v, ins.q_pos, ins.k_pos)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 200:
+            break
+    us = float(np.median(times)) * 1e6
+    return {
+        "value": decode_bytes(32768, 512) / (us * 1e-6) / 1e9,
+        "unit": "GB/s",
+        "us_per_step": us,
+        "cores": threads,
+        "host_cpus": os.cpu_count(),
+        "kind": "port",
+        "sample": f"{len(times)} decode steps of the headline workload (hd512, S=32768, 8 heads), median",
+    }
+
+
+def schedule_35_layers(ctx, steps, warmup):
+    """one token of the 35-layer Gemma-4-E2B attention schedule at 32768 context.
+    Layers 4,9,...,34 are global (hd512, full context); the rest local (hd256, 512-slot ring).
+    Layers 15..34 reuse the KV of layer 14 (global) or 13 (local) (rust/src/config.rs:152-159),
+    so 3 global caches and 12 local rings exist."""
+    S, seed = 32768, 4
+    layer_types = ["full" if (i % 5 == 4) else "sliding" for i in range(35)]
+    first_shared = 35 - 20
+    src = []
+    for i in range(35):
+        if i < first_shared:
+            src.append(i)
+        else:
+            src.append(max(j for j in range(first_shared) if layer_types[j] == layer_types[i]))
+    caches = {}
+    for li in sorted(set(src)):
+        if layer_types[li] == "full":
+            k = synth.rms_norm_rows(synth.normal_f32(seed * 100 + li, 1, S * 512).reshape(S, 1, 512))
+            v = synth.normal_f32(seed * 100 + li, 2, S * 512).reshape(S, 1, 512)
+        else:  # ring of 512 slots holding positions S-512..S-1 at slot p % 512
+            k = synth.rms_norm_rows(synth.normal_f32(seed * 100 + li, 1, 512 * 256).reshape(512, 1, 256))
+            v = synth.normal_f32(seed * 100 + li, 2, 512 * 256).reshape(512, 1, 256)
+        caches[li] = (ctx.upload(k), ctx.upload(v))
+    qs, outs = [], []
+    for i in range(35):
+        dh = 512 if layer_types[i] == "full" else 256
+        qs.append(ctx.upload(synth.rms_norm_rows(synth.normal_f32(seed * 100 + i, 0, HQ * dh).reshape(1, HQ, dh))))
+        outs.append(ctx.empty((1, HQ * dh)))
+
+    def token():
+        for i in range(35):
+            k, v = caches[src[i]]
+            if layer_types[i] == "full":
+                ctx.attention(qs[i].ptr, k.ptr, v.ptr, outs[i].ptr, T=1, S=S, Hq=HQ, Hkv=1, Dh=512, Dv=512,
+                              q_pos0=S - 1, k_pos0=0)
+            else:
+                ctx.attention(qs[i].ptr, k.ptr, v.ptr, outs[i].ptr, T=1, S=S, Hq=HQ, Hkv=1, Dh=256, Dv=256,
+                              q_pos0=S - 1, k_pos0=0, window=512, ring_cap=512)
+
+    ms, _ = time_steps(ctx, token, steps, warmup)
+    for a in list(qs) + list(outs) + [x for kv in caches.values() for x in kv]:
+        a.free()
+    algo = 7 * decode_bytes(S, 512) + 28 * decode_bytes(512, 256)
+    return {"us_per_token": ms * 1e3, "algorithmic_bytes": algo, "GB_s": algo / (ms * 1e-3) / 1e9}
+
+
+def prefill(ctx, T, Dh, window, steps, warmup):
+    ins = synth.gemma_inputs(T=T, S=T, Dh=Dh, seed=3, q_pos=np.arange(T))
+    q, k, v = ctx.upload(ins.q), ctx.upload(ins.k), ctx.upload(ins.v)
+    out = ctx.empty((T, HQ * Dh))
+
+    def call():
+        ctx.attention(q.ptr, k.ptr, v.ptr, out.ptr, T=T, S=T, Hq=HQ, Hkv=1, Dh=Dh, Dv=Dh, q_pos0=0, k_pos0=0,
+                      window=window)
+
+    ms, kms = time_steps(ctx, call, steps, warmup)
+    for a in (q, k, v, out):
+        a.free()
+    fl = prefill_flops(T, window, Dh)
+    return {"us": ms * 1e3, "kernel_us": kms * 1e3, "TFLOP_s": fl / (ms * 1e-3) / 1e12, "flops": fl,
+            "frac_fp32_mfma_peak": fl / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+
+
+def load_traffic():
+    p = REPO / "profiles" / "decode_hd512_s32768_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("bytes_per_launch")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline decode only (no extras, no CPU baseline)")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        return 2
+
+    ctx = g4a.Context(0)
+    info = ctx.device_info()
+    print(f"[bench] device {info.arch.decode()} with {info.compute_units} CUs", file=sys.stderr, flush=True)
+
+    # ---- headline: hd512 global decode at 32K context ----
+    head = Decode(ctx, S=32768, Dh=512, seed=4)
+    ms, kms = time_steps(ctx, head.step, args.steps, args.warmup)
+    plan = ctx.plan(**head.kw())
+    head.free()
+    algo = decode_bytes(32768, 512)
+    gbs = algo / (ms * 1e-3) / 1e9
+    kernel_gbs = algo / (kms * 1e-3) / 1e9
+    print(f"[bench] headline decode: {ms * 1e3:.2f} us/step ({gbs:.0f} GB/s); decode kernel {kms * 1e3:.2f} us",
+          file=sys.stderr, flush=True)
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "us_per_step": ms * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded unit-RMS Gaussian q/k, N(0,1) v (splitmix64 + Box-Muller, seed 4)",
+        "config": {
+            "workload": "hd512 global decode @ 32K context (global layer of configs[4])",
+            "q": [1, 8, 512], "kv": [32768, 1, 512], "scale": 1.0, "window": 0,
+            "splits": plan.splits, "keys_per_split": plan.keys_per_split,
+            "cache_busting": f"{BUST_COPIES} K/V copies rotated",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "g4a_decode_d512_g8",
+            "achieved": round(kernel_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
+            "traffic": load_traffic(),
+            "algorithmic_bytes_per_launch": algo,
+            "kernel_us": kms * 1e3,
+        },
+    }
+
+    if not args.quick:
+        extras = {}
+        for name, S, Dh, W, seed in [("configs[0] sliding hd256 S512", 512, 256, 512, 0),
+                                     ("configs[1] global hd512 S8192", 8192, 512, 0, 0),
+                                     ("configs[2] global hd512 S131072", 131072, 512, 0, 2)]:
+            d = Decode(ctx, S=S, Dh=Dh, seed=seed, window=W, copies=1 if S > 100000 else BUST_COPIES)
+            steps = max(10, args.steps // (4 if S > 100000 else 1))
+            m, km = time_steps(ctx, d.step, steps, min(args.warmup, 10))
+            b = decode_bytes(d.visible(), Dh)
+            extras[name] = {"us_per_step": m * 1e3, "kernel_us": km * 1e3, "GB_s": b / (m * 1e-3) / 1e9,
+                            "kernel_GB_s": b / (km * 1e-3) / 1e9, "splits": ctx.plan(**d.kw()).splits}
+            if S > 100000:
+                sweep = {}
+                for sp in (8, 16, 32, 64, 128, 256, 512):
+                    m2, _ = time_steps(ctx, lambda: d.step(sp), 10, 3)
+                    sweep[sp] = round(m2 * 1e3, 2)
+                extras[name]["split_sweep_us"] = sweep
+            d.free()
+            print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
+        for name, T, Dh, W in [("configs[3a] prefill hd256 T2048 window512", 2048, 256, 512),
+                               ("configs[3b] prefill hd512 T2048 causal", 2048, 512, 0)]:
+            extras[name] = prefill(ctx, T, Dh, W, steps=5, warmup=2)
+            print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
+        extras["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=20, warmup=3)
+        print(f"[bench] schedule: {extras['configs[4] 35-layer schedule @32768']}", file=sys.stderr, flush=True)
+        result["extra"] = extras
+        result["prefill_TFLOP_s"] = {k: round(v["TFLOP_s"], 2) for k, v in extras.items() if "prefill" in k}
+    if not (args.quick or args.no_cpu):
+        result["cpu_baseline"] = cpu_baseline()
+        print(f"[bench] cpu baseline: {result['cpu_baseline']}", file=sys.stderr, flush=True)
+    ctx.close()
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

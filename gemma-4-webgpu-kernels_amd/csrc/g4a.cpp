@@ -1,0 +1,548 @@
+// libg4a.so — host side of the MI355X attention path behind the C-ABI in
+// include/g4a.h. Loads the gfx950 code object (g4a_kernels.hsaco) with
+// hipModuleLoad and launches its kernels with hipModuleLaunchKernel on one
+// stream per context. Replaces the wgpu host dispatch of the reference
+// (WgpuBackend::attention / kv_append, rust/src/backend_wgpu.rs:895-1055).
+#include "g4a.h"
+
+#include <dlfcn.h>
+#include <hip/hip_runtime_api.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "kernels/g4a_params.h"
+
+namespace {
+
+// Keys per decode tile; the split-K granularity (a multiple of it).
+constexpr uint32_t TILE = 64;
+// Query tokens from which the query-tiled prefill kernel replaces decode.
+constexpr uint32_t PREFILL_MIN_T = 16;
+// Largest split-K count the LSE combine kernel takes (its LDS weight table).
+constexpr uint32_t MAX_SPLITS = 1024;
+
+std::string g_create_error;
+
+}  // namespace
+
+struct g4a_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipModule_t module = nullptr;
+    hipFunction_t decode[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};  // [dh512][group8]
+    hipFunction_t combine[2] = {nullptr, nullptr};                          // [dh512]
+    hipFunction_t generic = nullptr;
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+    hipEvent_t ev_staging = nullptr;  // last use of the pinned staging buffer
+    void* workspace = nullptr;
+    size_t workspace_bytes = 0;
+    uint32_t* pos_dev = nullptr;  // device copies of non-contiguous positions
+    size_t pos_dev_cap = 0;       // in u32
+    uint32_t* pos_host = nullptr;  // pinned staging for those copies
+    size_t pos_host_cap = 0;
+    int cu_count = 0;
+    // per-kernel event pairs (g4a_kernel_timing)
+    bool timing = false;
+    std::vector<hipEvent_t> kev;  // 2 * kMaxTimed
+    uint32_t kev_used = 0;
+    std::string err;
+};
+
+namespace {
+
+int fail(g4a_ctx* ctx, int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (ctx) ctx->err = buf;
+    else g_create_error = buf;
+    return code;
+}
+
+#define HIP_TRY(ctx, call)                                                                          \
+    do {                                                                                            \
+        hipError_t e_ = (call);                                                                     \
+        if (e_ != hipSuccess) return fail((ctx), G4A_E_HIP, "%s: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+std::string default_hsaco_path() {
+    Dl_info info;
+    if (dladdr(reinterpret_cast<void*>(&g4a_create), &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        size_t slash = p.rfind('/');
+        std::string dir = slash == std::string::npos ? "." : p.substr(0, slash);
+        return dir + "/g4a_kernels.hsaco";
+    }
+    return "g4a_kernels.hsaco";
+}
+
+int get_fn(g4a_ctx* ctx, hipFunction_t* f, const char* name) {
+    hipError_t e = hipModuleGetFunction(f, ctx->module, name);
+    if (e != hipSuccess) return fail(ctx, G4A_E_MODULE, "kernel %s missing from code object: %s", name, hipGetErrorString(e));
+    return G4A_OK;
+}
+
+int ensure_workspace(g4a_ctx* ctx, size_t bytes) {
+    if (bytes <= ctx->workspace_bytes) return G4A_OK;
+    if (ctx->workspace) {
+        // the old buffer may still be read by queued kernels
+        HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        HIP_TRY(ctx, hipFree(ctx->workspace));
+        ctx->workspace = nullptr;
+        ctx->workspace_bytes = 0;
+    }
+    size_t want = std::max<size_t>(bytes, size_t(8) << 20);
+    hipError_t e = hipMalloc(&ctx->workspace, want);
+    if (e != hipSuccess) return fail(ctx, G4A_E_NOMEM, "workspace of %zu bytes: %s", want, hipGetErrorString(e));
+    ctx->workspace_bytes = want;
+    return G4A_OK;
+}
+
+// Stages up to two host position arrays into device memory (stream-ordered).
+// The pinned staging buffer is reused only after its previous copy finished.
+int upload_positions(g4a_ctx* ctx, const uint32_t* a, size_t na, const uint32_t* b, size_t nb, const uint32_t** da,
+                     const uint32_t** db) {
+    const size_t n = na + nb;
+    if (n == 0) return G4A_OK;
+    if (n > ctx->pos_dev_cap) {
+        if (ctx->pos_dev) {
+            HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+            HIP_TRY(ctx, hipFree(ctx->pos_dev));
+            ctx->pos_dev = nullptr;
+        }
+        size_t cap = std::max<size_t>(n, 1 << 16);
+        if (hipMalloc(&ctx->pos_dev, cap * sizeof(uint32_t)) != hipSuccess)
+            return fail(ctx, G4A_E_NOMEM, "position buffer of %zu entries", cap);
+        ctx->pos_dev_cap = cap;
+    }
+    HIP_TRY(ctx, hipEventSynchronize(ctx->ev_staging));
+    if (n > ctx->pos_host_cap) {
+        if (ctx->pos_host) HIP_TRY(ctx, hipHostFree(ctx->pos_host));
+        ctx->pos_host = nullptr;
+        size_t cap = std::max<size_t>(n, 1 << 16);
+        if (hipHostMalloc(reinterpret_cast<void**>(&ctx->pos_host), cap * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
+            return fail(ctx, G4A_E_NOMEM, "pinned staging of %zu entries", cap);
+        ctx->pos_host_cap = cap;
+    }
+    if (na) memcpy(ctx->pos_host, a, na * sizeof(uint32_t));
+    if (nb) memcpy(ctx->pos_host + na, b, nb * sizeof(uint32_t));
+    HIP_TRY(ctx, hipMemcpyAsync(ctx->pos_dev, ctx->pos_host, n * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(ctx, hipEventRecord(ctx->ev_staging, ctx->stream));
+    if (da) *da = na ? ctx->pos_dev : nullptr;
+    if (db) *db = nb ? ctx->pos_dev + na : nullptr;
+    return G4A_OK;
+}
+
+constexpr uint32_t kMaxTimed = 4096;
+
+// Launches one kernel; `timed` brackets it with an event pair when per-kernel
+// timing is on (the main kernel of an attention call).
+template <typename P>
+int launch(g4a_ctx* ctx, hipFunction_t f, dim3 grid, dim3 block, const P& params, const char* what,
+           bool timed = false) {
+    P copy = params;
+    void* args[] = {&copy};
+    const bool rec = timed && ctx->timing && ctx->kev_used < kMaxTimed;
+    if (rec) HIP_TRY(ctx, hipEventRecord(ctx->kev[2 * ctx->kev_used], ctx->stream));
+    hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, ctx->stream, args, nullptr);
+    if (e != hipSuccess) return fail(ctx, G4A_E_HIP, "launch %s: %s", what, hipGetErrorString(e));
+    if (rec) {
+        HIP_TRY(ctx, hipEventRecord(ctx->kev[2 * ctx->kev_used + 1], ctx->stream));
+        ++ctx->kev_used;
+    }
+    return G4A_OK;
+}
+
+// Host-side analysis shared by g4a_attention and g4a_attention_plan.
+struct Analysis {
+    g4a_attn_plan plan{};
+    bool q_contig = true, k_contig = true, k_ascending = true;
+    uint32_t qmin = 0, qmax = 0;
+    bool fast_shape = false;
+};
+
+uint32_t kpos_at(const g4a_attn_args* a, uint32_t j) { return a->k_pos ? a->k_pos[j] : a->k_pos0 + j; }
+
+// First index j in [0, S) for which pred(kpos(j)) is false, for a predicate
+// that is true on a prefix (Rust's slice::partition_point).
+template <typename Pred>
+uint32_t partition_point(const g4a_attn_args* a, Pred pred) {
+    uint32_t lo = 0, hi = a->S;
+    while (lo < hi) {
+        uint32_t mid = lo + (hi - lo) / 2;
+        if (pred(kpos_at(a, mid))) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+int analyse(g4a_ctx* ctx, const g4a_attn_args* a, Analysis* an, bool check_pointers) {
+    if (!a) return fail(ctx, G4A_E_ARG, "null args");
+    if (a->Hq == 0 || a->Hkv == 0 || a->Dh == 0 || a->Dv == 0)
+        return fail(ctx, G4A_E_SHAPE, "zero dimension (Hq=%u Hkv=%u Dh=%u Dv=%u)", a->Hq, a->Hkv, a->Dh, a->Dv);
+    if (a->Hq % a->Hkv != 0) return fail(ctx, G4A_E_SHAPE, "Hq=%u is not a multiple of Hkv=%u", a->Hq, a->Hkv);
+    if (!(a->attn_softcap >= 0.0f)) return fail(ctx, G4A_E_ARG, "attn_softcap must be >= 0");
+    Analysis& r = *an;
+    r = Analysis{};
+    if (a->T == 0) return G4A_OK;
+    if (check_pointers) {
+        if (!a->q || !a->out) return fail(ctx, G4A_E_ARG, "null q/out");
+        if (a->S > 0 && (!a->k || !a->v)) return fail(ctx, G4A_E_ARG, "null k/v");
+    }
+    // query positions
+    if (a->q_pos) {
+        r.qmin = r.qmax = a->q_pos[0];
+        for (uint32_t i = 0; i < a->T; ++i) {
+            uint32_t p = a->q_pos[i];
+            r.qmin = std::min(r.qmin, p);
+            r.qmax = std::max(r.qmax, p);
+            if (p != a->q_pos[0] + i) r.q_contig = false;
+        }
+    } else {
+        r.qmin = a->q_pos0;
+        r.qmax = a->q_pos0 + (a->T - 1);
+    }
+    if (a->k_pos) {
+        for (uint32_t j = 0; j < a->S; ++j) {
+            if (a->k_pos[j] != a->k_pos[0] + j) r.k_contig = false;
+            if (j && a->k_pos[j] < a->k_pos[j - 1]) r.k_ascending = false;
+        }
+    }
+    // active key range shared by every query (rust/src/backend_wgpu.rs:929-936)
+    uint32_t k_start = 0, k_end = a->S;
+    if (r.k_ascending) {
+        const uint64_t qmax = r.qmax, qmin = r.qmin, win = a->sliding_window;
+        k_end = partition_point(a, [&](uint32_t kp) { return uint64_t(kp) <= qmax; });
+        if (win > 0 && qmin >= win)
+            k_start = std::min(k_end, partition_point(a, [&](uint32_t kp) { return uint64_t(kp) + win <= qmin; }));
+    }
+    r.plan.k_start = k_start;
+    r.plan.k_end = k_end;
+    if (a->kv_ring_cap && k_end - k_start > a->kv_ring_cap)
+        return fail(ctx, G4A_E_SHAPE, "visible key range [%u, %u) exceeds the KV ring of %u rows", k_start, k_end,
+                    a->kv_ring_cap);
+    const uint32_t group = a->Hq / a->Hkv;
+    r.fast_shape = (group == 4 || group == 8) && a->Dh == a->Dv && (a->Dh == 256 || a->Dh == 512) &&
+                   r.k_ascending && (a->kv_ring_cap == 0 || a->kv_ring_cap >= TILE);
+    const uint32_t nkeys = k_end - k_start;
+    if (nkeys == 0) {
+        r.plan.kernel = G4A_KERNEL_NONE;  // every row sees no key: zero output
+        return G4A_OK;
+    }
+    if (!r.fast_shape) {
+        if (a->Dh > 1024 || a->Dv > 1024)
+            return fail(ctx, G4A_E_UNSUPPORTED, "generic attention handles Dh, Dv <= 1024 (got %u, %u)", a->Dh, a->Dv);
+        r.plan.kernel = G4A_KERNEL_GENERIC;
+        r.plan.splits = 1;
+        r.plan.keys_per_split = nkeys;
+        return G4A_OK;
+    }
+    r.plan.kernel = G4A_KERNEL_DECODE;
+    const uint32_t kt = 4 / (group / 4);  // key-tile slots per workgroup
+    const uint32_t tiles = (nkeys + TILE - 1) / TILE;
+    uint32_t splits;
+    if (a->splits) {
+        splits = std::min(a->splits, tiles);
+    } else {
+        // fill the GPU with one sequence: about two workgroups per CU
+        const uint64_t target = uint64_t(2) * std::max(ctx ? ctx->cu_count : 256, 1);
+        const uint64_t per_query = std::max<uint64_t>(1, target / (uint64_t(a->T) * a->Hkv));
+        splits = uint32_t(std::min<uint64_t>(per_query, (tiles + kt - 1) / kt));
+    }
+    splits = std::min(std::max(splits, 1u), MAX_SPLITS);
+    uint32_t kps = (nkeys + splits - 1) / splits;
+    kps = (kps + TILE - 1) / TILE * TILE;
+    splits = (nkeys + kps - 1) / kps;
+    r.plan.splits = splits;
+    r.plan.keys_per_split = kps;
+    r.plan.workspace_bytes = splits > 1 ? size_t(a->T) * a->Hq * splits * (a->Dh + 2) * sizeof(float) : 0;
+    return G4A_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
+    if (!out) return fail(nullptr, G4A_E_ARG, "null out");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) return fail(nullptr, G4A_E_HIP, "no HIP device (%s)", hipGetErrorString(e));
+    if (device < 0 || device >= n) return fail(nullptr, G4A_E_ARG, "device %d out of range [0, %d)", device, n);
+    g4a_ctx* ctx = new g4a_ctx();
+    ctx->device = device;
+    auto bail = [&](int code) {
+        g_create_error = ctx->err;
+        g4a_destroy(ctx);
+        return code;
+    };
+    if (hipSetDevice(device) != hipSuccess) {
+        fail(ctx, G4A_E_HIP, "hipSetDevice(%d) failed", device);
+        return bail(G4A_E_HIP);
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        fail(ctx, G4A_E_HIP, "hipGetDeviceProperties failed");
+        return bail(G4A_E_HIP);
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        fail(ctx, G4A_E_UNSUPPORTED, "device %d is %s; this build targets gfx950 (MI355X)", device, prop.gcnArchName);
+        return bail(G4A_E_UNSUPPORTED);
+    }
+    ctx->cu_count = prop.multiProcessorCount;
+    std::string path = hsaco_path ? std::string(hsaco_path) : default_hsaco_path();
+    e = hipModuleLoad(&ctx->module, path.c_str());
+    if (e != hipSuccess) {
+        fail(ctx, G4A_E_MODULE, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
+        return bail(G4A_E_MODULE);
+    }
+    const char* names[2][2] = {{"g4a_decode_d256_g4", "g4a_decode_d256_g8"}, {"g4a_decode_d512_g4", "g4a_decode_d512_g8"}};
+    for (int d = 0; d < 2; ++d)
+        for (int g = 0; g < 2; ++g)
+            if (int rc = get_fn(ctx, &ctx->decode[d][g], names[d][g])) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->combine[0], "g4a_combine_d256")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->combine[1], "g4a_combine_d512")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->generic, "g4a_generic_attention")) return bail(rc);
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&ctx->ev_start) != hipSuccess || hipEventCreate(&ctx->ev_stop) != hipSuccess ||
+        hipEventCreateWithFlags(&ctx->ev_staging, hipEventDisableTiming) != hipSuccess) {
+        fail(ctx, G4A_E_HIP, "stream/event creation failed");
+        return bail(G4A_E_HIP);
+    }
+    *out = ctx;
+    return G4A_OK;
+}
+
+void g4a_destroy(g4a_ctx* ctx) {
+    if (!ctx) return;
+    if (ctx->stream) hipStreamSynchronize(ctx->stream);
+    for (hipEvent_t ev : ctx->kev) hipEventDestroy(ev);
+    if (ctx->workspace) hipFree(ctx->workspace);
+    if (ctx->pos_dev) hipFree(ctx->pos_dev);
+    if (ctx->pos_host) hipHostFree(ctx->pos_host);
+    if (ctx->ev_start) hipEventDestroy(ctx->ev_start);
+    if (ctx->ev_stop) hipEventDestroy(ctx->ev_stop);
+    if (ctx->ev_staging) hipEventDestroy(ctx->ev_staging);
+    if (ctx->stream) hipStreamDestroy(ctx->stream);
+    if (ctx->module) hipModuleUnload(ctx->module);
+    delete ctx;
+}
+
+const char* g4a_last_error(const g4a_ctx* ctx) { return ctx ? ctx->err.c_str() : g_create_error.c_str(); }
+
+int g4a_malloc(g4a_ctx* ctx, size_t bytes, void** dptr) {
+    if (!ctx || !dptr) return fail(ctx, G4A_E_ARG, "null ctx/dptr");
+    hipError_t e = hipMalloc(dptr, std::max<size_t>(bytes, 16));
+    if (e != hipSuccess) return fail(ctx, G4A_E_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    return G4A_OK;
+}
+
+int g4a_free(g4a_ctx* ctx, void* dptr) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (dptr) HIP_TRY(ctx, hipFree(dptr));
+    return G4A_OK;
+}
+
+int g4a_h2d(g4a_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return fail(ctx, G4A_E_ARG, "null pointer");
+    if (bytes) HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    // the caller may reuse `src` on return: make the copy complete
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return G4A_OK;
+}
+
+int g4a_d2h(g4a_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return fail(ctx, G4A_E_ARG, "null pointer");
+    if (bytes) HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return G4A_OK;
+}
+
+int g4a_d2d(g4a_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return fail(ctx, G4A_E_ARG, "null pointer");
+    if (bytes) HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return G4A_OK;
+}
+
+int g4a_zero(g4a_ctx* ctx, void* dst, size_t bytes) {
+    if (!ctx || (bytes && !dst)) return fail(ctx, G4A_E_ARG, "null pointer");
+    if (bytes) HIP_TRY(ctx, hipMemsetAsync(dst, 0, bytes, ctx->stream));
+    return G4A_OK;
+}
+
+int g4a_sync(g4a_ctx* ctx) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return G4A_OK;
+}
+
+int g4a_attention_plan(g4a_ctx* ctx, const g4a_attn_args* a, g4a_attn_plan* plan) {
+    if (!plan) return fail(ctx, G4A_E_ARG, "null plan");
+    Analysis an;
+    if (int rc = analyse(ctx, a, &an, false)) return rc;
+    *plan = an.plan;
+    return G4A_OK;
+}
+
+int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    Analysis an;
+    if (int rc = analyse(ctx, a, &an, true)) return rc;
+    const g4a_attn_plan& pl = an.plan;
+    if (a->T == 0) return G4A_OK;
+    const size_t out_bytes = size_t(a->T) * a->Hq * a->Dv * sizeof(float);
+    if (pl.kernel == G4A_KERNEL_NONE) {
+        HIP_TRY(ctx, hipMemsetAsync(a->out, 0, out_bytes, ctx->stream));
+        return G4A_OK;
+    }
+    const uint32_t group = a->Hq / a->Hkv;
+    if (pl.kernel == G4A_KERNEL_GENERIC) {
+        const uint32_t *qd = nullptr, *kd = nullptr;
+        std::vector<uint32_t> qtmp, ktmp;
+        const uint32_t* qh = a->q_pos;
+        const uint32_t* kh = a->k_pos;
+        if (!qh) {
+            qtmp.resize(a->T);
+            for (uint32_t i = 0; i < a->T; ++i) qtmp[i] = a->q_pos0 + i;
+            qh = qtmp.data();
+        }
+        if (!kh) {
+            ktmp.resize(a->S);
+            for (uint32_t j = 0; j < a->S; ++j) ktmp[j] = a->k_pos0 + j;
+            kh = ktmp.data();
+        }
+        if (int rc = upload_positions(ctx, qh, a->T, kh, a->S, &qd, &kd)) return rc;
+        G4aGenericParams gp{a->q, a->k, a->v, a->out, qd, kd, a->T, a->S, a->Hq, a->Hkv, a->Dh, a->Dv,
+                            pl.k_start, pl.k_end, a->kv_ring_cap, a->sliding_window, a->scale, a->attn_softcap};
+        return launch(ctx, ctx->generic, dim3(a->Hq, a->T, 1), dim3(64, 1, 1), gp, "generic attention", true);
+    }
+    // split-K flash-decode (+ combine)
+    const uint32_t *qd = nullptr, *kd = nullptr;
+    if (!an.q_contig || !an.k_contig) {
+        if (int rc = upload_positions(ctx, an.q_contig ? nullptr : a->q_pos, an.q_contig ? 0 : a->T,
+                                      an.k_contig ? nullptr : a->k_pos, an.k_contig ? 0 : a->S, &qd, &kd))
+            return rc;
+    }
+    if (pl.splits > 1)
+        if (int rc = ensure_workspace(ctx, pl.workspace_bytes)) return rc;
+    G4aDecodeParams dp{};
+    dp.q = a->q;
+    dp.k = a->k;
+    dp.v = a->v;
+    dp.out = a->out;
+    dp.part = static_cast<float*>(ctx->workspace);
+    dp.q_pos = qd;
+    dp.k_pos = kd;
+    dp.q_pos0 = a->q_pos ? a->q_pos[0] : a->q_pos0;
+    dp.k_pos0 = a->k_pos ? (a->S ? a->k_pos[0] : 0) : a->k_pos0;
+    dp.T = a->T;
+    dp.Hq = a->Hq;
+    dp.Hkv = a->Hkv;
+    dp.k_start = pl.k_start;
+    dp.k_end = pl.k_end;
+    dp.keys_per_split = pl.keys_per_split;
+    dp.nsplit = pl.splits;
+    dp.ring_cap = a->kv_ring_cap;
+    dp.window = a->sliding_window;
+    dp.scale = a->scale;
+    dp.softcap = a->attn_softcap;
+    const int d512 = a->Dh == 512 ? 1 : 0;
+    const int g8 = group == 8 ? 1 : 0;
+    if (int rc = launch(ctx, ctx->decode[d512][g8], dim3(pl.splits, a->T, a->Hkv), dim3(256, 1, 1), dp, "decode", true))
+        return rc;
+    if (pl.splits > 1) {
+        G4aCombineParams cp{dp.part, a->out, a->T, a->Hq, pl.splits, a->Dh};
+        if (int rc = launch(ctx, ctx->combine[d512], dim3(a->Dh / 64, a->Hq, a->T), dim3(256, 1, 1), cp, "combine"))
+            return rc;
+    }
+    return G4A_OK;
+}
+
+int g4a_kv_write(g4a_ctx* ctx, float* cache, uint32_t ring_cap, uint32_t row_elems, uint32_t dst_row, const float* src,
+                 uint32_t n_rows) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (n_rows == 0) return G4A_OK;
+    if (!cache || !src || row_elems == 0) return fail(ctx, G4A_E_ARG, "null cache/src or zero row size");
+    const size_t row_bytes = size_t(row_elems) * sizeof(float);
+    if (ring_cap == 0) {
+        HIP_TRY(ctx, hipMemcpyAsync(cache + size_t(dst_row) * row_elems, src, n_rows * row_bytes,
+                                    hipMemcpyDeviceToDevice, ctx->stream));
+        return G4A_OK;
+    }
+    // only the last ring_cap rows survive
+    uint32_t skip = n_rows > ring_cap ? n_rows - ring_cap : 0;
+    uint64_t first = uint64_t(dst_row) + skip;
+    uint32_t n = n_rows - skip;
+    uint32_t slot = uint32_t(first % ring_cap);
+    uint32_t n1 = std::min(n, ring_cap - slot);
+    HIP_TRY(ctx, hipMemcpyAsync(cache + size_t(slot) * row_elems, src + size_t(skip) * row_elems, n1 * row_bytes,
+                                hipMemcpyDeviceToDevice, ctx->stream));
+    if (n1 < n)
+        HIP_TRY(ctx, hipMemcpyAsync(cache, src + size_t(skip + n1) * row_elems, size_t(n - n1) * row_bytes,
+                                    hipMemcpyDeviceToDevice, ctx->stream));
+    return G4A_OK;
+}
+
+int g4a_timer_start(g4a_ctx* ctx) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    HIP_TRY(ctx, hipEventRecord(ctx->ev_start, ctx->stream));
+    return G4A_OK;
+}
+
+int g4a_timer_stop(g4a_ctx* ctx, float* ms) {
+    if (!ctx || !ms) return fail(ctx, G4A_E_ARG, "null ctx/ms");
+    HIP_TRY(ctx, hipEventRecord(ctx->ev_stop, ctx->stream));
+    HIP_TRY(ctx, hipEventSynchronize(ctx->ev_stop));
+    HIP_TRY(ctx, hipEventElapsedTime(ms, ctx->ev_start, ctx->ev_stop));
+    return G4A_OK;
+}
+
+int g4a_kernel_timing(g4a_ctx* ctx, int enable) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (enable && ctx->kev.empty()) {
+        ctx->kev.resize(2 * kMaxTimed, nullptr);
+        for (auto& ev : ctx->kev) HIP_TRY(ctx, hipEventCreate(&ev));
+    }
+    if (ctx->kev_used) HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    ctx->timing = enable != 0;
+    ctx->kev_used = 0;
+    return G4A_OK;
+}
+
+int g4a_kernel_timing_read(g4a_ctx* ctx, double* total_ms, uint32_t* count) {
+    if (!ctx || !total_ms || !count) return fail(ctx, G4A_E_ARG, "null argument");
+    double sum = 0.0;
+    for (uint32_t i = 0; i < ctx->kev_used; ++i) {
+        float ms = 0.0f;
+        HIP_TRY(ctx, hipEventSynchronize(ctx->kev[2 * i + 1]));
+        HIP_TRY(ctx, hipEventElapsedTime(&ms, ctx->kev[2 * i], ctx->kev[2 * i + 1]));
+        sum += ms;
+    }
+    *total_ms = sum;
+    *count = ctx->kev_used;
+    ctx->kev_used = 0;
+    return G4A_OK;
+}
+
+int g4a_get_device_info(g4a_ctx* ctx, g4a_device_info* info) {
+    if (!ctx || !info) return fail(ctx, G4A_E_ARG, "null ctx/info");
+    hipDeviceProp_t prop;
+    HIP_TRY(ctx, hipGetDeviceProperties(&prop, ctx->device));
+    memset(info, 0, sizeof *info);
+    info->device = ctx->device;
+    info->compute_units = prop.multiProcessorCount;
+    info->clock_khz = prop.clockRate;
+    info->total_mem = prop.totalGlobalMem;
+    snprintf(info->arch, sizeof info->arch, "%s", prop.gcnArchName);
+    return G4A_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,291 @@
+"""Python binding of libg4a.so (include/g4a.h) over ctypes.
+
+Host-side plumbing for the tests and the benchmark: device buffers, the
+attention op with the reference's AttnOpts semantics
+(rust/src/backend.rs:59-69), KV writes and stream timers. Every call goes
+through the C-ABI; nothing here computes attention. Loading fails loudly when
+the library or its gfx950 code object has not been built.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Optional, Sequence
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parents[1]
+BUILD_DIR = PKG_DIR / "_build"
+LIB_PATH = BUILD_DIR / "libg4a.so"
+HSACO_PATH = BUILD_DIR / "g4a_kernels.hsaco"
+HEADER_PATH = PKG_DIR.parent / "include" / "g4a.h"
+
+G4A_OK = 0
+KERNEL_NAMES = {0: "none", 1: "decode", 2: "prefill", 3: "generic"}
+
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_f32p = ctypes.c_void_p
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("out", ctypes.c_void_p),
+        ("T", ctypes.c_uint32), ("S", ctypes.c_uint32), ("Hq", ctypes.c_uint32), ("Hkv", ctypes.c_uint32),
+        ("Dh", ctypes.c_uint32), ("Dv", ctypes.c_uint32),
+        ("q_pos", _u32p), ("k_pos", _u32p), ("q_pos0", ctypes.c_uint32), ("k_pos0", ctypes.c_uint32),
+        ("scale", ctypes.c_float), ("sliding_window", ctypes.c_uint32), ("attn_softcap", ctypes.c_float),
+        ("kv_ring_cap", ctypes.c_uint32), ("splits", ctypes.c_uint32),
+    ]
+
+
+class AttnPlan(ctypes.Structure):
+    _fields_ = [
+        ("kernel", ctypes.c_uint32), ("k_start", ctypes.c_uint32), ("k_end", ctypes.c_uint32),
+        ("splits", ctypes.c_uint32), ("keys_per_split", ctypes.c_uint32), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [
+        ("device", ctypes.c_int), ("compute_units", ctypes.c_int), ("clock_khz", ctypes.c_int),
+        ("total_mem", ctypes.c_size_t), ("arch", ctypes.c_char * 64),
+    ]
+
+
+class G4aError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"g4a error {code}: {msg}")
+        self.code = code
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
+    """Load libg4a.so and declare its C-ABI. Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not Path(path).exists():
+        raise RuntimeError(f"{path} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()')")
+    lib = ctypes.CDLL(str(path))
+    vp, sz, c_int = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+    ctxp = ctypes.c_void_p
+    sig = {
+        "g4a_create": (c_int, [c_int, ctypes.c_char_p, ctypes.POINTER(ctxp)]),
+        "g4a_destroy": (None, [ctxp]),
+        "g4a_last_error": (ctypes.c_char_p, [ctxp]),
+        "g4a_malloc": (c_int, [ctxp, sz, ctypes.POINTER(vp)]),
+        "g4a_free": (c_int, [ctxp, vp]),
+        "g4a_h2d": (c_int, [ctxp, vp, vp, sz]),
+        "g4a_d2h": (c_int, [ctxp, vp, vp, sz]),
+        "g4a_d2d": (c_int, [ctxp, vp, vp, sz]),
+        "g4a_zero": (c_int, [ctxp, vp, sz]),
+        "g4a_sync": (c_int, [ctxp]),
+        "g4a_attention": (c_int, [ctxp, ctypes.POINTER(AttnArgs)]),
+        "g4a_attention_plan": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.POINTER(AttnPlan)]),
+        "g4a_kv_write": (c_int, [ctxp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32]),
+        "g4a_timer_start": (c_int, [ctxp]),
+        "g4a_timer_stop": (c_int, [ctxp, ctypes.POINTER(ctypes.c_float)]),
+        "g4a_get_device_info": (c_int, [ctxp, ctypes.POINTER(DeviceInfo)]),
+        "g4a_kernel_timing": (c_int, [ctxp, c_int]),
+        "g4a_kernel_timing_read": (c_int, [ctxp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_uint32)]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def header_functions(header: Path = HEADER_PATH) -> list[str]:
+    """Names of every function include/g4a.h declares."""
+    import re
+    text = Path(header).read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|void|const char \*)\s*\**\s*(g4a_\w+)\s*\(", text, re.M)))
+
+
+def _u32_array(xs: Optional[Sequence[int]]):
+    if xs is None:
+        return None, None
+    arr = np.ascontiguousarray(np.asarray(xs, dtype=np.uint32))
+    return arr, arr.ctypes.data_as(_u32p)
+
+
+def make_args(q=0, k=0, v=0, out=0, *, T, S, Hq, Hkv, Dh, Dv, q_pos=None, k_pos=None, q_pos0=0, k_pos0=0,
+              scale=1.0, window=0, softcap=0.0, ring_cap=0, splits=0):
+    """Build g4a_attn_args. Returns (args, keepalive) — keep the second alive during the call."""
+    qa, qp = _u32_array(q_pos)
+    ka, kp = _u32_array(k_pos)
+    a = AttnArgs(q or None, k or None, v or None, out or None, T, S, Hq, Hkv, Dh, Dv, qp, kp, q_pos0, k_pos0,
+                 scale, window, softcap, ring_cap, splits)
+    return a, (qa, ka)
+
+
+def plan(ctx: Optional["Context"] = None, **kw) -> AttnPlan:
+    """Launch plan for an attention call (host-only; works without a GPU when ctx is None)."""
+    lib = load_library()
+    a, keep = make_args(**kw)
+    p = AttnPlan()
+    rc = lib.g4a_attention_plan(ctx.handle if ctx else None, ctypes.byref(a), ctypes.byref(p))
+    if rc != G4A_OK:
+        raise G4aError(rc, lib.g4a_last_error(ctx.handle if ctx else None).decode())
+    return p
+
+
+@dataclass
+class DeviceArray:
+    ctx: "Context"
+    ptr: int
+    shape: tuple
+    dtype: np.dtype
+
+    @property
+    def nbytes(self) -> int:
+        return int(np.prod(self.shape, dtype=np.int64)) * np.dtype(self.dtype).itemsize
+
+    def to_host(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.dtype)
+        self.ctx.d2h(out, self.ptr)
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            self.ctx.free(self.ptr)
+            self.ptr = 0
+
+
+class Context:
+    """One g4a context: a device, its gfx950 module, one stream."""
+
+    def __init__(self, device: int = 0, hsaco: Optional[Path] = None):
+        self.lib = load_library()
+        h = ctypes.c_void_p()
+        path = str(hsaco).encode() if hsaco else None
+        rc = self.lib.g4a_create(device, path, ctypes.byref(h))
+        if rc != G4A_OK:
+            raise G4aError(rc, self.lib.g4a_last_error(None).decode())
+        self.handle = h
+
+    def _check(self, rc: int) -> None:
+        if rc != G4A_OK:
+            raise G4aError(rc, self.lib.g4a_last_error(self.handle).decode())
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.g4a_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ---- memory ----
+    def malloc(self, nbytes: int) -> int:
+        p = ctypes.c_void_p()
+        self._check(self.lib.g4a_malloc(self.handle, nbytes, ctypes.byref(p)))
+        return p.value
+
+    def free(self, ptr: int) -> None:
+        self._check(self.lib.g4a_free(self.handle, ptr))
+
+    def h2d(self, dst: int, host: np.ndarray) -> None:
+        host = np.ascontiguousarray(host)
+        self._check(self.lib.g4a_h2d(self.handle, dst, host.ctypes.data, host.nbytes))
+
+    def d2h(self, host: np.ndarray, src: int) -> None:
+        assert host.flags.c_contiguous
+        self._check(self.lib.g4a_d2h(self.handle, host.ctypes.data, src, host.nbytes))
+
+    def d2d(self, dst: int, src: int, nbytes: int) -> None:
+        self._check(self.lib.g4a_d2d(self.handle, dst, src, nbytes))
+
+    def zero(self, dst: int, nbytes: int) -> None:
+        self._check(self.lib.g4a_zero(self.handle, dst, nbytes))
+
+    def sync(self) -> None:
+        self._check(self.lib.g4a_sync(self.handle))
+
+    def upload(self, host: np.ndarray) -> DeviceArray:
+        host = np.ascontiguousarray(host)
+        ptr = self.malloc(max(host.nbytes, 16))
+        self.h2d(ptr, host)
+        return DeviceArray(self, ptr, tuple(host.shape), host.dtype)
+
+    def empty(self, shape, dtype=np.float32) -> DeviceArray:
+        n = int(np.prod(shape, dtype=np.int64)) * np.dtype(dtype).itemsize
+        return DeviceArray(self, self.malloc(max(n, 16)), tuple(shape), np.dtype(dtype))
+
+    # ---- ops ----
+    def attention(self, q: int, k: int, v: int, out: int, **kw) -> None:
+        a, keep = make_args(q, k, v, out, **kw)
+        self._check(self.lib.g4a_attention(self.handle, ctypes.byref(a)))
+
+    def plan(self, **kw) -> AttnPlan:
+        return plan(self, **kw)
+
+    def kv_write(self, cache: int, ring_cap: int, row_elems: int, dst_row: int, src: int, n_rows: int) -> None:
+        self._check(self.lib.g4a_kv_write(self.handle, cache, ring_cap, row_elems, dst_row, src, n_rows))
+
+    def timer_start(self) -> None:
+        self._check(self.lib.g4a_timer_start(self.handle))
+
+    def timer_stop(self) -> float:
+        ms = ctypes.c_float()
+        self._check(self.lib.g4a_timer_stop(self.handle, ctypes.byref(ms)))
+        return float(ms.value)
+
+    def kernel_timing(self, enable: bool) -> None:
+        self._check(self.lib.g4a_kernel_timing(self.handle, 1 if enable else 0))
+
+    def kernel_timing_read(self) -> tuple[float, int]:
+        """(summed ms, count) of the main-kernel event pairs recorded since the last read."""
+        ms, n = ctypes.c_double(), ctypes.c_uint32()
+        self._check(self.lib.g4a_kernel_timing_read(self.handle, ctypes.byref(ms), ctypes.byref(n)))
+        return float(ms.value), int(n.value)
+
+    def device_info(self) -> DeviceInfo:
+        info = DeviceInfo()
+        self._check(self.lib.g4a_get_device_info(self.handle, ctypes.byref(info)))
+        return info
+
+
+def attention_host(ctx: Context, q: np.ndarray, k: np.ndarray, v: np.ndarray, *, q_pos=None, k_pos=None,
+                   scale: float = 1.0, window: int = 0, softcap: float = 0.0, splits: int = 0,
+                   contiguous_positions: bool = True) -> np.ndarray:
+    """Backend::attention on host arrays: q [T,Hq,Dh], k [S,Hkv,Dh], v [S,Hkv,Dv] -> [T, Hq*Dv].
+
+    Positions default to the model's convention (k_pos = 0..S-1, q_pos = the
+    last T positions). With contiguous_positions the ranges are passed as
+    scalars (no upload), otherwise as explicit host arrays.
+    """
+    T, Hq, Dh = q.shape
+    S, Hkv, _ = k.shape
+    Dv = v.shape[2]
+    if k_pos is None:
+        k_pos = np.arange(S, dtype=np.uint32)
+    if q_pos is None:
+        q_pos = np.arange(S - T, S, dtype=np.uint32) if S >= T else np.arange(T, dtype=np.uint32)
+    q_pos = np.asarray(q_pos, np.uint32)
+    k_pos = np.asarray(k_pos, np.uint32)
+    bufs = [ctx.upload(np.ascontiguousarray(x, np.float32)) for x in (q, k, v)]
+    out = ctx.empty((T, Hq * Dv))
+    try:
+        kw = dict(T=T, S=S, Hq=Hq, Hkv=Hkv, Dh=Dh, Dv=Dv, scale=scale, window=window, softcap=softcap,
+                  splits=splits)
+        q_contig = T == 0 or bool(np.all(q_pos == q_pos[0] + np.arange(T, dtype=np.uint32)))
+        k_contig = S == 0 or bool(np.all(k_pos == k_pos[0] + np.arange(S, dtype=np.uint32)))
+        if contiguous_positions and q_contig and k_contig:
+            kw.update(q_pos0=int(q_pos[0]) if T else 0, k_pos0=int(k_pos[0]) if S else 0)
+        else:
+            kw.update(q_pos=q_pos, k_pos=k_pos)
+        ctx.attention(bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, out.ptr, **kw)
+        return out.to_host()
+    finally:
+        for b in bufs:
+            b.free()
+        out.free()

@@ -1,0 +1,174 @@
+"""Deterministic synthetic inputs for the attention path.
+
+Two generators:
+
+* `normal_f32(seed, stream, n)` — splitmix64 -> Box–Muller N(0,1) -> f32, the
+  generator of the benchmark configurations. The reference has only uniform
+  RNGs (rust/tests/common/mod.rs:15-42, rust/src/main.rs:306-333), so this one
+  is ours; it is fully specified here so any implementation can reproduce it.
+* `Lcg` — the LCG of the reference's parity tests
+  (rust/tests/common/mod.rs:29-42), bit-exact in f32, so the inputs of
+  `grouped_attention_parity` / `kernel_parity` can be regenerated.
+
+Query and key rows are RMS-normalised per head with the reference's unweighted
+rms_norm (rust/src/backend_cpu.rs:149-172, eps 1e-6 from
+rust/assets/config.json): sequential f32 sum of squares, inv = 1/sqrt(ss/d+eps),
+y = x*inv.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+_GOLDEN = np.uint64(0x9E3779B97F4A7C15)
+_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_M2 = np.uint64(0x94D049BB133111EB)
+RMS_EPS = np.float32(1e-6)
+
+
+def _mix(z: np.ndarray) -> np.ndarray:
+    z = (z ^ (z >> np.uint64(30))) * _M1
+    z = (z ^ (z >> np.uint64(27))) * _M2
+    return z ^ (z >> np.uint64(31))
+
+
+def splitmix64(seed: int, stream: int, n: int) -> np.ndarray:
+    """n outputs of splitmix64 whose state starts at mix(seed*16 + stream)."""
+    with np.errstate(over="ignore"):
+        base = _mix(np.array([np.uint64(seed * 16 + stream)], dtype=np.uint64))[0]
+        idx = np.arange(1, n + 1, dtype=np.uint64)
+        return _mix(base + idx * _GOLDEN)
+
+
+def normal_f32(seed: int, stream: int, n: int) -> np.ndarray:
+    """n N(0,1) samples: Box–Muller on pairs of 53-bit uniforms, computed in f64, rounded to f32."""
+    m = (n + 1) // 2
+    bits = splitmix64(seed, stream, 2 * m) >> np.uint64(11)
+    u1 = (bits[0::2].astype(np.float64) + 1.0) * (1.0 / 9007199254740992.0)  # (0, 1]
+    u2 = bits[1::2].astype(np.float64) * (1.0 / 9007199254740992.0)  # [0, 1)
+    r = np.sqrt(-2.0 * np.log(u1))
+    t = 2.0 * np.pi * u2
+    out = np.empty(2 * m, dtype=np.float64)
+    out[0::2] = r * np.cos(t)
+    out[1::2] = r * np.sin(t)
+    return out[:n].astype(np.float32)
+
+
+def rms_norm_rows(x: np.ndarray, eps: np.float32 = RMS_EPS) -> np.ndarray:
+    """Unweighted per-row RMSNorm over the last axis with the reference's f32 arithmetic order."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    d = x.shape[-1]
+    flat = x.reshape(-1, d)
+    ss = np.zeros(flat.shape[0], dtype=np.float32)
+    for j in range(d):  # sequential sum, vectorised across rows
+        col = flat[:, j]
+        ss = ss + col * col
+    inv = np.float32(1.0) / np.sqrt(ss / np.float32(d) + eps)
+    return (flat * inv[:, None]).reshape(x.shape).astype(np.float32)
+
+
+@dataclass
+class AttnInputs:
+    q: np.ndarray  # [T, Hq, Dh]
+    k: np.ndarray  # [S, Hkv, Dh]
+    v: np.ndarray  # [S, Hkv, Dv]
+    q_pos: np.ndarray  # [T] u32
+    k_pos: np.ndarray  # [S] u32
+
+
+def gemma_inputs(T: int, S: int, Dh: int, seed: int, Hq: int = 8, Hkv: int = 1, Dv: int | None = None,
+                 q_pos: np.ndarray | None = None) -> AttnInputs:
+    """The benchmark distribution: q, k ~ N(0,1) then RMS-normalised per head; v ~ N(0,1).
+
+    Streams: q = 0, k = 1, v = 2. Positions: k_pos = 0..S-1; q_pos defaults to
+    the last T positions (decode: S-1; prefill with T == S: 0..S-1).
+    """
+    Dv = Dh if Dv is None else Dv
+    q = rms_norm_rows(normal_f32(seed, 0, T * Hq * Dh).reshape(T, Hq, Dh))
+    k = rms_norm_rows(normal_f32(seed, 1, S * Hkv * Dh).reshape(S, Hkv, Dh))
+    v = normal_f32(seed, 2, S * Hkv * Dv).reshape(S, Hkv, Dv)
+    k_pos = np.arange(S, dtype=np.uint32)
+    if q_pos is None:
+        q_pos = np.arange(S - T, S, dtype=np.uint32)
+    return AttnInputs(q, k, v, np.asarray(q_pos, dtype=np.uint32), k_pos)
+
+
+class Lcg:
+    """rust/tests/common/mod.rs:29-42: s = (s*1103515245 + 12345) & 0x7fffffff;
+    f = (s as f32) / (0x7fffffff as f32); rand = (f*2 - 1)*scale, all in f32."""
+
+    _DEN = np.float32(0x7FFFFFFF)  # rounds to 2^31 in f32, as `0x7fffffff as f32` does
+
+    def __init__(self, seed: int):
+        self.s = seed & 0xFFFFFFFF
+
+    def states(self, n: int) -> np.ndarray:
+        out = np.empty(n, dtype=np.uint32)
+        s = self.s
+        for i in range(n):
+            s = (s * 1103515245 + 12345) & 0x7FFFFFFF
+            out[i] = s
+        self.s = s
+        return out
+
+    def rand(self, n: int, scale: float) -> np.ndarray:
+        f = self.states(n).astype(np.float32) / self._DEN
+        return ((f * np.float32(2.0) - np.float32(1.0)) * np.float32(scale)).astype(np.float32)
+
+    def skip(self, n: int) -> None:
+        self.states(n)
+
+
+# The 8 cases of the reference's grouped_attention_parity (rust/tests/gpu.rs:268-277):
+# (T, S, Hq, Hkv, Dh, window); Lcg seed 21, q/k/v drawn per case in order with scale 0.5,
+# q_pos = last T positions, k_pos = 0..S-1, scale = 1/sqrt(Dh) (rust/tests/gpu.rs:278-291).
+GROUPED_CASES = [
+    (3, 300, 8, 1, 256, 0),
+    (3, 300, 8, 1, 256, 150),
+    (1, 700, 8, 1, 512, 0),
+    (1, 900, 8, 1, 256, 512),
+    (5, 5, 8, 1, 256, 0),
+    (6, 70, 8, 1, 256, 3),
+    (2, 200, 4, 1, 256, 0),
+    (1, 64, 8, 2, 512, 0),
+]
+
+
+def grouped_parity_inputs():
+    """Yield (case, q, k, v, q_pos, k_pos, scale, window) for rust/tests/gpu.rs:262-293."""
+    r = Lcg(21)
+    for (t, s, hq, hkv, dh, window) in GROUPED_CASES:
+        q = r.rand(t * hq * dh, 0.5).reshape(t, hq, dh)
+        k = r.rand(s * hkv * dh, 0.5).reshape(s, hkv, dh)
+        v = r.rand(s * hkv * dh, 0.5).reshape(s, hkv, dh)
+        kpos = np.arange(s, dtype=np.uint32)
+        qpos = np.arange(s - t, s, dtype=np.uint32)
+        scale = np.float32(1.0) / np.sqrt(np.float32(dh))
+        yield (t, s, hq, hkv, dh, window), q, k, v, qpos, kpos, float(scale), window
+
+
+def kernel_parity_attention_inputs():
+    """The attention cases of kernel_parity (rust/tests/gpu.rs:122-142), Lcg seed 7.
+
+    The earlier draws of that test are skipped by count: linear 17*40 + 23*40 +
+    40, rmsNorm 5*48 + 48, elementwise 100 + 100, embed 30*16, rope 4*2*16,
+    slice 4*20 + 2*20 + 3*20, kvAppend 3*200*8 (rust/tests/gpu.rs:43-121).
+    """
+    r = Lcg(7)
+    r.skip(17 * 40 + 23 * 40 + 40 + 5 * 48 + 48 + 100 + 100 + 30 * 16 + 4 * 2 * 16 + 4 * 20 + 2 * 20 + 3 * 20
+           + 3 * 200 * 8)
+    t, s, hq, hkv, dh = 6, 6, 4, 1, 16
+    q = r.rand(t * hq * dh, 1.0).reshape(t, hq, dh)
+    k = r.rand(s * hkv * dh, 1.0).reshape(s, hkv, dh)
+    v = r.rand(s * hkv * dh, 1.0).reshape(s, hkv, dh)
+    pos = np.arange(6, dtype=np.uint32)
+    yield "attention(GQA,sliding)", q, k, v, pos, pos, 0.25, 3
+    t, s, hq, hkv, dh = 3, 300, 2, 1, 32
+    q = r.rand(t * hq * dh, 0.5).reshape(t, hq, dh)
+    k = r.rand(s * hkv * dh, 0.5).reshape(s, hkv, dh)
+    v = r.rand(s * hkv * dh, 0.5).reshape(s, hkv, dh)
+    kpos = np.arange(300, dtype=np.uint32)
+    qpos = np.array([297, 298, 299], dtype=np.uint32)
+    for window in (0, 150):
+        yield f"attention(S=300, window={window})", q, k, v, qpos, kpos, 1.0, window

@@ -1,0 +1,170 @@
+/*
+ * g4a — Gemma-4 attention on MI355X (gfx950): the C-ABI of libg4a.so.
+ *
+ * This is the drop-in boundary for the attention ops of the reference's
+ * backend-agnostic op trait (rust/src/backend.rs:88-180). A Rust `HipBackend`
+ * implements `Backend::attention` / `Backend::kv_append` over these calls
+ * (see the FFI binding in INTEGRATION.md); the C++ mirror of the trait lives in
+ * gemma-4-webgpu-kernels_amd/csrc/hip_backend.hpp.
+ *
+ * Conventions
+ *   - Every call returns G4A_OK (0) or a negative g4a_status; the message of
+ *     the last failure is g4a_last_error(ctx). Ops are "infallible" in the
+ *     reference (they panic); the Rust binding panics on a nonzero status.
+ *   - A context owns one HIP stream; every op is stream-ordered and returns
+ *     before the GPU runs it (rust/src/backend_wgpu.rs:1-6). Only g4a_d2h and
+ *     g4a_sync block. A context is not thread-safe (the reference backend is
+ *     `RefCell`-based and !Sync, rust/src/backend_wgpu.rs:241).
+ *   - Tensors are plain device pointers to row-major f32 data with the shapes
+ *     the trait uses: q [T,Hq,Dh], k [S,Hkv,Dh], v [S,Hkv,Dv], out [T,Hq*Dv].
+ *   - Position slices are HOST pointers borrowed for the duration of the call,
+ *     exactly like AttnOpts::q_pos / k_pos (rust/src/backend.rs:61-64).
+ */
+#ifndef G4A_H
+#define G4A_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct g4a_ctx g4a_ctx;
+
+typedef enum g4a_status {
+    G4A_OK = 0,
+    G4A_E_HIP = -1,         /* a HIP runtime call failed */
+    G4A_E_ARG = -2,         /* null pointer / invalid argument */
+    G4A_E_SHAPE = -3,       /* inconsistent shapes */
+    G4A_E_UNSUPPORTED = -4, /* a combination this build does not handle */
+    G4A_E_MODULE = -5,      /* the gfx950 code object could not be loaded */
+    G4A_E_NOMEM = -6,       /* device allocation failed */
+} g4a_status;
+
+/* ---- context and memory ------------------------------------------------
+ * Replaces WgpuBackend::create (rust/src/backend_wgpu.rs:283) and the wgpu
+ * device acquisition (rust/src/device.rs:25-66). `hsaco_path` NULL loads
+ * g4a_kernels.hsaco from the directory of libg4a.so. */
+int g4a_create(int device, const char *hsaco_path, g4a_ctx **out);
+void g4a_destroy(g4a_ctx *ctx);
+/* Message of the last failed call on this context ("" if none). With a NULL
+ * ctx: the message of the last failed g4a_create in this process. */
+const char *g4a_last_error(const g4a_ctx *ctx);
+
+/* Device buffers. Replace raw_buf / alloc_in (rust/src/backend_wgpu.rs:371-402)
+ * and free_tensor (rust/src/backend_wgpu.rs:1126-1130). */
+int g4a_malloc(g4a_ctx *ctx, size_t bytes, void **dptr);
+int g4a_free(g4a_ctx *ctx, void *dptr);
+/* Host -> device copy of `bytes`; the host buffer may be reused on return
+ * (Backend::tensor, rust/src/backend_wgpu.rs:428-439). */
+int g4a_h2d(g4a_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Device -> host copy; waits for all prior work on the context's stream
+ * (Backend::readback, rust/src/backend_wgpu.rs:1057-1085). */
+int g4a_d2h(g4a_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Stream-ordered device -> device copy (COPY, rust/src/kernels/copy.wgsl:1-14). */
+int g4a_d2d(g4a_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Stream-ordered fill with zero bytes (Backend::zeros, rust/src/backend.rs:95). */
+int g4a_zero(g4a_ctx *ctx, void *dst, size_t bytes);
+/* Wait for all work on the context's stream (Backend::flush + device poll). */
+int g4a_sync(g4a_ctx *ctx);
+
+/* ---- attention -----------------------------------------------------------
+ * Backend::attention (rust/src/backend.rs:119-120) with AttnOpts
+ * (rust/src/backend.rs:59-69); semantics of CpuBackend::attention
+ * (rust/src/backend_cpu.rs:270-336): query head h reads kv head h/(Hq/Hkv);
+ * key j is visible to query i iff kpos <= qpos && (window == 0 ||
+ * qpos - kpos < window); a row with no visible key is 0. Host dispatch replaces
+ * WgpuBackend::attention (rust/src/backend_wgpu.rs:895-970).
+ *
+ * Positions: q_pos (T entries) and k_pos (S entries) are borrowed host arrays
+ * as in AttnOpts. A NULL array means the contiguous range q_pos0 + i /
+ * k_pos0 + j (what the model always passes, rust/src/engine.rs:155,233), which
+ * needs no upload. k_pos must be ascending (the reference's key-range trim,
+ * rust/src/backend_wgpu.rs:924-936, relies on it too).
+ *
+ * KV layout: kv_ring_cap == 0 means logical key row j is physical row j of
+ * k/v. kv_ring_cap > 0 means k/v are rings of kv_ring_cap rows and logical row
+ * j lives in slot j % kv_ring_cap; every key the queries can see must still be
+ * in the ring (G4A_E_SHAPE otherwise).
+ *
+ * splits: 0 picks the split-K count so a single sequence fills the GPU; > 0
+ * forces it (clamped to the number of 64-key tiles).
+ * attn_softcap > 0 applies cap*tanh(s/cap) after the scale
+ * (rust/src/backend_cpu.rs:303-305). */
+typedef struct g4a_attn_args {
+    const float *q;
+    const float *k;
+    const float *v;
+    float *out;
+    uint32_t T, S, Hq, Hkv, Dh, Dv;
+    const uint32_t *q_pos; /* host [T] or NULL */
+    const uint32_t *k_pos; /* host [S] or NULL */
+    uint32_t q_pos0, k_pos0;
+    float scale;
+    uint32_t sliding_window;
+    float attn_softcap;
+    uint32_t kv_ring_cap;
+    uint32_t splits;
+} g4a_attn_args;
+
+int g4a_attention(g4a_ctx *ctx, const g4a_attn_args *args);
+
+/* The launch plan g4a_attention would use for `args` (no GPU work): the
+ * trimmed key range [k_start, k_end) (rust/src/backend_wgpu.rs:929-936), the
+ * kernel family and the split-K decomposition. */
+typedef enum g4a_kernel_kind {
+    G4A_KERNEL_NONE = 0,    /* nothing to launch (T == 0) or zero fill only */
+    G4A_KERNEL_DECODE = 1,  /* split-K flash-decode (+ LSE combine if splits > 1) */
+    G4A_KERNEL_PREFILL = 2, /* query-tiled prefill */
+    G4A_KERNEL_GENERIC = 3, /* per-(query, head) fallback for other shapes */
+} g4a_kernel_kind;
+
+typedef struct g4a_attn_plan {
+    uint32_t kernel; /* g4a_kernel_kind */
+    uint32_t k_start, k_end;
+    uint32_t splits, keys_per_split;
+    size_t workspace_bytes;
+} g4a_attn_plan;
+
+int g4a_attention_plan(g4a_ctx *ctx, const g4a_attn_args *args, g4a_attn_plan *plan);
+
+/* ---- KV cache writes -----------------------------------------------------
+ * Writes n_rows rows of row_elems floats from src (device) into the cache at
+ * logical rows dst_row .. dst_row+n_rows-1. ring_cap == 0: linear cache,
+ * logical row r is physical row r (the capacity buffer of
+ * WgpuBackend::kv_append, rust/src/backend_wgpu.rs:1014-1055, whose growth the
+ * caller manages). ring_cap > 0: logical row r lands in slot r % ring_cap; when
+ * n_rows > ring_cap only the last ring_cap rows are written (the others would
+ * be overwritten anyway). Stream-ordered. */
+int g4a_kv_write(g4a_ctx *ctx, float *cache, uint32_t ring_cap, uint32_t row_elems, uint32_t dst_row,
+                 const float *src, uint32_t n_rows);
+
+/* ---- timing (HIP events on the context's stream) ----------------------- */
+int g4a_timer_start(g4a_ctx *ctx);
+/* Records the stop event, waits for it and returns the elapsed milliseconds. */
+int g4a_timer_stop(g4a_ctx *ctx, float *ms);
+
+/* Per-kernel timing: while enabled, every g4a_attention call records a HIP
+ * event pair on the context's stream around its main kernel (decode, prefill
+ * or generic; not the LSE combine). g4a_kernel_timing_read waits for the
+ * recorded pairs and returns their summed milliseconds and count, then clears
+ * them. At most 4096 pairs are kept per read. Enabling clears old pairs. */
+int g4a_kernel_timing(g4a_ctx *ctx, int enable);
+int g4a_kernel_timing_read(g4a_ctx *ctx, double *total_ms, uint32_t *count);
+
+/* ---- device facts --------------------------------------------------------- */
+typedef struct g4a_device_info {
+    int device;
+    int compute_units;
+    int clock_khz;
+    size_t total_mem;
+    char arch[64];
+} g4a_device_info;
+
+int g4a_get_device_info(g4a_ctx *ctx, g4a_device_info *info);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* G4A_H */

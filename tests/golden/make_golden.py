@@ -1,0 +1,32 @@
+"""Writes tests/golden/attention_golden.npz: for every recipe in golden_io, the
+sha256 of its regenerated inputs and the CPU oracle's output on them.
+
+Run from the repository root after building the oracle:
+    python tests/golden/make_golden.py
+"""
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+REPO = HERE.parents[1]
+sys.path[:0] = [str(HERE), str(REPO / "gemma-4-webgpu-kernels_amd"), str(REPO / "oracle")]
+
+import numpy as np  # noqa: E402
+
+import oracle  # noqa: E402
+from golden_io import GOLDEN_PATH, input_hash, recipes  # noqa: E402
+
+
+def main():
+    arrays = {}
+    for name, c in recipes().items():
+        out = oracle.attention(c.q, c.k, c.v, c.q_pos, c.k_pos, scale=c.scale, window=c.window, softcap=c.softcap)
+        arrays[name + "__out"] = out
+        arrays[name + "__hash"] = np.array(input_hash(c))
+        print(f"{name}: out {out.shape}")
+    np.savez_compressed(GOLDEN_PATH, **arrays)
+    print("wrote", GOLDEN_PATH, GOLDEN_PATH.stat().st_size, "bytes")
+
+
+if __name__ == "__main__":
+    main()

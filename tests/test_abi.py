@@ -1,0 +1,111 @@
+"""The C-ABI library without a GPU: it loads, exports every function
+include/g4a.h declares, and its host-side planning follows the reference's
+dispatch rules (key-range trim rust/src/backend_wgpu.rs:924-936, split-K
+decomposition, argument errors). No compute calls. CPU only."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import g4a
+
+
+def test_library_loads_and_exports_every_header_function():
+    lib = g4a.load_library()
+    names = g4a.header_functions()
+    assert len(names) >= 15, names
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared in include/g4a.h but not exported: {missing}"
+
+
+def test_code_object_was_built_for_gfx950():
+    data = g4a.HSACO_PATH.read_bytes()
+    assert data[:4] == b"\x7fELF" or data.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+    for name in (b"g4a_decode_d512_g8", b"g4a_decode_d256_g8", b"g4a_combine_d512", b"g4a_generic_attention"):
+        assert name in data, name
+    assert b"gfx950" in data
+
+
+def _plan(**kw):
+    base = dict(T=1, S=512, Hq=8, Hkv=1, Dh=256, Dv=256)
+    base.update(kw)
+    return g4a.plan(None, **base)
+
+
+def test_decode_trim_for_sliding_window_keeps_last_window_keys():
+    # decode at position 8191 with window 512: keys 7680..8191 only
+    p = _plan(S=8192, q_pos0=8191, window=512)
+    assert (p.k_start, p.k_end) == (8192 - 512, 8192)
+    assert g4a.KERNEL_NAMES[p.kernel] == "decode"
+
+
+def test_trim_matches_reference_partition_points_on_explicit_positions():
+    rng = np.random.default_rng(0)
+    kp = np.sort(rng.choice(10000, size=700, replace=False)).astype(np.uint32)
+    for qpos, w in [(5000, 0), (5000, 300), (9999, 100), (3, 0), (kp[0], 1)]:
+        p = _plan(S=700, q_pos=[qpos], k_pos=kp, window=w)
+        k_end = int(np.searchsorted(kp, qpos, side="right"))
+        k_start = int(np.searchsorted(kp, qpos - w, side="right")) if (w and qpos >= w) else 0
+        assert (p.k_start, p.k_end) == (min(k_start, k_end), k_end)
+
+
+def test_multi_query_trim_uses_min_and_max_query():
+    p = _plan(T=3, S=300, q_pos=[297, 298, 299], window=150)
+    assert (p.k_start, p.k_end) == (297 - 150 + 1, 300)
+
+
+def test_no_visible_key_plans_a_zero_fill():
+    p = _plan(S=100, k_pos0=50, q_pos0=10)
+    assert g4a.KERNEL_NAMES[p.kernel] == "none" and p.k_end == 0
+
+
+@pytest.mark.parametrize("S,Dh", [(512, 256), (8192, 512), (32768, 512), (131072, 512)])
+def test_auto_splits_cover_the_range_in_64_key_tiles(S, Dh):
+    p = _plan(S=S, Dh=Dh, Dv=Dh, q_pos0=S - 1)
+    assert p.keys_per_split % 64 == 0
+    assert p.splits * p.keys_per_split >= S > (p.splits - 1) * p.keys_per_split
+    assert p.splits <= 2 * 256  # about two workgroups per CU at most
+    if p.splits > 1:
+        assert p.workspace_bytes == 8 * p.splits * (Dh + 2) * 4
+
+
+def test_forced_split_counts_for_the_long_context_sweep():
+    for want in (8, 16, 32, 64, 128, 256, 512):
+        p = _plan(S=131072, Dh=512, Dv=512, q_pos0=131071, splits=want)
+        assert p.splits == want and p.keys_per_split == 131072 // want
+
+
+def test_shapes_outside_the_fast_path_use_the_generic_kernel():
+    assert g4a.KERNEL_NAMES[_plan(T=6, S=6, Hq=4, Dh=16, Dv=16).kernel] == "generic"
+    assert g4a.KERNEL_NAMES[_plan(Hq=2, Dh=32, Dv=32).kernel] == "generic"
+    assert g4a.KERNEL_NAMES[_plan(Hq=8, Hkv=2, Dh=512, Dv=512).kernel] == "decode"  # group 4
+    assert g4a.KERNEL_NAMES[_plan(Dh=256, Dv=128).kernel] == "generic"
+
+
+def test_argument_errors_are_reported_not_crashed():
+    with pytest.raises(g4a.G4aError) as e:
+        _plan(Hq=6, Hkv=4)
+    assert e.value.code == -3
+    with pytest.raises(g4a.G4aError) as e:
+        _plan(softcap=-1.0)
+    assert e.value.code == -2
+    with pytest.raises(g4a.G4aError) as e:
+        _plan(S=2048, q_pos0=2047, window=0, ring_cap=512)  # 2048 visible keys cannot live in a 512-row ring
+    assert e.value.code == -3
+    assert "ring" in g4a.load_library().g4a_last_error(None).decode()
+
+
+def test_ring_plan_accepts_window_inside_ring():
+    p = _plan(S=40000, q_pos0=39999, window=512, ring_cap=512)
+    assert (p.k_start, p.k_end) == (40000 - 512, 40000)
+
+
+def test_create_without_gpu_fails_cleanly():
+    import os
+    lib = g4a.load_library()
+    h = ctypes.c_void_p()
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU may be present")
+    rc = lib.g4a_create(0, None, ctypes.byref(h))
+    assert rc != 0 and not h.value
+    assert lib.g4a_last_error(None)
