@@ -41,6 +41,7 @@ struct g4a_ctx {
     hipEvent_t ev_staging = nullptr;  // last use of the pinned staging buffer
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
+    float* dummy = nullptr;  // 4 KiB of zeros: the load target of idle decode tiles
     uint32_t* pos_dev = nullptr;  // device copies of non-contiguous positions
     size_t pos_dev_cap = 0;       // in u32
     uint32_t* pos_host = nullptr;  // pinned staging for those copies
@@ -245,14 +246,14 @@ int analyse(g4a_ctx* ctx, const g4a_attn_args* a, Analysis* an, bool check_point
         return G4A_OK;
     }
     r.plan.kernel = G4A_KERNEL_DECODE;
-    const uint32_t kt = 4 / (group / 4);  // key-tile slots per workgroup
+    const uint32_t kt = 8 / (group / 2);  // key-tile slots per 8-wave workgroup (2 heads per wave)
     const uint32_t tiles = (nkeys + TILE - 1) / TILE;
     uint32_t splits;
     if (a->splits) {
         splits = std::min(a->splits, tiles);
     } else {
-        // fill the GPU with one sequence: about two workgroups per CU
-        const uint64_t target = uint64_t(2) * std::max(ctx ? ctx->cu_count : 256, 1);
+        // fill the GPU with one sequence: one 8-wave workgroup per CU (2 waves per SIMD)
+        const uint64_t target = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1));
         const uint64_t per_query = std::max<uint64_t>(1, target / (uint64_t(a->T) * a->Hkv));
         splits = uint32_t(std::min<uint64_t>(per_query, (tiles + kt - 1) / kt));
     }
@@ -311,6 +312,11 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->combine[0], "g4a_combine_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->combine[1], "g4a_combine_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->generic, "g4a_generic_attention")) return bail(rc);
+    if (hipMalloc(reinterpret_cast<void**>(&ctx->dummy), 4096) != hipSuccess ||
+        hipMemset(ctx->dummy, 0, 4096) != hipSuccess) {
+        fail(ctx, G4A_E_NOMEM, "dummy buffer allocation failed");
+        return bail(G4A_E_NOMEM);
+    }
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreate(&ctx->ev_start) != hipSuccess || hipEventCreate(&ctx->ev_stop) != hipSuccess ||
         hipEventCreateWithFlags(&ctx->ev_staging, hipEventDisableTiming) != hipSuccess) {
@@ -326,6 +332,7 @@ void g4a_destroy(g4a_ctx* ctx) {
     if (ctx->stream) hipStreamSynchronize(ctx->stream);
     for (hipEvent_t ev : ctx->kev) hipEventDestroy(ev);
     if (ctx->workspace) hipFree(ctx->workspace);
+    if (ctx->dummy) hipFree(ctx->dummy);
     if (ctx->pos_dev) hipFree(ctx->pos_dev);
     if (ctx->pos_host) hipHostFree(ctx->pos_host);
     if (ctx->ev_start) hipEventDestroy(ctx->ev_start);
@@ -439,6 +446,7 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
     dp.v = a->v;
     dp.out = a->out;
     dp.part = static_cast<float*>(ctx->workspace);
+    dp.dummy = ctx->dummy;
     dp.q_pos = qd;
     dp.k_pos = kd;
     dp.q_pos0 = a->q_pos ? a->q_pos[0] : a->q_pos0;
@@ -456,7 +464,7 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
     dp.softcap = a->attn_softcap;
     const int d512 = a->Dh == 512 ? 1 : 0;
     const int g8 = group == 8 ? 1 : 0;
-    if (int rc = launch(ctx, ctx->decode[d512][g8], dim3(pl.splits, a->T, a->Hkv), dim3(256, 1, 1), dp, "decode", true))
+    if (int rc = launch(ctx, ctx->decode[d512][g8], dim3(pl.splits, a->T, a->Hkv), dim3(512, 1, 1), dp, "decode", true))
         return rc;
     if (pl.splits > 1) {
         G4aCombineParams cp{dp.part, a->out, a->T, a->Hq, pl.splits, a->Dh};

@@ -89,71 +89,153 @@ __device__ __forceinline__ void qk_chunk(float (&s)[4], cfloat* __restrict__ qh,
     }
 }
 
+// Sixteen dims (16B .. 16B+15 of a 64-dim stage) of the exact dots of the two
+// heads of a wave, lane = key: dot = ((dot + q[d]*k[d]) + q[d+1]*k[d+1]) + ...,
+// every multiply and add rounded separately, in the CPU reference's order.
+// q[h][16B + j] sits in lane j of every 16-lane row of qv[h][B]; each multiply
+// takes it through a DPP row broadcast (row_newbcast:j) as its first operand,
+// so the hot loop issues no scalar loads. Written as one asm block so every
+// multiply is a single v_mul_f32_dpp; the leading s_nop covers the 2 wait
+// states a DPP read needs after a VALU write of its source.
+__device__ __forceinline__ void qk_dims16(float (&s)[2], float q0, float q1, const float4 (&k)[4]) {
+    float t0, t1;
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k0] row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k0] row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k1] row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k1] row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k2] row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k2] row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k3] row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k3] row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k4] row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k4] row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k5] row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k5] row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k6] row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k6] row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k7] row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k7] row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k8] row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k8] row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k9] row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k9] row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k10] row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k10] row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k11] row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k11] row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k12] row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k12] row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k13] row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k13] row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k14] row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k14] row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        "v_mul_f32_dpp %[t0], %[q0], %[k15] row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q1], %[k15] row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
+        : [a0] "+v"(s[0]), [a1] "+v"(s[1]), [t0] "=&v"(t0), [t1] "=&v"(t1)
+        : [q0] "v"(q0), [q1] "v"(q1), [k0] "v"(k[0].x), [k1] "v"(k[0].y), [k2] "v"(k[0].z), [k3] "v"(k[0].w), [k4] "v"(k[1].x), [k5] "v"(k[1].y), [k6] "v"(k[1].z), [k7] "v"(k[1].w), [k8] "v"(k[2].x), [k9] "v"(k[2].y), [k10] "v"(k[2].z), [k11] "v"(k[2].w), [k12] "v"(k[3].x), [k13] "v"(k[3].y), [k14] "v"(k[3].z), [k15] "v"(k[3].w));
+}
+
 template <int DH, int GROUP>
 struct DecodeCfg {
-    static constexpr int HG = GROUP / 4;                 // head-group waves per key-tile slot
-    static constexpr int KT = 4 / HG;                    // key-tile slots per workgroup
-    static constexpr int DC = KT == 2 ? 64 : 32;         // dims per K stage
-    static constexpr int NST = DH / DC;                  // K stages per tile
-    static constexpr int C4 = DC / 4;                    // float4 per row per stage
-    static constexpr int RS = DC + 4;                    // LDS row stride in floats (padded: no bank conflicts)
-    static constexpr int SLOT_THREADS = 64 * HG;
-    static constexpr int LPT = 64 * C4 / SLOT_THREADS;   // float4 loads per thread per stage
+    static constexpr int HGW = GROUP / 2;                // waves per key-tile slot (2 heads each)
+    static constexpr int KT = 8 / HGW;                   // key-tile slots per 8-wave workgroup
+    static constexpr int SLOT_THREADS = 64 * HGW;
+    static constexpr int LPT = 1024 / SLOT_THREADS;      // float4 per thread per 16 KiB chunk
+    static constexpr int D = 16 / LPT;                   // chunks in flight per slot (64 VGPRs of loads)
+    static constexpr int NKS = DH / 64;                  // K chunks per tile: 64 keys x 64 dims
+    static constexpr int NVC = DH / 64;                  // V chunks per tile: KPC keys x DH dims
+    static constexpr int NCH = NKS + NVC;
+    static constexpr int KPC = 64 / NVC;                 // keys per V chunk
+    static constexpr int PVK = KPC / HGW;                // keys per wave per V chunk
+    static constexpr int RS = 68;                        // padded K row stride in LDS (floats)
+    static constexpr int BUF = 64 * RS;                  // floats per chunk buffer
     static constexpr int NV4 = DH / 256;                 // V float4 per lane per row
-    static constexpr int PVK = 64 / HG;                  // keys per wave in the P.V phase
-    static constexpr int VB = 8;                         // V prefetch depth (keys)
     static constexpr int NHQ = GROUP / 4;                // MFMA head quarters
-    // shared memory (floats)
-    static constexpr int KST = KT * 2 * 64 * RS;         // double-buffered K stages
-    static constexpr int MERGE = 4 * GROUP * DH;         // end-of-kernel merge (overlays KST)
-    static constexpr int BIG = KST > MERGE ? KST : MERGE;
-    static constexpr int PBUF = KT * 64 * 4 * HG;        // probabilities [slot][key][i][hh]
-    static constexpr int CORR = KT * GROUP;
-    static constexpr int ML = KT * 2 * GROUP;
-    static constexpr int SMEM = BIG + PBUF + CORR + ML;
-    static_assert(LPT * SLOT_THREADS == 64 * C4, "stage must split evenly over the slot's threads");
-    static_assert(PVK % VB == 0, "P.V key range must be a multiple of the prefetch depth");
+    static constexpr int RING = KT * 2 * BUF;
+    static constexpr int MERGE = 8 * GROUP * DH;
+    static constexpr int BIG = RING > MERGE ? RING : MERGE;
+    static constexpr int PBUF = KT * 64 * GROUP;
+    static constexpr int QS = GROUP * DH;                // the kv group's query rows
+    static constexpr int SMEM = BIG + PBUF + KT * GROUP + KT * 2 * GROUP + QS;
+    static_assert(NCH % D == 0, "the register ring index must be static within a tile");
+    static_assert(KPC * DH <= BUF, "a V chunk must fit a chunk buffer");
+    static_assert(PVK >= 1, "every wave of a slot folds at least one key per V chunk");
 };
 
-// Split-K flash decode: see the file header for the decomposition.
+// Split-K flash decode (see the file header). An 8-wave workgroup owns one key
+// split of one (query, kv head); its waves form KT key-tile slots of HGW waves,
+// each wave owning 2 query heads. Every slot streams, per 64-key tile, DH/64 K
+// chunks (64 keys x 64 dims) and DH/64 V chunks (KPC keys x DH dims) of 16 KiB
+// through registers into a double-buffered LDS chunk, D chunks ahead, so K and V
+// loads form one continuous stream across phases and tiles.
 template <int DH, int GROUP>
 __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
     static_assert(DH == 256 || DH == 512, "fast decode handles head_dim 256 / 512");
     static_assert(GROUP == 4 || GROUP == 8, "fast decode handles groups of 4 / 8 heads");
     using C = DecodeCfg<DH, GROUP>;
-    constexpr int HG = C::HG, KT = C::KT, DC = C::DC, NST = C::NST, C4 = C::C4, RS = C::RS, LPT = C::LPT,
-                  NV4 = C::NV4, PVK = C::PVK, VB = C::VB, NHQ = C::NHQ, SLOT_THREADS = C::SLOT_THREADS;
+    constexpr int HGW = C::HGW, KT = C::KT, SLOT_THREADS = C::SLOT_THREADS, LPT = C::LPT, D = C::D,
+                  NKS = C::NKS, NCH = C::NCH, KPC = C::KPC, PVK = C::PVK, RS = C::RS, BUF = C::BUF,
+                  NV4 = C::NV4, NHQ = C::NHQ;
 
     __shared__ __attribute__((aligned(16))) float smem[C::SMEM];
-    float* const kst = smem;                          // [KT][2][64*RS]
-    float* const mrg = smem;                          // [4][GROUP][DH] after the tile loop
-    float* const pbuf = smem + C::BIG;                // [KT][64][4][HG]
-    float* const corrbuf = pbuf + C::PBUF;            // [KT][GROUP]
-    float* const mlbuf = corrbuf + C::CORR;           // [KT][2][GROUP]
+    float* const ring = smem;                     // [KT][2][BUF]
+    float* const mrg = smem;                      // [8][GROUP][DH] after the tile loop
+    float* const pbuf = smem + C::BIG;            // [KT][64 keys][4][NHQ]
+    float* const corrbuf = pbuf + C::PBUF;        // [KT][GROUP]
+    float* const mlbuf = corrbuf + KT * GROUP;    // [KT][2][GROUP]
+    float* const qs = mlbuf + KT * 2 * GROUP;     // [GROUP][DH] query rows of this kv group
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int hg = w % HG;
-    const int kt = w / HG;
-    const int stid = hg * 64 + lane;
+    const int g = w % HGW;   // head pair within the kv group: heads 2g, 2g+1
+    const int kt = w / HGW;  // key-tile slot
+    const int stid = g * 64 + lane;
     const uint32_t split = blockIdx.x, qi = blockIdx.y, kvh = blockIdx.z;
     const uint32_t qpos = p.q_pos ? p.q_pos[qi] : p.q_pos0 + qi;
     const uint32_t ks = p.k_start + split * p.keys_per_split;
     const uint32_t ke = min(ks + p.keys_per_split, p.k_end);
     const uint32_t h0 = kvh * GROUP;
-    cfloat* __restrict__ qh = as_const(p.q + ((size_t)qi * p.Hq + h0 + hg * 4) * DH);
     const size_t row_stride = (size_t)p.Hkv * DH;
     const float* __restrict__ kbase = p.k + (size_t)kvh * DH;
-    const float* __restrict__ vbase = p.v + (size_t)kvh * DH + 4 * lane;
-    float* const my_kst = kst + kt * 2 * 64 * RS;
-    float* const my_pbuf = pbuf + kt * 64 * 4 * HG;
+    const float* __restrict__ vbase = p.v + (size_t)kvh * DH;
+    float* const my_ring = ring + kt * 2 * BUF;
+    float* const my_pbuf = pbuf + kt * 64 * GROUP;
 
-    float m[4], lpart[4];
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-        m[h] = NEG_INF;
-        lpart[h] = 0.0f;
-    }
+    float m[2] = {NEG_INF, NEG_INF}, lpart[2] = {0.0f, 0.0f};
     f4v acc[NHQ][NV4][4];
 #pragma unroll
     for (int a = 0; a < NHQ; ++a)
@@ -164,137 +246,166 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
 
     const uint32_t ntiles = ke > ks ? (ke - ks + 63) / 64 : 0;
     const uint32_t niter = (ntiles + KT - 1) / KT;
-    for (uint32_t it = 0; it < niter; ++it) {
+
+    // Loads are issued for every chunk step whether or not the slot has a tile,
+    // so the number of loads in flight is the same on every path and each
+    // chunk's wait is exact; an idle slot reads the small dummy buffer (which
+    // stays in L2) instead of K/V.
+    struct Tile {
+        uint32_t t0, row0, nk;
+        bool active;
+        const float* kb;
+        const float* vb;
+    };
+    auto tile_info = [&](uint32_t it) -> Tile {
+        Tile T;
         const uint32_t t = it * KT + kt;
-        const uint32_t t0 = ks + t * 64;
-        bool active = t < ntiles;
-        if (active) {
-            const uint32_t kpos_first = p.k_pos ? p.k_pos[t0] : p.k_pos0 + t0;
-            active = kpos_first <= qpos;  // ascending positions: a future first key means a future tile
+        T.t0 = ks + t * 64;
+        T.active = it < niter && t < ntiles;
+        if (T.active) {
+            const uint32_t kpos_first = p.k_pos ? p.k_pos[T.t0] : p.k_pos0 + T.t0;
+            T.active = kpos_first <= qpos;  // ascending positions: a future first key means a future tile
         }
-        const uint32_t nk = active ? min(64u, ke - t0) : 1u;
-        const uint32_t row0 = active ? phys_row(t0, p.ring_cap) : 0u;
-        auto prow = [&](uint32_t r) -> uint32_t {  // physical row of tile key r (clamped to the tile)
-            uint32_t x = row0 + min(r, nk - 1);
-            if (p.ring_cap && x >= p.ring_cap) x -= p.ring_cap;
-            return x;
-        };
-
-        // ---- scores: K streams through LDS in stages of DC dims, lane = key ----
-        float4 kreg[2][LPT];
-        auto load_stage = [&](int st, float4 (&r)[LPT]) {
+        T.nk = T.active ? min(64u, ke - T.t0) : 1u;
+        T.row0 = T.active ? phys_row(T.t0, p.ring_cap) : 0u;
+        T.kb = T.active ? kbase : p.dummy;
+        T.vb = T.active ? vbase : p.dummy;
+        return T;
+    };
+    auto prow = [&](const Tile& T, uint32_t r) -> uint32_t {  // physical row of tile key r, clamped to the tile
+        uint32_t x = T.row0 + min(r, T.nk - 1);
+        if (p.ring_cap && x >= p.ring_cap) x -= p.ring_cap;
+        return x;
+    };
+    // chunk c of a tile into registers: K chunks c < NKS (dims 64c..64c+63 of the 64 keys),
+    // V chunks c >= NKS (keys KPC*(c-NKS) .. +KPC-1, all DH dims)
+    auto load_chunk = [&](const Tile& T, int c, float4 (&r)[LPT]) {
 #pragma unroll
-            for (int i = 0; i < LPT; ++i) {
-                const int f = stid + SLOT_THREADS * i;
-                r[i] = ld4(kbase + (size_t)prow(f / C4) * row_stride + st * DC + 4 * (f % C4));
+        for (int i = 0; i < LPT; ++i) {
+            const int f = stid + SLOT_THREADS * i;
+            if (c < NKS) {
+                r[i] = ld4(T.kb + (size_t)prow(T, f / 16) * row_stride + 64 * c + 4 * (f % 16));
+            } else {
+                const int key = (c - NKS) * KPC + f / (DH / 4);
+                r[i] = ld4(T.vb + (size_t)prow(T, key) * row_stride + 4 * (f % (DH / 4)));
             }
-        };
-        auto store_stage = [&](int buf, const float4 (&r)[LPT]) {
-#pragma unroll
-            for (int i = 0; i < LPT; ++i) {
-                const int f = stid + SLOT_THREADS * i;
-                *reinterpret_cast<float4*>(my_kst + buf * 64 * RS + (f / C4) * RS + 4 * (f % C4)) = r[i];
-            }
-        };
-        float4 vb[VB][NV4];
-        const uint32_t kv0 = hg * PVK;  // first key of this wave's P.V range
-        auto load_v = [&](uint32_t kk, float4 (&r)[NV4]) {
-            const float* vr = vbase + (size_t)prow(kk) * row_stride;
-#pragma unroll
-            for (int q4 = 0; q4 < NV4; ++q4) r[q4] = ld4(vr + 256 * q4);
-        };
-
-        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (active) {
-            load_stage(0, kreg[0]);
-            if (NST > 1) load_stage(1, kreg[1]);
         }
+    };
+    auto store_chunk = [&](int c, float* buf, const float4 (&r)[LPT]) {
 #pragma unroll
-        for (int st = 0; st < NST; ++st) {
-            if (active) store_stage(st & 1, kreg[st & 1]);
+        for (int i = 0; i < LPT; ++i) {
+            const int f = stid + SLOT_THREADS * i;
+            float* dst = c < NKS ? buf + (f / 16) * RS + 4 * (f % 16) : buf + (f / (DH / 4)) * DH + 4 * (f % (DH / 4));
+            *reinterpret_cast<float4*>(dst) = r[i];
+        }
+    };
+
+    {
+        const float* qsrc = p.q + ((size_t)qi * p.Hq + h0) * DH;
+        for (int i = threadIdx.x; i < GROUP * DH / 4; i += 512)
+            *reinterpret_cast<float4*>(qs + 4 * i) = ld4(qsrc + 4 * i);
+    }
+    const float* const my_q = qs + 2 * g * DH;  // heads 2g, 2g+1
+
+    float4 kreg[D][LPT];
+    Tile cur = tile_info(0);
+#pragma unroll
+    for (int c = 0; c < D; ++c) load_chunk(cur, c, kreg[c]);
+
+    for (uint32_t it = 0; it < niter; ++it) {
+        const Tile nxt = tile_info(it + 1);
+        float s[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            float* const buf = my_ring + (c & 1) * BUF;
+            if (cur.active) store_chunk(c, buf, kreg[c % D]);
             __syncthreads();
-            if (active) {
-                if (st + 2 < NST) load_stage(st + 2, kreg[st & 1]);
-                if (st == NST - 1) {
+            // keep D chunks in flight: chunk c+D of this tile or of the next one
+            if (c + D < NCH) load_chunk(cur, c + D, kreg[c % D]);
+            else load_chunk(nxt, c + D - NCH, kreg[c % D]);
+            if (!cur.active) continue;
+            if (c < NKS) {
+                // exact sequential dots, lane = key, heads 2g and 2g+1, dims 64c .. 64c+63;
+                // q comes from 8 VGPRs (16 values each, one per 16-lane row) via DPP broadcast
+                const float* kr = buf + lane * RS;
 #pragma unroll
-                    for (int b = 0; b < VB; ++b) load_v(kv0 + b, vb[b]);  // overlap V latency with the last stage
+                for (int b = 0; b < 4; ++b) {
+                    const float q0 = my_q[64 * c + 16 * b + (lane & 15)];
+                    const float q1 = my_q[DH + 64 * c + 16 * b + (lane & 15)];
+                    float4 k4[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) k4[i] = *reinterpret_cast<const float4*>(kr + 16 * b + 4 * i);
+                    qk_dims16(s, q0, q1, k4);
                 }
-                const float* kr = my_kst + (st & 1) * 64 * RS + lane * RS;
+                if (c == NKS - 1) {
+                    // online softmax for heads 2g, 2g+1 over the tile (lane = key)
+                    const uint32_t j = cur.t0 + min((uint32_t)lane, cur.nk - 1);
+                    const uint32_t kp = p.k_pos ? p.k_pos[j] : p.k_pos0 + j;
+                    const bool vis = (uint32_t)lane < cur.nk && kp <= qpos && (p.window == 0 || qpos - kp < p.window);
 #pragma unroll
-                for (int c = 0; c < C4; ++c) {
-                    const float4 kk = *reinterpret_cast<const float4*>(kr + 4 * c);
-                    qk_chunk<DH>(s, qh, st * DC + 4 * c, kk, c);
+                    for (int h = 0; h < 2; ++h) {
+                        const float sc = vis ? score_epilogue(s[h], p.scale, p.softcap) : NEG_INF;
+                        const float mn = fmaxf(m[h], wave_max(sc));
+                        const float corr = (m[h] == NEG_INF) ? 0.0f : expf(m[h] - mn);
+                        const float pr = (sc == NEG_INF) ? 0.0f : expf(sc - mn);
+                        lpart[h] = lpart[h] * corr + pr;
+                        m[h] = mn;
+                        const int hl = 2 * g + h;  // head within the kv group
+                        my_pbuf[lane * GROUP + (hl & 3) * NHQ + (hl >> 2)] = pr;
+                        if (lane == 0) corrbuf[kt * GROUP + hl] = corr;
+                    }
                 }
-            }
-        }
-
-        // ---- online softmax for this wave's 4 heads (lane = key) ----
-        if (active) {
-            const uint32_t j = t0 + min((uint32_t)lane, nk - 1);
-            const uint32_t kp = p.k_pos ? p.k_pos[j] : p.k_pos0 + j;
-            const bool vis = (uint32_t)lane < nk && kp <= qpos && (p.window == 0 || qpos - kp < p.window);
+            } else {
+                const int vc = c - NKS;
+                if (vc == 0) {
+                    // rescale the running output of every head by its correction factor
 #pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                const float sc = vis ? score_epilogue(s[h], p.scale, p.softcap) : NEG_INF;
-                const float mn = fmaxf(m[h], wave_max(sc));
-                const float corr = (m[h] == NEG_INF) ? 0.0f : expf(m[h] - mn);
-                const float pr = (sc == NEG_INF) ? 0.0f : expf(sc - mn);
-                lpart[h] = lpart[h] * corr + pr;
-                m[h] = mn;
-                my_pbuf[lane * 4 * HG + h * HG + hg] = pr;
-                if (lane == 0) corrbuf[kt * GROUP + hg * 4 + h] = corr;
-            }
-        }
-        __syncthreads();
-
-        // ---- P.V on the matrix cores: this wave's PVK keys, all GROUP heads ----
-        // v_mfma_f32_4x4x1_16b_f32: 16 blocks of D[4 heads][4 dims] += P[head] * V[dim];
-        // lane l gives A = P[hq*4 + l%4] and B = V[key][256*q4 + 4*l + e]; its
-        // result register r holds out[hq*4 + r][256*q4 + 4*l + e].
-        if (active) {
+                    for (int hq = 0; hq < NHQ; ++hq) {
+                        const float* cb = corrbuf + kt * GROUP + hq * 4;
+                        const f4v cr = f4v{cb[0], cb[1], cb[2], cb[3]};
 #pragma unroll
-            for (int hq = 0; hq < NHQ; ++hq) {
-                const float* cb = corrbuf + kt * GROUP + hq * 4;
-                const f4v cr = f4v{cb[0], cb[1], cb[2], cb[3]};
+                        for (int q4 = 0; q4 < NV4; ++q4)
 #pragma unroll
-                for (int q4 = 0; q4 < NV4; ++q4)
+                            for (int e = 0; e < 4; ++e) acc[hq][q4][e] *= cr;
+                    }
+                }
+                // P.V on the matrix cores (v_mfma_f32_4x4x1_16b_f32): lane l gives A = P[hq*4 + l%4]
+                // and B = V[key][256*q4 + 4*l + e]; result register r = out[hq*4 + r][256*q4 + 4*l + e]
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[hq][q4][e] *= cr;
-            }
-            const float* pb = my_pbuf + (lane & 3) * HG;
-            for (int kb = 0; kb < PVK; kb += VB) {
-#pragma unroll
-                for (int b = 0; b < VB; ++b) {
-                    const uint32_t kk = kv0 + kb + b;
+                for (int u = 0; u < PVK; ++u) {
+                    const int kr = g * PVK + u;  // key within the chunk
+                    const int kk = vc * KPC + kr;  // key within the tile
                     float a[NHQ];
 #pragma unroll
-                    for (int hq = 0; hq < NHQ; ++hq) a[hq] = pb[kk * 4 * HG + hq];
+                    for (int hq = 0; hq < NHQ; ++hq) a[hq] = my_pbuf[kk * GROUP + (lane & 3) * NHQ + hq];
 #pragma unroll
-                    for (int hq = 0; hq < NHQ; ++hq)
+                    for (int q4 = 0; q4 < NV4; ++q4) {
+                        const float4 vv = *reinterpret_cast<const float4*>(buf + kr * DH + 256 * q4 + 4 * lane);
 #pragma unroll
-                        for (int q4 = 0; q4 < NV4; ++q4) {
-                            acc[hq][q4][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vb[b][q4].x, acc[hq][q4][0], 0, 0, 0);
-                            acc[hq][q4][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vb[b][q4].y, acc[hq][q4][1], 0, 0, 0);
-                            acc[hq][q4][2] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vb[b][q4].z, acc[hq][q4][2], 0, 0, 0);
-                            acc[hq][q4][3] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vb[b][q4].w, acc[hq][q4][3], 0, 0, 0);
+                        for (int hq = 0; hq < NHQ; ++hq) {
+                            acc[hq][q4][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vv.x, acc[hq][q4][0], 0, 0, 0);
+                            acc[hq][q4][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vv.y, acc[hq][q4][1], 0, 0, 0);
+                            acc[hq][q4][2] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vv.z, acc[hq][q4][2], 0, 0, 0);
+                            acc[hq][q4][3] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vv.w, acc[hq][q4][3], 0, 0, 0);
                         }
-                    if (kb + VB < PVK) load_v(kk + VB, vb[b]);
+                    }
                 }
             }
         }
+        cur = nxt;
     }
 
-    // ---- per-slot (m, l), then merge the 4 waves' accumulators through LDS ----
+    // ---- per-slot (m, l); merge the 8 waves' accumulators through LDS ----
 #pragma unroll
-    for (int h = 0; h < 4; ++h) lpart[h] = wave_sum(lpart[h]);
+    for (int h = 0; h < 2; ++h) lpart[h] = wave_sum(lpart[h]);
     if (lane == 0) {
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            mlbuf[kt * 2 * GROUP + hg * 4 + h] = m[h];
-            mlbuf[kt * 2 * GROUP + GROUP + hg * 4 + h] = lpart[h];
+        for (int h = 0; h < 2; ++h) {
+            mlbuf[kt * 2 * GROUP + 2 * g + h] = m[h];
+            mlbuf[kt * 2 * GROUP + GROUP + 2 * g + h] = lpart[h];
         }
     }
-    __syncthreads();  // every wave is done with the K stages: the merge buffer may overlay them
+    __syncthreads();  // every wave is done with the chunk ring: the merge buffer overlays it
 #pragma unroll
     for (int hq = 0; hq < NHQ; ++hq)
 #pragma unroll
@@ -304,47 +415,43 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
                 *reinterpret_cast<float4*>(mrg + ((size_t)w * GROUP + hq * 4 + r) * DH + 256 * q4 + 4 * lane) =
                     make_float4(acc[hq][q4][0][r], acc[hq][q4][1][r], acc[hq][q4][2][r], acc[hq][q4][3][r]);
     __syncthreads();
-    // wave w finalises heads [w*GROUP/4, (w+1)*GROUP/4)
+    // wave w finalises head w % GROUP over the q4 blocks w / GROUP, w / GROUP + 8 / GROUP, ...
+    const int h = w % GROUP;
+    float M = NEG_INF;
 #pragma unroll
-    for (int hh = 0; hh < GROUP / 4; ++hh) {
-        const int h = w * (GROUP / 4) + hh;
-        float M = NEG_INF;
+    for (int sl = 0; sl < KT; ++sl) M = fmaxf(M, mlbuf[sl * 2 * GROUP + h]);
+    float L = 0.0f, es[KT];
 #pragma unroll
-        for (int sl = 0; sl < KT; ++sl) M = fmaxf(M, mlbuf[sl * 2 * GROUP + h]);
-        float L = 0.0f, es[KT];
+    for (int sl = 0; sl < KT; ++sl) {
+        const float ms = mlbuf[sl * 2 * GROUP + h];
+        es[sl] = (ms == NEG_INF) ? 0.0f : expf(ms - M);
+        L += mlbuf[sl * 2 * GROUP + GROUP + h] * es[sl];
+    }
+    const size_t ih = (size_t)qi * p.Hq + h0 + h;
+    for (int q4 = w / GROUP; q4 < NV4; q4 += 8 / GROUP) {
+        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (int sl = 0; sl < KT; ++sl) {
-            const float ms = mlbuf[sl * 2 * GROUP + h];
-            es[sl] = (ms == NEG_INF) ? 0.0f : expf(ms - M);
-            L += mlbuf[sl * 2 * GROUP + GROUP + h] * es[sl];
-        }
-        const size_t ih = (size_t)qi * p.Hq + h0 + h;
+            float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int q4 = 0; q4 < NV4; ++q4) {
-            float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-            for (int sl = 0; sl < KT; ++sl) {
-                float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-                for (int g = 0; g < HG; ++g) {
-                    const float4 x = *reinterpret_cast<const float4*>(mrg + ((size_t)(sl * HG + g) * GROUP + h) * DH + 256 * q4 + 4 * lane);
-                    a.x += x.x; a.y += x.y; a.z += x.z; a.w += x.w;
-                }
-                o.x += a.x * es[sl]; o.y += a.y * es[sl]; o.z += a.z * es[sl]; o.w += a.w * es[sl];
+            for (int gg = 0; gg < HGW; ++gg) {
+                const float4 x = *reinterpret_cast<const float4*>(mrg + ((size_t)(sl * HGW + gg) * GROUP + h) * DH + 256 * q4 + 4 * lane);
+                a.x += x.x; a.y += x.y; a.z += x.z; a.w += x.w;
             }
-            if (p.nsplit == 1) {
-                const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-                *reinterpret_cast<float4*>(p.out + ih * DH + 256 * q4 + 4 * lane) =
-                    make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
-            } else {
-                *reinterpret_cast<float4*>(p.part + (ih * p.nsplit + split) * DH + 256 * q4 + 4 * lane) = o;
-            }
+            o.x += a.x * es[sl]; o.y += a.y * es[sl]; o.z += a.z * es[sl]; o.w += a.w * es[sl];
         }
-        if (p.nsplit > 1 && lane == 0) {
-            float* ml = p.part + (size_t)p.T * p.Hq * p.nsplit * DH + (ih * p.nsplit + split) * 2;
-            ml[0] = M;
-            ml[1] = L;
+        if (p.nsplit == 1) {
+            const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+            *reinterpret_cast<float4*>(p.out + ih * DH + 256 * q4 + 4 * lane) =
+                make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+        } else {
+            *reinterpret_cast<float4*>(p.part + (ih * p.nsplit + split) * DH + 256 * q4 + 4 * lane) = o;
         }
+    }
+    if (p.nsplit > 1 && lane == 0 && w < GROUP) {
+        float* ml = p.part + (size_t)p.T * p.Hq * p.nsplit * DH + (ih * p.nsplit + split) * 2;
+        ml[0] = M;
+        ml[1] = L;
     }
 }
 
@@ -467,10 +574,10 @@ __device__ __forceinline__ void generic_attention(const G4aGenericParams& p) {
 }  // namespace
 
 extern "C" {
-__global__ __launch_bounds__(256) void g4a_decode_d256_g8(G4aDecodeParams p) { decode_split<256, 8>(p); }
-__global__ __launch_bounds__(256) void g4a_decode_d512_g8(G4aDecodeParams p) { decode_split<512, 8>(p); }
-__global__ __launch_bounds__(256) void g4a_decode_d256_g4(G4aDecodeParams p) { decode_split<256, 4>(p); }
-__global__ __launch_bounds__(256) void g4a_decode_d512_g4(G4aDecodeParams p) { decode_split<512, 4>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d256_g8(G4aDecodeParams p) { decode_split<256, 8>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d512_g8(G4aDecodeParams p) { decode_split<512, 8>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d256_g4(G4aDecodeParams p) { decode_split<256, 4>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d512_g4(G4aDecodeParams p) { decode_split<512, 4>(p); }
 __global__ __launch_bounds__(256) void g4a_combine_d256(G4aCombineParams p) { combine<256>(p); }
 __global__ __launch_bounds__(256) void g4a_combine_d512(G4aCombineParams p) { combine<512>(p); }
 __global__ __launch_bounds__(64) void g4a_generic_attention(G4aGenericParams p) { generic_attention(p); }

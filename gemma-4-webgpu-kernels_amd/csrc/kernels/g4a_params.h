@@ -19,6 +19,7 @@ struct G4aDecodeParams {
     const float* v;        // [rows, Hkv, Dh]
     float* out;            // [T, Hq*Dh]
     float* part;           // nsplit > 1: acc [T*Hq][nsplit][Dh] then (m,l) [T*Hq][nsplit][2]
+    const float* dummy;    // >= 4 KiB of readable device memory: the load target of idle tiles
     const uint32_t* q_pos; // device [T] or null
     const uint32_t* k_pos; // device [S] or null
     uint32_t q_pos0, k_pos0;
