@@ -6,6 +6,7 @@
 #include "g4a.h"
 
 #include <dlfcn.h>
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime_api.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -37,6 +38,7 @@ struct g4a_ctx {
     hipFunction_t decode[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};  // [dh512][group8]
     hipFunction_t combine[2] = {nullptr, nullptr};                          // [dh512]
     hipFunction_t generic = nullptr;
+    hipFunction_t prefill[2] = {nullptr, nullptr};                          // [dh512]
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     hipEvent_t ev_staging = nullptr;  // last use of the pinned staging buffer
     void* workspace = nullptr;
@@ -151,13 +153,18 @@ int launch(g4a_ctx* ctx, hipFunction_t f, dim3 grid, dim3 block, const P& params
     P copy = params;
     void* args[] = {&copy};
     const bool rec = timed && ctx->timing && ctx->kev_used < kMaxTimed;
-    if (rec) HIP_TRY(ctx, hipEventRecord(ctx->kev[2 * ctx->kev_used], ctx->stream));
-    hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, ctx->stream, args, nullptr);
-    if (e != hipSuccess) return fail(ctx, G4A_E_HIP, "launch %s: %s", what, hipGetErrorString(e));
+    hipError_t e;
     if (rec) {
-        HIP_TRY(ctx, hipEventRecord(ctx->kev[2 * ctx->kev_used + 1], ctx->stream));
-        ++ctx->kev_used;
+        // events attached to the dispatch itself: they bracket the kernel's execution,
+        // not the host-side enqueue, so they agree with a profiler's kernel duration
+        e = hipExtModuleLaunchKernel(f, grid.x * block.x, grid.y * block.y, grid.z * block.z, block.x, block.y,
+                                     block.z, 0, ctx->stream, args, nullptr, ctx->kev[2 * ctx->kev_used],
+                                     ctx->kev[2 * ctx->kev_used + 1], 0);
+        if (e == hipSuccess) ++ctx->kev_used;
+    } else {
+        e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, ctx->stream, args, nullptr);
     }
+    if (e != hipSuccess) return fail(ctx, G4A_E_HIP, "launch %s: %s", what, hipGetErrorString(e));
     return G4A_OK;
 }
 
@@ -245,6 +252,14 @@ int analyse(g4a_ctx* ctx, const g4a_attn_args* a, Analysis* an, bool check_point
         r.plan.keys_per_split = nkeys;
         return G4A_OK;
     }
+    if (a->T >= PREFILL_MIN_T && group == 8 && r.q_contig && r.k_contig && a->attn_softcap == 0.0f &&
+        a->S < (1u << 28)) {
+        // query-tiled prefill: 8 queries x 8 heads per workgroup, keys in 16-key tiles
+        r.plan.kernel = G4A_KERNEL_PREFILL;
+        r.plan.splits = 1;
+        r.plan.keys_per_split = nkeys;
+        return G4A_OK;
+    }
     r.plan.kernel = G4A_KERNEL_DECODE;
     const uint32_t kt = 8 / (group / 2);  // key-tile slots per 8-wave workgroup (2 heads per wave)
     const uint32_t tiles = (nkeys + TILE - 1) / TILE;
@@ -312,6 +327,8 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->combine[0], "g4a_combine_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->combine[1], "g4a_combine_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->generic, "g4a_generic_attention")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->prefill[0], "g4a_prefill_d256")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->prefill[1], "g4a_prefill_d512")) return bail(rc);
     if (hipMalloc(reinterpret_cast<void**>(&ctx->dummy), 4096) != hipSuccess ||
         hipMemset(ctx->dummy, 0, 4096) != hipSuccess) {
         fail(ctx, G4A_E_NOMEM, "dummy buffer allocation failed");
@@ -431,6 +448,24 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
                             pl.k_start, pl.k_end, a->kv_ring_cap, a->sliding_window, a->scale, a->attn_softcap};
         return launch(ctx, ctx->generic, dim3(a->Hq, a->T, 1), dim3(64, 1, 1), gp, "generic attention", true);
     }
+    if (pl.kernel == G4A_KERNEL_PREFILL) {
+        G4aPrefillParams pp{};
+        pp.q = a->q;
+        pp.k = a->k;
+        pp.v = a->v;
+        pp.out = a->out;
+        pp.T = a->T;
+        pp.S = a->S;
+        pp.Hq = a->Hq;
+        pp.Hkv = a->Hkv;
+        pp.q_pos0 = a->q_pos ? a->q_pos[0] : a->q_pos0;
+        pp.k_pos0 = a->k_pos ? (a->S ? a->k_pos[0] : 0) : a->k_pos0;
+        pp.ring_cap = a->kv_ring_cap;
+        pp.window = a->sliding_window;
+        pp.scale = a->scale;
+        return launch(ctx, ctx->prefill[a->Dh == 512 ? 1 : 0], dim3((a->T + 7) / 8, a->Hkv, 1), dim3(256, 1, 1), pp,
+                      "prefill", true);
+    }
     // split-K flash-decode (+ combine)
     const uint32_t *qd = nullptr, *kd = nullptr;
     if (!an.q_contig || !an.k_contig) {
@@ -468,7 +503,7 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
         return rc;
     if (pl.splits > 1) {
         G4aCombineParams cp{dp.part, a->out, a->T, a->Hq, pl.splits, a->Dh};
-        if (int rc = launch(ctx, ctx->combine[d512], dim3(a->Dh / 64, a->Hq, a->T), dim3(256, 1, 1), cp, "combine"))
+        if (int rc = launch(ctx, ctx->combine[d512], dim3(a->Dh / 16, a->Hq, a->T), dim3(256, 1, 1), cp, "combine"))
             return rc;
     }
     return G4A_OK;

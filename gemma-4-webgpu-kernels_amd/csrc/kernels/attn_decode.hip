@@ -457,21 +457,24 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
 
 // out = sum_s acc_s * e^(m_s - M) / sum_s l_s * e^(m_s - M), M = max_s m_s; 0 when the
 // denominator is 0 (the semantics of rust/src/kernels/attention_combine.wgsl:1-28).
-// One block per (64 output dims, head, query). The split weights e^(m_s - M) are
-// computed once per block into LDS; the 4 waves then stream disjoint quarters of
-// the splits with several loads in flight per lane and reduce through LDS.
+// One block per (16 output dims, head, query): wide enough that a decode
+// step's partials are read by the whole GPU. The split weights e^(m_s - M) are
+// computed once per block into LDS; thread (group g, dim i) then sums splits
+// s = g, g + 16, ... with several loads in flight, and the 16 groups reduce
+// through LDS.
 constexpr int COMBINE_MAX_SPLITS = 1024;
 
 template <int DH>
 __device__ __forceinline__ void combine(const G4aCombineParams& p) {
     __shared__ float wgt[COMBINE_MAX_SPLITS];
-    __shared__ float red[4][64];
+    __shared__ float red[16][17];
     __shared__ float redm[4], redl[4];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
-    const uint32_t d = blockIdx.x * 64 + lane;
+    const int i = tid & 15, grp = tid >> 4;
     const size_t ih = (size_t)blockIdx.z * p.Hq + blockIdx.y;
+    const uint32_t d = blockIdx.x * 16 + i;
     const float* __restrict__ ml = p.part + (size_t)p.T * p.Hq * p.nsplit * DH + ih * p.nsplit * 2;
     const float* __restrict__ acc = p.part + ih * p.nsplit * DH + d;
     const uint32_t ns = p.nsplit;
@@ -494,19 +497,21 @@ __device__ __forceinline__ void combine(const G4aCombineParams& p) {
     L = redl[0] + redl[1] + redl[2] + redl[3];
     constexpr int U = 8;
     float A = 0.0f;
-    uint32_t s = w;
-    for (; s + 4 * (U - 1) < ns; s += 4 * U) {
+    uint32_t s = grp;
+    for (; s + 16 * (U - 1) < ns; s += 16 * U) {
         float x[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) x[u] = acc[(size_t)(s + 4 * u) * DH];
+        for (int u = 0; u < U; ++u) x[u] = acc[(size_t)(s + 16 * u) * DH];
 #pragma unroll
-        for (int u = 0; u < U; ++u) A += x[u] * wgt[s + 4 * u];
+        for (int u = 0; u < U; ++u) A += x[u] * wgt[s + 16 * u];
     }
-    for (; s < ns; s += 4) A += acc[(size_t)s * DH] * wgt[s];
-    red[w][lane] = A;
+    for (; s < ns; s += 16) A += acc[(size_t)s * DH] * wgt[s];
+    red[grp][i] = A;
     __syncthreads();
-    if (w == 0) {
-        A = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+    if (tid < 16) {
+        A = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) A += red[g][tid];
         p.out[ih * DH + d] = L > 0.0f ? A / L : 0.0f;
     }
 }

@@ -1,3 +1,4 @@
 // The single gfx950 code object of libg4a.so (loaded with hipModuleLoad):
 // every kernel of the attention path, compiled as one translation unit.
 #include "attn_decode.hip"
+#include "attn_prefill.hip"

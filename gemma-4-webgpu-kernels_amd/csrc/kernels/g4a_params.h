@@ -53,3 +53,17 @@ struct G4aGenericParams {
     uint32_t window;
     float scale, softcap;
 };
+
+// Query-tiled causal / sliding-window prefill over contiguous positions:
+// query i has position q_pos0 + i, key j has position k_pos0 + j; group of 8
+// query heads per kv head; Dh == Dv in {256, 512}; no soft-cap.
+struct G4aPrefillParams {
+    const float* q;        // [T, Hq, Dh]
+    const float* k;        // [rows, Hkv, Dh]
+    const float* v;        // [rows, Hkv, Dh]
+    float* out;            // [T, Hq*Dh]
+    uint32_t T, S, Hq, Hkv;
+    uint32_t q_pos0, k_pos0;
+    uint32_t ring_cap, window;
+    float scale;
+};

@@ -1,0 +1,112 @@
+"""GPU parity of the query-tiled MFMA prefill kernel (approximate matrix-core
+scores + exact rescoring of every key near its row maximum) against the CPU
+oracle (rust/src/backend_cpu.rs:270-336), through the C-ABI. Same bar as
+decode: max-abs <= 1e-5, mean-abs <= 1e-6 in f32.
+
+Covers configs[3] at full size (2048-token prompts, sliding window 512 at
+head_dim 256 and full causal at 512), ragged query counts, chunked prefill
+continuing from a cache, KV rings, and degenerate near-tie inputs that
+overflow the per-wave candidate list (compaction and early correction)."""
+import numpy as np
+import pytest
+
+import g4a
+import g4a.synth as synth
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 1e-5, 1e-6
+
+
+def assert_parity(got, want, label):
+    d = np.abs(got.astype(np.float64) - np.asarray(want, np.float64))
+    mx, mean = float(d.max()), float(d.mean())
+    print(f"  {label}: max-abs {mx:.3e} mean-abs {mean:.3e}", flush=True)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, f"{label}: max-abs {mx:.3e} mean-abs {mean:.3e}"
+
+
+def run(ctx, ins, window, label, **kw):
+    print(f"[gpu] {label}", flush=True)
+    T, S = ins.q.shape[0], ins.k.shape[0]
+    plan = ctx.plan(T=T, S=S, Hq=ins.q.shape[1], Hkv=ins.k.shape[1], Dh=ins.q.shape[2], Dv=ins.v.shape[2],
+                    q_pos0=int(ins.q_pos[0]), k_pos0=int(ins.k_pos[0]), window=window)
+    assert g4a.KERNEL_NAMES[plan.kernel] == "prefill", label
+    want = oracle.attention(ins.q, ins.k, ins.v, ins.q_pos, ins.k_pos, window=window, **kw)
+    got = g4a.attention_host(ctx, ins.q, ins.k, ins.v, q_pos=ins.q_pos, k_pos=ins.k_pos, window=window, **kw)
+    assert_parity(got, want, label)
+    return got
+
+
+@pytest.mark.parametrize("name,T,Dh,W", [
+    ("configs[3a] local prefill hd256 T2048 window512", 2048, 256, 512),
+    ("configs[3b] global prefill hd512 T2048 causal", 2048, 512, 0),
+])
+def test_configs3_full_size(ctx, name, T, Dh, W):
+    ins = synth.gemma_inputs(T=T, S=T, Dh=Dh, seed=3, q_pos=np.arange(T))
+    run(ctx, ins, W, name)
+
+
+@pytest.mark.parametrize("T,S,Dh,W", [(16, 16, 256, 0), (37, 37, 256, 5), (29, 29, 512, 0), (100, 100, 512, 17),
+                                      (24, 900, 256, 512), (40, 3000, 512, 0), (64, 700, 256, 64)])
+def test_ragged_and_chunked(ctx, T, S, Dh, W):
+    # T queries are the last T positions of S keys (a prompt chunk after S - T cached tokens)
+    ins = synth.gemma_inputs(T=T, S=S, Dh=Dh, seed=T * 7 + S)
+    run(ctx, ins, W, f"T={T} S={S} Dh={Dh} window={W}")
+
+
+def test_scale_not_one(ctx):
+    ins = synth.gemma_inputs(T=48, S=48, Dh=256, seed=9, q_pos=np.arange(48))
+    run(ctx, ins, 0, "scale 1/16", scale=0.0625)
+
+
+def test_all_tied_scores_overflow_the_candidate_list(ctx):
+    # q = 0: every visible key ties at score 0, so every key is a candidate and the
+    # per-wave list overflows repeatedly; the answer is the mean of the visible values
+    for T, S, Dh, W in [(64, 2048, 256, 0), (32, 1500, 512, 0), (48, 2000, 256, 700)]:
+        ins = synth.gemma_inputs(T=T, S=S, Dh=Dh, seed=5)
+        ins.q[:] = 0.0
+        got = run(ctx, ins, W, f"q=0 T={T} S={S} Dh={Dh} window={W}")
+        i = T - 1
+        lo = max(0, S - 1 - W + 1) if W else 0
+        np.testing.assert_allclose(got[i].reshape(8, Dh)[0], ins.v[lo:S, 0].astype(np.float64).mean(0), atol=2e-6)
+
+
+def test_near_ties_from_repeated_keys(ctx):
+    # every key repeated 8 times: exact ties in the sequential order, tiny differences on the matrix cores
+    base = synth.gemma_inputs(T=64, S=256, Dh=256, seed=13, q_pos=np.arange(64))
+    k = np.repeat(base.k[:32], 8, axis=0)
+    ins = synth.AttnInputs(base.q, k, base.v, np.arange(192, 256, dtype=np.uint32), base.k_pos)
+    run(ctx, ins, 0, "repeated keys")
+
+
+def test_prefill_from_a_ring(ctx):
+    # a 1024-slot ring holding positions 976..1999; 24 new queries at 1976..1999 with window 512
+    L, cap, T, Dh, W = 2000, 1024, 24, 256, 512
+    ins = synth.gemma_inputs(T=T, S=L, Dh=Dh, seed=77)
+    want = oracle.attention(ins.q, ins.k, ins.v, ins.q_pos, ins.k_pos, window=W)
+    ring_k = np.zeros((cap, 1, Dh), np.float32)
+    ring_v = np.zeros((cap, 1, Dh), np.float32)
+    for p_ in range(L - cap, L):
+        ring_k[p_ % cap] = ins.k[p_]
+        ring_v[p_ % cap] = ins.v[p_]
+    dev = [ctx.upload(x) for x in (ins.q, ring_k, ring_v)]
+    out = ctx.empty((T, 8 * Dh))
+    try:
+        print("[gpu] prefill from ring", flush=True)
+        ctx.attention(dev[0].ptr, dev[1].ptr, dev[2].ptr, out.ptr, T=T, S=L, Hq=8, Hkv=1, Dh=Dh, Dv=Dh,
+                      q_pos0=L - T, k_pos0=0, window=W, ring_cap=cap)
+        got = out.to_host()
+    finally:
+        for d in dev:
+            d.free()
+        out.free()
+    assert_parity(got, want, "prefill from ring")
+
+
+def test_prefill_matches_decode_kernel_rows(ctx):
+    # the last query of a prefill equals a decode of that query (independent kernels)
+    ins = synth.gemma_inputs(T=32, S=32, Dh=512, seed=21, q_pos=np.arange(32))
+    full = run(ctx, ins, 0, "prefill T=32")
+    last = g4a.attention_host(ctx, ins.q[-1:], ins.k, ins.v, q_pos=[31], k_pos=ins.k_pos)
+    assert np.abs(full[-1] - last[0]).max() < 2e-6
