@@ -12,7 +12,7 @@ configs[3] prefill TFLOP/s, the configs[4] 35-layer schedule in us/token, and
 the CPU oracle (oracle/attn_oracle.c, the restatement of
 rust/src/backend_cpu.rs:270-336) timed on the host cores on a bounded sample.
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu] [--calibration-copy MIB]
 """
 from __future__ import annotations
 
@@ -201,6 +201,9 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline decode only (no extras, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
+                    help="first run 3 device-to-device copies of MIB MiB (the reference dispatch for "
+                         "scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters to bytes)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -210,6 +213,16 @@ def main(argv=None):
     ctx = g4a.Context(0)
     info = ctx.device_info()
     print(f"[bench] device {info.arch.decode()} with {info.compute_units} CUs", file=sys.stderr, flush=True)
+
+    if args.calibration_copy:
+        n = args.calibration_copy << 20
+        a, b = ctx.malloc(n), ctx.malloc(n)
+        ctx.zero(a, n)
+        for _ in range(3):
+            ctx.d2d(b, a, n)
+        ctx.sync()
+        ctx.free(a)
+        ctx.free(b)
 
     # ---- headline: hd512 global decode at 32K context ----
     head = Decode(ctx, S=32768, Dh=512, seed=4)

@@ -1,0 +1,342 @@
+// HipBackend: the attention-path subset of the reference's Backend trait over
+// libg4a.so's C-ABI. Declarations and conventions are in hip_backend.hpp.
+#include "hip_backend.hpp"
+
+#include <algorithm>
+#include <cstring>
+
+namespace g4a {
+
+namespace {
+
+// Recycled buffers kept per backend (the reference keeps 128 MiB,
+// rust/src/backend_wgpu.rs:191; a 288 GB device affords more).
+constexpr size_t kPoolMaxBytes = size_t(2) << 30;
+constexpr size_t kKvMinRows = 256;  // first KV allocation (rust/src/backend_wgpu.rs:1024)
+
+size_t product(const std::vector<size_t>& s) {
+    size_t n = 1;
+    for (size_t d : s) n *= d;
+    return n;
+}
+
+// pow2 bucket of at least 256 bytes (rust/src/backend_wgpu.rs:384-389)
+size_t bucket(size_t bytes) {
+    size_t size = 256;
+    while (size < std::max<size_t>(bytes, 16)) size <<= 1;
+    return size;
+}
+
+std::string shape_str(const std::vector<size_t>& s) {
+    std::string r = "[";
+    for (size_t i = 0; i < s.size(); ++i) r += (i ? ", " : "") + std::to_string(s[i]);
+    return r + "]";
+}
+
+[[noreturn]] void bad(const std::string& msg) { throw std::runtime_error("hip backend: " + msg); }
+
+}  // namespace
+
+DeviceBuffer::~DeviceBuffer() {
+    if (owner_) owner_->release(ptr_, bytes_);
+}
+
+std::unique_ptr<HipBackend> HipBackend::create(int device) {
+    g4a_ctx* ctx = nullptr;
+    if (int rc = g4a_create(device, nullptr, &ctx))
+        bad("g4a_create failed (" + std::to_string(rc) + "): " + g4a_last_error(nullptr));
+    return std::unique_ptr<HipBackend>(new HipBackend(ctx));
+}
+
+HipBackend::~HipBackend() {
+    if (!ctx_) return;
+    g4a_sync(ctx_);
+    for (auto& [size, p] : pool_) g4a_free(ctx_, p);
+    pool_.clear();
+    g4a_destroy(ctx_);
+}
+
+void HipBackend::check(int rc, const char* what) const {
+    if (rc != G4A_OK) bad(std::string(what) + " failed (" + std::to_string(rc) + "): " + g4a_last_error(ctx_));
+}
+
+std::shared_ptr<DeviceBuffer> HipBackend::alloc(size_t bytes) {
+    size_t size = bucket(bytes);
+    void* p = nullptr;
+    auto it = pool_.find(size);
+    if (it != pool_.end()) {
+        p = it->second;
+        pool_.erase(it);
+        pooled_bytes_ -= size;
+    } else {
+        check(g4a_malloc(ctx_, size, &p), "g4a_malloc");
+    }
+    return std::make_shared<DeviceBuffer>(this, p, size);
+}
+
+// Stream order makes reuse safe: an op that later receives this buffer is
+// enqueued after every op that used it (rust/src/backend_wgpu.rs:403-412 keeps
+// the same bound on pooled bytes, destroying the rest).
+void HipBackend::release(void* ptr, size_t bytes) {
+    if (pooled_bytes_ + bytes > kPoolMaxBytes) {
+        g4a_sync(ctx_);  // the GPU may still read it
+        g4a_free(ctx_, ptr);
+        return;
+    }
+    pool_.emplace(bytes, ptr);
+    pooled_bytes_ += bytes;
+}
+
+HipTensor HipBackend::alloc_tensor(std::vector<size_t> shape) {
+    HipTensor t;
+    t.buffer = alloc(product(shape) * sizeof(float));
+    t.shape = std::move(shape);
+    return t;
+}
+
+HipTensor HipBackend::tensor(const float* data, std::vector<size_t> shape) {
+    HipTensor t = alloc_tensor(std::move(shape));
+    check(g4a_h2d(ctx_, t.data(), data, t.size() * sizeof(float)), "g4a_h2d");
+    return t;
+}
+
+HipTensor HipBackend::zeros(std::vector<size_t> shape) {
+    HipTensor t = alloc_tensor(std::move(shape));
+    check(g4a_zero(ctx_, t.data(), t.size() * sizeof(float)), "g4a_zero");
+    return t;
+}
+
+// rust/src/backend_wgpu.rs:730-732: a view; a growing KV buffer's spare
+// capacity is not carried over. A ring view keeps its ring when the row count
+// (dim 0) is unchanged, since the rows are the same.
+HipTensor HipBackend::reshape(const HipTensor& x, std::vector<size_t> shape) {
+    if (product(shape) != x.size()) bad("reshape " + shape_str(x.shape) + " -> " + shape_str(shape));
+    if (x.ring_cap && (shape.empty() || shape[0] != x.shape[0])) bad("reshape of a KV ring must keep its row count");
+    HipTensor t;
+    t.buffer = x.buffer;
+    t.ring_cap = x.ring_cap;
+    t.shape = std::move(shape);
+    return t;
+}
+
+// rust/src/backend_wgpu.rs:895-969 (the attention dispatch) and
+// rust/src/backend.rs:119-120 (the contract).
+HipTensor HipBackend::attention(const HipTensor& q, const HipTensor& k, const HipTensor& v, const AttnOpts& o) {
+    if (q.shape.size() != 3 || k.shape.size() != 3 || v.shape.size() != 3)
+        bad("attention wants q [T,Hq,Dh], k [S,Hkv,Dh], v [S,Hkv,Dv]; got " + shape_str(q.shape) + " " +
+            shape_str(k.shape) + " " + shape_str(v.shape));
+    const size_t T = q.shape[0], Hq = q.shape[1], Dh = q.shape[2];
+    const size_t S = k.shape[0], Hkv = k.shape[1], Dv = v.shape[2];
+    if (k.shape[2] != Dh || v.shape[0] != S || v.shape[1] != Hkv) bad("attention: k/v shapes disagree");
+    if (o.n_q_pos != T || o.n_k_pos != S)
+        bad("attention: " + std::to_string(o.n_q_pos) + " q positions for " + std::to_string(T) + " queries, " +
+            std::to_string(o.n_k_pos) + " k positions for " + std::to_string(S) + " keys");
+    if (k.ring_cap != v.ring_cap) bad("attention: k and v use different KV layouts");
+    HipTensor out = alloc_tensor({T, Hq * Dv});
+    g4a_attn_args a{};
+    a.q = q.data();
+    a.k = k.data();
+    a.v = v.data();
+    a.out = out.data();
+    a.T = uint32_t(T);
+    a.S = uint32_t(S);
+    a.Hq = uint32_t(Hq);
+    a.Hkv = uint32_t(Hkv);
+    a.Dh = uint32_t(Dh);
+    a.Dv = uint32_t(Dv);
+    a.q_pos = o.q_pos;
+    a.k_pos = o.k_pos;
+    a.scale = o.scale;
+    a.sliding_window = o.sliding_window;
+    a.attn_softcap = o.attn_softcap;
+    a.kv_ring_cap = k.ring_cap;
+    check(g4a_attention(ctx_, &a), "g4a_attention");
+    return out;
+}
+
+HipTensor HipBackend::slice_rows(const HipTensor& x, size_t start, size_t count) {
+    if (x.ring_cap) bad("slice_rows of a KV ring");
+    if (x.shape.empty() || start + count > x.shape[0]) bad("slice_rows out of range");
+    const size_t dim = x.size() / std::max<size_t>(x.shape[0], 1);
+    HipTensor out = alloc_tensor({count, dim});
+    check(g4a_d2d(ctx_, out.data(), x.data() + start * dim, count * dim * sizeof(float)), "g4a_d2d");
+    return out;
+}
+
+HipTensor HipBackend::concat_rows(const HipTensor* a, const HipTensor& b) {
+    if (b.ring_cap || (a && a->ring_cap)) bad("concat_rows of a KV ring");
+    if (!a) {
+        HipTensor out = alloc_tensor(b.shape);
+        check(g4a_d2d(ctx_, out.data(), b.data(), b.size() * sizeof(float)), "g4a_d2d");
+        return out;
+    }
+    if (a->shape.size() != b.shape.size() || !std::equal(a->shape.begin() + 1, a->shape.end(), b.shape.begin() + 1))
+        bad("concat_rows " + shape_str(a->shape) + " + " + shape_str(b.shape));
+    std::vector<size_t> shape = a->shape;
+    shape[0] += b.shape[0];
+    HipTensor out = alloc_tensor(shape);
+    check(g4a_d2d(ctx_, out.data(), a->data(), a->size() * sizeof(float)), "g4a_d2d");
+    check(g4a_d2d(ctx_, out.data() + a->size(), b.data(), b.size() * sizeof(float)), "g4a_d2d");
+    return out;
+}
+
+// rust/src/backend_wgpu.rs:1014-1055: a capacity buffer of max(rows, 256) rows
+// that doubles (or grows to fit) when full; the old buffer is reported dead.
+KvAppend<HipTensor> HipBackend::kv_append(const HipTensor* existing, const HipTensor& add) {
+    if (add.shape.empty() || add.shape[0] == 0) bad("kv_append of an empty tensor");
+    if (existing && existing->ring_cap) bad("kv_append on a KV ring (use kv_append_ring)");
+    const size_t rows = add.shape[0];
+    const size_t dim = add.size() / rows;
+    auto make_buffer = [&](size_t cap) {
+        HipTensor t;
+        t.buffer = alloc(cap * dim * sizeof(float));
+        t.cap_rows = cap;
+        return t;
+    };
+    if (!existing) {
+        HipTensor t = make_buffer(std::max(rows, kKvMinRows));
+        check(g4a_d2d(ctx_, t.data(), add.data(), add.size() * sizeof(float)), "g4a_d2d");
+        t.shape = add.shape;
+        return {t, std::nullopt};
+    }
+    if (existing->size() / std::max<size_t>(existing->shape[0], 1) != dim) bad("kv_append row size mismatch");
+    const size_t len = existing->shape[0];
+    const size_t cap_rows = existing->cap_rows ? existing->cap_rows : len;
+    HipTensor dst = *existing;
+    dst.cap_rows = cap_rows;
+    std::optional<HipTensor> dead;
+    if (len + rows > cap_rows) {
+        dst = make_buffer(std::max(cap_rows * 2, len + rows));
+        check(g4a_d2d(ctx_, dst.data(), existing->data(), len * dim * sizeof(float)), "g4a_d2d");
+        dead = *existing;
+    }
+    check(g4a_kv_write(ctx_, dst.data(), 0, uint32_t(dim), uint32_t(len), add.data(), uint32_t(rows)), "g4a_kv_write");
+    HipTensor view;
+    view.buffer = dst.buffer;
+    view.shape = add.shape;
+    view.shape[0] = len + rows;
+    view.cap_rows = dst.cap_rows;
+    return {view, dead};
+}
+
+// Copy logical rows [first, first+count) between two KV layouts: a ring keeps
+// row j in slot j % cap, a linear buffer (cap 0) keeps row j at j - base.
+void HipBackend::copy_rows_ring(const HipTensor& src, uint32_t src_cap, HipTensor& dst, uint32_t dst_cap,
+                                uint64_t first, uint64_t count, size_t row_elems) {
+    const uint64_t end = first + count;
+    uint64_t j = first;
+    while (j < end) {
+        uint64_t s = src_cap ? j % src_cap : j;
+        uint64_t d = dst_cap ? j % dst_cap : j - first;
+        uint64_t run = end - j;
+        if (src_cap) run = std::min<uint64_t>(run, src_cap - s);
+        if (dst_cap) run = std::min<uint64_t>(run, dst_cap - d);
+        check(g4a_d2d(ctx_, dst.data() + d * row_elems, src.data() + s * row_elems, run * row_elems * sizeof(float)),
+              "g4a_d2d");
+        j += run;
+    }
+}
+
+// A sliding-window layer needs, for a chunk of `rows` new queries, the last
+// window + rows - 1 keys; older keys are never visible again. The ring holds
+// exactly that many slots (slot = logical row % ring_cap), so the cache stays
+// O(window) for any context length. A later, larger chunk re-lays the live
+// rows into a bigger ring, which is reported dead like kv_append's growth.
+KvAppend<HipTensor> HipBackend::kv_append_ring(const HipTensor* existing, const HipTensor& add, uint32_t window) {
+    if (window == 0) bad("kv_append_ring needs a sliding window");
+    if (add.shape.empty() || add.shape[0] == 0) bad("kv_append_ring of an empty tensor");
+    const size_t rows = add.shape[0];
+    const size_t dim = add.size() / rows;
+    const uint64_t need = uint64_t(window) + rows - 1;
+    if (need > UINT32_MAX) bad("kv_append_ring: ring too large");
+    auto make_ring = [&](uint64_t cap) {
+        HipTensor t;
+        t.buffer = alloc(cap * dim * sizeof(float));
+        t.ring_cap = uint32_t(cap);
+        return t;
+    };
+    HipTensor dst;
+    std::optional<HipTensor> dead;
+    uint64_t len = 0;
+    if (!existing) {
+        dst = make_ring(need);
+    } else {
+        if (!existing->ring_cap) bad("kv_append_ring on a linear KV tensor");
+        if (existing->size() / existing->shape[0] != dim) bad("kv_append_ring row size mismatch");
+        len = existing->shape[0];
+        dst = *existing;
+        if (existing->ring_cap < need) {
+            dst = make_ring(need);
+            const uint64_t live = std::min<uint64_t>(len, existing->ring_cap);
+            copy_rows_ring(*existing, existing->ring_cap, dst, dst.ring_cap, len - live, live, dim);
+            dead = *existing;
+        }
+    }
+    if (len + rows > UINT32_MAX) bad("kv_append_ring: position overflow");
+    check(g4a_kv_write(ctx_, dst.data(), dst.ring_cap, uint32_t(dim), uint32_t(len), add.data(), uint32_t(rows)),
+          "g4a_kv_write");
+    HipTensor view;
+    view.buffer = dst.buffer;
+    view.ring_cap = dst.ring_cap;
+    view.shape = add.shape;
+    view.shape[0] = len + rows;
+    return {view, dead};
+}
+
+// rust/src/backend_wgpu.rs:1057-1089: blocking read. A ring reads back its
+// resident rows (the last min(rows, ring_cap)) in logical order.
+std::vector<float> HipBackend::readback(const HipTensor& t) {
+    if (!t.ring_cap) {
+        std::vector<float> out(t.size());
+        check(g4a_d2h(ctx_, out.data(), t.data(), out.size() * sizeof(float)), "g4a_d2h");
+        return out;
+    }
+    const size_t dim = t.size() / t.shape[0];
+    const uint64_t live = std::min<uint64_t>(t.shape[0], t.ring_cap);
+    HipTensor lin = alloc_tensor({size_t(live), dim});
+    copy_rows_ring(t, t.ring_cap, lin, 0, t.shape[0] - live, live, dim);
+    std::vector<float> out(live * dim);
+    check(g4a_d2h(ctx_, out.data(), lin.data(), out.size() * sizeof(float)), "g4a_d2h");
+    return out;
+}
+
+// Launches are already submitted to the stream when an op returns.
+void HipBackend::flush() {}
+
+// rust/src/backend_wgpu.rs:1100-1124. Buffers return to the pool when their
+// last handle drops, so keep-sets need no bookkeeping here: dropping the
+// retired tensors is the whole job.
+void HipBackend::end_frame(const std::vector<HipTensor>& keep, std::vector<HipTensor> also_free) {
+    (void)keep;
+    also_free.clear();
+}
+
+void HipBackend::free_tensor(HipTensor t) { t.buffer.reset(); }
+
+std::pair<HipTensor, HipTensor> KvCache::append_and_read(HipBackend& b, size_t src_layer, const HipTensor& k_new,
+                                                        const HipTensor& v_new, uint32_t window) {
+    auto& slot = slots_.at(src_layer);
+    const HipTensor* k_old = slot ? &slot->first : nullptr;
+    const HipTensor* v_old = slot ? &slot->second : nullptr;
+    KvAppend<HipTensor> rk = window ? b.kv_append_ring(k_old, k_new, window) : b.kv_append(k_old, k_new);
+    KvAppend<HipTensor> rv = window ? b.kv_append_ring(v_old, v_new, window) : b.kv_append(v_old, v_new);
+    if (rk.dead) dead_.push_back(*rk.dead);
+    if (rv.dead) dead_.push_back(*rv.dead);
+    slot = std::make_pair(rk.tensor, rv.tensor);
+    return *slot;
+}
+
+void KvCache::reset(HipBackend& b) {
+    for (auto& s : slots_) {
+        if (s) {
+            b.free_tensor(s->first);
+            b.free_tensor(s->second);
+            s.reset();
+        }
+    }
+    for (auto& t : dead_) b.free_tensor(t);
+    dead_.clear();
+    positions.clear();
+}
+
+}  // namespace g4a

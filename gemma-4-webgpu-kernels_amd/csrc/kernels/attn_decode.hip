@@ -14,15 +14,23 @@
 // scores reach ~90, so any other summation order moves them by ~1e-5 and the
 // output by up to ~5e-5; bit-equal scores keep the output within ~1e-7.
 //
-// Work decomposition. A workgroup is 4 waves and owns one key split of one
-// (query, kv head). Each wave owns 4 query heads ("head group") and walks
-// 64-key tiles of its split: in the score phase lane = key, each lane runs 4
-// sequential dots (q is wave-uniform, so it streams through the scalar cache),
-// then an online softmax per head; in the P.V phase lane = output dims and the
-// wave's probabilities are broadcast from LDS. The 4 waves of a workgroup are
-// (key-tile slot, head group) pairs; at the end the key-tile slots of a head
-// group merge through LDS and the split's (m, l, acc) partial is written,
-// or the normalised output when there is a single split.
+// Work decomposition. A workgroup is 8 waves (512 threads) and owns one key
+// split of one (query, kv head); the host picks the split count so the grid
+// covers every CU (k_start/k_end already trimmed to the visible range). The
+// waves form KT key-tile slots of GROUP/2 waves, each wave owning 2 query
+// heads, and each slot walks 64-key tiles of the split. Per tile, a slot
+// streams DH/64 K chunks (64 keys x 64 dims) and DH/64 V chunks (64/(DH/64)
+// keys x DH dims) of 16 KiB each from HBM through registers into a
+// double-buffered LDS chunk, D chunks ahead, so K and V loads form one
+// continuous stream across phases and tiles:
+//   - scores: lane = key; the two heads' query rows sit in LDS and reach the
+//     multiplies through DPP row broadcasts (no scalar loads in the loop);
+//   - online softmax per head (wave max / exp / sum, lane = key);
+//   - P.V on the matrix cores (v_mfma_f32_4x4x1_16b_f32), probabilities
+//     broadcast from LDS.
+// At the end the slots' accumulators merge through LDS and the split's
+// (m, l, acc) partial is written, or the normalised output when there is a
+// single split; a separate combine kernel merges the partials (log-sum-exp).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -47,16 +55,6 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
-// Read-only, wave-uniform data (the query rows) is addressed through the
-// constant address space so the compiler can fetch it with scalar loads into
-// SGPRs instead of per-lane vector loads.
-typedef __attribute__((address_space(4))) const float cfloat;
-__device__ __forceinline__ cfloat* as_const(const float* p) { return (cfloat*)(p); }
-
-__device__ __forceinline__ float f4get(const float4& v, int e) {
-    return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
-}
-
 // Physical row of logical key j: a ring of ring_cap slots, or the identity.
 __device__ __forceinline__ uint32_t phys_row(uint32_t j, uint32_t ring_cap) {
     return ring_cap ? j % ring_cap : j;
@@ -69,25 +67,6 @@ __device__ __forceinline__ float score_epilogue(float dot, float scale, float so
 }
 
 typedef float f4v __attribute__((ext_vector_type(4)));  // MFMA accumulator (4 VGPRs)
-
-// One float4 chunk (dims d..d+3) of the 4 per-lane dots of a head group:
-// for each head, dot = (((dot + q[d]k[d]) + q[d+1]k[d+1]) + ...) with separately
-// rounded multiplies and adds, exactly the CPU reference's order.
-template <int DH>
-__device__ __forceinline__ void qk_chunk(float (&s)[4], cfloat* __restrict__ qh, int d, const float4& kk, int c) {
-    // bound how far the scheduler hoists the scalar q loads (SGPR budget)
-    if ((c & 1) == 0) __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-        cfloat* qd = qh + h * DH + d;
-        float a = s[h];
-        a = a + qd[0] * kk.x;
-        a = a + qd[1] * kk.y;
-        a = a + qd[2] * kk.z;
-        a = a + qd[3] * kk.w;
-        s[h] = a;
-    }
-}
 
 // Sixteen dims (16B .. 16B+15 of a 64-dim stage) of the exact dots of the two
 // heads of a wave, lane = key: dot = ((dot + q[d]*k[d]) + q[d+1]*k[d+1]) + ...,

@@ -4,7 +4,7 @@ Produces, in-tree (so the files travel with the repository snapshot):
   gemma-4-webgpu-kernels_amd/_build/g4a_kernels.hsaco  gfx950 code object (hipModuleLoad)
   gemma-4-webgpu-kernels_amd/_build/libg4a.so          C-ABI host library (include/g4a.h)
   gemma-4-webgpu-kernels_amd/_build/libg4a_backend.so  C++ mirror of the Backend trait
-  gemma-4-webgpu-kernels_amd/_build/test_backend       C++ parity driver for that mirror
+  tests/cpp/_build/test_backend                        C++ parity driver for that mirror (test infrastructure)
   oracle/_build/liboracle.so                           CPU oracle (test infrastructure)
 
 Every call recompiles everything (it is the "does it build" check).
@@ -37,7 +37,7 @@ DEVICE_FLAGS = [
 HSACO = OUT / "g4a_kernels.hsaco"
 LIBG4A = OUT / "libg4a.so"
 LIBBACKEND = OUT / "libg4a_backend.so"
-TEST_BACKEND = OUT / "test_backend"
+TEST_BACKEND = REPO / "tests" / "cpp" / "_build" / "test_backend"
 LIBORACLE = ORACLE_OUT / "liboracle.so"
 
 
@@ -73,10 +73,14 @@ def build_backend(verbose: bool = False) -> Path:
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", f"-I{INCLUDE}", f"-I{CSRC}", CSRC / "hip_backend.cpp",
           "-o", tmp, f"-L{OUT}", "-lg4a", f"-Wl,-rpath,$ORIGIN"], verbose)
     tmp.replace(LIBBACKEND)
+    TEST_BACKEND.parent.mkdir(parents=True, exist_ok=True)
     tmp = TEST_BACKEND.with_suffix(".tmp")
-    _run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", f"-I{INCLUDE}", f"-I{CSRC}", f"-I{ORACLE_DIR}",
-          REPO / "tests" / "cpp" / "test_backend.cpp", ORACLE_DIR / "attn_oracle.c",
-          "-o", tmp, f"-L{OUT}", "-lg4a_backend", "-lg4a", f"-Wl,-rpath,$ORIGIN", "-lpthread", "-lm"], verbose)
+    oracle_obj = TEST_BACKEND.parent / "attn_oracle.o"
+    _run(["gcc", "-O2", "-std=gnu11", "-ffp-contract=off", "-fno-fast-math", "-c", ORACLE_DIR / "attn_oracle.c",
+          "-o", oracle_obj], verbose)
+    _run(["g++", "-O2", "-std=c++17", f"-I{INCLUDE}", f"-I{CSRC}", REPO / "tests" / "cpp" / "test_backend.cpp",
+          oracle_obj, "-o", tmp, f"-L{OUT}", "-lg4a_backend", "-lg4a", "-Wl,-rpath,$ORIGIN/../../../gemma-4-webgpu-kernels_amd/_build", "-lpthread", "-lm"],
+         verbose)
     tmp.replace(TEST_BACKEND)
     return LIBBACKEND
 

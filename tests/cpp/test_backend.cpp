@@ -1,0 +1,258 @@
+// Parity driver for the C++ HipBackend (gemma-4-webgpu-kernels_amd/csrc/hip_backend.hpp):
+// the reference's backend tests for this path, run through the op surface a
+// Rust HipBackend would call, checked against the CPU oracle
+// (oracle/attn_oracle.c, a restatement of rust/src/backend_cpu.rs:270-336).
+//
+//   grouped_attention_parity   rust/tests/gpu.rs:262-293 (same cases, Lcg seed 21)
+//   slice/concat/kv_append     rust/tests/gpu.rs:96-120 (three 200-row appends: growth)
+//   kv_cache_decode            prefill chunks + decode steps through KvCache, with a
+//                              sliding layer on a ring (incl. regrowth and wrap-around)
+//                              and a global layer on the growing buffer, every step
+//                              checked against the oracle over the full history
+//
+// The bar is the north star's: max-abs <= 1e-5 and mean-abs <= 1e-6 (f32),
+// exact equality for the copies. Exit status 0 = all passed.
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "hip_backend.hpp"
+
+extern "C" int oracle_attention(const float* q, const float* k, const float* v, float* out, size_t T, size_t S,
+                                size_t Hq, size_t Hkv, size_t Dh, size_t Dv, const uint32_t* q_pos,
+                                const uint32_t* k_pos, float scale, uint32_t window, float softcap,
+                                int requested_threads);
+
+namespace {
+
+int g_failures = 0;
+
+// rust/tests/common/mod.rs:30-42
+struct Lcg {
+    uint32_t s;
+    explicit Lcg(uint32_t seed) : s(seed) {}
+    float next() {
+        s = (s * 1103515245u + 12345u) & 0x7fffffffu;
+        return float(s) / float(0x7fffffff);
+    }
+    std::vector<float> rand(size_t n, float scale) {
+        std::vector<float> out(n);
+        for (auto& x : out) x = (next() * 2.0f - 1.0f) * scale;
+        return out;
+    }
+};
+
+void expect(bool ok, const std::string& label) {
+    std::printf("  %s %s\n", ok ? "ok  " : "FAIL", label.c_str());
+    std::fflush(stdout);
+    if (!ok) ++g_failures;
+}
+
+void close(const std::string& label, const std::vector<float>& got, const std::vector<float>& want) {
+    if (got.size() != want.size()) {
+        expect(false, label + ": size " + std::to_string(got.size()) + " != " + std::to_string(want.size()));
+        return;
+    }
+    double mx = 0.0, sum = 0.0;
+    for (size_t i = 0; i < got.size(); ++i) {
+        double d = std::fabs(double(got[i]) - double(want[i]));
+        if (!(d <= mx)) mx = d;  // NaN-propagating
+        sum += d;
+    }
+    double mean = got.empty() ? 0.0 : sum / double(got.size());
+    char buf[160];
+    std::snprintf(buf, sizeof buf, " (max-abs %.3e mean-abs %.3e)", mx, mean);
+    expect(mx <= 1e-5 && mean <= 1e-6, label + buf);
+}
+
+std::vector<float> oracle(const std::vector<float>& q, const std::vector<float>& k, const std::vector<float>& v,
+                          size_t T, size_t S, size_t Hq, size_t Hkv, size_t Dh, const std::vector<uint32_t>& qp,
+                          const std::vector<uint32_t>& kp, float scale, uint32_t window) {
+    std::vector<float> out(T * Hq * Dh);
+    oracle_attention(q.data(), k.data(), v.data(), out.data(), T, S, Hq, Hkv, Dh, Dh, qp.data(), kp.data(), scale,
+                     window, 0.0f, 0);
+    return out;
+}
+
+std::vector<uint32_t> iota(uint32_t from, uint32_t to) {
+    std::vector<uint32_t> r;
+    for (uint32_t i = from; i < to; ++i) r.push_back(i);
+    return r;
+}
+
+void grouped_attention_parity(g4a::HipBackend& b) {
+    std::printf("grouped_attention_parity\n");
+    Lcg r(21);
+    struct Case { size_t t, s, hq, hkv, dh; uint32_t window; };
+    const Case cases[] = {{3, 300, 8, 1, 256, 0}, {3, 300, 8, 1, 256, 150}, {1, 700, 8, 1, 512, 0},
+                          {1, 900, 8, 1, 256, 512}, {5, 5, 8, 1, 256, 0},     {6, 70, 8, 1, 256, 3},
+                          {2, 200, 4, 1, 256, 0},   {1, 64, 8, 2, 512, 0}};
+    for (const Case& c : cases) {
+        auto q = r.rand(c.t * c.hq * c.dh, 0.5f);
+        auto k = r.rand(c.s * c.hkv * c.dh, 0.5f);
+        auto v = r.rand(c.s * c.hkv * c.dh, 0.5f);
+        auto kpos = iota(0, uint32_t(c.s));
+        auto qpos = iota(uint32_t(c.s - c.t), uint32_t(c.s));
+        const float scale = 1.0f / std::sqrt(float(c.dh));
+        g4a::AttnOpts o;
+        o.q_pos = qpos.data();
+        o.n_q_pos = qpos.size();
+        o.k_pos = kpos.data();
+        o.n_k_pos = kpos.size();
+        o.scale = scale;
+        o.sliding_window = c.window;
+        auto out = b.attention(b.tensor(q.data(), {c.t, c.hq, c.dh}), b.tensor(k.data(), {c.s, c.hkv, c.dh}),
+                               b.tensor(v.data(), {c.s, c.hkv, c.dh}), o);
+        if (out.shape != std::vector<size_t>{c.t, c.hq * c.dh}) expect(false, "attention output shape");
+        char label[128];
+        std::snprintf(label, sizeof label, "grouped attention (T=%zu, S=%zu, Hq=%zu, Hkv=%zu, Dh=%zu, window=%u)", c.t,
+                      c.s, c.hq, c.hkv, c.dh, c.window);
+        close(label, b.readback(out), oracle(q, k, v, c.t, c.s, c.hq, c.hkv, c.dh, qpos, kpos, scale, c.window));
+    }
+}
+
+void copies_and_kv_append(g4a::HipBackend& b) {
+    std::printf("slice_rows / concat_rows / kv_append\n");
+    Lcg r(7);
+    const size_t rows = 4, stride = 13;
+    auto x = r.rand(rows * stride, 1.0f);
+    auto sl = b.readback(b.slice_rows(b.tensor(x.data(), {rows, stride}), 2, 2));
+    expect(sl == std::vector<float>(x.begin() + 2 * stride, x.begin() + 4 * stride), "slice_rows");
+    auto a = r.rand(2 * stride, 1.0f);
+    auto c = r.rand(3 * stride, 1.0f);
+    auto ta = b.tensor(a.data(), {2, stride});
+    auto tc = b.tensor(c.data(), {3, stride});
+    auto cat = b.concat_rows(&ta, tc);
+    std::vector<float> want = a;
+    want.insert(want.end(), c.begin(), c.end());
+    expect(cat.shape == std::vector<size_t>{5, stride} && b.readback(cat) == want, "concat_rows");
+    expect(b.readback(b.concat_rows(nullptr, tc)) == c, "concat_rows (None)");
+
+    // three appends of 200 rows: capacity 256 -> 512 -> 1024 (rust/tests/gpu.rs:108-120)
+    const size_t dim = 8;
+    std::optional<g4a::HipTensor> t;
+    std::vector<float> host;
+    const size_t caps[] = {256, 512, 1024};
+    const bool dead[] = {false, true, true};
+    for (int i = 0; i < 3; ++i) {
+        auto chunk = r.rand(200 * dim, 1.0f);
+        host.insert(host.end(), chunk.begin(), chunk.end());
+        auto res = b.kv_append(t ? &*t : nullptr, b.tensor(chunk.data(), {200, dim}));
+        expect(res.tensor.cap_rows == caps[i] && res.dead.has_value() == dead[i],
+               "kv_append step " + std::to_string(i) + ": capacity " + std::to_string(res.tensor.cap_rows));
+        t = res.tensor;
+    }
+    expect(t->shape == std::vector<size_t>{600, dim}, "kv_append shape [600, 8]");
+    expect(b.readback(*t) == host, "kv_append (growth) contents");
+    // an append that fits reuses the buffer in place
+    auto extra = r.rand(10 * dim, 1.0f);
+    auto res = b.kv_append(&*t, b.tensor(extra.data(), {10, dim}));
+    host.insert(host.end(), extra.begin(), extra.end());
+    expect(!res.dead && res.tensor.buffer == t->buffer && b.readback(res.tensor) == host, "kv_append in place");
+}
+
+// A two-layer stack: layer 0 slides (window 512, Dh 256, ring), layer 1 is
+// global (Dh 512, growing buffer). Chunk sizes force a ring regrowth (a chunk
+// wider than the ring allows) and wrap-around (history longer than the ring).
+void kv_cache_decode(g4a::HipBackend& b) {
+    std::printf("kv_cache_decode (ring sliding layer + growing global layer)\n");
+    const uint32_t W = 512;
+    const size_t Hq = 8, Hkv = 1, D0 = 256, D1 = 512;
+    std::vector<size_t> chunks = {100};
+    for (int i = 0; i < 20; ++i) chunks.push_back(1);
+    chunks.push_back(450);
+    for (int i = 0; i < 10; ++i) chunks.push_back(1);
+    chunks.push_back(64);
+    for (int i = 0; i < 420; ++i) chunks.push_back(1);
+    chunks.push_back(33);
+    for (int i = 0; i < 4; ++i) chunks.push_back(1);
+
+    Lcg r(99);
+    g4a::KvCache cache(2);
+    std::vector<float> k0, v0, k1, v1;  // full host history per layer
+    uint32_t pos = 0;
+    size_t step = 0, checked = 0;
+    uint32_t last_ring = 0;
+    for (size_t rows : chunks) {
+        auto qpos = iota(pos, pos + uint32_t(rows));
+        cache.push_positions(qpos.data(), qpos.size());
+        const auto& kpos = cache.positions;
+        const size_t S = kpos.size();
+        for (int layer = 0; layer < 2; ++layer) {
+            const size_t D = layer ? D1 : D0;
+            const uint32_t window = layer ? 0 : W;
+            const float scale = layer ? 1.0f : 1.0f / 16.0f;
+            auto q = r.rand(rows * Hq * D, 1.0f);
+            auto kn = r.rand(rows * Hkv * D, 1.0f);
+            auto vn = r.rand(rows * Hkv * D, 1.0f);
+            auto& kh = layer ? k1 : k0;
+            auto& vh = layer ? v1 : v0;
+            kh.insert(kh.end(), kn.begin(), kn.end());
+            vh.insert(vh.end(), vn.begin(), vn.end());
+            auto [k, v] = cache.append_and_read(b, layer, b.tensor(kn.data(), {rows, Hkv, D}),
+                                                b.tensor(vn.data(), {rows, Hkv, D}), window);
+            if (k.shape[0] != S) expect(false, "cache rows != positions");
+            g4a::AttnOpts o;
+            o.q_pos = qpos.data();
+            o.n_q_pos = qpos.size();
+            o.k_pos = kpos.data();
+            o.n_k_pos = S;
+            o.scale = scale;
+            o.sliding_window = window;
+            auto out = b.attention(b.tensor(q.data(), {rows, Hq, D}), k, v, o);
+            // every chunk, and every 16th decode step, is checked against the oracle
+            if (rows > 1 || step % 16 == 0 || step + 1 == chunks.size()) {
+                char label[160];
+                std::snprintf(label, sizeof label, "layer %d step %zu: T=%zu S=%zu%s", layer, step, rows, S,
+                              layer ? "" : (" ring " + std::to_string(k.ring_cap)).c_str());
+                close(label, b.readback(out), oracle(q, kh, vh, rows, S, Hq, Hkv, D, qpos, kpos, scale, window));
+                ++checked;
+            }
+            if (layer == 0) {
+                if (k.ring_cap != last_ring) std::printf("  ring capacity %u at S=%zu\n", k.ring_cap, S);
+                last_ring = k.ring_cap;
+                if (k.ring_cap < W + rows - 1) expect(false, "ring smaller than window + chunk - 1");
+            }
+        }
+        pos += uint32_t(rows);
+        ++step;
+        auto dead = cache.take_dead();
+        b.end_frame({}, std::move(dead));
+    }
+    // the ring reads back its resident rows in logical order
+    const auto* slot = cache.read(0);
+    const size_t S = cache.positions.size();
+    const size_t live = std::min<size_t>(S, slot->first.ring_cap);
+    auto got = b.readback(slot->first);
+    std::vector<float> want(k0.end() - live * D0, k0.end());
+    expect(S > slot->first.ring_cap && got == want, "ring wrapped and holds the last " + std::to_string(live) + " keys");
+    const auto* g = cache.read(1);
+    expect(b.readback(g->second) == v1, "global layer holds the whole history");
+    std::printf("  %zu attention calls checked over %zu tokens\n", checked, S);
+    cache.reset(b);
+}
+
+}  // namespace
+
+int main() {
+    std::unique_ptr<g4a::HipBackend> b;
+    try {
+        b = g4a::HipBackend::create(0);
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "test_backend: %s\n", e.what());
+        return 2;
+    }
+    try {
+        grouped_attention_parity(*b);
+        copies_and_kv_append(*b);
+        kv_cache_decode(*b);
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "test_backend: exception: %s\n", e.what());
+        return 1;
+    }
+    std::printf("%s: %d failure(s)\n", g_failures ? "FAILED" : "PASSED", g_failures);
+    return g_failures ? 1 : 0;
+}

@@ -109,3 +109,18 @@ def test_create_without_gpu_fails_cleanly():
     rc = lib.g4a_create(0, None, ctypes.byref(h))
     assert rc != 0 and not h.value
     assert lib.g4a_last_error(None)
+
+
+def test_backend_mirror_driver_links_and_reports_a_missing_device():
+    """The C++ Backend mirror and its parity driver link and start; without a
+    device, construction fails with an error (like WgpuBackend::create's Err)."""
+    import subprocess
+    from g4a import build
+    if not build.TEST_BACKEND.exists():
+        pytest.skip("C++ backend driver not built")
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present: the gpu test runs the driver")
+    r = subprocess.run([str(build.TEST_BACKEND)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2, (r.returncode, r.stdout, r.stderr)
+    assert "g4a_create failed" in r.stderr
