@@ -66,10 +66,9 @@ class Decode:
         return dict(T=1, S=self.S, Hq=HQ, Hkv=1, Dh=self.Dh, Dv=self.Dh, q_pos0=self.S - 1, k_pos0=0,
                     window=self.window, ring_cap=self.ring_cap, splits=splits)
 
-    def step(self, splits=0):
-        k, v = self.kv[self.i % len(self.kv)]
-        self.i += 1
-        self.ctx.attention(self.q.ptr, k.ptr, v.ptr, self.out.ptr, **self.kw(splits))
+    def calls(self, splits=0):
+        """One step per K/V copy: [[kw], [kw], ...] for time_steps."""
+        return [[dict(q=self.q.ptr, k=k.ptr, v=v.ptr, out=self.out.ptr, **self.kw(splits))] for k, v in self.kv]
 
     def visible(self):
         return min(self.S, self.window) if self.window else self.S
@@ -79,17 +78,31 @@ class Decode:
             a.free()
 
 
-def time_steps(ctx, fn, steps, warmup):
-    """Event-timed region of `steps` calls after `warmup` untimed ones; also the
-    main kernel's own event-timed duration. Returns (ms/step, kernel ms/launch)."""
-    for _ in range(warmup):
-        fn()
+def time_steps(ctx, calls, steps, warmup):
+    """Times `steps` steps of the hot path after `warmup` untimed ones. `calls`
+    lists the attention() keyword sets of consecutive steps (cycled); a step is
+    len(calls[i]) attention calls. All steps of a region are enqueued through
+    one g4a_attention_batch call, so the region measures the library (host
+    dispatch + kernels), not Python's per-call overhead.
+
+    Two timed regions, both bracketed by HIP events on the library's stream:
+    first the steps alone (ms/step), then the same steps again with the main
+    kernel of every call carrying dispatch-attached start/stop events (its
+    average duration). The per-dispatch events add a few microseconds between
+    launches, so they stay out of the region that gives ms/step.
+    Returns (ms/step, main-kernel ms/launch)."""
+    def batch(n):
+        return [kw for i in range(n) for kw in calls[i % len(calls)]]
+    warm, timed = ctx.prepare_batch(batch(warmup)), ctx.prepare_batch(batch(steps))
+    if warmup:
+        ctx.attention_batch(warm)
     ctx.sync()
-    ctx.kernel_timing(True)
     ctx.timer_start()
-    for _ in range(steps):
-        fn()
+    ctx.attention_batch(timed)
     total = ctx.timer_stop()
+    ctx.kernel_timing(True)
+    ctx.attention_batch(timed)
+    ctx.sync()
     kms, n = ctx.kernel_timing_read()
     ctx.kernel_timing(False)
     return total / steps, (kms / n if n else float("nan"))
@@ -150,17 +163,17 @@ def schedule_35_layers(ctx, steps, warmup):
         qs.append(ctx.upload(synth.rms_norm_rows(synth.normal_f32(seed * 100 + i, 0, HQ * dh).reshape(1, HQ, dh))))
         outs.append(ctx.empty((1, HQ * dh)))
 
-    def token():
-        for i in range(35):
-            k, v = caches[src[i]]
-            if layer_types[i] == "full":
-                ctx.attention(qs[i].ptr, k.ptr, v.ptr, outs[i].ptr, T=1, S=S, Hq=HQ, Hkv=1, Dh=512, Dv=512,
-                              q_pos0=S - 1, k_pos0=0)
-            else:
-                ctx.attention(qs[i].ptr, k.ptr, v.ptr, outs[i].ptr, T=1, S=S, Hq=HQ, Hkv=1, Dh=256, Dv=256,
-                              q_pos0=S - 1, k_pos0=0, window=512, ring_cap=512)
+    token = []
+    for i in range(35):
+        k, v = caches[src[i]]
+        if layer_types[i] == "full":
+            token.append(dict(q=qs[i].ptr, k=k.ptr, v=v.ptr, out=outs[i].ptr, T=1, S=S, Hq=HQ, Hkv=1, Dh=512, Dv=512,
+                              q_pos0=S - 1, k_pos0=0))
+        else:
+            token.append(dict(q=qs[i].ptr, k=k.ptr, v=v.ptr, out=outs[i].ptr, T=1, S=S, Hq=HQ, Hkv=1, Dh=256, Dv=256,
+                              q_pos0=S - 1, k_pos0=0, window=512, ring_cap=512))
 
-    ms, _ = time_steps(ctx, token, steps, warmup)
+    ms, _ = time_steps(ctx, [token], steps, warmup)
     for a in list(qs) + list(outs) + [x for kv in caches.values() for x in kv]:
         a.free()
     algo = 7 * decode_bytes(S, 512) + 28 * decode_bytes(512, 256)
@@ -172,11 +185,9 @@ def prefill(ctx, T, Dh, window, steps, warmup):
     q, k, v = ctx.upload(ins.q), ctx.upload(ins.k), ctx.upload(ins.v)
     out = ctx.empty((T, HQ * Dh))
 
-    def call():
-        ctx.attention(q.ptr, k.ptr, v.ptr, out.ptr, T=T, S=T, Hq=HQ, Hkv=1, Dh=Dh, Dv=Dh, q_pos0=0, k_pos0=0,
-                      window=window)
-
-    ms, kms = time_steps(ctx, call, steps, warmup)
+    call = [dict(q=q.ptr, k=k.ptr, v=v.ptr, out=out.ptr, T=T, S=T, Hq=HQ, Hkv=1, Dh=Dh, Dv=Dh, q_pos0=0, k_pos0=0,
+                 window=window)]
+    ms, kms = time_steps(ctx, [call], steps, warmup)
     for a in (q, k, v, out):
         a.free()
     fl = prefill_flops(T, window, Dh)
@@ -198,7 +209,7 @@ def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="headline decode only (no extras, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
@@ -226,7 +237,7 @@ def main(argv=None):
 
     # ---- headline: hd512 global decode at 32K context ----
     head = Decode(ctx, S=32768, Dh=512, seed=4)
-    ms, kms = time_steps(ctx, head.step, args.steps, args.warmup)
+    ms, kms = time_steps(ctx, head.calls(), args.steps, args.warmup)
     plan = ctx.plan(**head.kw())
     head.free()
     algo = decode_bytes(32768, 512)
@@ -275,14 +286,14 @@ def main(argv=None):
                                      ("configs[2] global hd512 S131072", 131072, 512, 0, 2)]:
             d = Decode(ctx, S=S, Dh=Dh, seed=seed, window=W, copies=1 if S > 100000 else BUST_COPIES)
             steps = max(10, args.steps // (4 if S > 100000 else 1))
-            m, km = time_steps(ctx, d.step, steps, min(args.warmup, 10))
+            m, km = time_steps(ctx, d.calls(), steps, min(args.warmup, 10))
             b = decode_bytes(d.visible(), Dh)
             extras[name] = {"us_per_step": m * 1e3, "kernel_us": km * 1e3, "GB_s": b / (m * 1e-3) / 1e9,
                             "kernel_GB_s": b / (km * 1e-3) / 1e9, "splits": ctx.plan(**d.kw()).splits}
             if S > 100000:
                 sweep = {}
                 for sp in (8, 16, 32, 64, 128, 256, 512):
-                    m2, _ = time_steps(ctx, lambda: d.step(sp), 10, 3)
+                    m2, _ = time_steps(ctx, d.calls(sp), 10, 3)
                     sweep[sp] = round(m2 * 1e3, 2)
                 extras[name]["split_sweep_us"] = sweep
             d.free()

@@ -35,7 +35,7 @@ struct g4a_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     hipModule_t module = nullptr;
-    hipFunction_t decode[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};  // [dh512][group8]
+    hipFunction_t decode[2][2][2] = {};  // [dh512][group8][explicit key positions]
     hipFunction_t combine[2] = {nullptr, nullptr};                          // [dh512]
     hipFunction_t generic = nullptr;
     hipFunction_t prefill[2] = {nullptr, nullptr};                          // [dh512]
@@ -320,10 +320,13 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
         fail(ctx, G4A_E_MODULE, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
         return bail(G4A_E_MODULE);
     }
-    const char* names[2][2] = {{"g4a_decode_d256_g4", "g4a_decode_d256_g8"}, {"g4a_decode_d512_g4", "g4a_decode_d512_g8"}};
     for (int d = 0; d < 2; ++d)
         for (int g = 0; g < 2; ++g)
-            if (int rc = get_fn(ctx, &ctx->decode[d][g], names[d][g])) return bail(rc);
+            for (int kp = 0; kp < 2; ++kp) {
+                char name[64];
+                snprintf(name, sizeof name, "g4a_decode_d%d_g%d%s", d ? 512 : 256, g ? 8 : 4, kp ? "_kpos" : "");
+                if (int rc = get_fn(ctx, &ctx->decode[d][g][kp], name)) return bail(rc);
+            }
     if (int rc = get_fn(ctx, &ctx->combine[0], "g4a_combine_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->combine[1], "g4a_combine_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->generic, "g4a_generic_attention")) return bail(rc);
@@ -499,13 +502,22 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
     dp.softcap = a->attn_softcap;
     const int d512 = a->Dh == 512 ? 1 : 0;
     const int g8 = group == 8 ? 1 : 0;
-    if (int rc = launch(ctx, ctx->decode[d512][g8], dim3(pl.splits, a->T, a->Hkv), dim3(512, 1, 1), dp, "decode", true))
+    if (int rc = launch(ctx, ctx->decode[d512][g8][kd ? 1 : 0], dim3(pl.splits, a->T, a->Hkv), dim3(512, 1, 1), dp,
+                        "decode", true))
         return rc;
     if (pl.splits > 1) {
         G4aCombineParams cp{dp.part, a->out, a->T, a->Hq, pl.splits, a->Dh};
         if (int rc = launch(ctx, ctx->combine[d512], dim3(a->Dh / 16, a->Hq, a->T), dim3(256, 1, 1), cp, "combine"))
             return rc;
     }
+    return G4A_OK;
+}
+
+int g4a_attention_batch(g4a_ctx* ctx, const g4a_attn_args* args, uint32_t n) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (n && !args) return fail(ctx, G4A_E_ARG, "null args");
+    for (uint32_t i = 0; i < n; ++i)
+        if (int rc = g4a_attention(ctx, &args[i])) return rc;
     return G4A_OK;
 }
 

@@ -150,59 +150,112 @@ __device__ __forceinline__ void qk_dims16(float (&s)[2], float q0, float q1, con
 
 template <int DH, int GROUP>
 struct DecodeCfg {
-    static constexpr int HGW = GROUP / 2;                // waves per key-tile slot (2 heads each)
+    static constexpr int HGW = GROUP / 2;                // waves per key-tile slot (2 heads each in the score phase)
     static constexpr int KT = 8 / HGW;                   // key-tile slots per 8-wave workgroup
     static constexpr int SLOT_THREADS = 64 * HGW;
-    static constexpr int LPT = 1024 / SLOT_THREADS;      // float4 per thread per 16 KiB chunk
-    static constexpr int D = 16 / LPT;                   // chunks in flight per slot (64 VGPRs of loads)
+    static constexpr int LPT = 1024 / SLOT_THREADS;      // 16-byte copies per lane per 16 KiB chunk
+    static constexpr int NB = 8 / KT;                    // chunk buffers per slot (128 KiB ring in all)
+    static constexpr int AHEAD = NB - 1;                 // chunks in flight ahead of the one in use
     static constexpr int NKS = DH / 64;                  // K chunks per tile: 64 keys x 64 dims
     static constexpr int NVC = DH / 64;                  // V chunks per tile: KPC keys x DH dims
     static constexpr int NCH = NKS + NVC;
     static constexpr int KPC = 64 / NVC;                 // keys per V chunk
-    static constexpr int PVK = KPC / HGW;                // keys per wave per V chunk
-    static constexpr int RS = 68;                        // padded K row stride in LDS (floats)
-    static constexpr int BUF = 64 * RS;                  // floats per chunk buffer
-    static constexpr int NV4 = DH / 256;                 // V float4 per lane per row
+    static constexpr int BUF = 4096;                     // floats per chunk buffer (16 KiB)
+    static constexpr int WD = DH / HGW;                  // output dims per wave in the P.V phase
+    static constexpr int NDG = WD / 64;                  // 64-dim MFMA groups per wave
     static constexpr int NHQ = GROUP / 4;                // MFMA head quarters
-    static constexpr int RING = KT * 2 * BUF;
-    static constexpr int MERGE = 8 * GROUP * DH;
-    static constexpr int BIG = RING > MERGE ? RING : MERGE;
+    static constexpr int RING = KT * NB * BUF;
+    static constexpr int MERGE = (KT - 1) * HGW * NHQ * NDG * 256;  // slots 1.. hand their accumulators to slot 0
     static constexpr int PBUF = KT * 64 * GROUP;
     static constexpr int QS = GROUP * DH;                // the kv group's query rows
-    static constexpr int SMEM = BIG + PBUF + KT * GROUP + KT * 2 * GROUP + QS;
-    static_assert(NCH % D == 0, "the register ring index must be static within a tile");
-    static_assert(KPC * DH <= BUF, "a V chunk must fit a chunk buffer");
-    static_assert(PVK >= 1, "every wave of a slot folds at least one key per V chunk");
+    static constexpr int SMEM = RING + PBUF + KT * GROUP + KT * 2 * GROUP + QS;
+    static_assert(MERGE <= RING, "the merge buffer overlays the chunk ring");
+    static_assert(NCH % NB == 0, "the ring buffer of a chunk must be static within a tile");
+    static_assert(KPC * DH == BUF, "a V chunk fills a chunk buffer");
+    static_assert(NDG >= 1, "a wave owns at least one 64-dim group");
+    static_assert(QS % 256 == 0, "the query rows are copied in 1 KiB wave copies");
+    static_assert(LPT * (AHEAD - 1) + 2 * (QS / 256 + 7) / 8 < 64, "vmcnt immediate range");
 };
 
+// Asynchronous 16-byte-per-lane copy global -> LDS (global_load_lds_dwordx4):
+// lane l's 16 bytes at `src` land at lds_dst + 16*l; lds_dst must be
+// wave-uniform (it goes through M0, after which the copy needs one wait state).
+// Completion is tracked by vmcnt like any vector load. Written as inline asm so
+// the compiler does not serialise every later LDS read behind all copies in
+// flight: the kernel waits for each chunk itself (wait_vm) before a barrier.
+// M0 is not otherwise live in these kernels.
+__device__ __forceinline__ void copy16_to_lds(const float* src, float* lds_dst) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) float*)lds_dst);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
+}
+
+// Wait until at most N vector-memory operations of this wave are in flight
+// (they retire in issue order, so every copy issued before the last N has landed).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// wait_vm<n>() for an n known only after loop unrolling (it folds to one
+// s_waitcnt); counts above 16 wait for everything, which is always safe.
+__device__ __forceinline__ void wait_vm_upto16(int n) {
+    switch (n) {
+#define G4A_WAIT_CASE(k) \
+    case k: wait_vm<k>(); break;
+        G4A_WAIT_CASE(1) G4A_WAIT_CASE(2) G4A_WAIT_CASE(3) G4A_WAIT_CASE(4) G4A_WAIT_CASE(5) G4A_WAIT_CASE(6)
+        G4A_WAIT_CASE(7) G4A_WAIT_CASE(8) G4A_WAIT_CASE(9) G4A_WAIT_CASE(10) G4A_WAIT_CASE(11) G4A_WAIT_CASE(12)
+        G4A_WAIT_CASE(13) G4A_WAIT_CASE(14) G4A_WAIT_CASE(15) G4A_WAIT_CASE(16)
+#undef G4A_WAIT_CASE
+        default: wait_vm<0>(); break;
+    }
+}
+
+// Workgroup barrier for LDS hand-offs: this wave's LDS reads and writes are
+// complete (lgkmcnt(0)) before it arrives. Unlike __syncthreads it does not
+// wait for outstanding global->LDS copies, which keep streaming across it.
+__device__ __forceinline__ void barrier_lds() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Split-K flash decode (see the file header). An 8-wave workgroup owns one key
-// split of one (query, kv head); its waves form KT key-tile slots of HGW waves,
-// each wave owning 2 query heads. Every slot streams, per 64-key tile, DH/64 K
-// chunks (64 keys x 64 dims) and DH/64 V chunks (KPC keys x DH dims) of 16 KiB
-// through registers into a double-buffered LDS chunk, D chunks ahead, so K and V
-// loads form one continuous stream across phases and tiles.
-template <int DH, int GROUP>
+// split of one (query, kv head); its waves form KT key-tile slots of HGW waves.
+// Every slot streams, per 64-key tile, DH/64 K chunks (64 keys x 64 dims) and
+// DH/64 V chunks (KPC keys x DH dims) of 16 KiB straight from HBM into a ring
+// of NB LDS chunk buffers with global->LDS copies, AHEAD chunks ahead of the
+// one in use, so K and V form one continuous stream across phases and tiles.
+// In LDS a K chunk is stored row-major (64 floats per key) with the 16-byte
+// column index XOR-swizzled by the key's low 4 bits, so the lane = key reads of
+// the score phase hit distinct banks.
+//   score phase: wave g of a slot owns heads 2g, 2g+1 (lane = key);
+//   P.V phase:   wave g of a slot owns output dims [g*WD, (g+1)*WD) of all
+//                GROUP heads, so a slot's accumulators never need summing;
+//   end:         slots 1.. hand (m, l, acc) to slot 0 through LDS, which
+//                merges them and writes the split's partial (or the output).
+//
+// KPOS selects explicit key positions (p.k_pos, a device array) over contiguous
+// ones (k_pos0 + j). It is a template parameter so the contiguous kernel issues
+// no vector loads of its own inside the streaming loop: every vector-memory
+// wait there is one of the kernel's own chunk waits.
+template <int DH, int GROUP, bool KPOS>
 __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
     static_assert(DH == 256 || DH == 512, "fast decode handles head_dim 256 / 512");
     static_assert(GROUP == 4 || GROUP == 8, "fast decode handles groups of 4 / 8 heads");
     using C = DecodeCfg<DH, GROUP>;
-    constexpr int HGW = C::HGW, KT = C::KT, SLOT_THREADS = C::SLOT_THREADS, LPT = C::LPT, D = C::D,
-                  NKS = C::NKS, NCH = C::NCH, KPC = C::KPC, PVK = C::PVK, RS = C::RS, BUF = C::BUF,
-                  NV4 = C::NV4, NHQ = C::NHQ;
+    constexpr int HGW = C::HGW, KT = C::KT, LPT = C::LPT, NB = C::NB, AHEAD = C::AHEAD, NKS = C::NKS,
+                  NCH = C::NCH, KPC = C::KPC, BUF = C::BUF, WD = C::WD, NDG = C::NDG, NHQ = C::NHQ;
 
     __shared__ __attribute__((aligned(16))) float smem[C::SMEM];
-    float* const ring = smem;                     // [KT][2][BUF]
-    float* const mrg = smem;                      // [8][GROUP][DH] after the tile loop
-    float* const pbuf = smem + C::BIG;            // [KT][64 keys][4][NHQ]
+    float* const ring = smem;                     // [KT][NB][BUF]
+    float* const mrg = smem;                      // [KT-1][HGW][NHQ][NDG][4][64] after the tile loop
+    float* const pbuf = smem + C::RING;           // [KT][64 keys][4][NHQ]
     float* const corrbuf = pbuf + C::PBUF;        // [KT][GROUP]
     float* const mlbuf = corrbuf + KT * GROUP;    // [KT][2][GROUP]
     float* const qs = mlbuf + KT * 2 * GROUP;     // [GROUP][DH] query rows of this kv group
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int g = w % HGW;   // head pair within the kv group: heads 2g, 2g+1
+    const int g = w % HGW;   // score phase: heads 2g, 2g+1; P.V phase: dims [g*WD, (g+1)*WD)
     const int kt = w / HGW;  // key-tile slot
-    const int stid = g * 64 + lane;
     const uint32_t split = blockIdx.x, qi = blockIdx.y, kvh = blockIdx.z;
     const uint32_t qpos = p.q_pos ? p.q_pos[qi] : p.q_pos0 + qi;
     const uint32_t ks = p.k_start + split * p.keys_per_split;
@@ -211,25 +264,30 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
     const size_t row_stride = (size_t)p.Hkv * DH;
     const float* __restrict__ kbase = p.k + (size_t)kvh * DH;
     const float* __restrict__ vbase = p.v + (size_t)kvh * DH;
-    float* const my_ring = ring + kt * 2 * BUF;
+    float* const my_ring = ring + kt * NB * BUF;
     float* const my_pbuf = pbuf + kt * 64 * GROUP;
 
+    // The query rows go to LDS first (copies issued before every chunk, so the
+    // first chunk wait covers them).
+    {
+        const float* qsrc = p.q + ((size_t)qi * p.Hq + h0) * DH;
+        for (int i = w; i < C::QS / 256; i += 8) copy16_to_lds(qsrc + 256 * i + 4 * lane, qs + 256 * i);
+    }
+
     float m[2] = {NEG_INF, NEG_INF}, lpart[2] = {0.0f, 0.0f};
-    f4v acc[NHQ][NV4][4];
+    f4v acc[NHQ][NDG];
 #pragma unroll
     for (int a = 0; a < NHQ; ++a)
 #pragma unroll
-        for (int b = 0; b < NV4; ++b)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[a][b][e] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int b = 0; b < NDG; ++b) acc[a][b] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 
     const uint32_t ntiles = ke > ks ? (ke - ks + 63) / 64 : 0;
     const uint32_t niter = (ntiles + KT - 1) / KT;
 
-    // Loads are issued for every chunk step whether or not the slot has a tile,
-    // so the number of loads in flight is the same on every path and each
-    // chunk's wait is exact; an idle slot reads the small dummy buffer (which
-    // stays in L2) instead of K/V.
+    // Copies are issued for every chunk step whether or not the slot has a tile,
+    // so the number in flight is the same on every path and each chunk's wait
+    // count is exact; an idle slot copies from the small dummy buffer (which
+    // stays in L2) into its ring instead of K/V.
     struct Tile {
         uint32_t t0, row0, nk;
         bool active;
@@ -242,7 +300,7 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
         T.t0 = ks + t * 64;
         T.active = it < niter && t < ntiles;
         if (T.active) {
-            const uint32_t kpos_first = p.k_pos ? p.k_pos[T.t0] : p.k_pos0 + T.t0;
+            const uint32_t kpos_first = KPOS ? p.k_pos[T.t0] : p.k_pos0 + T.t0;
             T.active = kpos_first <= qpos;  // ascending positions: a future first key means a future tile
         }
         T.nk = T.active ? min(64u, ke - T.t0) : 1u;
@@ -256,70 +314,70 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
         if (p.ring_cap && x >= p.ring_cap) x -= p.ring_cap;
         return x;
     };
-    // chunk c of a tile into registers: K chunks c < NKS (dims 64c..64c+63 of the 64 keys),
-    // V chunks c >= NKS (keys KPC*(c-NKS) .. +KPC-1, all DH dims)
-    auto load_chunk = [&](const Tile& T, int c, float4 (&r)[LPT]) {
+    // chunk c of a tile into ring buffer `bi`: K chunks c < NKS (dims 64c..64c+63 of
+    // the 64 keys), V chunks c >= NKS (keys KPC*(c-NKS) .. +KPC-1, all DH dims).
+    // Wave g of the slot fills float4 slots (i*HGW + g)*64 + lane, i < LPT.
+    auto issue_chunk = [&](const Tile& T, int c, int bi) {
+        float* const dst = my_ring + bi * BUF;
 #pragma unroll
         for (int i = 0; i < LPT; ++i) {
-            const int f = stid + SLOT_THREADS * i;
+            const int sl = (i * HGW + g) * 64 + lane;
+            const float* src;
             if (c < NKS) {
-                r[i] = ld4(T.kb + (size_t)prow(T, f / 16) * row_stride + 64 * c + 4 * (f % 16));
+                const int r = sl >> 4;
+                const int j = (sl & 15) ^ (r & 15);
+                src = T.kb + (size_t)prow(T, r) * row_stride + 64 * c + 4 * j;
             } else {
-                const int key = (c - NKS) * KPC + f / (DH / 4);
-                r[i] = ld4(T.vb + (size_t)prow(T, key) * row_stride + 4 * (f % (DH / 4)));
+                const int key = (c - NKS) * KPC + sl / (DH / 4);
+                src = T.vb + (size_t)prow(T, key) * row_stride + 4 * (sl % (DH / 4));
             }
-        }
-    };
-    auto store_chunk = [&](int c, float* buf, const float4 (&r)[LPT]) {
-#pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int f = stid + SLOT_THREADS * i;
-            float* dst = c < NKS ? buf + (f / 16) * RS + 4 * (f % 16) : buf + (f / (DH / 4)) * DH + 4 * (f % (DH / 4));
-            *reinterpret_cast<float4*>(dst) = r[i];
+            copy16_to_lds(src, dst + (i * HGW + g) * 256);
         }
     };
 
-    {
-        const float* qsrc = p.q + ((size_t)qi * p.Hq + h0) * DH;
-        for (int i = threadIdx.x; i < GROUP * DH / 4; i += 512)
-            *reinterpret_cast<float4*>(qs + 4 * i) = ld4(qsrc + 4 * i);
-    }
-    const float* const my_q = qs + 2 * g * DH;  // heads 2g, 2g+1
-
-    float4 kreg[D][LPT];
     Tile cur = tile_info(0);
 #pragma unroll
-    for (int c = 0; c < D; ++c) load_chunk(cur, c, kreg[c]);
+    for (int c = 0; c < AHEAD; ++c) issue_chunk(cur, c, c % NB);
+
+    const float* const my_q = qs + 2 * g * DH;  // heads 2g, 2g+1
+    // this lane's key row in a K chunk and its swizzled float4 columns
+    const float* kcol[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) kcol[j] = my_ring + lane * 64 + 4 * (j ^ (lane & 15));
 
     for (uint32_t it = 0; it < niter; ++it) {
+        const bool last = it + 1 == niter;  // no copies beyond the last tile step
         const Tile nxt = tile_info(it + 1);
         float s[2] = {0.0f, 0.0f};
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
-            float* const buf = my_ring + (c & 1) * BUF;
-            if (cur.active) store_chunk(c, buf, kreg[c % D]);
-            __syncthreads();
-            // keep D chunks in flight: chunk c+D of this tile or of the next one
-            if (c + D < NCH) load_chunk(cur, c + D, kreg[c % D]);
-            else load_chunk(nxt, c + D - NCH, kreg[c % D]);
+            const int bi = c % NB;
+            const float* const buf = my_ring + bi * BUF;
+            // this wave's part of chunk c has landed (the copies issued after it are the
+            // next AHEAD-1 chunks, fewer at the end of the last tile); after the barrier
+            // every wave's has, and every wave is done with the buffer the next copy refills
+            if (c + AHEAD > NCH && last) wait_vm_upto16(LPT * (NCH - 1 - c));
+            else wait_vm<LPT * (AHEAD - 1)>();
+            barrier_lds();
+            if (c + AHEAD < NCH) issue_chunk(cur, c + AHEAD, (c + AHEAD) % NB);
+            else if (!last) issue_chunk(nxt, c + AHEAD - NCH, (c + AHEAD) % NB);
             if (!cur.active) continue;
             if (c < NKS) {
                 // exact sequential dots, lane = key, heads 2g and 2g+1, dims 64c .. 64c+63;
-                // q comes from 8 VGPRs (16 values each, one per 16-lane row) via DPP broadcast
-                const float* kr = buf + lane * RS;
+                // q comes from LDS, one value per lane of each 16-lane row, via DPP broadcast
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
                     const float q0 = my_q[64 * c + 16 * b + (lane & 15)];
                     const float q1 = my_q[DH + 64 * c + 16 * b + (lane & 15)];
                     float4 k4[4];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) k4[i] = *reinterpret_cast<const float4*>(kr + 16 * b + 4 * i);
+                    for (int i = 0; i < 4; ++i) k4[i] = *reinterpret_cast<const float4*>(kcol[4 * b + i] + bi * BUF);
                     qk_dims16(s, q0, q1, k4);
                 }
                 if (c == NKS - 1) {
                     // online softmax for heads 2g, 2g+1 over the tile (lane = key)
                     const uint32_t j = cur.t0 + min((uint32_t)lane, cur.nk - 1);
-                    const uint32_t kp = p.k_pos ? p.k_pos[j] : p.k_pos0 + j;
+                    const uint32_t kp = KPOS ? p.k_pos[j] : p.k_pos0 + j;
                     const bool vis = (uint32_t)lane < cur.nk && kp <= qpos && (p.window == 0 || qpos - kp < p.window);
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
@@ -343,30 +401,24 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
                         const float* cb = corrbuf + kt * GROUP + hq * 4;
                         const f4v cr = f4v{cb[0], cb[1], cb[2], cb[3]};
 #pragma unroll
-                        for (int q4 = 0; q4 < NV4; ++q4)
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) acc[hq][q4][e] *= cr;
+                        for (int dg = 0; dg < NDG; ++dg) acc[hq][dg] *= cr;
                     }
                 }
-                // P.V on the matrix cores (v_mfma_f32_4x4x1_16b_f32): lane l gives A = P[hq*4 + l%4]
-                // and B = V[key][256*q4 + 4*l + e]; result register r = out[hq*4 + r][256*q4 + 4*l + e]
+                // P.V on the matrix cores (v_mfma_f32_4x4x1_16b_f32), one key per step:
+                // lane l gives A = P[key][4hq + l%4] and B = V[key][g*WD + 64dg + l];
+                // register r of the result is out[4hq + r][g*WD + 64dg + l]
 #pragma unroll
-                for (int u = 0; u < PVK; ++u) {
-                    const int kr = g * PVK + u;  // key within the chunk
+                for (int kr = 0; kr < KPC; ++kr) {
                     const int kk = vc * KPC + kr;  // key within the tile
                     float a[NHQ];
 #pragma unroll
                     for (int hq = 0; hq < NHQ; ++hq) a[hq] = my_pbuf[kk * GROUP + (lane & 3) * NHQ + hq];
 #pragma unroll
-                    for (int q4 = 0; q4 < NV4; ++q4) {
-                        const float4 vv = *reinterpret_cast<const float4*>(buf + kr * DH + 256 * q4 + 4 * lane);
+                    for (int dg = 0; dg < NDG; ++dg) {
+                        const float vv = buf[kr * DH + g * WD + 64 * dg + lane];
 #pragma unroll
-                        for (int hq = 0; hq < NHQ; ++hq) {
-                            acc[hq][q4][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vv.x, acc[hq][q4][0], 0, 0, 0);
-                            acc[hq][q4][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vv.y, acc[hq][q4][1], 0, 0, 0);
-                            acc[hq][q4][2] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vv.z, acc[hq][q4][2], 0, 0, 0);
-                            acc[hq][q4][3] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vv.w, acc[hq][q4][3], 0, 0, 0);
-                        }
+                        for (int hq = 0; hq < NHQ; ++hq)
+                            acc[hq][dg] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vv, acc[hq][dg], 0, 0, 0);
                     }
                 }
             }
@@ -374,7 +426,8 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
         cur = nxt;
     }
 
-    // ---- per-slot (m, l); merge the 8 waves' accumulators through LDS ----
+    wait_vm<0>();  // no copy may still be landing in the ring the merge buffer overlays
+    // ---- per-slot (m, l) through LDS; slots 1.. hand their accumulators to slot 0 ----
 #pragma unroll
     for (int h = 0; h < 2; ++h) lpart[h] = wave_sum(lpart[h]);
     if (lane == 0) {
@@ -385,52 +438,52 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
         }
     }
     __syncthreads();  // every wave is done with the chunk ring: the merge buffer overlays it
+    auto mslot = [&](int sl, int hq, int dg, int r) -> float* {
+        return mrg + (((((size_t)(sl - 1) * HGW + g) * NHQ + hq) * NDG + dg) * 4 + r) * 64 + lane;
+    };
+    if (kt > 0) {
 #pragma unroll
-    for (int hq = 0; hq < NHQ; ++hq)
+        for (int hq = 0; hq < NHQ; ++hq)
 #pragma unroll
-        for (int q4 = 0; q4 < NV4; ++q4)
+            for (int dg = 0; dg < NDG; ++dg)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                *reinterpret_cast<float4*>(mrg + ((size_t)w * GROUP + hq * 4 + r) * DH + 256 * q4 + 4 * lane) =
-                    make_float4(acc[hq][q4][0][r], acc[hq][q4][1][r], acc[hq][q4][2][r], acc[hq][q4][3][r]);
+                for (int r = 0; r < 4; ++r) *mslot(kt, hq, dg, r) = acc[hq][dg][r];
+    }
     __syncthreads();
-    // wave w finalises head w % GROUP over the q4 blocks w / GROUP, w / GROUP + 8 / GROUP, ...
-    const int h = w % GROUP;
-    float M = NEG_INF;
+    if (kt == 0) {
 #pragma unroll
-    for (int sl = 0; sl < KT; ++sl) M = fmaxf(M, mlbuf[sl * 2 * GROUP + h]);
-    float L = 0.0f, es[KT];
+        for (int hq = 0; hq < NHQ; ++hq) {
 #pragma unroll
-    for (int sl = 0; sl < KT; ++sl) {
-        const float ms = mlbuf[sl * 2 * GROUP + h];
-        es[sl] = (ms == NEG_INF) ? 0.0f : expf(ms - M);
-        L += mlbuf[sl * 2 * GROUP + GROUP + h] * es[sl];
-    }
-    const size_t ih = (size_t)qi * p.Hq + h0 + h;
-    for (int q4 = w / GROUP; q4 < NV4; q4 += 8 / GROUP) {
-        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int r = 0; r < 4; ++r) {
+                const int h = 4 * hq + r;
+                float M = NEG_INF;
 #pragma unroll
-        for (int sl = 0; sl < KT; ++sl) {
-            float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                for (int sl = 0; sl < KT; ++sl) M = fmaxf(M, mlbuf[sl * 2 * GROUP + h]);
+                float L = 0.0f, es[KT];
 #pragma unroll
-            for (int gg = 0; gg < HGW; ++gg) {
-                const float4 x = *reinterpret_cast<const float4*>(mrg + ((size_t)(sl * HGW + gg) * GROUP + h) * DH + 256 * q4 + 4 * lane);
-                a.x += x.x; a.y += x.y; a.z += x.z; a.w += x.w;
+                for (int sl = 0; sl < KT; ++sl) {
+                    const float ms = mlbuf[sl * 2 * GROUP + h];
+                    es[sl] = (ms == NEG_INF) ? 0.0f : expf(ms - M);
+                    L += mlbuf[sl * 2 * GROUP + GROUP + h] * es[sl];
+                }
+                const size_t ih = (size_t)qi * p.Hq + h0 + h;
+                const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+#pragma unroll
+                for (int dg = 0; dg < NDG; ++dg) {
+                    float o = acc[hq][dg][r] * es[0];
+#pragma unroll
+                    for (int sl = 1; sl < KT; ++sl) o += *mslot(sl, hq, dg, r) * es[sl];
+                    const int d = g * WD + 64 * dg + lane;
+                    if (p.nsplit == 1) p.out[ih * DH + d] = o * inv;
+                    else p.part[(ih * p.nsplit + split) * DH + d] = o;
+                }
+                if (p.nsplit > 1 && g == 0 && lane == 0) {
+                    float* ml = p.part + (size_t)p.T * p.Hq * p.nsplit * DH + (ih * p.nsplit + split) * 2;
+                    ml[0] = M;
+                    ml[1] = L;
+                }
             }
-            o.x += a.x * es[sl]; o.y += a.y * es[sl]; o.z += a.z * es[sl]; o.w += a.w * es[sl];
         }
-        if (p.nsplit == 1) {
-            const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-            *reinterpret_cast<float4*>(p.out + ih * DH + 256 * q4 + 4 * lane) =
-                make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
-        } else {
-            *reinterpret_cast<float4*>(p.part + (ih * p.nsplit + split) * DH + 256 * q4 + 4 * lane) = o;
-        }
-    }
-    if (p.nsplit > 1 && lane == 0 && w < GROUP) {
-        float* ml = p.part + (size_t)p.T * p.Hq * p.nsplit * DH + (ih * p.nsplit + split) * 2;
-        ml[0] = M;
-        ml[1] = L;
     }
 }
 
@@ -558,10 +611,14 @@ __device__ __forceinline__ void generic_attention(const G4aGenericParams& p) {
 }  // namespace
 
 extern "C" {
-__global__ __launch_bounds__(512) void g4a_decode_d256_g8(G4aDecodeParams p) { decode_split<256, 8>(p); }
-__global__ __launch_bounds__(512) void g4a_decode_d512_g8(G4aDecodeParams p) { decode_split<512, 8>(p); }
-__global__ __launch_bounds__(512) void g4a_decode_d256_g4(G4aDecodeParams p) { decode_split<256, 4>(p); }
-__global__ __launch_bounds__(512) void g4a_decode_d512_g4(G4aDecodeParams p) { decode_split<512, 4>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d256_g8(G4aDecodeParams p) { decode_split<256, 8, false>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d512_g8(G4aDecodeParams p) { decode_split<512, 8, false>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d256_g4(G4aDecodeParams p) { decode_split<256, 4, false>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d512_g4(G4aDecodeParams p) { decode_split<512, 4, false>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d256_g8_kpos(G4aDecodeParams p) { decode_split<256, 8, true>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d512_g8_kpos(G4aDecodeParams p) { decode_split<512, 8, true>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d256_g4_kpos(G4aDecodeParams p) { decode_split<256, 4, true>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d512_g4_kpos(G4aDecodeParams p) { decode_split<512, 4, true>(p); }
 __global__ __launch_bounds__(256) void g4a_combine_d256(G4aCombineParams p) { combine<256>(p); }
 __global__ __launch_bounds__(256) void g4a_combine_d512(G4aCombineParams p) { combine<512>(p); }
 __global__ __launch_bounds__(64) void g4a_generic_attention(G4aGenericParams p) { generic_attention(p); }

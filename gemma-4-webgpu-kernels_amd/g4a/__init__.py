@@ -84,6 +84,7 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "g4a_zero": (c_int, [ctxp, vp, sz]),
         "g4a_sync": (c_int, [ctxp]),
         "g4a_attention": (c_int, [ctxp, ctypes.POINTER(AttnArgs)]),
+        "g4a_attention_batch": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.c_uint32]),
         "g4a_attention_plan": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.POINTER(AttnPlan)]),
         "g4a_kv_write": (c_int, [ctxp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32]),
         "g4a_timer_start": (c_int, [ctxp]),
@@ -224,6 +225,20 @@ class Context:
     def attention(self, q: int, k: int, v: int, out: int, **kw) -> None:
         a, keep = make_args(q, k, v, out, **kw)
         self._check(self.lib.g4a_attention(self.handle, ctypes.byref(a)))
+
+    @staticmethod
+    def prepare_batch(calls: list[dict]) -> tuple:
+        """Marshal a list of attention() keyword sets into a g4a_attn_args array
+        (built once, so a timed region holds only the library call)."""
+        built = [make_args(**kw) for kw in calls]
+        arr = (AttnArgs * len(built))(*[a for a, _ in built])
+        return arr, len(built), [k for _, k in built]
+
+    def attention_batch(self, calls) -> None:
+        """One g4a_attention_batch crossing: `calls` is a list of attention() keyword
+        sets or the result of prepare_batch()."""
+        arr, n, _keep = calls if isinstance(calls, tuple) else self.prepare_batch(calls)
+        self._check(self.lib.g4a_attention_batch(self.handle, arr, n))
 
     def plan(self, **kw) -> AttnPlan:
         return plan(self, **kw)

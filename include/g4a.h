@@ -110,6 +110,14 @@ typedef struct g4a_attn_args {
 
 int g4a_attention(g4a_ctx *ctx, const g4a_attn_args *args);
 
+/* n attention calls enqueued back-to-back on the context's stream, args[i]
+ * exactly as for g4a_attention; stops at the first failing call and returns
+ * its status (calls before it stay enqueued). No counterpart in the
+ * reference: a batched Backend::attention for callers that issue many calls
+ * per step (a token's layer schedule, a benchmark loop) and want one FFI
+ * crossing for all of them. */
+int g4a_attention_batch(g4a_ctx *ctx, const g4a_attn_args *args, uint32_t n);
+
 /* The launch plan g4a_attention would use for `args` (no GPU work): the
  * trimmed key range [k_start, k_end) (rust/src/backend_wgpu.rs:929-936), the
  * kernel family and the split-K decomposition. */
