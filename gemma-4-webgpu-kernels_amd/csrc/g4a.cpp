@@ -261,16 +261,17 @@ int analyse(g4a_ctx* ctx, const g4a_attn_args* a, Analysis* an, bool check_point
         return G4A_OK;
     }
     r.plan.kernel = G4A_KERNEL_DECODE;
-    const uint32_t kt = 8 / (group / 2);  // key-tile slots per 8-wave workgroup (2 heads per wave)
     const uint32_t tiles = (nkeys + TILE - 1) / TILE;
     uint32_t splits;
     if (a->splits) {
         splits = std::min(a->splits, tiles);
     } else {
-        // fill the GPU with one sequence: one 8-wave workgroup per CU (2 waves per SIMD)
+        // fill the GPU with one sequence: one 8-wave workgroup per CU (the LDS ring
+        // allows one per CU), at least one 64-key tile each. Below 2 tiles per CU a
+        // workgroup's second key-tile slot idles, which still beats idle CUs.
         const uint64_t target = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1));
         const uint64_t per_query = std::max<uint64_t>(1, target / (uint64_t(a->T) * a->Hkv));
-        splits = uint32_t(std::min<uint64_t>(per_query, (tiles + kt - 1) / kt));
+        splits = uint32_t(std::min<uint64_t>(per_query, tiles));
     }
     splits = std::min(std::max(splits, 1u), MAX_SPLITS);
     uint32_t kps = (nkeys + splits - 1) / splits;
