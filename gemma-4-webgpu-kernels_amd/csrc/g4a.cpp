@@ -331,7 +331,7 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->combine[0], "g4a_combine_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->combine[1], "g4a_combine_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->generic, "g4a_generic_attention")) return bail(rc);
-    if (int rc = get_fn(ctx, &ctx->prefill[0], "g4a_prefill_d256")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->prefill[0], "g4a_prefill2_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->prefill[1], "g4a_prefill_d512")) return bail(rc);
     if (hipMalloc(reinterpret_cast<void**>(&ctx->dummy), 4096) != hipSuccess ||
         hipMemset(ctx->dummy, 0, 4096) != hipSuccess) {
@@ -467,8 +467,10 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
         pp.ring_cap = a->kv_ring_cap;
         pp.window = a->sliding_window;
         pp.scale = a->scale;
-        return launch(ctx, ctx->prefill[a->Dh == 512 ? 1 : 0], dim3((a->T + 7) / 8, a->Hkv, 1), dim3(256, 1, 1), pp,
-                      "prefill", true);
+        // head_dim 256: 8 waves (two key parities per 16-row block); 512: 4 waves
+        const bool d512 = a->Dh == 512;
+        return launch(ctx, ctx->prefill[d512 ? 1 : 0], dim3((a->T + 7) / 8, a->Hkv, 1), dim3(d512 ? 256 : 512, 1, 1),
+                      pp, "prefill", true);
     }
     // split-K flash-decode (+ combine)
     const uint32_t *qd = nullptr, *kd = nullptr;

@@ -29,6 +29,7 @@
 namespace {
 
 constexpr float PF_TAU = 10.0f;
+constexpr float PF_RESCALE = 8.0f;  // e^8 ~ 3e3: probability headroom before O and l are rescaled
 
 template <int DH>
 struct PrefillCfg {
@@ -39,7 +40,9 @@ struct PrefillCfg {
     static constexpr int NC = DH / 64;                   // O column groups (x4 MFMA blocks)
     static constexpr int QT = DH / 16;                   // Q float4 per lane
     static constexpr int CAP = DH == 256 ? 2048 : 640;   // candidate entries per wave
+    static constexpr int STAGE = (64 + 16) * 36;         // per-wave staging floats at the end (in the tile buffers)
     static constexpr int SMEM = 2 * TILE + 4 * 2 * CAP + 4 * 16;
+    static_assert(4 * STAGE <= 2 * TILE, "the end-of-kernel staging areas fit in the tile buffers");
 };
 
 __device__ __forceinline__ uint64_t ballot(bool b) { return __ballot(b); }
@@ -72,29 +75,29 @@ __device__ __forceinline__ void prefill(const G4aPrefillParams& p) {
     float* const my_s = smem + 2 * C::TILE + w * 2 * CAP + CAP;
     float* const my_m = smem + 2 * C::TILE + 4 * 2 * CAP + w * 16;
 
-    // visible key-index range [lo, hi) of query i
-    auto key_hi = [&](int64_t i) -> int64_t {
+    // visible key-index range [lo, hi) of query i, clamped to [0, S] (S < 2^28)
+    auto key_hi = [&](int64_t i) -> int32_t {
         const int64_t lim = (int64_t)p.q_pos0 + i - (int64_t)p.k_pos0 + 1;
-        return lim <= 0 ? 0 : (lim < (int64_t)p.S ? lim : (int64_t)p.S);
+        return (int32_t)(lim <= 0 ? 0 : (lim < (int64_t)p.S ? lim : (int64_t)p.S));
     };
-    auto key_lo = [&](int64_t i) -> int64_t {
+    auto key_lo = [&](int64_t i) -> int32_t {
         if (p.window == 0) return 0;
         const int64_t lo = (int64_t)p.q_pos0 + i - (int64_t)p.k_pos0 - (int64_t)p.window + 1;
-        return lo > 0 ? lo : 0;
+        return (int32_t)(lo <= 0 ? 0 : (lo < (int64_t)p.S ? lo : (int64_t)p.S));
     };
     auto prow = [&](uint32_t j) -> size_t { return p.ring_cap ? j % p.ring_cap : j; };
 
     const uint32_t qlast = min(qb + 7, p.T - 1);
-    const int64_t wg_lo = key_lo(qb), wg_hi = key_hi(qlast);
+    const int32_t wg_lo = key_lo(qb), wg_hi = key_hi(qlast);
     const uint32_t nt = wg_hi > wg_lo ? (uint32_t)((wg_hi - wg_lo + BK - 1) / BK) : 0;
     const bool wave_valid = qw < p.T;
-    const int64_t w_lo = wave_valid ? key_lo(qw) : 0;
-    const int64_t w_hi = wave_valid ? key_hi(min(qw + 1, p.T - 1)) : 0;
+    const int32_t w_lo = wave_valid ? key_lo(qw) : 0;
+    const int32_t w_hi = wave_valid ? key_hi(min(qw + 1, p.T - 1)) : 0;
 
     // this lane's softmax row: query qw + rl/8, head h0 + rl%8
     const uint32_t myq = qw + (rl >> 3);
     const bool qvalid = myq < p.T;
-    const int64_t my_lo = key_lo(myq), my_hi = qvalid ? key_hi(myq) : 0;
+    const int32_t my_lo = key_lo(myq), my_hi = qvalid ? key_hi(myq) : 0;
     float4 qr[QT];
     {
         const float* qrow = p.q + ((size_t)min(myq, p.T - 1) * p.Hq + h0 + (rl & 7)) * DH + 4 * g;
@@ -102,15 +105,38 @@ __device__ __forceinline__ void prefill(const G4aPrefillParams& p) {
         for (int t = 0; t < QT; ++t) qr[t] = ld4(qrow + 16 * t);
     }
 
-    auto load_tile = [&](uint32_t t, float4 (&r)[LPT]) {
-        const int64_t t0 = wg_lo + (int64_t)t * BK;
+    // Tile t holds keys t0 .. t0+BK-1, t0 = wg_lo + t*BK. Thread tid loads, for
+    // i < LPT, the float4 at key t0 + kf(i) and dims df(i) of K (i < LPT/2) or V,
+    // clamped to the last visible key. Physical rows follow the ring
+    // incrementally: ring_base = t0 % ring_cap is advanced per tile, and
+    // t0 + kf - t0 < BK <= ring_cap needs at most one wrap.
+    uint32_t ring_base = p.ring_cap ? (uint32_t)wg_lo % p.ring_cap : 0u;
+    // Thread tid's loads all sit at dims 4*(tid % (DH/4)) of keys
+    // tid/(DH/4) + i*KSTEP: one constant per-lane offset plus a uniform
+    // (scalar) tile base on the common path.
+    constexpr int KSTEP = 1024 / DH;
+    const uint32_t lane_off = (uint32_t)(tid / (DH / 4)) * (uint32_t)row_stride + 4u * (uint32_t)(tid % (DH / 4));
+    auto load_tile = [&](uint32_t t0, uint32_t rbase, float4 (&r)[LPT]) {
+        if (p.ring_cap == 0 && t0 + BK <= (uint32_t)wg_hi) {
+            const float* kt = kbase + (size_t)t0 * row_stride;
+            const float* vt = vbase + (size_t)t0 * row_stride;
+#pragma unroll
+            for (int i = 0; i < LPT / 2; ++i) r[i] = ld4(kt + (size_t)(i * KSTEP) * row_stride + lane_off);
+#pragma unroll
+            for (int i = 0; i < LPT / 2; ++i) r[LPT / 2 + i] = ld4(vt + (size_t)(i * KSTEP) * row_stride + lane_off);
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < LPT; ++i) {
             const int f = (tid + 256 * i) % (BK * DH / 4);
-            int64_t key = t0 + f / (DH / 4);
-            if (key > wg_hi - 1) key = wg_hi - 1;
+            const uint32_t kc = min(t0 + (uint32_t)(f / (DH / 4)), (uint32_t)wg_hi - 1u);
+            uint32_t row = kc;
+            if (p.ring_cap) {
+                row = rbase + (kc - t0);
+                if (row >= p.ring_cap) row -= p.ring_cap;
+            }
             const float* base = i < LPT / 2 ? kbase : vbase;
-            r[i] = ld4(base + prow((uint32_t)key) * row_stride + 4 * (f % (DH / 4)));
+            r[i] = ld4(base + (size_t)row * row_stride + 4 * (f % (DH / 4)));
         }
     };
     auto store_tile = [&](float* buf, const float4 (&r)[LPT]) {
@@ -123,7 +149,11 @@ __device__ __forceinline__ void prefill(const G4aPrefillParams& p) {
         }
     };
 
-    float m_run = NEG_INF, l_part = 0.0f;
+    // m_run: the row's running maximum (candidate threshold). m_ref: the
+    // maximum O and l are currently scaled to; it only moves when m_run gets
+    // more than RESCALE above it (a wave-uniform, rare rescale), so the
+    // probabilities e^{s - m_ref} stay below e^RESCALE.
+    float m_run = NEG_INF, m_ref = NEG_INF, l_part = 0.0f;
     f4v O[NC][4];
 #pragma unroll
     for (int c = 0; c < NC; ++c)
@@ -159,81 +189,201 @@ __device__ __forceinline__ void prefill(const G4aPrefillParams& p) {
     };
     // Exact rescoring of every recorded candidate and correction of O and l,
     // against the published maxima (the scale O and l are currently held at).
+    // 64 candidates per pass, lane = candidate:
+    //   1. exact dot in the reference's order (q and k rows from global memory,
+    //      64 dims of both in flight per step);
+    //   2. delta = e^{s_exact - m} - e^{s_approx - m} added to l of its row;
+    //   3. O += Delta V on the matrix cores, Delta[row][cand] = delta if the
+    //      candidate belongs to the row, else 0: K-step s of the 16x16x4 chain
+    //      takes candidates 4s..4s+3 (lane l: A = Delta[l%16][4s + l/16],
+    //      B = V[key(4s + l/16)][64c + 4(l%16) + e]), so each lane loads the V
+    //      float4s it feeds straight from memory.
     auto flush = [&]() {
         for (int base = 0; base < cnt; base += 64) {
             const int e = base + lane;
             const bool has = e < cnt;
             const uint32_t pk = has ? my_keys[e] : 0u;
-            const uint32_t rho = pk >> 28, kap = pk & 0x0fffffffu;
+            const uint32_t rho = pk >> 28, kap = has ? (pk & 0x0fffffffu) : (uint32_t)wg_lo;
             float delta = 0.0f;
-            if (has) {
-                const float* qrow = p.q + ((size_t)(qw + (rho >> 3)) * p.Hq + h0 + (rho & 7)) * DH;
+            {
+                const float* qrow = p.q + ((size_t)min(qw + (rho >> 3), p.T - 1) * p.Hq + h0 + (rho & 7)) * DH;
                 const float* krow = kbase + prow(kap) * row_stride;
                 float dot = 0.0f;
-#pragma unroll 4
-                for (int d = 0; d < DH; d += 16) {
-                    float4 qa[4], ka[4];
+                for (int d = 0; d < DH; d += 64) {
+                    float4 qa[16], ka[16];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
+                    for (int u = 0; u < 16; ++u) {
                         qa[u] = ld4(qrow + d + 4 * u);
                         ka[u] = ld4(krow + d + 4 * u);
                     }
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
+                    for (int u = 0; u < 16; ++u) {
                         dot = dot + qa[u].x * ka[u].x;
                         dot = dot + qa[u].y * ka[u].y;
                         dot = dot + qa[u].z * ka[u].z;
                         dot = dot + qa[u].w * ka[u].w;
                     }
                 }
-                const float sx = dot * p.scale;
-                const float m = my_m[rho];
-                delta = expf(sx - m) - expf(my_s[e] - m);
+                if (has) {
+                    const float m = my_m[rho];
+                    delta = expf(dot * p.scale - m) - expf(my_s[e] - m);
+                }
             }
             const int nb = min(64, cnt - base);
+            // l of row rho (lanes with rl == rho hold partial sums of that row)
             for (int i = 0; i < nb; ++i) {
-                const float di = __builtin_amdgcn_readlane(__float_as_int(delta), i) == 0
-                                     ? 0.0f
-                                     : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(delta), i));
-                if (di == 0.0f) continue;
+                const float di = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(delta), i));
                 const uint32_t ri = __builtin_amdgcn_readlane(rho, i);
-                const uint32_t ki = __builtin_amdgcn_readlane(kap, i);
                 if (lane == (int)ri) l_part += di;
-                if (g == (int)(ri >> 2)) {
-                    const float* vrow = vbase + prow(ki) * row_stride + 4 * rl;
+            }
+            for (int s4 = 0; s4 < nb; s4 += 4) {
+                const int src = s4 + g;
+                const float dl = __shfl(delta, src, 64);
+                const uint32_t rr = (uint32_t)__shfl((int)rho, src, 64);
+                const uint32_t kk = (uint32_t)__shfl((int)kap, src, 64);
+                const float a = rr == (uint32_t)rl ? dl : 0.0f;
+                const float* vrow = vbase + prow(kk) * row_stride + 4 * rl;
+                float4 vb[NC];
 #pragma unroll
-                    for (int c = 0; c < NC; ++c) {
-                        const float4 v4 = ld4(vrow + 64 * c);
-                        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+                for (int c = 0; c < NC; ++c) vb[c] = ld4(vrow + 64 * c);
 #pragma unroll
-                        for (int ee = 0; ee < 4; ++ee) {
-                            switch (ri & 3) {
-                                case 0: O[c][ee][0] = __builtin_fmaf(di, vv[ee], O[c][ee][0]); break;
-                                case 1: O[c][ee][1] = __builtin_fmaf(di, vv[ee], O[c][ee][1]); break;
-                                case 2: O[c][ee][2] = __builtin_fmaf(di, vv[ee], O[c][ee][2]); break;
-                                default: O[c][ee][3] = __builtin_fmaf(di, vv[ee], O[c][ee][3]); break;
-                            }
-                        }
-                    }
+                for (int c = 0; c < NC; ++c) {
+                    O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].x, O[c][0], 0, 0, 0);
+                    O[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].y, O[c][1], 0, 0, 0);
+                    O[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].z, O[c][2], 0, 0, 0);
+                    O[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].w, O[c][3], 0, 0, 0);
                 }
             }
         }
         cnt = 0;
     };
 
-    float4 pre[LPT];
-    if (nt > 0) load_tile(0, pre);  // no visible key at all: nothing to load (the clamp needs wg_hi >= 1)
-    for (uint32_t t = 0; t < nt; ++t) {
-        float* const buf = smem + (t & 1) * C::TILE;
-        store_tile(buf, pre);
-        __syncthreads();
-        load_tile(min(t + 1, nt - 1), pre);  // always issued: exact load counting; the last one re-reads
-        const int64_t t0 = wg_lo + (int64_t)t * BK;
-        if (!wave_valid || t0 >= w_hi || t0 + BK <= w_lo) continue;
-        const float* Kt = buf;
-        const float* Vt = buf + BK * KRS;
+    // The same correction at the end of the kernel, when the tile buffers are
+    // free: instead of each lane streaming its own q and k rows (64 scattered
+    // rows per load instruction), the wave stages 32-dim segments of its 16 q
+    // rows and of the 64 candidates' k rows in its LDS area with coalesced
+    // 128-byte reads (8 rows per instruction, two segments in flight), and
+    // each lane runs its sequential dot from LDS. The Delta V products take
+    // their V rows two K-steps ahead.
+    auto flush_staged = [&](float* stage) {
+        constexpr int SR = 36;                 // staged row stride (floats)
+        constexpr int NSEG = DH / 32;
+        float* const kst = stage;              // [64 candidates][SR]
+        float* const qst = stage + 64 * SR;    // [16 rows][SR]
+        const int seg = lane >> 3, part = lane & 7;
+        const float* const q0 = p.q + ((size_t)min(qw, p.T - 1) * p.Hq + h0 + seg) * DH + 4 * part;
+        const float* const q1 = p.q + ((size_t)min(qw + 1, p.T - 1) * p.Hq + h0 + seg) * DH + 4 * part;
+        for (int base = 0; base < cnt; base += 64) {
+            const int e = base + lane;
+            const bool has = e < cnt;
+            const uint32_t pk = has ? my_keys[e] : 0u;
+            const uint32_t rho = pk >> 28, kap = has ? (pk & 0x0fffffffu) : (uint32_t)wg_lo;
+            const float* krow[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t ki = (uint32_t)__shfl((int)kap, 8 * i + seg, 64);
+                krow[i] = kbase + prow(ki) * row_stride + 4 * part;
+            }
+            // two register buffers (A, B) for alternate segments, no runtime indexing
+            float4 kA[8], qA[2], kB[8], qB[2];
+            auto load_seg = [&](int sg, float4 (&kk)[8], float4 (&qq)[2]) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) kk[i] = ld4(krow[i] + 32 * sg);
+                qq[0] = ld4(q0 + 32 * sg);
+                qq[1] = ld4(q1 + 32 * sg);
+            };
+            float dot = 0.0f;
+            auto consume = [&](int sg, float4 (&kk)[8], float4 (&qq)[2]) {
+                wave_sync();  // the previous segment's reads are done
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    *reinterpret_cast<float4*>(kst + (8 * i + seg) * SR + 4 * part) = kk[i];
+                *reinterpret_cast<float4*>(qst + seg * SR + 4 * part) = qq[0];
+                *reinterpret_cast<float4*>(qst + (8 + seg) * SR + 4 * part) = qq[1];
+                if (sg + 2 < NSEG) load_seg(sg + 2, kk, qq);
+                wave_sync();
+                const float* kr = kst + lane * SR;
+                const float* qv = qst + rho * SR;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * u);
+                    const float4 q4 = *reinterpret_cast<const float4*>(qv + 4 * u);
+                    dot = dot + q4.x * k4.x;
+                    dot = dot + q4.y * k4.y;
+                    dot = dot + q4.z * k4.z;
+                    dot = dot + q4.w * k4.w;
+                }
+            };
+            static_assert(NSEG % 2 == 0, "segments are consumed in pairs");
+            load_seg(0, kA, qA);
+            load_seg(1, kB, qB);
+            // not unrolled: the loads of later segments must not be hoisted (registers)
+#pragma unroll 1
+            for (int sg = 0; sg < NSEG; sg += 2) {
+                consume(sg, kA, qA);
+                consume(sg + 1, kB, qB);
+            }
+            float delta = 0.0f;
+            if (has) {
+                const float m = my_m[rho];
+                delta = expf(dot * p.scale - m) - expf(my_s[e] - m);
+            }
+            const int nb = min(64, cnt - base);
+            for (int i = 0; i < nb; ++i) {
+                const float di = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(delta), i));
+                const uint32_t ri = __builtin_amdgcn_readlane(rho, i);
+                if (lane == (int)ri) l_part += di;
+            }
+            float4 vA[NC], vB[NC];
+            auto load_v = [&](int s4, float4 (&vb)[NC]) {
+                const uint32_t kk = (uint32_t)__shfl((int)kap, s4 + g, 64);
+                const float* vrow = vbase + prow(kk) * row_stride + 4 * rl;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) vb[c] = ld4(vrow + 64 * c);
+            };
+            auto apply_v = [&](int s4, const float4 (&vb)[NC]) {
+                const float dl = __shfl(delta, s4 + g, 64);
+                const uint32_t rr = (uint32_t)__shfl((int)rho, s4 + g, 64);
+                const float a = rr == (uint32_t)rl ? dl : 0.0f;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].x, O[c][0], 0, 0, 0);
+                    O[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].y, O[c][1], 0, 0, 0);
+                    O[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].z, O[c][2], 0, 0, 0);
+                    O[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].w, O[c][3], 0, 0, 0);
+                }
+            };
+            load_v(0, vA);
+            if (4 < nb) load_v(4, vB);
+            for (int s4 = 0; s4 < nb; s4 += 8) {
+                apply_v(s4, vA);
+                if (s4 + 8 < nb) load_v(s4 + 8, vA);
+                if (s4 + 4 < nb) {
+                    apply_v(s4 + 4, vB);
+                    if (s4 + 12 < nb) load_v(s4 + 12, vB);
+                }
+            }
+        }
+        cnt = 0;
+    };
 
-        // ---- approximate scores S^T = K Q^T: lane holds keys 4g + r of row rl ----
+    // ---- software-pipelined tile loop ----
+    // Iteration t holds tiles t and t+1 in the two LDS buffers and tile t+2 in
+    // registers. It issues the score MFMAs of tile t+1 first, so the matrix
+    // cores are busy while the VALU runs tile t's softmax and candidate
+    // bookkeeping (scores of tile t come from the previous iteration), then
+    // the P.V MFMAs of tile t. Two barriers per tile: one before a buffer is
+    // refilled, one after.
+    auto tile_active = [&](uint32_t t) -> bool {
+        const int32_t t0 = wg_lo + (int32_t)(t * BK);
+        return wave_valid && t < nt && t0 < w_hi && t0 + BK > w_lo;
+    };
+    auto tile_rbase = [&](uint32_t rb) -> uint32_t {  // ring base of the next tile
+        if (!p.ring_cap) return 0u;
+        rb += BK;
+        return rb >= p.ring_cap ? rb - p.ring_cap : rb;
+    };
+    auto qk = [&](const float* Kt) -> f4v {
         f4v S = f4v{0.0f, 0.0f, 0.0f, 0.0f};
         const float* kr = Kt + rl * KRS + 4 * g;
 #pragma unroll
@@ -244,73 +394,119 @@ __device__ __forceinline__ void prefill(const G4aPrefillParams& p) {
             S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, qr[tt].z, S, 0, 0, 0);
             S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, qr[tt].w, S, 0, 0, 0);
         }
-        float s[4];
-        bool vis[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t j = t0 + 4 * g + r;
-            vis[r] = j >= my_lo && j < my_hi;
-            s[r] = vis[r] ? S[r] * p.scale : NEG_INF;
-        }
-        float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-        tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
-        tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
-        const float mn = fmaxf(m_run, tm);
+        return S;
+    };
 
-        // ---- record the keys within TAU of the running maximum ----
-        if (cnt + 4 * 64 > CAP) {
-            publish_m(mn);
-            compact();
-            if (cnt + 4 * 64 > CAP) {
-                publish_m(m_run);  // O and l are still held at m_run
-                flush();
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const bool cand = vis[r] && s[r] > mn - PF_TAU;
-            const uint64_t b = ballot(cand);
-            if (cand) {
-                const int pos = cnt + lanes_below(b);
-                my_keys[pos] = ((uint32_t)rl << 28) | (uint32_t)(t0 + 4 * g + r);
-                my_s[pos] = s[r];
-            }
-            cnt += __builtin_popcountll(b);
-        }
-
-        // ---- online softmax (row rl) and P.V on the matrix cores ----
-        float pr[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? expf(s[r] - mn) : 0.0f;
-        const float corr = (m_run == NEG_INF) ? 0.0f : expf(m_run - mn);
-        l_part = l_part * corr + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-        m_run = mn;
-        // O rows are 4g + r'; their correction factors live in lanes 4g + r'
-        const f4v cr = f4v{__shfl(corr, 4 * g + 0, 64), __shfl(corr, 4 * g + 1, 64), __shfl(corr, 4 * g + 2, 64),
-                           __shfl(corr, 4 * g + 3, 64)};
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) O[c][e] *= cr;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float* vr = Vt + (4 * g + r) * DH + 4 * rl;
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const float4 vv = *reinterpret_cast<const float4*>(vr + 64 * c);
-                O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.x, O[c][0], 0, 0, 0);
-                O[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.y, O[c][1], 0, 0, 0);
-                O[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.z, O[c][2], 0, 0, 0);
-                O[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.w, O[c][3], 0, 0, 0);
-            }
-        }
+    float4 pre[LPT];
+    f4v Scur = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    if (nt > 0) {
+        load_tile((uint32_t)wg_lo, ring_base, pre);
+        store_tile(smem, pre);
+        __syncthreads();
+        // registers: tile 1 (tile 0 again when there is no tile 1)
+        const uint32_t rb1 = nt > 1 ? tile_rbase(ring_base) : ring_base;
+        load_tile(nt > 1 ? (uint32_t)wg_lo + BK : (uint32_t)wg_lo, rb1, pre);
+        ring_base = rb1;
+        if (tile_active(0)) Scur = qk(smem);
     }
+    for (uint32_t t = 0; t < nt; ++t) {
+        const uint32_t t0 = (uint32_t)wg_lo + t * BK;
+        float* const cur = smem + (t & 1) * C::TILE;
+        float* const nxt = smem + ((t + 1) & 1) * C::TILE;
+        // tile t+1 into the other buffer (its previous tile t-1 is done: barrier at the end of t-1)
+        store_tile(nxt, pre);
+        __syncthreads();
+        {
+            // registers: tile t+2 (always issued; past the end it re-reads the last tile)
+            const bool more = t + 2 < nt;
+            const uint32_t rb2 = more ? tile_rbase(ring_base) : ring_base;
+            load_tile(more ? t0 + 2 * BK : (uint32_t)wg_lo + (nt - 1) * BK, rb2, pre);
+            if (more) ring_base = rb2;
+        }
+        const bool act = tile_active(t);
+        const bool act_next = tile_active(t + 1);
+        f4v Snext = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+        if (act_next) Snext = qk(nxt);
+        if (act) {
+            float s[4];
+            bool vis[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int32_t j = (int32_t)t0 + 4 * g + r;
+                vis[r] = j >= my_lo && j < my_hi;
+                s[r] = vis[r] ? Scur[r] * p.scale : NEG_INF;
+            }
+            float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+            tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
+            tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+            const float mn = fmaxf(m_run, tm);
+
+            // ---- record the keys within TAU of the running maximum ----
+            if (cnt + 4 * 64 > CAP) {
+                publish_m(mn);
+                compact();
+                if (cnt + 4 * 64 > CAP) {
+                    publish_m(m_ref);  // O and l are held at m_ref
+                    flush();
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool cand = vis[r] && s[r] > mn - PF_TAU;
+                const uint64_t b = ballot(cand);
+                if (cand) {
+                    const int pos = cnt + lanes_below(b);
+                    my_keys[pos] = ((uint32_t)rl << 28) | (uint32_t)(t0 + 4 * g + r);
+                    my_s[pos] = s[r];
+                }
+                cnt += __builtin_popcountll(b);
+            }
+            m_run = mn;
+
+            // ---- rescale O and l when some row's maximum moved RESCALE above its reference ----
+            if (ballot(mn > m_ref + PF_RESCALE) != 0) {
+                const float corr = (m_ref == NEG_INF) ? 0.0f : expf(m_ref - mn);
+                l_part *= corr;
+                m_ref = mn;
+                // O rows are 4g + r'; their correction factors live in lanes 4g + r'
+                const f4v cr = f4v{__shfl(corr, 4 * g + 0, 64), __shfl(corr, 4 * g + 1, 64),
+                                   __shfl(corr, 4 * g + 2, 64), __shfl(corr, 4 * g + 3, 64)};
+#pragma unroll
+                for (int c = 0; c < NC; ++c)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) O[c][e] *= cr;
+            }
+
+            // ---- probabilities against m_ref and P.V on the matrix cores ----
+            float pr[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? expf(s[r] - m_ref) : 0.0f;
+            l_part += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+            const float* Vt = cur + BK * KRS;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float* vr = Vt + (4 * g + r) * DH + 4 * rl;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const float4 vv = *reinterpret_cast<const float4*>(vr + 64 * c);
+                    O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.x, O[c][0], 0, 0, 0);
+                    O[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.y, O[c][1], 0, 0, 0);
+                    O[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.z, O[c][2], 0, 0, 0);
+                    O[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.w, O[c][3], 0, 0, 0);
+                }
+            }
+        }
+        Scur = Snext;
+        __syncthreads();  // every wave is done with buffer t before it is refilled with tile t+2
+    }
+    __syncthreads();  // every wave is done with the tile buffers: they become the staging areas
     if (!wave_valid) return;  // no barrier follows
 
     // ---- exact corrections for the keys still within TAU of the final maxima ----
     publish_m(m_run);
     compact();
-    flush();
+    publish_m(m_ref);
+    flush_staged(smem + w * (C::STAGE));
 
     // ---- normalise and write: O row 4g + r' is query qw + row/8, head h0 + row%8 ----
     float l = l_part;
@@ -331,9 +527,438 @@ __device__ __forceinline__ void prefill(const G4aPrefillParams& p) {
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Head-dim 256 prefill with two waves per SIMD. A workgroup is 8 waves over the
+// same 8 queries as above: wave w owns rows 16*(w%4) .. +15 (2 queries x 8
+// heads) and the tiles of parity w/4 (even or odd 16-key tiles), so the two
+// waves sharing a SIMD (w and w+4) never wait on each other and the hardware
+// overlaps one wave's softmax, LDS and bookkeeping with the other's MFMAs. Per
+// step both tiles sit in LDS (register-staged prefetch of the next pair). At
+// the end each wave compacts its candidates against the maximum over both
+// parities, corrects them exactly, and the parities merge through LDS.
+template <int DH>
+struct PairCfg {
+    static constexpr int BK = 16;
+    static constexpr int KRS = DH + 4;
+    static constexpr int TILE = BK * KRS + BK * DH;
+    static constexpr int RPW = 2 * 2 * BK * (DH / 256) / 8;  // 1 KiB row copies per wave per tile pair
+    static constexpr int NC = DH / 64;
+    static constexpr int QT = DH / 16;
+    static constexpr int CAP = 256;                          // candidate entries per wave
+    static constexpr int SR = 20;                            // staged row stride (floats): 16 dims + pad
+    static constexpr int STAGE = (64 + 16) * SR;             // per-wave staging floats at the end
+    static constexpr int MERGE = 4 * (NC * 16 * 64 + 2 * 64);  // odd-parity O, l, m of the 4 row blocks
+    static constexpr int BIG0 = 4 * TILE > 8 * STAGE ? 4 * TILE : 8 * STAGE;  // two tile pairs in flight
+    static constexpr int BIG = BIG0 > MERGE ? BIG0 : MERGE;
+    static constexpr int SMEM = BIG + 8 * 2 * CAP + 8 * 16;
+    static_assert(RPW * 8 * 256 == 2 * 2 * BK * DH, "tile pair split into 1 KiB row copies");
+    static_assert(DH % 256 == 0, "rows are copied in 1 KiB pieces");
+};
+
+template <int DH>
+__device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
+    using C = PairCfg<DH>;
+    constexpr int BK = C::BK, KRS = C::KRS, RPW = C::RPW, NC = C::NC, QT = C::QT, CAP = C::CAP, SR = C::SR;
+    __shared__ __attribute__((aligned(16))) float smem[C::SMEM];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rb = w & 3, par = w >> 2;
+    const int g = lane >> 4, rl = lane & 15;
+    const uint32_t kvh = blockIdx.y;
+    const uint32_t qb = blockIdx.x * 8;
+    const uint32_t qw = qb + 2 * rb;
+    const uint32_t h0 = kvh * 8;
+    const size_t row_stride = (size_t)p.Hkv * DH;
+    const float* __restrict__ kbase = p.k + (size_t)kvh * DH;
+    const float* __restrict__ vbase = p.v + (size_t)kvh * DH;
+    uint32_t* const my_keys = reinterpret_cast<uint32_t*>(smem + C::BIG + w * 2 * CAP);
+    float* const my_s = smem + C::BIG + w * 2 * CAP + CAP;
+    float* const mtab = smem + C::BIG + 8 * 2 * CAP;  // [8 waves][16 rows]
+    float* const my_m = mtab + w * 16;
+
+    auto key_hi = [&](int64_t i) -> int32_t {
+        const int64_t lim = (int64_t)p.q_pos0 + i - (int64_t)p.k_pos0 + 1;
+        return (int32_t)(lim <= 0 ? 0 : (lim < (int64_t)p.S ? lim : (int64_t)p.S));
+    };
+    auto key_lo = [&](int64_t i) -> int32_t {
+        if (p.window == 0) return 0;
+        const int64_t lo = (int64_t)p.q_pos0 + i - (int64_t)p.k_pos0 - (int64_t)p.window + 1;
+        return (int32_t)(lo <= 0 ? 0 : (lo < (int64_t)p.S ? lo : (int64_t)p.S));
+    };
+    auto prow = [&](uint32_t j) -> size_t { return p.ring_cap ? j % p.ring_cap : j; };
+
+    const uint32_t qlast = min(qb + 7, p.T - 1);
+    const int32_t wg_lo = key_lo(qb), wg_hi = key_hi(qlast);
+    const uint32_t nt = wg_hi > wg_lo ? (uint32_t)((wg_hi - wg_lo + BK - 1) / BK) : 0;
+    const uint32_t nsteps = (nt + 1) / 2;
+    const bool wave_valid = qw < p.T;
+    const int32_t w_lo = wave_valid ? key_lo(qw) : 0;
+    const int32_t w_hi = wave_valid ? key_hi(min(qw + 1, p.T - 1)) : 0;
+    const uint32_t myq = qw + (rl >> 3);
+    const bool qvalid = myq < p.T;
+    const int32_t my_lo = key_lo(myq), my_hi = qvalid ? key_hi(myq) : 0;
+    float4 qr[QT];
+    {
+        const float* qrow = p.q + ((size_t)min(myq, p.T - 1) * p.Hq + h0 + (rl & 7)) * DH + 4 * g;
+#pragma unroll
+        for (int t = 0; t < QT; ++t) qr[t] = ld4(qrow + 16 * t);
+    }
+
+    // Tile pair of step st (tiles 2st and 2st+1) goes to ring slot st&1, each
+    // tile K (16 rows of KRS floats) then V (16 rows of DH), with global->LDS
+    // row copies: 64 rows of DH floats per pair, RPW 1 KiB copies per wave.
+    // Keys past the last visible key re-read it.
+    auto issue_pair = [&](uint32_t st) {
+        float* const slot = smem + (st & 1) * 2 * C::TILE;
+#pragma unroll
+        for (int j = 0; j < RPW; ++j) {
+            const int idx = w * RPW + j;                  // 1 KiB piece of the pair
+            const int row = idx / (DH / 256), piece = idx % (DH / 256);
+            const int tsel = row / (2 * BK), isv = (row / BK) & 1, kf = row % BK;
+            const uint32_t key = min((uint32_t)wg_lo + (2 * st + tsel) * BK + kf, (uint32_t)wg_hi - 1u);
+            const float* src = (isv ? vbase : kbase) + prow(key) * row_stride + 256 * piece + 4 * lane;
+            float* dst = slot + tsel * C::TILE + (isv ? BK * KRS + kf * DH : kf * KRS) + 256 * piece;
+            copy16_to_lds(src, dst);
+        }
+    };
+
+    float m_run = NEG_INF, m_ref = NEG_INF, l_part = 0.0f;
+    f4v O[NC][4];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) O[c][e] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    int cnt = 0;
+
+    auto publish_m = [&](float mref) {
+        if (g == 0) my_m[rl] = mref;
+        wave_sync();
+    };
+    auto compact = [&]() {
+        int nc = 0;
+        for (int base = 0; base < cnt; base += 64) {
+            const int e = base + lane;
+            const bool has = e < cnt;
+            const uint32_t pk = has ? my_keys[e] : 0u;
+            const float sa = has ? my_s[e] : 0.0f;
+            const bool keep = has && sa > my_m[pk >> 28] - PF_TAU;
+            wave_sync();
+            const uint64_t b = ballot(keep);
+            if (keep) {
+                const int pos = nc + lanes_below(b);
+                my_keys[pos] = pk;
+                my_s[pos] = sa;
+            }
+            nc += __builtin_popcountll(b);
+            wave_sync();
+        }
+        cnt = nc;
+    };
+    // Exact correction of the recorded candidates against the published
+    // maxima (the scale O and l are held at); see prefill<>::flush. The
+    // in-loop form reads q and k rows straight from memory 16 dims at a time
+    // (few registers; it only runs when a list overflows).
+    auto delta_and_l = [&](int base, bool has, uint32_t rho, float dot, int e) -> float {
+        float delta = 0.0f;
+        if (has) {
+            const float m = my_m[rho];
+            delta = expf(dot * p.scale - m) - expf(my_s[e] - m);
+        }
+        const int nb = min(64, cnt - base);
+        for (int i = 0; i < nb; ++i) {
+            const float di = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(delta), i));
+            const uint32_t ri = __builtin_amdgcn_readlane(rho, i);
+            if (lane == (int)ri) l_part += di;
+        }
+        return delta;
+    };
+    auto correct_o = [&](int base, float delta, uint32_t rho, uint32_t kap) {
+        __builtin_amdgcn_sched_barrier(0);  // its V loads stay after the dot products (registers)
+        const int nb = min(64, cnt - base);
+        float4 vA[NC], vB[NC];
+        auto load_v = [&](int s4, float4 (&vb)[NC]) {
+            const uint32_t kk = (uint32_t)__shfl((int)kap, s4 + g, 64);
+            const float* vrow = vbase + prow(kk) * row_stride + 4 * rl;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) vb[c] = ld4(vrow + 64 * c);
+        };
+        auto apply_v = [&](int s4, const float4 (&vb)[NC]) {
+            const float dl = __shfl(delta, s4 + g, 64);
+            const uint32_t rr = (uint32_t)__shfl((int)rho, s4 + g, 64);
+            const float a = rr == (uint32_t)rl ? dl : 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].x, O[c][0], 0, 0, 0);
+                O[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].y, O[c][1], 0, 0, 0);
+                O[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].z, O[c][2], 0, 0, 0);
+                O[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].w, O[c][3], 0, 0, 0);
+            }
+        };
+        load_v(0, vA);
+        if (4 < nb) load_v(4, vB);
+        for (int s4 = 0; s4 < nb; s4 += 8) {
+            apply_v(s4, vA);
+            if (s4 + 8 < nb) load_v(s4 + 8, vA);
+            if (s4 + 4 < nb) {
+                apply_v(s4 + 4, vB);
+                if (s4 + 12 < nb) load_v(s4 + 12, vB);
+            }
+        }
+    };
+    auto flush_light = [&]() {
+        for (int base = 0; base < cnt; base += 64) {
+            const int e = base + lane;
+            const bool has = e < cnt;
+            const uint32_t pk = has ? my_keys[e] : 0u;
+            const uint32_t rho = pk >> 28, kap = has ? (pk & 0x0fffffffu) : (uint32_t)wg_lo;
+            const float* qrow = p.q + ((size_t)min(qw + (rho >> 3), p.T - 1) * p.Hq + h0 + (rho & 7)) * DH;
+            const float* krow = kbase + prow(kap) * row_stride;
+            float dot = 0.0f;
+#pragma unroll 1
+            for (int d = 0; d < DH; d += 16) {
+                float4 qa[4], ka[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    qa[u] = ld4(qrow + d + 4 * u);
+                    ka[u] = ld4(krow + d + 4 * u);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    dot = dot + qa[u].x * ka[u].x;
+                    dot = dot + qa[u].y * ka[u].y;
+                    dot = dot + qa[u].z * ka[u].z;
+                    dot = dot + qa[u].w * ka[u].w;
+                }
+            }
+            const float delta = delta_and_l(base, has, rho, dot, e);
+            correct_o(base, delta, rho, kap);
+        }
+        cnt = 0;
+    };
+    // End-of-kernel form: 16-dim segments of the wave's q rows and of the
+    // candidates' k rows staged in LDS with coalesced reads (4 candidates per
+    // load instruction), two segments in flight, each lane running its
+    // sequential dot from LDS (see prefill<>::flush_staged).
+    auto flush_staged = [&](float* stage) {
+        constexpr int NSEG = DH / 16;
+        float* const kst = stage;
+        float* const qst = stage + 64 * SR;
+        const int seg = lane >> 2, part = lane & 3;
+        const float* const qrow = p.q + ((size_t)min(qw + (seg >> 3), p.T - 1) * p.Hq + h0 + (seg & 7)) * DH + 4 * part;
+        for (int base = 0; base < cnt; base += 64) {
+            const int e = base + lane;
+            const bool has = e < cnt;
+            const uint32_t pk = has ? my_keys[e] : 0u;
+            const uint32_t rho = pk >> 28, kap = has ? (pk & 0x0fffffffu) : (uint32_t)wg_lo;
+            const float* krow[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t ki = (uint32_t)__shfl((int)kap, 16 * i + seg, 64);
+                krow[i] = kbase + prow(ki) * row_stride + 4 * part;
+            }
+            float4 kA[4], qA, kB[4], qB;
+            auto load_seg = [&](int sg, float4 (&kk)[4], float4& qq) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) kk[i] = ld4(krow[i] + 16 * sg);
+                qq = ld4(qrow + 16 * sg);
+            };
+            float dot = 0.0f;
+            auto consume = [&](int sg, float4 (&kk)[4], float4& qq) {
+                wave_sync();
+#pragma unroll
+                for (int i = 0; i < 4; ++i) *reinterpret_cast<float4*>(kst + (16 * i + seg) * SR + 4 * part) = kk[i];
+                *reinterpret_cast<float4*>(qst + seg * SR + 4 * part) = qq;
+                if (sg + 2 < NSEG) load_seg(sg + 2, kk, qq);
+                wave_sync();
+                const float* kr = kst + lane * SR;
+                const float* qv = qst + rho * SR;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * u);
+                    const float4 q4 = *reinterpret_cast<const float4*>(qv + 4 * u);
+                    dot = dot + q4.x * k4.x;
+                    dot = dot + q4.y * k4.y;
+                    dot = dot + q4.z * k4.z;
+                    dot = dot + q4.w * k4.w;
+                }
+            };
+            load_seg(0, kA, qA);
+            load_seg(1, kB, qB);
+#pragma unroll 1
+            for (int sg = 0; sg < NSEG; sg += 2) {
+                consume(sg, kA, qA);
+                consume(sg + 1, kB, qB);
+            }
+            const float delta = delta_and_l(base, has, rho, dot, e);
+            correct_o(base, delta, rho, kap);
+        }
+        cnt = 0;
+    };
+
+    if (nsteps > 0) issue_pair(0);
+    for (uint32_t st = 0; st < nsteps; ++st) {
+        wait_vm<0>();   // this wave's copies of pair st have landed (nothing else is in flight)
+        barrier_lds();  // every wave's have; every wave is done with slot (st+1)&1 (pair st-1)
+        if (st + 1 < nsteps) issue_pair(st + 1);
+        const uint32_t t = 2 * st + par;
+        const int32_t t0 = wg_lo + (int32_t)(t * BK);
+        if (!wave_valid || t >= nt || t0 >= w_hi || t0 + BK <= w_lo) continue;
+        const float* Kt = smem + (st & 1) * 2 * C::TILE + par * C::TILE;
+        const float* Vt = Kt + BK * KRS;
+
+        f4v S = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+        const float* kr = Kt + rl * KRS + 4 * g;
+#pragma unroll
+        for (int tt = 0; tt < QT; ++tt) {
+            const float4 kk = *reinterpret_cast<const float4*>(kr + 16 * tt);
+            S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.x, qr[tt].x, S, 0, 0, 0);
+            S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.y, qr[tt].y, S, 0, 0, 0);
+            S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, qr[tt].z, S, 0, 0, 0);
+            S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, qr[tt].w, S, 0, 0, 0);
+        }
+        float s[4];
+        bool vis[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int32_t j = t0 + 4 * g + r;
+            vis[r] = j >= my_lo && j < my_hi;
+            s[r] = vis[r] ? S[r] * p.scale : NEG_INF;
+        }
+        float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
+        tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+        const float mn = fmaxf(m_run, tm);
+
+        // candidates: count first, make room if needed, then record
+        bool cand[4];
+        uint64_t bal[4];
+        int nnew = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            cand[r] = vis[r] && s[r] > mn - PF_TAU;
+            bal[r] = ballot(cand[r]);
+            nnew += __builtin_popcountll(bal[r]);
+        }
+        if (cnt + nnew > CAP) {
+            publish_m(mn);
+            compact();
+            if (cnt + nnew > CAP) {
+                publish_m(m_ref);
+                flush_light();
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (cand[r]) {
+                const int pos = cnt + lanes_below(bal[r]);
+                my_keys[pos] = ((uint32_t)rl << 28) | (uint32_t)(t0 + 4 * g + r);
+                my_s[pos] = s[r];
+            }
+            cnt += __builtin_popcountll(bal[r]);
+        }
+        m_run = mn;
+
+        if (ballot(mn > m_ref + PF_RESCALE) != 0) {
+            const float corr = (m_ref == NEG_INF) ? 0.0f : expf(m_ref - mn);
+            l_part *= corr;
+            m_ref = mn;
+            const f4v cr = f4v{__shfl(corr, 4 * g + 0, 64), __shfl(corr, 4 * g + 1, 64), __shfl(corr, 4 * g + 2, 64),
+                               __shfl(corr, 4 * g + 3, 64)};
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) O[c][e] *= cr;
+        }
+
+        float pr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? expf(s[r] - m_ref) : 0.0f;
+        l_part += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float* vr = Vt + (4 * g + r) * DH + 4 * rl;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const float4 vv = *reinterpret_cast<const float4*>(vr + 64 * c);
+                O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.x, O[c][0], 0, 0, 0);
+                O[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.y, O[c][1], 0, 0, 0);
+                O[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.z, O[c][2], 0, 0, 0);
+                O[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.w, O[c][3], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- end: compact against the maximum over both parities, correct, merge ----
+    wait_vm<0>();
+    publish_m(m_run);
+    __syncthreads();  // tile buffers free; both parities' maxima published
+    {
+        const float mo = mtab[(w ^ 4) * 16 + rl];  // the other parity's running maximum of row rl
+        publish_m(fmaxf(m_run, mo));
+    }
+    if (wave_valid) {
+        compact();
+        publish_m(m_ref);
+        flush_staged(smem + w * C::STAGE);
+    }
+    float l = l_part;
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    __syncthreads();  // staging done: the merge area overlays it
+    float* const mo_ = smem + rb * (NC * 16 * 64 + 2 * 64);  // odd parity -> even parity, per row block
+    if (par == 1) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) mo_[((c * 4 + e) * 4 + r) * 64 + lane] = O[c][e][r];
+        mo_[NC * 16 * 64 + lane] = l;
+        mo_[NC * 16 * 64 + 64 + lane] = m_ref;
+    }
+    __syncthreads();
+    if (par == 1 || !wave_valid) return;
+    {
+        // rows: lane (g, rl) holds l and m of row rl; O register r of lane (g, rl) is row 4g + r
+        const float l1 = mo_[NC * 16 * 64 + lane];
+        const float m1 = mo_[NC * 16 * 64 + 64 + lane];
+        const float M = fmaxf(m_ref, m1);
+        const float e0 = (m_ref == NEG_INF) ? 0.0f : expf(m_ref - M);
+        const float e1 = (m1 == NEG_INF) ? 0.0f : expf(m1 - M);
+        const float lt = l * e0 + l1 * e1;
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        float a0[4], a1[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float iv = __shfl(inv, 4 * g + r, 64);
+            a0[r] = __shfl(e0, 4 * g + r, 64) * iv;
+            a1[r] = __shfl(e1, 4 * g + r, 64) * iv;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 4 * g + r;
+            const uint32_t qi = qw + (row >> 3);
+            if (qi >= p.T) continue;
+            float* orow = p.out + ((size_t)qi * p.Hq + h0 + (row & 7)) * DH + 4 * rl;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                float4 o;
+                o.x = O[c][0][r] * a0[r] + mo_[((c * 4 + 0) * 4 + r) * 64 + lane] * a1[r];
+                o.y = O[c][1][r] * a0[r] + mo_[((c * 4 + 1) * 4 + r) * 64 + lane] * a1[r];
+                o.z = O[c][2][r] * a0[r] + mo_[((c * 4 + 2) * 4 + r) * 64 + lane] * a1[r];
+                o.w = O[c][3][r] * a0[r] + mo_[((c * 4 + 3) * 4 + r) * 64 + lane] * a1[r];
+                *reinterpret_cast<float4*>(orow + 64 * c) = o;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 extern "C" {
 __global__ __launch_bounds__(256) void g4a_prefill_d256(G4aPrefillParams p) { prefill<256>(p); }
 __global__ __launch_bounds__(256) void g4a_prefill_d512(G4aPrefillParams p) { prefill<512>(p); }
+__global__ __launch_bounds__(512) void g4a_prefill2_d256(G4aPrefillParams p) { prefill_pair<256>(p); }
 }
