@@ -28,7 +28,7 @@
 
 namespace {
 
-constexpr float PF_TAU = 10.0f;
+constexpr float PF_TAU = 6.0f;
 constexpr float PF_RESCALE = 8.0f;  // e^8 ~ 3e3: probability headroom before O and l are rescaled
 
 template <int DH>
@@ -547,9 +547,13 @@ struct PairCfg {
     static constexpr int QT = DH / 16;
     static constexpr int CAP = 256;                          // candidate entries per wave
     static constexpr int SR = 20;                            // staged row stride (floats): 16 dims + pad
-    static constexpr int STAGE = (64 + 16) * SR;             // per-wave staging floats at the end
+    static constexpr int STAGE = (64 + 16) * SR;             // per-wave staging floats (in-loop overflow path)
+    static constexpr int QRS = DH + 4;                       // q row stride in the end-of-kernel LDS copy
+    static constexpr int FB = 8;                             // candidates per end-of-kernel batch
+    static constexpr int FLUSH = 4 * 16 * QRS + 8 * FB * DH; // q rows of the 4 row blocks + each wave's k rows
     static constexpr int MERGE = 4 * (NC * 16 * 64 + 2 * 64);  // odd-parity O, l, m of the 4 row blocks
-    static constexpr int BIG0 = 4 * TILE > 8 * STAGE ? 4 * TILE : 8 * STAGE;  // two tile pairs in flight
+    static constexpr int BIG00 = 4 * TILE > 8 * STAGE ? 4 * TILE : 8 * STAGE;  // two tile pairs in flight
+    static constexpr int BIG0 = BIG00 > FLUSH ? BIG00 : FLUSH;
     static constexpr int BIG = BIG0 > MERGE ? BIG0 : MERGE;
     static constexpr int SMEM = BIG + 8 * 2 * CAP + 8 * 16;
     static_assert(RPW * 8 * 256 == 2 * 2 * BK * DH, "tile pair split into 1 KiB row copies");
@@ -674,37 +678,62 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         }
         return delta;
     };
-    auto correct_o = [&](int base, float delta, uint32_t rho, uint32_t kap) {
-        __builtin_amdgcn_sched_barrier(0);  // its V loads stay after the dot products (registers)
+    // O += Delta V (see prefill<>::flush), V rows DEPTH K-steps ahead
+    // (DEPTH 4 at the end of the kernel, 2 in the loop where registers are short).
+    auto load_v = [&](int s4, uint32_t kap, float4 (&vb)[NC]) {
+        const uint32_t kk = (uint32_t)__shfl((int)kap, s4 + g, 64);
+        const float* vrow = vbase + prow(kk) * row_stride + 4 * rl;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) vb[c] = ld4(vrow + 64 * c);
+    };
+    auto apply_v = [&](int s4, float delta, uint32_t rho, const float4 (&vb)[NC]) {
+        const float dl = __shfl(delta, s4 + g, 64);
+        const uint32_t rr = (uint32_t)__shfl((int)rho, s4 + g, 64);
+        const float a = rr == (uint32_t)rl ? dl : 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].x, O[c][0], 0, 0, 0);
+            O[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].y, O[c][1], 0, 0, 0);
+            O[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].z, O[c][2], 0, 0, 0);
+            O[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].w, O[c][3], 0, 0, 0);
+        }
+    };
+    auto correct_o2 = [&](int base, float delta, uint32_t rho, uint32_t kap) {
+        __builtin_amdgcn_sched_barrier(0);
         const int nb = min(64, cnt - base);
         float4 vA[NC], vB[NC];
-        auto load_v = [&](int s4, float4 (&vb)[NC]) {
-            const uint32_t kk = (uint32_t)__shfl((int)kap, s4 + g, 64);
-            const float* vrow = vbase + prow(kk) * row_stride + 4 * rl;
-#pragma unroll
-            for (int c = 0; c < NC; ++c) vb[c] = ld4(vrow + 64 * c);
-        };
-        auto apply_v = [&](int s4, const float4 (&vb)[NC]) {
-            const float dl = __shfl(delta, s4 + g, 64);
-            const uint32_t rr = (uint32_t)__shfl((int)rho, s4 + g, 64);
-            const float a = rr == (uint32_t)rl ? dl : 0.0f;
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].x, O[c][0], 0, 0, 0);
-                O[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].y, O[c][1], 0, 0, 0);
-                O[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].z, O[c][2], 0, 0, 0);
-                O[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].w, O[c][3], 0, 0, 0);
+        auto step = [&](int s4, float4 (&vb)[NC]) {
+            if (s4 < nb) {
+                apply_v(s4, delta, rho, vb);
+                if (s4 + 8 < nb) load_v(s4 + 8, kap, vb);
             }
         };
-        load_v(0, vA);
-        if (4 < nb) load_v(4, vB);
+        load_v(0, kap, vA);
+        if (4 < nb) load_v(4, kap, vB);
         for (int s4 = 0; s4 < nb; s4 += 8) {
-            apply_v(s4, vA);
-            if (s4 + 8 < nb) load_v(s4 + 8, vA);
-            if (s4 + 4 < nb) {
-                apply_v(s4 + 4, vB);
-                if (s4 + 12 < nb) load_v(s4 + 12, vB);
+            step(s4, vA);
+            step(s4 + 4, vB);
+        }
+    };
+    auto correct_o4 = [&](int base, float delta, uint32_t rho, uint32_t kap) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int nb = min(64, cnt - base);
+        float4 vA[NC], vB[NC], vC[NC], vD[NC];
+        auto step = [&](int s4, float4 (&vb)[NC]) {
+            if (s4 < nb) {
+                apply_v(s4, delta, rho, vb);
+                if (s4 + 16 < nb) load_v(s4 + 16, kap, vb);
             }
+        };
+        load_v(0, kap, vA);
+        if (4 < nb) load_v(4, kap, vB);
+        if (8 < nb) load_v(8, kap, vC);
+        if (12 < nb) load_v(12, kap, vD);
+        for (int s4 = 0; s4 < nb; s4 += 16) {
+            step(s4, vA);
+            step(s4 + 4, vB);
+            step(s4 + 8, vC);
+            step(s4 + 12, vD);
         }
     };
     auto flush_light = [&]() {
@@ -733,66 +762,74 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
                 }
             }
             const float delta = delta_and_l(base, has, rho, dot, e);
-            correct_o(base, delta, rho, kap);
+            correct_o2(base, delta, rho, kap);
         }
         cnt = 0;
     };
-    // End-of-kernel form: 16-dim segments of the wave's q rows and of the
-    // candidates' k rows staged in LDS with coalesced reads (4 candidates per
-    // load instruction), two segments in flight, each lane running its
-    // sequential dot from LDS (see prefill<>::flush_staged).
-    auto flush_staged = [&](float* stage) {
-        constexpr int NSEG = DH / 16;
-        float* const kst = stage;
-        float* const qst = stage + 64 * SR;
-        const int seg = lane >> 2, part = lane & 3;
-        const float* const qrow = p.q + ((size_t)min(qw + (seg >> 3), p.T - 1) * p.Hq + h0 + (seg & 7)) * DH + 4 * part;
-        for (int base = 0; base < cnt; base += 64) {
-            const int e = base + lane;
+    // End-of-kernel form, FB candidates per batch. The q rows of the wave's
+    // row block already sit in LDS (copied from registers, qlds); per batch
+    // the FB candidates' k rows are copied to the wave's LDS area (one 1 KiB
+    // global->LDS row copy each, 16-byte columns XOR-swizzled by the slot so
+    // the lanes' reads hit distinct banks) while their V rows load into
+    // registers, so a batch costs one memory round trip. Lanes j (and their
+    // replicas j + 8i) run candidate j's sequential dot; Delta V takes two
+    // 16x16x4 K-steps (candidates 0-3, 4-7).
+    auto flush_rows = [&](const float* qlds, float* kbuf) {
+        constexpr int FB = C::FB, QRS = C::QRS;
+        static_assert(FB == 8 && DH % 256 == 0, "batch layout");
+        const int j = lane & 7;
+        for (int base = 0; base < cnt; base += FB) {
+            const int e = base + j;
             const bool has = e < cnt;
             const uint32_t pk = has ? my_keys[e] : 0u;
             const uint32_t rho = pk >> 28, kap = has ? (pk & 0x0fffffffu) : (uint32_t)wg_lo;
-            const float* krow[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t ki = (uint32_t)__shfl((int)kap, 16 * i + seg, 64);
-                krow[i] = kbase + prow(ki) * row_stride + 4 * part;
+            for (int c = 0; c < FB; ++c) {
+                const uint32_t kc = (uint32_t)__builtin_amdgcn_readlane((int)kap, c);
+                const float* src = kbase + prow(kc) * row_stride;
+#pragma unroll
+                for (int pc = 0; pc < DH / 256; ++pc)
+                    copy16_to_lds(src + 256 * pc + 4 * ((lane ^ c) & 63), kbuf + c * DH + 256 * pc);
             }
-            float4 kA[4], qA, kB[4], qB;
-            auto load_seg = [&](int sg, float4 (&kk)[4], float4& qq) {
+            float4 vb0[NC], vb1[NC];
+            {
+                const uint32_t k0 = (uint32_t)__shfl((int)kap, g, 64), k1 = (uint32_t)__shfl((int)kap, 4 + g, 64);
+                const float* v0 = vbase + prow(k0) * row_stride + 4 * rl;
+                const float* v1 = vbase + prow(k1) * row_stride + 4 * rl;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) kk[i] = ld4(krow[i] + 16 * sg);
-                qq = ld4(qrow + 16 * sg);
-            };
-            float dot = 0.0f;
-            auto consume = [&](int sg, float4 (&kk)[4], float4& qq) {
-                wave_sync();
-#pragma unroll
-                for (int i = 0; i < 4; ++i) *reinterpret_cast<float4*>(kst + (16 * i + seg) * SR + 4 * part) = kk[i];
-                *reinterpret_cast<float4*>(qst + seg * SR + 4 * part) = qq;
-                if (sg + 2 < NSEG) load_seg(sg + 2, kk, qq);
-                wave_sync();
-                const float* kr = kst + lane * SR;
-                const float* qv = qst + rho * SR;
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * u);
-                    const float4 q4 = *reinterpret_cast<const float4*>(qv + 4 * u);
-                    dot = dot + q4.x * k4.x;
-                    dot = dot + q4.y * k4.y;
-                    dot = dot + q4.z * k4.z;
-                    dot = dot + q4.w * k4.w;
+                for (int c = 0; c < NC; ++c) {
+                    vb0[c] = ld4(v0 + 64 * c);
+                    vb1[c] = ld4(v1 + 64 * c);
                 }
-            };
-            load_seg(0, kA, qA);
-            load_seg(1, kB, qB);
-#pragma unroll 1
-            for (int sg = 0; sg < NSEG; sg += 2) {
-                consume(sg, kA, qA);
-                consume(sg + 1, kB, qB);
             }
-            const float delta = delta_and_l(base, has, rho, dot, e);
-            correct_o(base, delta, rho, kap);
+            wait_vm<0>();  // this wave's k-row copies (and V rows) have landed
+            // sequential dot of candidate j: k from its swizzled row, q row rho from qlds
+            const float* kr = kbuf + j * DH;
+            const float* qv = qlds + rho * QRS;
+            float dot = 0.0f;
+#pragma unroll 16
+            for (int d4 = 0; d4 < DH / 4; ++d4) {
+                const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * ((d4 & ~63) | ((d4 ^ j) & 63)));
+                const float4 q4 = *reinterpret_cast<const float4*>(qv + 4 * d4);
+                dot = dot + q4.x * k4.x;
+                dot = dot + q4.y * k4.y;
+                dot = dot + q4.z * k4.z;
+                dot = dot + q4.w * k4.w;
+            }
+            float delta = 0.0f;
+            if (has) {
+                const float m = my_m[rho];
+                delta = expf(dot * p.scale - m) - expf(my_s[e] - m);
+            }
+            const int nb = min(FB, cnt - base);
+            for (int i = 0; i < nb; ++i) {
+                const float di = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(delta), i));
+                const uint32_t ri = __builtin_amdgcn_readlane(rho, i);
+                if (lane == (int)ri) l_part += di;
+            }
+            apply_v(0, delta, rho, vb0);
+            if (nb > 4) apply_v(4, delta, rho, vb1);
+            wave_sync();  // the dot reads of kbuf are done before the next batch's copies
         }
         cnt = 0;
     };
@@ -898,11 +935,17 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         const float mo = mtab[(w ^ 4) * 16 + rl];  // the other parity's running maximum of row rl
         publish_m(fmaxf(m_run, mo));
     }
-    if (wave_valid) {
-        compact();
-        publish_m(m_ref);
-        flush_staged(smem + w * C::STAGE);
+    float* const qlds = smem + rb * 16 * C::QRS;
+    float* const kbuf = smem + 4 * 16 * C::QRS + w * C::FB * DH;
+    if (par == 0) {
+        // q row rl (query qw + rl/8, head rl%8) of this row block: lane (g, rl) holds dims 16t + 4g .. +3
+#pragma unroll
+        for (int t = 0; t < QT; ++t) *reinterpret_cast<float4*>(qlds + rl * C::QRS + 16 * t + 4 * g) = qr[t];
     }
+    if (wave_valid) compact();
+    publish_m(m_ref);
+    __syncthreads();  // the q rows are visible
+    if (wave_valid) flush_rows(qlds, kbuf);
     float l = l_part;
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
