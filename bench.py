@@ -180,6 +180,10 @@ def schedule_35_layers(ctx, steps, warmup):
     return {"us_per_token": ms * 1e3, "algorithmic_bytes": algo, "GB_s": algo / (ms * 1e-3) / 1e9}
 
 
+PREFILL_CONFIGS = [("configs[3a] prefill hd256 T2048 window512", 2048, 256, 512),
+                   ("configs[3b] prefill hd512 T2048 causal", 2048, 512, 0)]
+
+
 def prefill(ctx, T, Dh, window, steps, warmup):
     ins = synth.gemma_inputs(T=T, S=T, Dh=Dh, seed=3, q_pos=np.arange(T))
     q, k, v = ctx.upload(ins.q), ctx.upload(ins.k), ctx.upload(ins.v)
@@ -212,6 +216,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="headline decode only (no extras, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["prefill", "schedule"], default=None,
+                    help="run only these extra workloads (for profiling) and print their JSON line")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="first run 3 device-to-device copies of MIB MiB (the reference dispatch for "
                          "scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters to bytes)")
@@ -224,6 +230,18 @@ def main(argv=None):
     ctx = g4a.Context(0)
     info = ctx.device_info()
     print(f"[bench] device {info.arch.decode()} with {info.compute_units} CUs", file=sys.stderr, flush=True)
+
+    if args.only:
+        out = {}
+        if args.only == "prefill":
+            for name, T, Dh, W in PREFILL_CONFIGS:
+                out[name] = prefill(ctx, T, Dh, W, steps=args.steps, warmup=args.warmup)
+                print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
+        else:
+            out["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=args.steps, warmup=args.warmup)
+        ctx.close()
+        print(json.dumps({"only": args.only, "results": out}))
+        return 0
 
     if args.calibration_copy:
         n = args.calibration_copy << 20
@@ -298,8 +316,7 @@ def main(argv=None):
                 extras[name]["split_sweep_us"] = sweep
             d.free()
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
-        for name, T, Dh, W in [("configs[3a] prefill hd256 T2048 window512", 2048, 256, 512),
-                               ("configs[3b] prefill hd512 T2048 causal", 2048, 512, 0)]:
+        for name, T, Dh, W in PREFILL_CONFIGS:
             extras[name] = prefill(ctx, T, Dh, W, steps=5, warmup=2)
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
         extras["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=20, warmup=3)

@@ -16,21 +16,18 @@
 //
 // Work decomposition. A workgroup is 8 waves (512 threads) and owns one key
 // split of one (query, kv head); the host picks the split count so the grid
-// covers every CU (k_start/k_end already trimmed to the visible range). The
-// waves form KT key-tile slots of GROUP/2 waves, each wave owning 2 query
-// heads, and each slot walks 64-key tiles of the split. Per tile, a slot
-// streams DH/64 K chunks (64 keys x 64 dims) and DH/64 V chunks (64/(DH/64)
-// keys x DH dims) of 16 KiB each from HBM through registers into a
-// double-buffered LDS chunk, D chunks ahead, so K and V loads form one
-// continuous stream across phases and tiles:
-//   - scores: lane = key; the two heads' query rows sit in LDS and reach the
-//     multiplies through DPP row broadcasts (no scalar loads in the loop);
-//   - online softmax per head (wave max / exp / sum, lane = key);
-//   - P.V on the matrix cores (v_mfma_f32_4x4x1_16b_f32), probabilities
-//     broadcast from LDS.
-// At the end the slots' accumulators merge through LDS and the split's
-// (m, l, acc) partial is written, or the normalised output when there is a
-// single split; a separate combine kernel merges the partials (log-sum-exp).
+// covers every CU (k_start/k_end already trimmed to the visible range). K and
+// V stream from HBM straight into LDS with global->LDS copies
+// (global_load_lds_dwordx4), several chunks ahead of the one in use.
+//   - decode_wave (groups of 8 heads, Gemma-4's MQA): every wave streams its
+//     own 16-key wave tiles through a private LDS ring and never waits for
+//     another wave inside the loop; lane = (key, head pair) for the scores,
+//     lane = output dims for P.V (fused multiply-adds);
+//   - decode_split (groups of 4 heads): slots of waves share 64-key tiles
+//     through a common ring with a barrier per chunk; P.V on the matrix cores.
+// At the end the waves' partials merge through LDS and the split's (m, l, acc)
+// partial is written, or the normalised output when there is a single split;
+// a separate combine kernel merges the partials (log-sum-exp).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -150,22 +147,25 @@ __device__ __forceinline__ void qk_dims16(float (&s)[2], float q0, float q1, con
 
 template <int DH, int GROUP>
 struct DecodeCfg {
+    static constexpr int KCD = 64;                       // dims per K chunk (64 keys x KCD dims)
+    static constexpr int NCOL = KCD / 4;                 // 16-byte columns of a K chunk row
     static constexpr int HGW = GROUP / 2;                // waves per key-tile slot (2 heads each in the score phase)
     static constexpr int KT = 8 / HGW;                   // key-tile slots per 8-wave workgroup
     static constexpr int SLOT_THREADS = 64 * HGW;
-    static constexpr int LPT = 1024 / SLOT_THREADS;      // 16-byte copies per lane per 16 KiB chunk
-    static constexpr int NB = 8 / KT;                    // chunk buffers per slot (128 KiB ring in all)
+    static constexpr int LPT = 16 * KCD / SLOT_THREADS;  // 16-byte copies per lane per chunk
+    static constexpr int NB = (8 / KT) * (64 / KCD);     // chunk buffers per slot (128 KiB ring in all)
     static constexpr int AHEAD = NB - 1;                 // chunks in flight ahead of the one in use
-    static constexpr int NKS = DH / 64;                  // K chunks per tile: 64 keys x 64 dims
-    static constexpr int NVC = DH / 64;                  // V chunks per tile: KPC keys x DH dims
+    static constexpr int NKS = DH / KCD;                 // K chunks per tile: 64 keys x KCD dims
+    static constexpr int NVC = DH / KCD;                 // V chunks per tile: KPC keys x DH dims
     static constexpr int NCH = NKS + NVC;
     static constexpr int KPC = 64 / NVC;                 // keys per V chunk
-    static constexpr int BUF = 4096;                     // floats per chunk buffer (16 KiB)
+    static constexpr int BUF = 64 * KCD;                 // floats per chunk buffer
     static constexpr int WD = DH / HGW;                  // output dims per wave in the P.V phase
     static constexpr int NDG = WD / 64;                  // 64-dim MFMA groups per wave
-    static constexpr int NHQ = GROUP / 4;                // MFMA head quarters
+    static constexpr int NHQ = GROUP / 4;                // head quarters (4x4x1 P.V)
+    static constexpr int NACC = NHQ * NDG;               // 4-register accumulators per wave
     static constexpr int RING = KT * NB * BUF;
-    static constexpr int MERGE = (KT - 1) * HGW * NHQ * NDG * 256;  // slots 1.. hand their accumulators to slot 0
+    static constexpr int MERGE = (KT - 1) * HGW * NACC * 256;  // slots 1.. hand their accumulators to slot 0
     static constexpr int PBUF = KT * 64 * GROUP;
     static constexpr int QS = GROUP * DH;                // the kv group's query rows
     static constexpr int SMEM = RING + PBUF + KT * GROUP + KT * 2 * GROUP + QS;
@@ -242,11 +242,13 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
     static_assert(GROUP == 4 || GROUP == 8, "fast decode handles groups of 4 / 8 heads");
     using C = DecodeCfg<DH, GROUP>;
     constexpr int HGW = C::HGW, KT = C::KT, LPT = C::LPT, NB = C::NB, AHEAD = C::AHEAD, NKS = C::NKS,
-                  NCH = C::NCH, KPC = C::KPC, BUF = C::BUF, WD = C::WD, NDG = C::NDG, NHQ = C::NHQ;
+                  KCD = C::KCD, NCOL = C::NCOL,
+                  NCH = C::NCH, KPC = C::KPC, BUF = C::BUF, WD = C::WD, NDG = C::NDG, NHQ = C::NHQ,
+                  NACC = C::NACC;
 
     __shared__ __attribute__((aligned(16))) float smem[C::SMEM];
     float* const ring = smem;                     // [KT][NB][BUF]
-    float* const mrg = smem;                      // [KT-1][HGW][NHQ][NDG][4][64] after the tile loop
+    float* const mrg = smem;                      // [KT-1][HGW][NACC][4][64] after the tile loop
     float* const pbuf = smem + C::RING;           // [KT][64 keys][4][NHQ]
     float* const corrbuf = pbuf + C::PBUF;        // [KT][GROUP]
     float* const mlbuf = corrbuf + KT * GROUP;    // [KT][2][GROUP]
@@ -275,11 +277,10 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
     }
 
     float m[2] = {NEG_INF, NEG_INF}, lpart[2] = {0.0f, 0.0f};
-    f4v acc[NHQ][NDG];
+    // acc[NDG*hq + dg] register r of lane l is head 4*hq + r, dim g*WD + 64*dg + l.
+    f4v acc[NACC];
 #pragma unroll
-    for (int a = 0; a < NHQ; ++a)
-#pragma unroll
-        for (int b = 0; b < NDG; ++b) acc[a][b] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int a = 0; a < NACC; ++a) acc[a] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 
     const uint32_t ntiles = ke > ks ? (ke - ks + 63) / 64 : 0;
     const uint32_t niter = (ntiles + KT - 1) / KT;
@@ -324,9 +325,9 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
             const int sl = (i * HGW + g) * 64 + lane;
             const float* src;
             if (c < NKS) {
-                const int r = sl >> 4;
-                const int j = (sl & 15) ^ (r & 15);
-                src = T.kb + (size_t)prow(T, r) * row_stride + 64 * c + 4 * j;
+                const int r = sl / NCOL;
+                const int j = (sl % NCOL) ^ (r % NCOL);
+                src = T.kb + (size_t)prow(T, r) * row_stride + KCD * c + 4 * j;
             } else {
                 const int key = (c - NKS) * KPC + sl / (DH / 4);
                 src = T.vb + (size_t)prow(T, key) * row_stride + 4 * (sl % (DH / 4));
@@ -341,9 +342,9 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
 
     const float* const my_q = qs + 2 * g * DH;  // heads 2g, 2g+1
     // this lane's key row in a K chunk and its swizzled float4 columns
-    const float* kcol[16];
+    const float* kcol[NCOL];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) kcol[j] = my_ring + lane * 64 + 4 * (j ^ (lane & 15));
+    for (int j = 0; j < NCOL; ++j) kcol[j] = my_ring + lane * KCD + 4 * (j ^ (lane % NCOL));
 
     for (uint32_t it = 0; it < niter; ++it) {
         const bool last = it + 1 == niter;  // no copies beyond the last tile step
@@ -366,9 +367,9 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
                 // exact sequential dots, lane = key, heads 2g and 2g+1, dims 64c .. 64c+63;
                 // q comes from LDS, one value per lane of each 16-lane row, via DPP broadcast
 #pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const float q0 = my_q[64 * c + 16 * b + (lane & 15)];
-                    const float q1 = my_q[DH + 64 * c + 16 * b + (lane & 15)];
+                for (int b = 0; b < KCD / 16; ++b) {
+                    const float q0 = my_q[KCD * c + 16 * b + (lane & 15)];
+                    const float q1 = my_q[DH + KCD * c + 16 * b + (lane & 15)];
                     float4 k4[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) k4[i] = *reinterpret_cast<const float4*>(kcol[4 * b + i] + bi * BUF);
@@ -401,10 +402,10 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
                         const float* cb = corrbuf + kt * GROUP + hq * 4;
                         const f4v cr = f4v{cb[0], cb[1], cb[2], cb[3]};
 #pragma unroll
-                        for (int dg = 0; dg < NDG; ++dg) acc[hq][dg] *= cr;
+                        for (int dg = 0; dg < NDG; ++dg) acc[NDG * hq + dg] *= cr;
                     }
                 }
-                // P.V on the matrix cores (v_mfma_f32_4x4x1_16b_f32), one key per step:
+                // P.V on v_mfma_f32_4x4x1_16b_f32, one key per step:
                 // lane l gives A = P[key][4hq + l%4] and B = V[key][g*WD + 64dg + l];
                 // register r of the result is out[4hq + r][g*WD + 64dg + l]
 #pragma unroll
@@ -418,7 +419,8 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
                         const float vv = buf[kr * DH + g * WD + 64 * dg + lane];
 #pragma unroll
                         for (int hq = 0; hq < NHQ; ++hq)
-                            acc[hq][dg] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vv, acc[hq][dg], 0, 0, 0);
+                            acc[NDG * hq + dg] =
+                                __builtin_amdgcn_mfma_f32_4x4x1f32(a[hq], vv, acc[NDG * hq + dg], 0, 0, 0);
                     }
                 }
             }
@@ -438,52 +440,367 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
         }
     }
     __syncthreads();  // every wave is done with the chunk ring: the merge buffer overlays it
-    auto mslot = [&](int sl, int hq, int dg, int r) -> float* {
-        return mrg + (((((size_t)(sl - 1) * HGW + g) * NHQ + hq) * NDG + dg) * 4 + r) * 64 + lane;
+    auto mslot = [&](int sl, int a, int r) -> float* {
+        return mrg + ((((size_t)(sl - 1) * HGW + g) * NACC + a) * 4 + r) * 64 + lane;
     };
     if (kt > 0) {
 #pragma unroll
-        for (int hq = 0; hq < NHQ; ++hq)
+        for (int a = 0; a < NACC; ++a)
 #pragma unroll
-            for (int dg = 0; dg < NDG; ++dg)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) *mslot(kt, hq, dg, r) = acc[hq][dg][r];
+            for (int r = 0; r < 4; ++r) *mslot(kt, a, r) = acc[a][r];
     }
     __syncthreads();
-    if (kt == 0) {
+    if (kt != 0) return;
+    // head h of the kv group: M = max over slots, L = sum of l * e^(m - M), es = slot weights
+    auto head_stats = [&](int h, float& M, float& L, float (&es)[KT]) {
+        M = NEG_INF;
 #pragma unroll
-        for (int hq = 0; hq < NHQ; ++hq) {
+        for (int sl = 0; sl < KT; ++sl) M = fmaxf(M, mlbuf[sl * 2 * GROUP + h]);
+        L = 0.0f;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int h = 4 * hq + r;
-                float M = NEG_INF;
+        for (int sl = 0; sl < KT; ++sl) {
+            const float ms = mlbuf[sl * 2 * GROUP + h];
+            es[sl] = (ms == NEG_INF) ? 0.0f : expf(ms - M);
+            L += mlbuf[sl * 2 * GROUP + GROUP + h] * es[sl];
+        }
+    };
+    auto merged = [&](int a, int r, const float (&es)[KT]) -> float {
+        float o = acc[a][r] * es[0];
 #pragma unroll
-                for (int sl = 0; sl < KT; ++sl) M = fmaxf(M, mlbuf[sl * 2 * GROUP + h]);
-                float L = 0.0f, es[KT];
+        for (int sl = 1; sl < KT; ++sl) o += *mslot(sl, a, r) * es[sl];
+        return o;
+    };
+    auto write_ml = [&](size_t ih, float M, float L) {
+        float* ml = p.part + (size_t)p.T * p.Hq * p.nsplit * DH + (ih * p.nsplit + split) * 2;
+        ml[0] = M;
+        ml[1] = L;
+    };
 #pragma unroll
-                for (int sl = 0; sl < KT; ++sl) {
-                    const float ms = mlbuf[sl * 2 * GROUP + h];
-                    es[sl] = (ms == NEG_INF) ? 0.0f : expf(ms - M);
-                    L += mlbuf[sl * 2 * GROUP + GROUP + h] * es[sl];
+    for (int hq = 0; hq < NHQ; ++hq) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int h = 4 * hq + r;
+            float M, L, es[KT];
+            head_stats(h, M, L, es);
+            const size_t ih = (size_t)qi * p.Hq + h0 + h;
+            const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+#pragma unroll
+            for (int dg = 0; dg < NDG; ++dg) {
+                const float o = merged(NDG * hq + dg, r, es);
+                const int d = g * WD + 64 * dg + lane;
+                if (p.nsplit == 1) p.out[ih * DH + d] = o * inv;
+                else p.part[(ih * p.nsplit + split) * DH + d] = o;
+            }
+            if (p.nsplit > 1 && g == 0 && lane == 0) write_ml(ih, M, L);
+        }
+    }
+}
+
+// Per-wave streaming decode for groups of 8 query heads (Gemma-4's 8:1 MQA).
+// An 8-wave workgroup owns one key split of one (query, kv head), as in
+// decode_split, but its waves never synchronise inside the streaming loop:
+// wave w owns 16-key wave tiles t = 8*it + w of the split and streams their K
+// and V rows into a private LDS ring of NB 4 KiB chunks, AHEAD chunks ahead, so
+// each wave waits only for its own copies (vmcnt) and a slow wave delays
+// nobody. Per wave tile, DH/64 K chunks (16 keys x 64 dims, 16-byte columns
+// XOR-swizzled by key) then 16/KPC V chunks (KPC keys x DH dims):
+//   scores: lane l = (key l%16, head pair l/16): heads 2(l/16), 2(l/16)+1 of
+//           key l%16, the exact sequential dot of qk_dims16 (each 16-lane row
+//           broadcasts its own head pair's query values);
+//   softmax: online, per head, over the 16 keys of a row;
+//   P.V:    lane l owns dims 4l..4l+3 (+256 for DH 512) of all 8 heads, fused
+//           multiply-adds with the probabilities broadcast from LDS.
+// At the end the 8 wave partials (m, l, acc) merge through LDS (wave w merges
+// head w) into the split's partial, or the normalised output for one split.
+template <int DH>
+struct WaveCfg {
+    static constexpr int GROUP = 8;
+    static constexpr int KEYS = 16;                   // keys per wave tile
+    static constexpr int BUF = 1024;                  // floats per chunk buffer (4 KiB)
+    static constexpr int NB = 4;                      // chunk buffers per wave (16 KiB)
+    static constexpr int AHEAD = NB - 1;
+    static constexpr int LPT = BUF / 256;             // 16-byte copies per lane per chunk
+    static constexpr int NKS = DH / 64;               // K chunks per wave tile
+    static constexpr int KPC = BUF / DH;              // keys per V chunk
+    static constexpr int NVC = KEYS / KPC;            // V chunks per wave tile
+    static constexpr int NCH = NKS + NVC;
+    static constexpr int ND = DH / 256;               // float4 dim groups per lane in P.V
+    static constexpr int RING = 8 * NB * BUF;
+    static constexpr int MERGE = GROUP * DH;          // a wave's partial, in its own ring after the loop
+    static constexpr int QS = GROUP * DH;
+    static constexpr int PB = 8 * KEYS * GROUP;       // [wave][key][head]
+    static constexpr int SMEM = RING + QS + PB + 8 * GROUP + 8 * 2 * GROUP + 8;
+    static_assert(MERGE <= NB * BUF, "a wave's partial fits its ring");
+    static_assert(KPC * DH == BUF && KEYS % KPC == 0, "V chunks hold whole keys of the tile");
+    static_assert(QS % 2048 == 0, "the query rows are copied in 8 waves x 1 KiB copies");
+    static_assert(LPT * AHEAD + QS / 2048 < 64, "vmcnt immediate range");
+    static_assert(LPT * AHEAD <= 16, "tail waits go through wait_vm_upto16");
+};
+
+template <int DH, bool KPOS>
+__device__ __forceinline__ void decode_wave(const G4aDecodeParams& p) {
+    using C = WaveCfg<DH>;
+    constexpr int GROUP = C::GROUP, KEYS = C::KEYS, BUF = C::BUF, NB = C::NB, AHEAD = C::AHEAD, LPT = C::LPT,
+                  NKS = C::NKS, KPC = C::KPC, NCH = C::NCH, ND = C::ND;
+
+    __shared__ __attribute__((aligned(16))) float smem[C::SMEM];
+    float* const ring = smem;                   // [8 waves][NB][BUF]; after the loop wave w's
+                                                // [GROUP][DH] partial in its ring
+    float* const qs = smem + C::RING;           // [GROUP][DH]
+    float* const pbuf = qs + C::QS;             // [8 waves][KEYS][GROUP]
+    float* const corrbuf = pbuf + C::PB;        // [8 waves][GROUP]
+    float* const mlbuf = corrbuf + 8 * GROUP;   // [8 waves][2][GROUP]
+    int* const progress = reinterpret_cast<int*>(mlbuf + 8 * 2 * GROUP);  // [8 waves] chunk steps done
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int key = lane & 15;  // score phase: key of the wave tile
+    const int hp = lane >> 4;   // score phase: heads 2hp, 2hp+1
+    const uint32_t split = blockIdx.x, qi = blockIdx.y, kvh = blockIdx.z;
+    const uint32_t qpos = p.q_pos ? p.q_pos[qi] : p.q_pos0 + qi;
+    const uint32_t ks = p.k_start + split * p.keys_per_split;
+    const uint32_t ke = min(ks + p.keys_per_split, p.k_end);
+    const uint32_t h0 = kvh * GROUP;
+    const size_t row_stride = (size_t)p.Hkv * DH;
+    const float* __restrict__ kbase = p.k + (size_t)kvh * DH;
+    const float* __restrict__ vbase = p.v + (size_t)kvh * DH;
+    float* const my_ring = ring + w * NB * BUF;
+    float* const my_pbuf = pbuf + w * KEYS * GROUP;
+    float* const my_corr = corrbuf + w * GROUP;
+
+    // query rows: wave w copies 1 KiB pieces w, w + 8, ... (issued before any chunk)
+    {
+        const float* qsrc = p.q + ((size_t)qi * p.Hq + h0) * DH;
+#pragma unroll
+        for (int i = 0; i < C::QS / 2048; ++i)
+            copy16_to_lds(qsrc + 256 * (w + 8 * i) + 4 * lane, qs + 256 * (w + 8 * i));
+    }
+
+    const uint32_t ntiles = ke > ks ? (ke - ks + KEYS - 1) / KEYS : 0;
+    const uint32_t niter = (ntiles + 7) / 8;
+
+    // As in decode_split, every chunk step issues its copies (idle tiles copy the
+    // dummy buffer), so each wait count below is exact.
+    struct Tile {
+        uint32_t t0, row0, nk;
+        bool active;
+        const float* kb;
+        const float* vb;
+    };
+    auto tile_info = [&](uint32_t it) -> Tile {
+        Tile T;
+        const uint32_t t = it * 8 + w;
+        T.t0 = ks + t * KEYS;
+        T.active = it < niter && t < ntiles;
+        if (T.active) {
+            const uint32_t kpos_first = KPOS ? p.k_pos[T.t0] : p.k_pos0 + T.t0;
+            T.active = kpos_first <= qpos;  // ascending positions: a future first key means a future tile
+        }
+        T.nk = T.active ? min((uint32_t)KEYS, ke - T.t0) : 1u;
+        T.row0 = T.active ? phys_row(T.t0, p.ring_cap) : 0u;
+        T.kb = T.active ? kbase : p.dummy;
+        T.vb = T.active ? vbase : p.dummy;
+        return T;
+    };
+    auto prow = [&](const Tile& T, uint32_t r) -> uint32_t {  // physical row of tile key r, clamped to the tile
+        uint32_t x = T.row0 + min(r, T.nk - 1);
+        if (p.ring_cap && x >= p.ring_cap) x -= p.ring_cap;
+        return x;
+    };
+    // chunk c of a wave tile into ring buffer bi: K chunks c < NKS hold dims
+    // 64c..64c+63 of the 16 keys (key r's 16-byte column j at slot j ^ r), V chunks
+    // hold keys KPC*(c-NKS) .. +KPC-1, all DH dims. Lane l fills 16-byte slot 64i + l.
+    auto issue_chunk = [&](const Tile& T, int c, int bi) {
+        float* const dst = my_ring + bi * BUF;
+#pragma unroll
+        for (int i = 0; i < LPT; ++i) {
+            const int sl = 64 * i + lane;
+            const float* src;
+            if (c < NKS) {
+                const int r = sl >> 4;
+                const int j = (sl & 15) ^ r;
+                src = T.kb + (size_t)prow(T, r) * row_stride + 64 * c + 4 * j;
+            } else {
+                const int kr = (c - NKS) * KPC + sl / (DH / 4);
+                src = T.vb + (size_t)prow(T, kr) * row_stride + 4 * (sl % (DH / 4));
+            }
+            copy16_to_lds(src, dst + 256 * i);
+        }
+    };
+
+    Tile cur = tile_info(0);
+#pragma unroll
+    for (int c = 0; c < AHEAD; ++c) issue_chunk(cur, c, c);
+    if (lane == 0) progress[w] = -1;
+    wait_vm<LPT * AHEAD>();  // this wave's query pieces have landed
+    barrier_lds();           // ... and every wave's
+
+    const float* const q0row = qs + (2 * hp) * DH + key;      // head 2hp, dims d + key
+    const float* const q1row = qs + (2 * hp + 1) * DH + key;  // head 2hp + 1
+    const float* kcol[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) kcol[j] = my_ring + key * 64 + 4 * (j ^ key);
+
+    float m[2] = {NEG_INF, NEG_INF}, lpart[2] = {0.0f, 0.0f};
+    float4 acc[GROUP][ND];
+#pragma unroll
+    for (int h = 0; h < GROUP; ++h)
+#pragma unroll
+        for (int e = 0; e < ND; ++e) acc[h][e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+
+    for (uint32_t it = 0; it < niter; ++it) {
+        const bool last = it + 1 == niter;  // no copies beyond the last wave tile
+        const Tile nxt = tile_info(it + 1);
+        float s[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int bi = c % NB;
+            const float* const buf = my_ring + bi * BUF;
+            // this wave's reads of chunk c-1 are complete, so its buffer can be refilled
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (c + AHEAD < NCH) issue_chunk(cur, c + AHEAD, (c + AHEAD) % NB);
+            else if (!last) issue_chunk(nxt, c + AHEAD - NCH, (c + AHEAD) % NB);
+            // chunk c has landed: the copies issued after it are the next AHEAD chunks
+            // (fewer at the end of the last wave tile)
+            if (last && c + AHEAD >= NCH) wait_vm_upto16(LPT * (NCH - 1 - c));
+            else wait_vm<LPT * AHEAD>();
+            {
+                // The two waves sharing a SIMD (w and w ^ 4) would otherwise issue oldest
+                // first, starving the younger one: a wave behind its partner raises its
+                // issue priority until it catches up.
+                const int done = (int)(it * NCH) + c;
+                progress[w] = done;
+                const int other = __builtin_amdgcn_readfirstlane(progress[w ^ 4]);
+                if (other > done) __builtin_amdgcn_s_setprio(1);
+                else __builtin_amdgcn_s_setprio(0);
+            }
+            if (!cur.active) continue;
+            if (c < NKS) {
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const float q0 = q0row[64 * c + 16 * b];
+                    const float q1 = q1row[64 * c + 16 * b];
+                    float4 k4[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) k4[i] = ld4(kcol[4 * b + i] + bi * BUF);
+                    qk_dims16(s, q0, q1, k4);
                 }
-                const size_t ih = (size_t)qi * p.Hq + h0 + h;
-                const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+                if (c == NKS - 1) {
+                    // online softmax of heads 2hp, 2hp+1 over the row's 16 keys
+                    const uint32_t j = cur.t0 + min((uint32_t)key, cur.nk - 1);
+                    const uint32_t kp = KPOS ? p.k_pos[j] : p.k_pos0 + j;
+                    const bool vis =
+                        (uint32_t)key < cur.nk && kp <= qpos && (p.window == 0 || qpos - kp < p.window);
 #pragma unroll
-                for (int dg = 0; dg < NDG; ++dg) {
-                    float o = acc[hq][dg][r] * es[0];
+                    for (int h = 0; h < 2; ++h) {
+                        const float sc = vis ? score_epilogue(s[h], p.scale, p.softcap) : NEG_INF;
+                        float rm = sc;
 #pragma unroll
-                    for (int sl = 1; sl < KT; ++sl) o += *mslot(sl, hq, dg, r) * es[sl];
-                    const int d = g * WD + 64 * dg + lane;
-                    if (p.nsplit == 1) p.out[ih * DH + d] = o * inv;
-                    else p.part[(ih * p.nsplit + split) * DH + d] = o;
+                        for (int o = 8; o > 0; o >>= 1) rm = fmaxf(rm, __shfl_xor(rm, o, 64));
+                        const float mn = fmaxf(m[h], rm);
+                        const float corr = (m[h] == NEG_INF) ? 0.0f : expf(m[h] - mn);
+                        const float pr = (sc == NEG_INF) ? 0.0f : expf(sc - mn);
+                        lpart[h] = lpart[h] * corr + pr;
+                        m[h] = mn;
+                        my_pbuf[key * GROUP + 2 * hp + h] = pr;
+                        if (key == 0) my_corr[2 * hp + h] = corr;
+                    }
                 }
-                if (p.nsplit > 1 && g == 0 && lane == 0) {
-                    float* ml = p.part + (size_t)p.T * p.Hq * p.nsplit * DH + (ih * p.nsplit + split) * 2;
-                    ml[0] = M;
-                    ml[1] = L;
+            } else {
+                const int vc = c - NKS;
+                if (vc == 0) {
+                    // rescale the running output of every head by its correction factor
+                    const float4 c0 = ld4(my_corr), c1 = ld4(my_corr + 4);
+                    const float cr[GROUP] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+                    for (int h = 0; h < GROUP; ++h)
+#pragma unroll
+                        for (int e = 0; e < ND; ++e) {
+                            acc[h][e].x *= cr[h];
+                            acc[h][e].y *= cr[h];
+                            acc[h][e].z *= cr[h];
+                            acc[h][e].w *= cr[h];
+                        }
+                }
+#pragma unroll
+                for (int kr = 0; kr < KPC; ++kr) {
+                    const float* const prow8 = my_pbuf + (vc * KPC + kr) * GROUP;
+                    const float4 p0 = ld4(prow8), p1 = ld4(prow8 + 4);
+                    const float pk[GROUP] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+                    for (int e = 0; e < ND; ++e) {
+                        const float4 v4 = ld4(buf + kr * DH + 256 * e + 4 * lane);
+#pragma unroll
+                        for (int h = 0; h < GROUP; ++h) {
+                            acc[h][e].x = __builtin_fmaf(pk[h], v4.x, acc[h][e].x);
+                            acc[h][e].y = __builtin_fmaf(pk[h], v4.y, acc[h][e].y);
+                            acc[h][e].z = __builtin_fmaf(pk[h], v4.z, acc[h][e].z);
+                            acc[h][e].w = __builtin_fmaf(pk[h], v4.w, acc[h][e].w);
+                        }
+                    }
                 }
             }
         }
+        cur = nxt;
+    }
+
+    // The wave's partial goes into its own ring (free once its copies have landed),
+    // so no wave waits for another before writing.
+    __builtin_amdgcn_s_setprio(0);
+    wait_vm<0>();
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) lpart[h] += __shfl_xor(lpart[h], o, 64);
+    if (key == 0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            mlbuf[w * 2 * GROUP + 2 * hp + h] = m[h];
+            mlbuf[w * 2 * GROUP + GROUP + 2 * hp + h] = lpart[h];
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < GROUP; ++h)
+#pragma unroll
+        for (int e = 0; e < ND; ++e)
+            *reinterpret_cast<float4*>(my_ring + h * DH + 256 * e + 4 * lane) = acc[h][e];
+    __syncthreads();
+    // wave w merges head w: M = max over waves, L = sum of l * e^(m - M)
+    const int h = w;
+    float M = NEG_INF;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) M = fmaxf(M, mlbuf[x * 2 * GROUP + h]);
+    float L = 0.0f, es[8];
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+        const float mx = mlbuf[x * 2 * GROUP + h];
+        es[x] = (mx == NEG_INF) ? 0.0f : expf(mx - M);
+        L += mlbuf[x * 2 * GROUP + GROUP + h] * es[x];
+    }
+    const size_t ih = (size_t)qi * p.Hq + h0 + h;
+    const float sc = p.nsplit == 1 ? (L > 0.0f ? 1.0f / L : 0.0f) : 1.0f;
+    float* const dst = p.nsplit == 1 ? p.out + ih * DH : p.part + (ih * p.nsplit + split) * DH;
+#pragma unroll
+    for (int e = 0; e < ND; ++e) {
+        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+            const float4 a = ld4(ring + x * NB * BUF + h * DH + 256 * e + 4 * lane);
+            o.x += a.x * es[x];
+            o.y += a.y * es[x];
+            o.z += a.z * es[x];
+            o.w += a.w * es[x];
+        }
+        o.x *= sc;
+        o.y *= sc;
+        o.z *= sc;
+        o.w *= sc;
+        *reinterpret_cast<float4*>(dst + 256 * e + 4 * lane) = o;
+    }
+    if (p.nsplit > 1 && lane == 0) {
+        float* ml = p.part + (size_t)p.T * p.Hq * p.nsplit * DH + (ih * p.nsplit + split) * 2;
+        ml[0] = M;
+        ml[1] = L;
     }
 }
 
@@ -611,12 +928,12 @@ __device__ __forceinline__ void generic_attention(const G4aGenericParams& p) {
 }  // namespace
 
 extern "C" {
-__global__ __launch_bounds__(512) void g4a_decode_d256_g8(G4aDecodeParams p) { decode_split<256, 8, false>(p); }
-__global__ __launch_bounds__(512) void g4a_decode_d512_g8(G4aDecodeParams p) { decode_split<512, 8, false>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d256_g8(G4aDecodeParams p) { decode_wave<256, false>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d512_g8(G4aDecodeParams p) { decode_wave<512, false>(p); }
 __global__ __launch_bounds__(512) void g4a_decode_d256_g4(G4aDecodeParams p) { decode_split<256, 4, false>(p); }
 __global__ __launch_bounds__(512) void g4a_decode_d512_g4(G4aDecodeParams p) { decode_split<512, 4, false>(p); }
-__global__ __launch_bounds__(512) void g4a_decode_d256_g8_kpos(G4aDecodeParams p) { decode_split<256, 8, true>(p); }
-__global__ __launch_bounds__(512) void g4a_decode_d512_g8_kpos(G4aDecodeParams p) { decode_split<512, 8, true>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d256_g8_kpos(G4aDecodeParams p) { decode_wave<256, true>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d512_g8_kpos(G4aDecodeParams p) { decode_wave<512, true>(p); }
 __global__ __launch_bounds__(512) void g4a_decode_d256_g4_kpos(G4aDecodeParams p) { decode_split<256, 4, true>(p); }
 __global__ __launch_bounds__(512) void g4a_decode_d512_g4_kpos(G4aDecodeParams p) { decode_split<512, 4, true>(p); }
 __global__ __launch_bounds__(256) void g4a_combine_d256(G4aCombineParams p) { combine<256>(p); }
