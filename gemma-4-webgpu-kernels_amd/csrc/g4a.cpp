@@ -39,6 +39,7 @@ struct g4a_ctx {
     hipFunction_t combine[2] = {nullptr, nullptr};                          // [dh512]
     hipFunction_t generic = nullptr;
     hipFunction_t prefill[2] = {nullptr, nullptr};                          // [dh512]
+    hipFunction_t split_k = nullptr;  // K -> bf16 hi/lo rows for the head_dim 256 prefill
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     hipEvent_t ev_staging = nullptr;  // last use of the pinned staging buffer
     void* workspace = nullptr;
@@ -333,6 +334,7 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->generic, "g4a_generic_attention")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->prefill[0], "g4a_prefill2_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->prefill[1], "g4a_prefill_d512")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->split_k, "g4a_split_k_bf16")) return bail(rc);
     if (hipMalloc(reinterpret_cast<void**>(&ctx->dummy), 4096) != hipSuccess ||
         hipMemset(ctx->dummy, 0, 4096) != hipSuccess) {
         fail(ctx, G4A_E_NOMEM, "dummy buffer allocation failed");
@@ -467,8 +469,23 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
         pp.ring_cap = a->kv_ring_cap;
         pp.window = a->sliding_window;
         pp.scale = a->scale;
-        // head_dim 256: 8 waves (two key parities per 16-row block); 512: 4 waves
+        // head_dim 256: 8 waves (two key parities per 16-row block), scores estimated from
+        // bf16 hi/lo splits of K made by a pre-pass into the workspace; 512: 4 waves
         const bool d512 = a->Dh == 512;
+        if (!d512) {
+            const uint32_t nkeys = pl.k_end - pl.k_start;
+            const size_t bytes = size_t(nkeys) * a->Hkv * a->Dh * sizeof(float);
+            if (int rc = ensure_workspace(ctx, bytes)) return rc;
+            G4aSplitParams sp{a->k, static_cast<float*>(ctx->workspace), pl.k_start, nkeys, a->Hkv, a->Dh,
+                              a->kv_ring_cap};
+            const uint64_t threads = uint64_t(nkeys) * a->Hkv * (a->Dh / 8);
+            if (int rc = launch(ctx, ctx->split_k, dim3(uint32_t((threads + 255) / 256), 1, 1), dim3(256, 1, 1), sp,
+                                "split K"))
+                return rc;
+            pp.ksplit = static_cast<const float*>(ctx->workspace);
+            pp.ksplit0 = pl.k_start;
+            pp.ksplit_n = nkeys;
+        }
         return launch(ctx, ctx->prefill[d512 ? 1 : 0], dim3((a->T + 7) / 8, a->Hkv, 1), dim3(d512 ? 256 : 512, 1, 1),
                       pp, "prefill", true);
     }

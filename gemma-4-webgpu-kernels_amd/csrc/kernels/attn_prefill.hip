@@ -28,7 +28,8 @@
 
 namespace {
 
-constexpr float PF_TAU = 6.0f;
+constexpr float PF_TAU = 6.0f;     // rescoring band of the f32 matrix-core scores (head_dim 512)
+constexpr float PF_TAU_BF = 7.0f;  // rescoring band of the split-bf16 scores (head_dim 256)
 constexpr float PF_RESCALE = 8.0f;  // e^8 ~ 3e3: probability headroom before O and l are rescaled
 
 template <int DH>
@@ -537,6 +538,38 @@ __device__ __forceinline__ void prefill(const G4aPrefillParams& p) {
 // step both tiles sit in LDS (register-staged prefetch of the next pair). At
 // the end each wave compacts its candidates against the maximum over both
 // parities, corrects them exactly, and the parities merge through LDS.
+typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
+
+// x = hi + lo + O(2^-16 |x|): hi = bf16(x), lo = bf16(x - hi), both rounded to nearest even.
+__device__ __forceinline__ void split8(const float4& x0, const float4& x1, bf8v& hi, bf8v& lo) {
+    const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        hi[i] = (__bf16)x[i];
+        lo[i] = (__bf16)(x[i] - (float)hi[i]);
+    }
+}
+
+// K rows -> bf16 hi/lo pairs (the G4aSplitParams layout), one thread per 8-dim block.
+__device__ __forceinline__ void split_k(const G4aSplitParams& p) {
+    const uint32_t nb = p.Dh / 8;
+    const size_t total = (size_t)p.nkeys * p.Hkv * nb;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const uint32_t b = (uint32_t)(i % nb);
+    const size_t rh = i / nb;
+    const uint32_t h = (uint32_t)(rh % p.Hkv);
+    const size_t jj = rh / p.Hkv;
+    const uint32_t j = p.k0 + (uint32_t)jj;
+    const size_t row = p.ring_cap ? j % p.ring_cap : j;
+    const float* src = p.k + (row * p.Hkv + h) * p.Dh + 8 * b;
+    bf8v hi, lo;
+    split8(ld4(src), ld4(src + 4), hi, lo);
+    float* dst = p.out + (jj * p.Hkv + h) * p.Dh + 8 * b;
+    *reinterpret_cast<bf8v*>(dst) = hi;
+    *reinterpret_cast<bf8v*>(dst + 4) = lo;
+}
+
 template <int DH>
 struct PairCfg {
     static constexpr int BK = 16;
@@ -549,8 +582,7 @@ struct PairCfg {
     static constexpr int SR = 20;                            // staged row stride (floats): 16 dims + pad
     static constexpr int STAGE = (64 + 16) * SR;             // per-wave staging floats (in-loop overflow path)
     static constexpr int QRS = DH + 4;                       // q row stride in the end-of-kernel LDS copy
-    static constexpr int FB = 8;                             // candidates per end-of-kernel batch
-    static constexpr int FLUSH = 4 * 16 * QRS + 8 * FB * DH; // q rows of the 4 row blocks + each wave's k rows
+    static constexpr int FLUSH = 4 * 16 * QRS;               // q rows of the 4 row blocks
     static constexpr int MERGE = 4 * (NC * 16 * 64 + 2 * 64);  // odd-parity O, l, m of the 4 row blocks
     static constexpr int BIG00 = 4 * TILE > 8 * STAGE ? 4 * TILE : 8 * STAGE;  // two tile pairs in flight
     static constexpr int BIG0 = BIG00 > FLUSH ? BIG00 : FLUSH;
@@ -603,17 +635,21 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
     const uint32_t myq = qw + (rl >> 3);
     const bool qvalid = myq < p.T;
     const int32_t my_lo = key_lo(myq), my_hi = qvalid ? key_hi(myq) : 0;
-    float4 qr[QT];
+    // q rows in the B layout of v_mfma_f32_16x16x32_bf16, split into bf16 hi/lo:
+    // lane (g, rl) holds row rl's dims 32kb + 8g .. +7
+    constexpr int QB = DH / 32;
+    bf8v qh[QB], ql[QB];
     {
-        const float* qrow = p.q + ((size_t)min(myq, p.T - 1) * p.Hq + h0 + (rl & 7)) * DH + 4 * g;
+        const float* qrow = p.q + ((size_t)min(myq, p.T - 1) * p.Hq + h0 + (rl & 7)) * DH + 8 * g;
 #pragma unroll
-        for (int t = 0; t < QT; ++t) qr[t] = ld4(qrow + 16 * t);
+        for (int kb = 0; kb < QB; ++kb) split8(ld4(qrow + 32 * kb), ld4(qrow + 32 * kb + 4), qh[kb], ql[kb]);
     }
+    const float* __restrict__ ksbase = p.ksplit + (size_t)kvh * DH;
 
     // Tile pair of step st (tiles 2st and 2st+1) goes to ring slot st&1, each
-    // tile K (16 rows of KRS floats) then V (16 rows of DH), with global->LDS
-    // row copies: 64 rows of DH floats per pair, RPW 1 KiB copies per wave.
-    // Keys past the last visible key re-read it.
+    // tile K (16 split rows of KRS 4-byte slots) then V (16 rows of DH floats),
+    // with global->LDS row copies: 64 rows of DH slots per pair, RPW 1 KiB
+    // copies per wave. Keys past the last visible key re-read it.
     auto issue_pair = [&](uint32_t st) {
         float* const slot = smem + (st & 1) * 2 * C::TILE;
 #pragma unroll
@@ -622,7 +658,10 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
             const int row = idx / (DH / 256), piece = idx % (DH / 256);
             const int tsel = row / (2 * BK), isv = (row / BK) & 1, kf = row % BK;
             const uint32_t key = min((uint32_t)wg_lo + (2 * st + tsel) * BK + kf, (uint32_t)wg_hi - 1u);
-            const float* src = (isv ? vbase : kbase) + prow(key) * row_stride + 256 * piece + 4 * lane;
+            // K rows come from the split copy (row key - ksplit0), V rows from the cache
+            const uint32_t ks = min(max(key, p.ksplit0) - p.ksplit0, p.ksplit_n - 1u);
+            const float* src = isv ? vbase + prow(key) * row_stride + 256 * piece + 4 * lane
+                                   : ksbase + (size_t)ks * row_stride + 256 * piece + 4 * lane;
             float* dst = slot + tsel * C::TILE + (isv ? BK * KRS + kf * DH : kf * KRS) + 256 * piece;
             copy16_to_lds(src, dst);
         }
@@ -647,7 +686,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
             const bool has = e < cnt;
             const uint32_t pk = has ? my_keys[e] : 0u;
             const float sa = has ? my_s[e] : 0.0f;
-            const bool keep = has && sa > my_m[pk >> 28] - PF_TAU;
+            const bool keep = has && sa > my_m[pk >> 28] - PF_TAU_BF;
             wave_sync();
             const uint64_t b = ballot(keep);
             if (keep) {
@@ -766,70 +805,48 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         }
         cnt = 0;
     };
-    // End-of-kernel form, FB candidates per batch. The q rows of the wave's
-    // row block already sit in LDS (copied from registers, qlds); per batch
-    // the FB candidates' k rows are copied to the wave's LDS area (one 1 KiB
-    // global->LDS row copy each, 16-byte columns XOR-swizzled by the slot so
-    // the lanes' reads hit distinct banks) while their V rows load into
-    // registers, so a batch costs one memory round trip. Lanes j (and their
-    // replicas j + 8i) run candidate j's sequential dot; Delta V takes two
-    // 16x16x4 K-steps (candidates 0-3, 4-7).
-    auto flush_rows = [&](const float* qlds, float* kbuf) {
-        constexpr int FB = C::FB, QRS = C::QRS;
-        static_assert(FB == 8 && DH % 256 == 0, "batch layout");
-        const int j = lane & 7;
-        for (int base = 0; base < cnt; base += FB) {
-            const int e = base + j;
+    // End-of-kernel form, one candidate per lane (64 per batch). Lane e runs
+    // candidate e's sequential dot: its q row from LDS (qlds, copied from the
+    // registers), its k row straight from memory (the keys of this workgroup
+    // were just streamed, so they sit in L2), 64 dims per register chunk with
+    // the next chunk already loading. Delta V then goes through correct_o4.
+    auto flush_rows = [&](const float* qlds) {
+        constexpr int QRS = C::QRS, NCH = DH / 64;
+        static_assert(NCH % 2 == 0, "chunks are processed in pairs");
+        for (int base = 0; base < cnt; base += 64) {
+            const int e = base + lane;
             const bool has = e < cnt;
             const uint32_t pk = has ? my_keys[e] : 0u;
             const uint32_t rho = pk >> 28, kap = has ? (pk & 0x0fffffffu) : (uint32_t)wg_lo;
+            const float* const krow = kbase + prow(kap) * row_stride;
+            const float* const qv = qlds + rho * QRS;
+            float4 kA[16], kB[16];
+            auto load_chunk = [&](int ch, float4 (&kc)[16]) {
 #pragma unroll
-            for (int c = 0; c < FB; ++c) {
-                const uint32_t kc = (uint32_t)__builtin_amdgcn_readlane((int)kap, c);
-                const float* src = kbase + prow(kc) * row_stride;
-#pragma unroll
-                for (int pc = 0; pc < DH / 256; ++pc)
-                    copy16_to_lds(src + 256 * pc + 4 * ((lane ^ c) & 63), kbuf + c * DH + 256 * pc);
-            }
-            float4 vb0[NC], vb1[NC];
-            {
-                const uint32_t k0 = (uint32_t)__shfl((int)kap, g, 64), k1 = (uint32_t)__shfl((int)kap, 4 + g, 64);
-                const float* v0 = vbase + prow(k0) * row_stride + 4 * rl;
-                const float* v1 = vbase + prow(k1) * row_stride + 4 * rl;
-#pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    vb0[c] = ld4(v0 + 64 * c);
-                    vb1[c] = ld4(v1 + 64 * c);
-                }
-            }
-            wait_vm<0>();  // this wave's k-row copies (and V rows) have landed
-            // sequential dot of candidate j: k from its swizzled row, q row rho from qlds
-            const float* kr = kbuf + j * DH;
-            const float* qv = qlds + rho * QRS;
+                for (int u = 0; u < 16; ++u) kc[u] = ld4(krow + 64 * ch + 4 * u);
+            };
             float dot = 0.0f;
-#pragma unroll 16
-            for (int d4 = 0; d4 < DH / 4; ++d4) {
-                const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * ((d4 & ~63) | ((d4 ^ j) & 63)));
-                const float4 q4 = *reinterpret_cast<const float4*>(qv + 4 * d4);
-                dot = dot + q4.x * k4.x;
-                dot = dot + q4.y * k4.y;
-                dot = dot + q4.z * k4.z;
-                dot = dot + q4.w * k4.w;
+            auto dot_chunk = [&](int ch, const float4 (&kc)[16]) {
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const float4 q4 = *reinterpret_cast<const float4*>(qv + 64 * ch + 4 * u);
+                    dot = dot + q4.x * kc[u].x;
+                    dot = dot + q4.y * kc[u].y;
+                    dot = dot + q4.z * kc[u].z;
+                    dot = dot + q4.w * kc[u].w;
+                }
+            };
+            load_chunk(0, kA);
+            load_chunk(1, kB);
+#pragma unroll
+            for (int ch = 0; ch < NCH; ch += 2) {
+                dot_chunk(ch, kA);
+                if (ch + 2 < NCH) load_chunk(ch + 2, kA);
+                dot_chunk(ch + 1, kB);
+                if (ch + 3 < NCH) load_chunk(ch + 3, kB);
             }
-            float delta = 0.0f;
-            if (has) {
-                const float m = my_m[rho];
-                delta = expf(dot * p.scale - m) - expf(my_s[e] - m);
-            }
-            const int nb = min(FB, cnt - base);
-            for (int i = 0; i < nb; ++i) {
-                const float di = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(delta), i));
-                const uint32_t ri = __builtin_amdgcn_readlane(rho, i);
-                if (lane == (int)ri) l_part += di;
-            }
-            apply_v(0, delta, rho, vb0);
-            if (nb > 4) apply_v(4, delta, rho, vb1);
-            wave_sync();  // the dot reads of kbuf are done before the next batch's copies
+            const float delta = delta_and_l(base, has, rho, dot, e);
+            correct_o4(base, delta, rho, kap);
         }
         cnt = 0;
     };
@@ -845,16 +862,22 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         const float* Kt = smem + (st & 1) * 2 * C::TILE + par * C::TILE;
         const float* Vt = Kt + BK * KRS;
 
-        f4v S = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-        const float* kr = Kt + rl * KRS + 4 * g;
+        // score estimate S^T = K Q^T from the bf16 splits: Khi Qhi + Klo Qhi + Khi Qlo
+        // (error ~2^-16 relative per term), three independent accumulators.
+        // Lane (g, rl) reads key rl's 8-dim block 4kb + g: hi then lo, 16 bytes each.
+        f4v SA[3];
 #pragma unroll
-        for (int tt = 0; tt < QT; ++tt) {
-            const float4 kk = *reinterpret_cast<const float4*>(kr + 16 * tt);
-            S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.x, qr[tt].x, S, 0, 0, 0);
-            S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.y, qr[tt].y, S, 0, 0, 0);
-            S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, qr[tt].z, S, 0, 0, 0);
-            S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, qr[tt].w, S, 0, 0, 0);
+        for (int a = 0; a < 3; ++a) SA[a] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+        const float* kr = Kt + rl * KRS + 8 * g;
+#pragma unroll
+        for (int kb = 0; kb < QB; ++kb) {
+            const bf8v khi = *reinterpret_cast<const bf8v*>(kr + 32 * kb);
+            const bf8v klo = *reinterpret_cast<const bf8v*>(kr + 32 * kb + 4);
+            SA[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qh[kb], SA[0], 0, 0, 0);
+            SA[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, qh[kb], SA[1], 0, 0, 0);
+            SA[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, ql[kb], SA[2], 0, 0, 0);
         }
+        const f4v S = (SA[0] + SA[1]) + SA[2];
         float s[4];
         bool vis[4];
 #pragma unroll
@@ -874,7 +897,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         int nnew = 0;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            cand[r] = vis[r] && s[r] > mn - PF_TAU;
+            cand[r] = vis[r] && s[r] > mn - PF_TAU_BF;
             bal[r] = ballot(cand[r]);
             nnew += __builtin_popcountll(bal[r]);
         }
@@ -936,16 +959,17 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         publish_m(fmaxf(m_run, mo));
     }
     float* const qlds = smem + rb * 16 * C::QRS;
-    float* const kbuf = smem + 4 * 16 * C::QRS + w * C::FB * DH;
     if (par == 0) {
-        // q row rl (query qw + rl/8, head rl%8) of this row block: lane (g, rl) holds dims 16t + 4g .. +3
+        // the f32 q rows of this row block (row rl: query qw + rl/8, head rl%8), from memory
+        const float* qrow = p.q + ((size_t)min(myq, p.T - 1) * p.Hq + h0 + (rl & 7)) * DH + 4 * g;
 #pragma unroll
-        for (int t = 0; t < QT; ++t) *reinterpret_cast<float4*>(qlds + rl * C::QRS + 16 * t + 4 * g) = qr[t];
+        for (int t = 0; t < QT; ++t)
+            *reinterpret_cast<float4*>(qlds + rl * C::QRS + 16 * t + 4 * g) = ld4(qrow + 16 * t);
     }
     if (wave_valid) compact();
     publish_m(m_ref);
     __syncthreads();  // the q rows are visible
-    if (wave_valid) flush_rows(qlds, kbuf);
+    if (wave_valid) flush_rows(qlds);
     float l = l_part;
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
@@ -1004,4 +1028,5 @@ extern "C" {
 __global__ __launch_bounds__(256) void g4a_prefill_d256(G4aPrefillParams p) { prefill<256>(p); }
 __global__ __launch_bounds__(256) void g4a_prefill_d512(G4aPrefillParams p) { prefill<512>(p); }
 __global__ __launch_bounds__(512) void g4a_prefill2_d256(G4aPrefillParams p) { prefill_pair<256>(p); }
+__global__ __launch_bounds__(256) void g4a_split_k_bf16(G4aSplitParams p) { split_k(p); }
 }

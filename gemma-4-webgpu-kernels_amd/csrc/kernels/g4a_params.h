@@ -62,8 +62,22 @@ struct G4aPrefillParams {
     const float* k;        // [rows, Hkv, Dh]
     const float* v;        // [rows, Hkv, Dh]
     float* out;            // [T, Hq*Dh]
+    const float* ksplit;   // head_dim 256: keys ksplit0.. as bf16 hi/lo pairs (g4a_split_k_bf16 layout)
     uint32_t T, S, Hq, Hkv;
     uint32_t q_pos0, k_pos0;
     uint32_t ring_cap, window;
+    uint32_t ksplit0, ksplit_n;
     float scale;
+};
+
+// K rows split into bf16 pairs for the matrix-core score estimate: key j of
+// [k0, k0 + nkeys) (logical, read through the ring) becomes row j - k0 of
+// `out`, same row stride as k (Hkv * Dh 4-byte slots); each 8-dim block of a
+// head occupies 8 slots: the 8 bf16 hi parts, then the 8 bf16 lo parts, with
+// hi = bf16(x) and lo = bf16(x - hi), both rounded to nearest even.
+struct G4aSplitParams {
+    const float* k;        // [rows, Hkv, Dh]
+    float* out;            // [nkeys, Hkv, Dh] slots
+    uint32_t k0, nkeys, Hkv, Dh;
+    uint32_t ring_cap;
 };
