@@ -725,10 +725,13 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) vb[c] = ld4(vrow + 64 * c);
     };
-    auto apply_v = [&](int s4, float delta, uint32_t rho, const float4 (&vb)[NC]) {
+    // With lc, the same A (Delta of 4 candidates by row) times a block of ones also
+    // accumulates each row's l correction: lc register r of lane (g, rl) is row 4g + r.
+    auto apply_v = [&](int s4, float delta, uint32_t rho, const float4 (&vb)[NC], f4v* lc) {
         const float dl = __shfl(delta, s4 + g, 64);
         const uint32_t rr = (uint32_t)__shfl((int)rho, s4 + g, 64);
         const float a = rr == (uint32_t)rl ? dl : 0.0f;
+        if (lc) *lc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, 1.0f, *lc, 0, 0, 0);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].x, O[c][0], 0, 0, 0);
@@ -743,7 +746,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         float4 vA[NC], vB[NC];
         auto step = [&](int s4, float4 (&vb)[NC]) {
             if (s4 < nb) {
-                apply_v(s4, delta, rho, vb);
+                apply_v(s4, delta, rho, vb, nullptr);
                 if (s4 + 8 < nb) load_v(s4 + 8, kap, vb);
             }
         };
@@ -754,13 +757,13 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
             step(s4 + 4, vB);
         }
     };
-    auto correct_o4 = [&](int base, float delta, uint32_t rho, uint32_t kap) {
+    auto correct_o4 = [&](int base, float delta, uint32_t rho, uint32_t kap, f4v* lc) {
         __builtin_amdgcn_sched_barrier(0);
         const int nb = min(64, cnt - base);
         float4 vA[NC], vB[NC], vC[NC], vD[NC];
         auto step = [&](int s4, float4 (&vb)[NC]) {
             if (s4 < nb) {
-                apply_v(s4, delta, rho, vb);
+                apply_v(s4, delta, rho, vb, lc);
                 if (s4 + 16 < nb) load_v(s4 + 16, kap, vb);
             }
         };
@@ -845,8 +848,20 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
                 dot_chunk(ch + 1, kB);
                 if (ch + 3 < NCH) load_chunk(ch + 3, kB);
             }
-            const float delta = delta_and_l(base, has, rho, dot, e);
-            correct_o4(base, delta, rho, kap);
+            float delta = 0.0f;
+            if (has) {
+                const float m = my_m[rho];
+                delta = expf(dot * p.scale - m) - expf(my_s[e] - m);
+            }
+            f4v lc = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+            correct_o4(base, delta, rho, kap, &lc);
+            // row rl's l correction sits in register rl%4 of lanes 16*(rl/4) ..; lanes g == 0 own l
+            const int src = 16 * (rl >> 2);
+            const float c0 = __shfl(lc[0], src, 64), c1 = __shfl(lc[1], src, 64);
+            const float c2 = __shfl(lc[2], src, 64), c3 = __shfl(lc[3], src, 64);
+            const int rr = rl & 3;
+            const float cl = rr == 0 ? c0 : (rr == 1 ? c1 : (rr == 2 ? c2 : c3));
+            if (g == 0) l_part += cl;
         }
         cnt = 0;
     };
