@@ -967,6 +967,14 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
 
     // ---- end: compact against the maximum over both parities, correct, merge ----
     wait_vm<0>();
+    // the f32 q rows of this row block (row rl: query qw + rl/8, head rl%8) for the
+    // exact rescoring load from memory while the lists are compacted
+    float4 qf[QT];
+    if (par == 0) {
+        const float* qrow = p.q + ((size_t)min(myq, p.T - 1) * p.Hq + h0 + (rl & 7)) * DH + 4 * g;
+#pragma unroll
+        for (int t = 0; t < QT; ++t) qf[t] = ld4(qrow + 16 * t);
+    }
     publish_m(m_run);
     __syncthreads();  // tile buffers free; both parities' maxima published
     {
@@ -974,14 +982,11 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         publish_m(fmaxf(m_run, mo));
     }
     float* const qlds = smem + rb * 16 * C::QRS;
-    if (par == 0) {
-        // the f32 q rows of this row block (row rl: query qw + rl/8, head rl%8), from memory
-        const float* qrow = p.q + ((size_t)min(myq, p.T - 1) * p.Hq + h0 + (rl & 7)) * DH + 4 * g;
-#pragma unroll
-        for (int t = 0; t < QT; ++t)
-            *reinterpret_cast<float4*>(qlds + rl * C::QRS + 16 * t + 4 * g) = ld4(qrow + 16 * t);
-    }
     if (wave_valid) compact();
+    if (par == 0) {
+#pragma unroll
+        for (int t = 0; t < QT; ++t) *reinterpret_cast<float4*>(qlds + rl * C::QRS + 16 * t + 4 * g) = qf[t];
+    }
     publish_m(m_ref);
     __syncthreads();  // the q rows are visible
     if (wave_valid) flush_rows(qlds);
