@@ -39,7 +39,8 @@ struct g4a_ctx {
     hipFunction_t combine[2] = {nullptr, nullptr};                          // [dh512]
     hipFunction_t generic = nullptr;
     hipFunction_t prefill[2] = {nullptr, nullptr};                          // [dh512]
-    hipFunction_t split_k = nullptr;  // K -> bf16 hi/lo rows for the head_dim 256 prefill
+    hipFunction_t split_kv = nullptr;  // K/V pre-split for the head_dim 256 prefill
+    uint32_t split_epoch = 0;          // tags each pre-split's V range flag
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     hipEvent_t ev_staging = nullptr;  // last use of the pinned staging buffer
     void* workspace = nullptr;
@@ -334,7 +335,7 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->generic, "g4a_generic_attention")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->prefill[0], "g4a_prefill2_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->prefill[1], "g4a_prefill_d512")) return bail(rc);
-    if (int rc = get_fn(ctx, &ctx->split_k, "g4a_split_k_bf16")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->split_kv, "g4a_split_kv")) return bail(rc);
     if (hipMalloc(reinterpret_cast<void**>(&ctx->dummy), 4096) != hipSuccess ||
         hipMemset(ctx->dummy, 0, 4096) != hipSuccess) {
         fail(ctx, G4A_E_NOMEM, "dummy buffer allocation failed");
@@ -473,18 +474,36 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
         // bf16 hi/lo splits of K made by a pre-pass into the workspace; 512: 4 waves
         const bool d512 = a->Dh == 512;
         if (!d512) {
-            const uint32_t nkeys = pl.k_end - pl.k_start;
-            const size_t bytes = size_t(nkeys) * a->Hkv * a->Dh * sizeof(float);
-            if (int rc = ensure_workspace(ctx, bytes)) return rc;
-            G4aSplitParams sp{a->k, static_cast<float*>(ctx->workspace), pl.k_start, nkeys, a->Hkv, a->Dh,
-                              a->kv_ring_cap};
-            const uint64_t threads = uint64_t(nkeys) * a->Hkv * (a->Dh / 8);
-            if (int rc = launch(ctx, ctx->split_k, dim3(uint32_t((threads + 255) / 256), 1, 1), dim3(256, 1, 1), sp,
-                                "split K"))
+            // keys [k_start, k_end) widened to multiples of 16 (the kernel's tile grid);
+            // workspace: the V range flag (first 256 bytes), then the K and V splits
+            const uint32_t k0 = pl.k_start & ~15u, nkeys = ((pl.k_end + 15u) & ~15u) - k0;
+            const size_t half = size_t(nkeys) * a->Hkv * a->Dh * sizeof(float);
+            if (int rc = ensure_workspace(ctx, 256 + 2 * half)) return rc;
+            char* const ws = static_cast<char*>(ctx->workspace);
+            if (++ctx->split_epoch == 0) ctx->split_epoch = 1;
+            G4aSplitParams sp{};
+            sp.k = a->k;
+            sp.v = a->v;
+            sp.kout = reinterpret_cast<float*>(ws + 256);
+            sp.vout = reinterpret_cast<float*>(ws + 256 + half);
+            sp.vflag = reinterpret_cast<uint32_t*>(ws);
+            sp.k0 = k0;
+            sp.nkeys = nkeys;
+            sp.S = a->S;
+            sp.Hkv = a->Hkv;
+            sp.Dh = a->Dh;
+            sp.ring_cap = a->kv_ring_cap;
+            sp.epoch = ctx->split_epoch;
+            const uint64_t threads = uint64_t(nkeys) * a->Hkv * (a->Dh / 8) + uint64_t(nkeys / 4) * a->Hkv * (a->Dh / 64) * 16;
+            if (int rc = launch(ctx, ctx->split_kv, dim3(uint32_t((threads + 255) / 256), 1, 1), dim3(256, 1, 1), sp,
+                                "split K/V"))
                 return rc;
-            pp.ksplit = static_cast<const float*>(ctx->workspace);
-            pp.ksplit0 = pl.k_start;
-            pp.ksplit_n = nkeys;
+            pp.ksplit = sp.kout;
+            pp.vsplit = sp.vout;
+            pp.vflag = sp.vflag;
+            pp.split0 = k0;
+            pp.split_n = nkeys;
+            pp.epoch = sp.epoch;
         }
         return launch(ctx, ctx->prefill[d512 ? 1 : 0], dim3((a->T + 7) / 8, a->Hkv, 1), dim3(d512 ? 256 : 512, 1, 1),
                       pp, "prefill", true);

@@ -550,24 +550,69 @@ __device__ __forceinline__ void split8(const float4& x0, const float4& x1, bf8v&
     }
 }
 
-// K rows -> bf16 hi/lo pairs (the G4aSplitParams layout), one thread per 8-dim block.
-__device__ __forceinline__ void split_k(const G4aSplitParams& p) {
-    const uint32_t nb = p.Dh / 8;
-    const size_t total = (size_t)p.nkeys * p.Hkv * nb;
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= total) return;
-    const uint32_t b = (uint32_t)(i % nb);
-    const size_t rh = i / nb;
-    const uint32_t h = (uint32_t)(rh % p.Hkv);
-    const size_t jj = rh / p.Hkv;
-    const uint32_t j = p.k0 + (uint32_t)jj;
-    const size_t row = p.ring_cap ? j % p.ring_cap : j;
-    const float* src = p.k + (row * p.Hkv + h) * p.Dh + 8 * b;
-    bf8v hi, lo;
-    split8(ld4(src), ld4(src + 4), hi, lo);
-    float* dst = p.out + (jj * p.Hkv + h) * p.Dh + 8 * b;
-    *reinterpret_cast<bf8v*>(dst) = hi;
-    *reinterpret_cast<bf8v*>(dst + 4) = lo;
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+
+// x = hi + lo + O(2^-22 |x|) (for |x| >= 2^-3; below, an absolute 2^-25):
+// hi = fp16(x), lo = fp16(x - hi), both rounded to nearest even.
+__device__ __forceinline__ void split16(float x, h4v& hi, h4v& lo, int i) {
+    const _Float16 h = (_Float16)x;
+    hi[i] = h;
+    lo[i] = (_Float16)(x - (float)h);
+}
+
+// The G4aSplitParams pre-pass: K rows -> bf16 hi/lo pairs (one thread per
+// 8-dim block), then V key quads -> fp16 hi/lo pairs (one thread per 4 dims
+// 64c + 4n .. +3 of a quad), flagging V values outside the fp16 range.
+__device__ __forceinline__ void split_kv(const G4aSplitParams& p) {
+    const uint32_t nbk = p.Dh / 8, nc = p.Dh / 64;
+    const size_t nk_items = (size_t)p.nkeys * p.Hkv * nbk;
+    const size_t nv_items = (size_t)(p.nkeys / 4) * p.Hkv * nc * 16;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    auto row_of = [&](size_t jj) -> size_t {  // physical row of key k0 + jj
+        uint32_t j = p.k0 + (uint32_t)jj;
+        if (!p.ring_cap && j >= p.S) j = p.S - 1;
+        return p.ring_cap ? j % p.ring_cap : j;
+    };
+    if (i < nk_items) {
+        const uint32_t b = (uint32_t)(i % nbk);
+        const size_t rh = i / nbk;
+        const uint32_t h = (uint32_t)(rh % p.Hkv);
+        const size_t jj = rh / p.Hkv;
+        const float* src = p.k + (row_of(jj) * p.Hkv + h) * p.Dh + 8 * b;
+        bf8v hi, lo;
+        split8(ld4(src), ld4(src + 4), hi, lo);
+        float* dst = p.kout + (jj * p.Hkv + h) * p.Dh + 8 * b;
+        *reinterpret_cast<bf8v*>(dst) = hi;
+        *reinterpret_cast<bf8v*>(dst + 4) = lo;
+        return;
+    }
+    i -= nk_items;
+    if (i >= nv_items) return;
+    const uint32_t n = (uint32_t)(i % 16);
+    size_t t = i / 16;
+    const uint32_t c = (uint32_t)(t % nc);
+    t /= nc;
+    const uint32_t h = (uint32_t)(t % p.Hkv);
+    const size_t qd = t / p.Hkv;
+    float4 x[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) x[kk] = ld4(p.v + (row_of(4 * qd + kk) * p.Hkv + h) * p.Dh + 64 * c + 4 * n);
+    float* const blk = p.vout + (qd * p.Hkv + h) * 4 * p.Dh;
+    bool bad = false;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        h4v hi, lo;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const float xv = e == 0 ? x[kk].x : (e == 1 ? x[kk].y : (e == 2 ? x[kk].z : x[kk].w));
+            bad |= !(fabsf(xv) <= 32768.0f);
+            split16(xv, hi, lo, kk);
+        }
+        float* const dst = blk + 4 * ((4 * c + e) * 16 + n);
+        *reinterpret_cast<h4v*>(dst) = hi;
+        *reinterpret_cast<h4v*>(dst + 2) = lo;
+    }
+    if (bad) *p.vflag = p.epoch;
 }
 
 template <int DH>
@@ -627,8 +672,13 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
 
     const uint32_t qlast = min(qb + 7, p.T - 1);
     const int32_t wg_lo = key_lo(qb), wg_hi = key_hi(qlast);
-    const uint32_t nt = wg_hi > wg_lo ? (uint32_t)((wg_hi - wg_lo + BK - 1) / BK) : 0;
+    // tiles start on multiples of BK (the pre-split V quads are aligned to them);
+    // keys of the first tile before wg_lo are masked like any invisible key
+    const int32_t wg_base = wg_lo & ~(BK - 1);
+    const uint32_t nt = wg_hi > wg_lo ? (uint32_t)((wg_hi - wg_base + BK - 1) / BK) : 0;
     const uint32_t nsteps = (nt + 1) / 2;
+    // P.V from fp16 hi/lo splits of P and V unless some V value is outside their range
+    const bool v16 = __builtin_amdgcn_readfirstlane(*p.vflag) != p.epoch;
     const bool wave_valid = qw < p.T;
     const int32_t w_lo = wave_valid ? key_lo(qw) : 0;
     const int32_t w_hi = wave_valid ? key_hi(min(qw + 1, p.T - 1)) : 0;
@@ -645,11 +695,12 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         for (int kb = 0; kb < QB; ++kb) split8(ld4(qrow + 32 * kb), ld4(qrow + 32 * kb + 4), qh[kb], ql[kb]);
     }
     const float* __restrict__ ksbase = p.ksplit + (size_t)kvh * DH;
+    static_assert(DH == 256, "the V quads of a tile are 16 1 KiB pieces");
 
     // Tile pair of step st (tiles 2st and 2st+1) goes to ring slot st&1, each
-    // tile K (16 split rows of KRS 4-byte slots) then V (16 rows of DH floats),
-    // with global->LDS row copies: 64 rows of DH slots per pair, RPW 1 KiB
-    // copies per wave. Keys past the last visible key re-read it.
+    // tile K (16 split rows of KRS 4-byte slots) then V (16 rows of DH floats,
+    // or its 4 pre-split key quads), with global->LDS copies: 64 pieces of 1 KiB
+    // per pair, RPW per wave. K rows past the last visible key re-read it.
     auto issue_pair = [&](uint32_t st) {
         float* const slot = smem + (st & 1) * 2 * C::TILE;
 #pragma unroll
@@ -657,11 +708,15 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
             const int idx = w * RPW + j;                  // 1 KiB piece of the pair
             const int row = idx / (DH / 256), piece = idx % (DH / 256);
             const int tsel = row / (2 * BK), isv = (row / BK) & 1, kf = row % BK;
-            const uint32_t key = min((uint32_t)wg_lo + (2 * st + tsel) * BK + kf, (uint32_t)wg_hi - 1u);
-            // K rows come from the split copy (row key - ksplit0), V rows from the cache
-            const uint32_t ks = min(max(key, p.ksplit0) - p.ksplit0, p.ksplit_n - 1u);
-            const float* src = isv ? vbase + prow(key) * row_stride + 256 * piece + 4 * lane
-                                   : ksbase + (size_t)ks * row_stride + 256 * piece + 4 * lane;
+            const uint32_t tile0 = (uint32_t)wg_base + (2 * st + tsel) * BK;
+            const uint32_t key = min(tile0 + kf, (uint32_t)wg_hi - 1u);
+            // K rows come from the split copy (row key - split0); V from the split
+            // quads (piece kf: quad kf/4, its 1 KiB piece kf%4) or the cache rows
+            const uint32_t ks = min(key - min(key, p.split0), p.split_n - 1u);
+            const uint32_t qd = min(tile0 - min(tile0, p.split0), p.split_n - (uint32_t)BK) / 4 + (kf >> 2);
+            const float* src = !isv ? ksbase + (size_t)ks * row_stride + 256 * piece + 4 * lane
+                               : v16 ? p.vsplit + ((size_t)qd * p.Hkv + kvh) * 4 * DH + 256 * (kf & 3) + 4 * lane
+                                     : vbase + prow(key) * row_stride + 256 * piece + 4 * lane;
             float* dst = slot + tsel * C::TILE + (isv ? BK * KRS + kf * DH : kf * KRS) + 256 * piece;
             copy16_to_lds(src, dst);
         }
@@ -872,7 +927,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         barrier_lds();  // every wave's have; every wave is done with slot (st+1)&1 (pair st-1)
         if (st + 1 < nsteps) issue_pair(st + 1);
         const uint32_t t = 2 * st + par;
-        const int32_t t0 = wg_lo + (int32_t)(t * BK);
+        const int32_t t0 = wg_base + (int32_t)(t * BK);
         if (!wave_valid || t >= nt || t0 >= w_hi || t0 + BK <= w_lo) continue;
         const float* Kt = smem + (st & 1) * 2 * C::TILE + par * C::TILE;
         const float* Vt = Kt + BK * KRS;
@@ -951,6 +1006,28 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? expf(s[r] - m_ref) : 0.0f;
         l_part += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+        if (v16) {
+            // O += P V on v_mfma_f32_16x16x16_f16: Phi Vhi + Phi Vlo + Plo Vhi (relative error
+            // ~2^-21). Lane (g, rl) gives A = P[row rl][keys 4g .. 4g+3] (its pr) and
+            // B = V[keys 4g .. 4g+3][dim 64c + 4rl + e]: quad g's 16 bytes (4 hi, 4 lo).
+            h4v ah, al;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) split16(pr[r], ah, al, r);
+            const float* const vq = Vt + g * 4 * DH + 4 * rl;
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float4 raw = *reinterpret_cast<const float4*>(vq + 4 * 16 * (4 * c + e));
+                    h4v bh, bl;
+                    __builtin_memcpy(&bh, &raw.x, 8);
+                    __builtin_memcpy(&bl, &raw.z, 8);
+                    O[c][e] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, O[c][e], 0, 0, 0);
+                    O[c][e] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, O[c][e], 0, 0, 0);
+                    O[c][e] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, O[c][e], 0, 0, 0);
+                }
+            continue;
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const float* vr = Vt + (4 * g + r) * DH + 4 * rl;
@@ -1048,5 +1125,5 @@ extern "C" {
 __global__ __launch_bounds__(256) void g4a_prefill_d256(G4aPrefillParams p) { prefill<256>(p); }
 __global__ __launch_bounds__(256) void g4a_prefill_d512(G4aPrefillParams p) { prefill<512>(p); }
 __global__ __launch_bounds__(512) void g4a_prefill2_d256(G4aPrefillParams p) { prefill_pair<256>(p); }
-__global__ __launch_bounds__(256) void g4a_split_k_bf16(G4aSplitParams p) { split_k(p); }
+__global__ __launch_bounds__(256) void g4a_split_kv(G4aSplitParams p) { split_kv(p); }
 }

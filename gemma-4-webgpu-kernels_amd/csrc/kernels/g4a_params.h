@@ -62,22 +62,34 @@ struct G4aPrefillParams {
     const float* k;        // [rows, Hkv, Dh]
     const float* v;        // [rows, Hkv, Dh]
     float* out;            // [T, Hq*Dh]
-    const float* ksplit;   // head_dim 256: keys ksplit0.. as bf16 hi/lo pairs (g4a_split_k_bf16 layout)
+    // head_dim 256: keys [split0, split0 + split_n) pre-split by g4a_split_kv (G4aSplitParams)
+    const float* ksplit;   // K rows as bf16 hi/lo pairs
+    const float* vsplit;   // V key quads as fp16 hi/lo pairs
+    const uint32_t* vflag; // == epoch: some V value is outside the fp16 split's range
     uint32_t T, S, Hq, Hkv;
     uint32_t q_pos0, k_pos0;
     uint32_t ring_cap, window;
-    uint32_t ksplit0, ksplit_n;
+    uint32_t split0, split_n, epoch;
     float scale;
 };
 
-// K rows split into bf16 pairs for the matrix-core score estimate: key j of
-// [k0, k0 + nkeys) (logical, read through the ring) becomes row j - k0 of
-// `out`, same row stride as k (Hkv * Dh 4-byte slots); each 8-dim block of a
-// head occupies 8 slots: the 8 bf16 hi parts, then the 8 bf16 lo parts, with
-// hi = bf16(x) and lo = bf16(x - hi), both rounded to nearest even.
+// Pre-split keys for the head_dim 256 prefill: keys [k0, k0 + nkeys) (logical,
+// read through the ring; keys past the cache re-read its last row), k0 and
+// nkeys multiples of 16.
+//   kout: key j -> row j - k0 (Hkv * Dh 4-byte slots); each 8-dim block of a
+//         head is 8 slots: 8 bf16 hi parts, then 8 bf16 lo parts (hi = bf16(x),
+//         lo = bf16(x - hi), both rounded to nearest even);
+//   vout: keys 4i .. 4i+3 (relative to k0) of head h form a 4*Dh-slot block at
+//         (i * Hkv + h) * 4 * Dh; dim 64c + 4n + e of it sits at slots
+//         4 * ((4c + e) * 16 + n) .. +3: the 4 keys' fp16 hi parts, then their
+//         fp16 lo parts (hi = fp16(x), lo = fp16(x - hi));
+//   vflag: set to epoch if some V value is not finite or beyond +-32768.
 struct G4aSplitParams {
     const float* k;        // [rows, Hkv, Dh]
-    float* out;            // [nkeys, Hkv, Dh] slots
-    uint32_t k0, nkeys, Hkv, Dh;
-    uint32_t ring_cap;
+    const float* v;        // [rows, Hkv, Dh]
+    float* kout;
+    float* vout;
+    uint32_t* vflag;
+    uint32_t k0, nkeys, S, Hkv, Dh;
+    uint32_t ring_cap, epoch;
 };

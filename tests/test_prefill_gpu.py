@@ -110,3 +110,27 @@ def test_prefill_matches_decode_kernel_rows(ctx):
     full = run(ctx, ins, 0, "prefill T=32")
     last = g4a.attention_host(ctx, ins.q[-1:], ins.k, ins.v, q_pos=[31], k_pos=ins.k_pos)
     assert np.abs(full[-1] - last[0]).max() < 2e-6
+
+
+def test_two_kv_heads(ctx):
+    # Hq 16 over Hkv 2 (groups of 8): the pre-split K rows and V key quads interleave the kv heads
+    for Dh, W in [(256, 40), (512, 0)]:
+        ins = synth.gemma_inputs(T=72, S=100, Dh=Dh, seed=31 + Dh, Hq=16, Hkv=2)
+        run(ctx, ins, W, f"Hq 16 / Hkv 2, Dh {Dh}, window {W}")
+
+
+@pytest.mark.parametrize("where", ["all", "one"])
+def test_v_beyond_the_fp16_split_range(ctx, where):
+    # V values past +-32768 cannot be split into fp16 parts: the kernel must take its f32 P.V
+    # path and stay exact; absolute errors scale with |v|, so compare in units of the scale
+    ins = synth.gemma_inputs(T=48, S=300, Dh=256, seed=5)
+    scale = 1e5 if where == "all" else 1.0
+    v = (ins.v * np.float32(scale)).astype(np.float32)
+    if where == "one":
+        v[123, 0, 77] = np.float32(5e4)  # a single out-of-range value, in a visible key
+    big = synth.AttnInputs(ins.q, ins.k, v, ins.q_pos, ins.k_pos)
+    print(f"[gpu] V beyond the fp16 range ({where})", flush=True)
+    want = oracle.attention(big.q, big.k, big.v, big.q_pos, big.k_pos, window=512)
+    got = g4a.attention_host(ctx, big.q, big.k, big.v, q_pos=big.q_pos, k_pos=big.k_pos, window=512)
+    unit = float(np.abs(v).max())
+    assert_parity(got / unit, np.asarray(want) / unit, f"V beyond the fp16 range ({where}), in units of max|v|")
