@@ -1,27 +1,30 @@
-// Query-tiled prefill attention on the fp32 matrix cores (gfx950), with exact
+// Query-tiled prefill attention on the matrix cores (gfx950), with exact
 // scores where they matter. Replaces the reference's per-query ATTN_SPLIT
 // dispatch for T > 1 (rust/src/backend_wgpu.rs:944-957, grid (T, Hkv, splits))
 // behind Backend::attention; results follow rust/src/backend_cpu.rs:270-336.
 //
-// Tiling. A workgroup (4 waves) owns 8 consecutive queries of one kv head; a
-// wave owns 16 rows = 2 queries x the 8 query heads of the kv group, all of
-// which read the same K/V (MQA). K/V stream through LDS in double-buffered
-// 16-key tiles (register-staged, one tile ahead). Per tile a wave computes
-// S^T = K Q^T with v_mfma_f32_16x16x4_f32 (A = K from LDS, B = Q held in
-// registers), so the scores land as lane = row, 4 keys per lane: exactly the
-// A-operand layout of the following P.V product (another 16x16x4 chain, B = V
-// from LDS), with no transpose.
+// Tiling. A wave owns 16 rows = 2 queries x the 8 query heads of the kv group,
+// all of which read the same K/V (MQA). K/V stream through LDS in 16-key tiles.
+// Per tile a wave computes S^T = K Q^T on the matrix cores (A = K from LDS,
+// B = Q held in registers), so the scores land as lane = row, 4 keys per lane:
+// exactly the A-operand layout of the following P.V product (B = V from LDS),
+// with no transpose. Two kernels:
+//   prefill<DH>       4 waves per workgroup, f32 MFMAs (head_dim 512);
+//   prefill_pair<256> 8 waves, two per row block taking even / odd tiles; scores
+//                     from bf16 hi/lo splits and P.V from fp16 hi/lo splits
+//                     (head_dim 256; K and V pre-split by split_kv).
 //
-// Exactness. The matrix cores sum the 256/512-term dots in their own order, a
-// few 1e-5 away from the CPU reference's sequential f32 sum - enough to move
-// outputs by up to ~1e-4 when two keys nearly tie. So every key whose
-// approximate score is within TAU of its row's running maximum is recorded
-// (per-wave list in LDS); once the row block is done, the survivors
-// (still within TAU of the final maximum) get their score recomputed in the
-// reference's exact order and their contribution corrected:
+// Exactness. The matrix cores sum the 256/512-term dots in their own order
+// (and the split forms round their inputs), up to ~5e-4 away from the CPU
+// reference's sequential f32 sum on scores of ~90 - enough to move outputs by
+// up to ~1e-4 when keys nearly tie. So every key whose approximate score is
+// within TAU of its row's running maximum is recorded (per-wave list in LDS);
+// once the row block is done, the survivors (still within TAU of the final
+// maximum) get their score recomputed in the reference's exact order and their
+// contribution corrected:
 //   O[row] += (e^{s_exact - m} - e^{s_approx - m}) * v[key],  l[row] += same.
-// Keys farther than TAU below the maximum carry weight < e^-10 relative to it,
-// so their ~1e-5 score error changes the output by < 1e-9. If the list fills
+// Keys farther than TAU below the maximum carry weight < e^-TAU relative to it,
+// and their score error moves the output by well under 1e-6. If the list fills
 // up (many near-ties), it is compacted against the current maxima and, if
 // still full, corrected on the spot.
 #include "g4a_params.h"
@@ -534,8 +537,8 @@ __device__ __forceinline__ void prefill(const G4aPrefillParams& p) {
 // same 8 queries as above: wave w owns rows 16*(w%4) .. +15 (2 queries x 8
 // heads) and the tiles of parity w/4 (even or odd 16-key tiles), so the two
 // waves sharing a SIMD (w and w+4) never wait on each other and the hardware
-// overlaps one wave's softmax, LDS and bookkeeping with the other's MFMAs. Per
-// step both tiles sit in LDS (register-staged prefetch of the next pair). At
+// overlaps one wave's LDS and memory waits with the other's work. Per step both
+// tiles sit in LDS (global->LDS copies of the next pair in flight meanwhile). At
 // the end each wave compacts its candidates against the maximum over both
 // parities, corrects them exactly, and the parities merge through LDS.
 typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
