@@ -306,8 +306,10 @@ def main(argv=None):
             steps = max(10, args.steps // (4 if S > 100000 else 1))
             m, km = time_steps(ctx, d.calls(), steps, min(args.warmup, 10))
             b = decode_bytes(d.visible(), Dh)
+            pl = ctx.plan(**d.kw())
             extras[name] = {"us_per_step": m * 1e3, "kernel_us": km * 1e3, "GB_s": b / (m * 1e-3) / 1e9,
-                            "kernel_GB_s": b / (km * 1e-3) / 1e9, "splits": ctx.plan(**d.kw()).splits}
+                            "kernel_GB_s": b / (km * 1e-3) / 1e9, "kernel": g4a.KERNEL_NAMES[pl.kernel],
+                            "splits": pl.splits}
             if S > 100000:
                 sweep = {}
                 for sp in (8, 16, 32, 64, 128, 256, 512):

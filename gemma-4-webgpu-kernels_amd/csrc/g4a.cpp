@@ -10,6 +10,7 @@
 #include <hip/hip_runtime_api.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -26,6 +27,8 @@ constexpr uint32_t TILE = 64;
 constexpr uint32_t PREFILL_MIN_T = 16;
 // Largest split-K count the LSE combine kernel takes (its LDS weight table).
 constexpr uint32_t MAX_SPLITS = 1024;
+// Keys per 4-wave workgroup of the short-context decode kernel (two 16-key tiles).
+constexpr uint32_t SHORT_KEYS = 32;
 
 std::string g_create_error;
 
@@ -37,6 +40,8 @@ struct g4a_ctx {
     hipModule_t module = nullptr;
     hipFunction_t decode[2][2][2] = {};  // [dh512][group8][explicit key positions]
     hipFunction_t combine[2] = {nullptr, nullptr};                          // [dh512]
+    hipFunction_t decode_short[2] = {nullptr, nullptr};  // [dh512]
+    bool short_decode = true;  // G4A_DECODE_SHORT=0 turns the short-context kernel off (for comparisons)
     hipFunction_t generic = nullptr;
     hipFunction_t prefill[2] = {nullptr, nullptr};                          // [dh512]
     hipFunction_t split_kv = nullptr;  // K/V pre-split for the head_dim 256 prefill
@@ -262,6 +267,19 @@ int analyse(g4a_ctx* ctx, const g4a_attn_args* a, Analysis* an, bool check_point
         r.plan.keys_per_split = nkeys;
         return G4A_OK;
     }
+    if (group == 8 && r.k_contig && a->splits == 0) {
+        // short context: 32-key splits with every load issued up front, when they
+        // fit one workgroup per CU
+        const uint64_t cus = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1));
+        const uint64_t splits = (nkeys + SHORT_KEYS - 1) / SHORT_KEYS;
+        if ((ctx ? ctx->short_decode : true) && splits * a->T * a->Hkv <= cus) {
+            r.plan.kernel = G4A_KERNEL_DECODE_SHORT;
+            r.plan.splits = uint32_t(splits);
+            r.plan.keys_per_split = SHORT_KEYS;
+            r.plan.workspace_bytes = splits > 1 ? size_t(a->T) * a->Hq * splits * (a->Dh + 2) * sizeof(float) : 0;
+            return G4A_OK;
+        }
+    }
     r.plan.kernel = G4A_KERNEL_DECODE;
     const uint32_t tiles = (nkeys + TILE - 1) / TILE;
     uint32_t splits;
@@ -330,6 +348,9 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
                 snprintf(name, sizeof name, "g4a_decode_d%d_g%d%s", d ? 512 : 256, g ? 8 : 4, kp ? "_kpos" : "");
                 if (int rc = get_fn(ctx, &ctx->decode[d][g][kp], name)) return bail(rc);
             }
+    if (int rc = get_fn(ctx, &ctx->decode_short[0], "g4a_decode_short_d256")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->decode_short[1], "g4a_decode_short_d512")) return bail(rc);
+    if (const char* env = getenv("G4A_DECODE_SHORT")) ctx->short_decode = atoi(env) != 0;
     if (int rc = get_fn(ctx, &ctx->combine[0], "g4a_combine_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->combine[1], "g4a_combine_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->generic, "g4a_generic_attention")) return bail(rc);
@@ -341,6 +362,7 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
         fail(ctx, G4A_E_NOMEM, "dummy buffer allocation failed");
         return bail(G4A_E_NOMEM);
     }
+
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreate(&ctx->ev_start) != hipSuccess || hipEventCreate(&ctx->ev_stop) != hipSuccess ||
         hipEventCreateWithFlags(&ctx->ev_staging, hipEventDisableTiming) != hipSuccess) {
@@ -541,9 +563,14 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
     dp.softcap = a->attn_softcap;
     const int d512 = a->Dh == 512 ? 1 : 0;
     const int g8 = group == 8 ? 1 : 0;
-    if (int rc = launch(ctx, ctx->decode[d512][g8][kd ? 1 : 0], dim3(pl.splits, a->T, a->Hkv), dim3(512, 1, 1), dp,
-                        "decode", true))
+    if (pl.kernel == G4A_KERNEL_DECODE_SHORT) {
+        if (int rc = launch(ctx, ctx->decode_short[d512], dim3(pl.splits, a->T, a->Hkv), dim3(256, 1, 1), dp,
+                            "short decode", true))
+            return rc;
+    } else if (int rc = launch(ctx, ctx->decode[d512][g8][kd ? 1 : 0], dim3(pl.splits, a->T, a->Hkv),
+                               dim3(512, 1, 1), dp, "decode", true)) {
         return rc;
+    }
     if (pl.splits > 1) {
         G4aCombineParams cp{dp.part, a->out, a->T, a->Hq, pl.splits, a->Dh};
         if (int rc = launch(ctx, ctx->combine[d512], dim3(a->Dh / 16, a->Hq, a->T), dim3(256, 1, 1), cp, "combine"))

@@ -804,6 +804,272 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p) {
     }
 }
 
+// Exact dots of 16 dims (16B .. 16B+15) for ONE head per lane: lane = key,
+// each 16-lane row a head. q[h][16B + j] sits in lane j of the row of head h;
+// each multiply takes it through a DPP row broadcast (row_newbcast:j), then
+// dot = dot + q*k, separately rounded, in the reference's order.
+__device__ __forceinline__ void qk1_dims16(float& s, float q, const float4 (&k)[4]) {
+    float t;
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k0] row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k1] row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k2] row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k3] row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k4] row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k5] row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k6] row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k7] row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k8] row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k9] row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k10] row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k11] row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k12] row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k13] row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k14] row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        "v_mul_f32_dpp %[t], %[q], %[k15] row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t]\n\t"
+        : [a] "+v"(s), [t] "=&v"(t)
+        : [q] "v"(q), [k0] "v"(k[0].x), [k1] "v"(k[0].y), [k2] "v"(k[0].z), [k3] "v"(k[0].w), [k4] "v"(k[1].x),
+          [k5] "v"(k[1].y), [k6] "v"(k[1].z), [k7] "v"(k[1].w), [k8] "v"(k[2].x), [k9] "v"(k[2].y), [k10] "v"(k[2].z),
+          [k11] "v"(k[2].w), [k12] "v"(k[3].x), [k13] "v"(k[3].y), [k14] "v"(k[3].z), [k15] "v"(k[3].w));
+}
+
+// Short-context decode for groups of 8 query heads: the sliding layers' 512-key
+// window and global layers up to 8K keys, where a call is bound by latency
+// rather than by HBM bandwidth.
+//
+// A 4-wave workgroup owns a key split of 32 keys = two 16-key tiles; wave
+// w = 2 * tile + half takes heads 4 * half .. +3 of its tile. Every copy of
+// the workgroup is issued up front (one memory round trip): query rows, K rows
+// and V rows go global -> LDS, each wave copying half of its tile's rows.
+//   scores: lane = (head: 16-lane row, key: lane % 16), ONE exact dot per lane
+//           (((0 + q0*k0) + q1*k1) + ..., separately rounded), q held in
+//           registers and broadcast along each row with DPP, K read from LDS
+//           (rows padded to DH + 4 floats: the 16 keys of a read sit on
+//           distinct banks), one 16-dim block ahead of its use;
+//   softmax: per head over the tile's 16 keys (4 xor-shuffles in the row);
+//   P.V:    lane l owns dims 4l..4l+3 (+256 for DH 512) of its 4 heads, fused
+//           multiply-adds over the tile's V rows in LDS;
+//   end:    the two tiles merge through LDS (wave w merges heads 2w, 2w+1)
+//           into the split's partial (m, l, acc), or the output for one split;
+//           the combine kernel merges the split partials.
+template <int DH>
+struct ShortCfg {
+    static constexpr int GROUP = 8;
+    static constexpr int KEYS = 16;              // keys per tile
+    static constexpr int TILES = 2;              // tiles per workgroup (4 waves)
+    static constexpr int RS = DH + 4;            // K row stride in LDS (floats)
+    static constexpr int QRS = DH + 16;          // query row stride in LDS: 4 rows x 16 floats on distinct banks
+    static constexpr int NRC = DH / 256;         // 1 KiB copies per row
+    static constexpr int ND = DH / 256;          // float4 dim groups per lane in P.V
+    static constexpr int NB = DH / 16;           // 16-dim blocks of a dot
+    static constexpr int QS = GROUP * QRS;
+    static constexpr int KS = TILES * KEYS * RS;
+    static constexpr int VS = TILES * KEYS * DH;
+    static constexpr int PB = 4 * KEYS * 4;      // [wave][key][4 heads]
+    static constexpr int ML = 4 * 2 * 4;         // [wave][m, l][4 heads]
+    static constexpr int MERGE = 4 * 4 * DH;     // [wave][4 heads][DH], over the K rows after the scores
+    static constexpr int SMEM = QS + KS + VS + PB + ML;
+    static constexpr int COPIES = 2 * NRC + 2 * (KEYS / 2) * NRC;  // per wave: query, K and V rows
+    static_assert(MERGE <= KS, "the wave partials fit over the K rows");
+    static_assert(SMEM * 4 <= 160 * 1024, "LDS budget of a CU");
+    static_assert(COPIES < 64, "vmcnt range");
+};
+
+template <int DH>
+__device__ __forceinline__ void decode_short(const G4aDecodeParams& p) {
+    using C = ShortCfg<DH>;
+    constexpr int GROUP = C::GROUP, KEYS = C::KEYS, RS = C::RS, QRS = C::QRS, NRC = C::NRC, ND = C::ND, NB = C::NB;
+
+    __shared__ __attribute__((aligned(16))) float smem[C::SMEM];
+    float* const qs = smem;              // [GROUP][QRS]
+    float* const kbuf = qs + C::QS;      // [TILES][KEYS][RS]; after the scores: [4 waves][4 heads][DH]
+    float* const vbuf = kbuf + C::KS;    // [TILES][KEYS][DH]
+    float* const pbuf = vbuf + C::VS;    // [4 waves][KEYS][4]
+    float* const mlbuf = pbuf + C::PB;   // [4 waves][2][4]
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tile = w >> 1, half = w & 1;
+    const int r = lane >> 4;     // score phase: head 4 * half + r
+    const int key = lane & 15;   // score phase: key of the tile
+    const uint32_t split = blockIdx.x, qi = blockIdx.y, kvh = blockIdx.z;
+    const uint32_t qpos = p.q_pos ? p.q_pos[qi] : p.q_pos0 + qi;
+    const uint32_t t0 = p.k_start + split * p.keys_per_split + tile * KEYS;
+    const uint32_t nk = t0 < p.k_end ? min((uint32_t)KEYS, p.k_end - t0) : 0u;
+    // contiguous key positions: a tile whose first key is in the future is idle
+    const bool active = nk > 0 && p.k_pos0 + t0 <= qpos;
+    const uint32_t h0 = kvh * GROUP;
+    const size_t row_stride = (size_t)p.Hkv * DH;
+    float* const tk = kbuf + tile * KEYS * RS;
+    float* const tv = vbuf + tile * KEYS * DH;
+    float* const my_p = pbuf + w * KEYS * 4;
+    float* const my_ml = mlbuf + w * 8;
+
+    // query rows: copy i (row i / NRC, 1 KiB piece i % NRC); wave w takes i = w, w + 4, ...
+    {
+        const float* qsrc = p.q + ((size_t)qi * p.Hq + h0) * DH;
+#pragma unroll
+        for (int c = 0; c < 2 * NRC; ++c) {
+            const int i = w + 4 * c;
+            copy16_to_lds(qsrc + (i / NRC) * DH + 256 * (i % NRC) + 4 * lane, qs + (i / NRC) * QRS + 256 * (i % NRC));
+        }
+    }
+    // this wave's half of its tile: rows 8 * half .. +7, clamped to the tile's last key
+    if (active) {
+        const float* const kb = p.k + (size_t)kvh * DH;
+        const float* const vb = p.v + (size_t)kvh * DH;
+        uint32_t rows[KEYS / 2];
+#pragma unroll
+        for (int i = 0; i < KEYS / 2; ++i)
+            rows[i] = phys_row(t0 + min((uint32_t)(8 * half + i), nk - 1), p.ring_cap);
+#pragma unroll
+        for (int i = 0; i < KEYS / 2; ++i)
+#pragma unroll
+            for (int c = 0; c < NRC; ++c)
+                copy16_to_lds(kb + rows[i] * row_stride + 256 * c + 4 * lane, tk + (8 * half + i) * RS + 256 * c);
+#pragma unroll
+        for (int i = 0; i < KEYS / 2; ++i)
+#pragma unroll
+            for (int c = 0; c < NRC; ++c)
+                copy16_to_lds(vb + rows[i] * row_stride + 256 * c + 4 * lane, tv + (8 * half + i) * DH + 256 * c);
+        wait_vm<(KEYS / 2) * NRC>();  // this wave's query pieces and K rows have landed
+    } else {
+        wait_vm<0>();
+    }
+    barrier_lds();  // ... and every wave's
+
+    float s = NEG_INF;  // score of (head 4 * half + r, key)
+    if (active) {
+        float qreg[NB];  // q[h][16b + key]: lane `key` of the head's row holds the block's value
+#pragma unroll
+        for (int b = 0; b < NB; ++b) qreg[b] = qs[(4 * half + r) * QRS + 16 * b + key];
+        const float* const krow = tk + key * RS;
+        float4 kc[4], kn[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kc[i] = ld4(krow + 4 * i);
+        float dot = 0.0f;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (b + 1 < NB) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) kn[i] = ld4(krow + 16 * (b + 1) + 4 * i);
+            }
+            qk1_dims16(dot, qreg[b], kc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kc[i] = kn[i];
+        }
+        const uint32_t kp = p.k_pos0 + t0 + key;
+        const bool vis = (uint32_t)key < nk && kp <= qpos && (p.window == 0 || qpos - kp < p.window);
+        if (vis) s = score_epilogue(dot, p.scale, p.softcap);
+    }
+    float m = s;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    const float pr = (s == NEG_INF) ? 0.0f : expf(s - m);
+    float l = pr;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o, 64);
+    my_p[key * 4 + r] = pr;
+    if (key == 0) {
+        my_ml[r] = m;
+        my_ml[4 + r] = l;
+    }
+
+    wait_vm<0>();   // this wave's V rows have landed
+    barrier_lds();  // ... and its partner's; every wave is done with the K rows
+    float4 acc[4][ND];
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int e = 0; e < ND; ++e) acc[h][e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (active) {
+#pragma unroll
+        for (int k0 = 0; k0 < KEYS; k0 += 8) {
+            float4 pk[8], vk[8][ND];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                pk[j] = ld4(my_p + (k0 + j) * 4);
+#pragma unroll
+                for (int e = 0; e < ND; ++e) vk[j][e] = ld4(tv + (k0 + j) * DH + 256 * e + 4 * lane);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float pw[4] = {pk[j].x, pk[j].y, pk[j].z, pk[j].w};
+#pragma unroll
+                for (int e = 0; e < ND; ++e)
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) {
+                        acc[h][e].x = __builtin_fmaf(pw[h], vk[j][e].x, acc[h][e].x);
+                        acc[h][e].y = __builtin_fmaf(pw[h], vk[j][e].y, acc[h][e].y);
+                        acc[h][e].z = __builtin_fmaf(pw[h], vk[j][e].z, acc[h][e].z);
+                        acc[h][e].w = __builtin_fmaf(pw[h], vk[j][e].w, acc[h][e].w);
+                    }
+            }
+        }
+    }
+
+    // merge the two tiles: wave w merges heads 2w, 2w + 1 (waves half and 2 + half hold them)
+    float* const merge = kbuf;
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int e = 0; e < ND; ++e)
+            *reinterpret_cast<float4*>(merge + (w * 4 + h) * DH + 256 * e + 4 * lane) = acc[h][e];
+    barrier_lds();
+    float* const mlp = p.part + (size_t)p.T * p.Hq * p.nsplit * DH;  // (m, l) pairs of the partials
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int h = 2 * w + i;               // head of the group
+        const int x0 = h >> 2, x1 = 2 + (h >> 2), hr = h & 3;
+        const float m0 = mlbuf[x0 * 8 + hr], m1 = mlbuf[x1 * 8 + hr];
+        const float l0 = mlbuf[x0 * 8 + 4 + hr], l1 = mlbuf[x1 * 8 + 4 + hr];
+        float4 a0[ND], a1[ND];
+#pragma unroll
+        for (int e = 0; e < ND; ++e) {
+            a0[e] = ld4(merge + (x0 * 4 + hr) * DH + 256 * e + 4 * lane);
+            a1[e] = ld4(merge + (x1 * 4 + hr) * DH + 256 * e + 4 * lane);
+        }
+        const float M = fmaxf(m0, m1);
+        const float e0 = (m0 == NEG_INF) ? 0.0f : expf(m0 - M);
+        const float e1 = (m1 == NEG_INF) ? 0.0f : expf(m1 - M);
+        const float L = l0 * e0 + l1 * e1;
+        const size_t ih = (size_t)qi * p.Hq + h0 + h;
+        const float sc = p.nsplit == 1 ? (L > 0.0f ? 1.0f / L : 0.0f) : 1.0f;
+        float* const dst = p.nsplit == 1 ? p.out + ih * DH : p.part + (ih * p.nsplit + split) * DH;
+#pragma unroll
+        for (int e = 0; e < ND; ++e) {
+            float4 o;
+            o.x = (a0[e].x * e0 + a1[e].x * e1) * sc;
+            o.y = (a0[e].y * e0 + a1[e].y * e1) * sc;
+            o.z = (a0[e].z * e0 + a1[e].z * e1) * sc;
+            o.w = (a0[e].w * e0 + a1[e].w * e1) * sc;
+            *reinterpret_cast<float4*>(dst + 256 * e + 4 * lane) = o;
+        }
+        if (p.nsplit > 1 && lane == 0) {
+            float* const ml = mlp + (ih * p.nsplit + split) * 2;
+            ml[0] = M;
+            ml[1] = L;
+        }
+    }
+}
+
 // out = sum_s acc_s * e^(m_s - M) / sum_s l_s * e^(m_s - M), M = max_s m_s; 0 when the
 // denominator is 0 (the semantics of rust/src/kernels/attention_combine.wgsl:1-28).
 // One block per (16 output dims, head, query): wide enough that a decode
@@ -936,6 +1202,8 @@ __global__ __launch_bounds__(512) void g4a_decode_d256_g8_kpos(G4aDecodeParams p
 __global__ __launch_bounds__(512) void g4a_decode_d512_g8_kpos(G4aDecodeParams p) { decode_wave<512, true>(p); }
 __global__ __launch_bounds__(512) void g4a_decode_d256_g4_kpos(G4aDecodeParams p) { decode_split<256, 4, true>(p); }
 __global__ __launch_bounds__(512) void g4a_decode_d512_g4_kpos(G4aDecodeParams p) { decode_split<512, 4, true>(p); }
+__global__ __launch_bounds__(256) void g4a_decode_short_d256(G4aDecodeParams p) { decode_short<256>(p); }
+__global__ __launch_bounds__(256) void g4a_decode_short_d512(G4aDecodeParams p) { decode_short<512>(p); }
 __global__ __launch_bounds__(256) void g4a_combine_d256(G4aCombineParams p) { combine<256>(p); }
 __global__ __launch_bounds__(256) void g4a_combine_d512(G4aCombineParams p) { combine<512>(p); }
 __global__ __launch_bounds__(64) void g4a_generic_attention(G4aGenericParams p) { generic_attention(p); }

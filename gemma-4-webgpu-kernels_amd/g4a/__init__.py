@@ -22,7 +22,7 @@ HSACO_PATH = BUILD_DIR / "g4a_kernels.hsaco"
 HEADER_PATH = PKG_DIR.parent / "include" / "g4a.h"
 
 G4A_OK = 0
-KERNEL_NAMES = {0: "none", 1: "decode", 2: "prefill", 3: "generic"}
+KERNEL_NAMES = {0: "none", 1: "decode", 2: "prefill", 3: "generic", 4: "decode_short"}
 
 _u32p = ctypes.POINTER(ctypes.c_uint32)
 _f32p = ctypes.c_void_p

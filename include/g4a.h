@@ -126,6 +126,7 @@ typedef enum g4a_kernel_kind {
     G4A_KERNEL_DECODE = 1,  /* split-K flash-decode (+ LSE combine if splits > 1) */
     G4A_KERNEL_PREFILL = 2, /* query-tiled prefill */
     G4A_KERNEL_GENERIC = 3, /* per-(query, head) fallback for other shapes */
+    G4A_KERNEL_DECODE_SHORT = 4, /* short-context split-K decode, 32-key splits (+ LSE combine if splits > 1) */
 } g4a_kernel_kind;
 
 typedef struct g4a_attn_plan {

@@ -36,7 +36,7 @@ def test_decode_trim_for_sliding_window_keeps_last_window_keys():
     # decode at position 8191 with window 512: keys 7680..8191 only
     p = _plan(S=8192, q_pos0=8191, window=512)
     assert (p.k_start, p.k_end) == (8192 - 512, 8192)
-    assert g4a.KERNEL_NAMES[p.kernel] == "decode"
+    assert g4a.KERNEL_NAMES[p.kernel] in ("decode", "decode_short")
 
 
 def test_trim_matches_reference_partition_points_on_explicit_positions():
@@ -60,9 +60,14 @@ def test_no_visible_key_plans_a_zero_fill():
 
 
 @pytest.mark.parametrize("S,Dh", [(512, 256), (8192, 512), (32768, 512), (131072, 512)])
-def test_auto_splits_cover_the_range_in_64_key_tiles(S, Dh):
+def test_auto_splits_cover_the_range(S, Dh):
     p = _plan(S=S, Dh=Dh, Dv=Dh, q_pos0=S - 1)
-    assert p.keys_per_split % 64 == 0
+    if g4a.KERNEL_NAMES[p.kernel] == "decode_short":
+        # 32-key splits (two 16-key tiles per 4-wave workgroup), at most one workgroup per CU
+        assert p.keys_per_split == 32 and S <= 256 * 32
+    else:
+        assert S > 256 * 32
+        assert p.keys_per_split % 64 == 0
     assert p.splits * p.keys_per_split >= S > (p.splits - 1) * p.keys_per_split
     assert p.splits <= 256  # one 8-wave workgroup per CU at most
     if p.splits > 1:
@@ -124,3 +129,23 @@ def test_backend_mirror_driver_links_and_reports_a_missing_device():
     r = subprocess.run([str(build.TEST_BACKEND)], capture_output=True, text=True, timeout=60)
     assert r.returncode == 2, (r.returncode, r.stdout, r.stderr)
     assert "g4a_create failed" in r.stderr
+
+
+def test_short_decode_rule():
+    """Contiguous-position decode of an 8-head group whose 32-key splits fit one
+    workgroup per CU takes the short kernel; explicit positions, 4-head groups
+    and forced split counts keep the streaming kernel."""
+    p = _plan(S=512, q_pos0=511, window=512)
+    assert g4a.KERNEL_NAMES[p.kernel] == "decode_short"
+    assert (p.splits, p.keys_per_split) == (16, 32)
+    assert p.workspace_bytes == 8 * 16 * (256 + 2) * 4
+    p = _plan(S=30, Dh=512, Dv=512, q_pos0=29)
+    assert g4a.KERNEL_NAMES[p.kernel] == "decode_short" and p.splits == 1 and p.workspace_bytes == 0
+    p = _plan(T=4, S=2048, Dh=512, Dv=512, q_pos0=2044)
+    assert g4a.KERNEL_NAMES[p.kernel] == "decode_short" and p.splits == 64
+    p = _plan(T=5, S=2048, Dh=512, Dv=512, q_pos0=2043)
+    assert g4a.KERNEL_NAMES[p.kernel] == "decode"  # 5 x 64 workgroups exceed one per CU
+    assert g4a.KERNEL_NAMES[_plan(S=8193, Dh=512, Dv=512, q_pos0=8192).kernel] == "decode"
+    assert g4a.KERNEL_NAMES[_plan(S=512, q_pos=[511], k_pos=np.arange(512) * 2).kernel] == "decode"
+    assert g4a.KERNEL_NAMES[_plan(S=512, Hq=4, q_pos0=511).kernel] == "decode"
+    assert g4a.KERNEL_NAMES[_plan(S=512, q_pos0=511, splits=8).kernel] == "decode"
