@@ -180,6 +180,59 @@ def schedule_35_layers(ctx, steps, warmup):
     return {"us_per_token": ms * 1e3, "algorithmic_bytes": algo, "GB_s": algo / (ms * 1e-3) / 1e9}
 
 
+def producer_bytes(T: int, Dh: int, Hq: int = HQ, Hkv: int = 1) -> int:
+    """Algorithmic bytes of one producer call: the q/k/v rows read and written once, plus the two norm weights."""
+    return 4 * (2 * T * (Hq + 2 * Hkv) * Dh + 2 * Dh)
+
+
+PRODUCER_CONFIGS = [
+    # name, T, Dh, theta, rotary_dim, position of token 0, ring capacity (0 = linear cache)
+    ("producer sliding decode hd256 (ring 512)", 1, 256, 1e4, 256, 32767, 512),
+    ("producer global decode hd512 @32768", 1, 512, 1e6, 128, 32767, 0),
+    ("producer global prefill hd512 T2048", 2048, 512, 1e6, 128, 0, 0),
+]
+
+
+def producer(ctx, T, Dh, theta, rot, pos0, ring_cap, steps, cpu_reps=3):
+    """The attention producer of one layer (per-head q/k RMSNorm + partial RoPE, v norm,
+    K/V rows into the cache): kernel time per call from dispatch-attached events (a
+    Python loop issues the calls, so host time is not what is measured), and the CPU
+    oracle's composition of the same ops on the host."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle
+    rows = max(T, ring_cap or (pos0 + T))
+    q_h = synth.normal_f32(7, 0, T * HQ * Dh).reshape(T, HQ, Dh)
+    k_h = synth.normal_f32(7, 1, T * Dh).reshape(T, 1, Dh)
+    v_h = synth.normal_f32(7, 2, T * Dh).reshape(T, 1, Dh)
+    w_h = (np.float32(1.0) + np.float32(0.1) * synth.normal_f32(7, 3, Dh)).astype(np.float32)
+    q, k, v, w = ctx.upload(q_h), ctx.upload(k_h), ctx.upload(v_h), ctx.upload(w_h)
+    qo, kc, vc = ctx.empty((T, HQ, Dh)), ctx.empty((rows, 1, Dh)), ctx.empty((rows, 1, Dh))
+    kw = dict(q=q.ptr, k=k.ptr, v=v.ptr, q_norm=w.ptr, k_norm=w.ptr, q_out=qo.ptr, k_cache=kc.ptr, v_cache=vc.ptr,
+              T=T, Hq=HQ, Hkv=1, Dh=Dh, rotary_dim=rot, pos0=pos0, cache_row=pos0, ring_cap=ring_cap, theta=theta,
+              eps=1e-6)
+    for _ in range(5):
+        ctx.attn_producer(**kw)
+    ctx.sync()
+    ctx.kernel_timing(True)
+    for _ in range(steps):
+        ctx.attn_producer(**kw)
+    ctx.sync()
+    kms, n = ctx.kernel_timing_read()
+    ctx.kernel_timing(False)
+    for a in (q, k, v, w, qo, kc, vc):
+        a.free()
+    pos = np.arange(pos0, pos0 + T, dtype=np.uint32)
+    times = []
+    for _ in range(cpu_reps):
+        t0 = time.perf_counter()
+        oracle.producer(q_h, k_h, v_h, w_h, w_h, pos, theta, rot, 1e-6)
+        times.append(time.perf_counter() - t0)
+    us = kms / n * 1e3
+    b = producer_bytes(T, Dh)
+    return {"kernel_us": us, "GB_s": b / (us * 1e-6) / 1e9, "frac_hbm_peak": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "bytes": b, "cpu_oracle_us": float(np.median(times)) * 1e6, "cpu_threads": 1}
+
+
 PREFILL_CONFIGS = [("configs[3a] prefill hd256 T2048 window512", 2048, 256, 512),
                    ("configs[3b] prefill hd512 T2048 causal", 2048, 512, 0)]
 
@@ -216,7 +269,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="headline decode only (no extras, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "schedule"], default=None,
+    ap.add_argument("--only", choices=["prefill", "schedule", "producer"], default=None,
                     help="run only these extra workloads (for profiling) and print their JSON line")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="first run 3 device-to-device copies of MIB MiB (the reference dispatch for "
@@ -236,6 +289,10 @@ def main(argv=None):
         if args.only == "prefill":
             for name, T, Dh, W in PREFILL_CONFIGS:
                 out[name] = prefill(ctx, T, Dh, W, steps=args.steps, warmup=args.warmup)
+                print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
+        elif args.only == "producer":
+            for name, T, Dh, theta, rot, pos0, cap in PRODUCER_CONFIGS:
+                out[name] = producer(ctx, T, Dh, theta, rot, pos0, cap, steps=args.steps)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         else:
             out["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=args.steps, warmup=args.warmup)
@@ -320,6 +377,9 @@ def main(argv=None):
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
         for name, T, Dh, W in PREFILL_CONFIGS:
             extras[name] = prefill(ctx, T, Dh, W, steps=5, warmup=2)
+            print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
+        for name, T, Dh, theta, rot, pos0, cap in PRODUCER_CONFIGS:
+            extras[name] = producer(ctx, T, Dh, theta, rot, pos0, cap, steps=50)
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
         extras["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=20, warmup=3)
         print(f"[bench] schedule: {extras['configs[4] 35-layer schedule @32768']}", file=sys.stderr, flush=True)

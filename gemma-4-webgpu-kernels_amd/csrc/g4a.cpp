@@ -6,6 +6,7 @@
 #include "g4a.h"
 
 #include <dlfcn.h>
+#include <math.h>
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime_api.h>
 #include <stdarg.h>
@@ -45,6 +46,15 @@ struct g4a_ctx {
     hipFunction_t generic = nullptr;
     hipFunction_t prefill[2] = {nullptr, nullptr};                          // [dh512]
     hipFunction_t split_kv = nullptr;  // K/V pre-split for the head_dim 256 prefill
+    hipFunction_t norm_rope = nullptr;  // the attention producer (RMSNorm + RoPE + KV write)
+    // RoPE frequency tables theta^(-2j/rot), one per (theta, rotary_dim) seen
+    struct FreqTable {
+        float theta;
+        uint32_t rot;
+        std::vector<float> host;
+        float* dev;
+    };
+    std::vector<FreqTable> freq_tables;
     uint32_t split_epoch = 0;          // tags each pre-split's V range flag
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     hipEvent_t ev_staging = nullptr;  // last use of the pinned staging buffer
@@ -357,6 +367,7 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->prefill[0], "g4a_prefill2_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->prefill[1], "g4a_prefill_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->split_kv, "g4a_split_kv")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->norm_rope, "g4a_norm_rope")) return bail(rc);
     if (hipMalloc(reinterpret_cast<void**>(&ctx->dummy), 4096) != hipSuccess ||
         hipMemset(ctx->dummy, 0, 4096) != hipSuccess) {
         fail(ctx, G4A_E_NOMEM, "dummy buffer allocation failed");
@@ -380,6 +391,7 @@ void g4a_destroy(g4a_ctx* ctx) {
     if (ctx->workspace) hipFree(ctx->workspace);
     if (ctx->dummy) hipFree(ctx->dummy);
     if (ctx->pos_dev) hipFree(ctx->pos_dev);
+    for (auto& ft : ctx->freq_tables) hipFree(ft.dev);
     if (ctx->pos_host) hipHostFree(ctx->pos_host);
     if (ctx->ev_start) hipEventDestroy(ctx->ev_start);
     if (ctx->ev_stop) hipEventDestroy(ctx->ev_stop);
@@ -610,6 +622,113 @@ int g4a_kv_write(g4a_ctx* ctx, float* cache, uint32_t ring_cap, uint32_t row_ele
         HIP_TRY(ctx, hipMemcpyAsync(cache, src + size_t(skip + n1) * row_elems, size_t(n - n1) * row_bytes,
                                     hipMemcpyDeviceToDevice, ctx->stream));
     return G4A_OK;
+}
+
+namespace {
+
+// Device table of the RoPE frequencies freq[j] = theta^(-2j/rot), j < rot/2,
+// computed with libm powf exactly as the reference computes them
+// (rust/src/backend_cpu.rs:257: theta.powf(-(2.0 * j as f32) / rotary_dim as f32)).
+int freq_table(g4a_ctx* ctx, float theta, uint32_t rot, const float** out) {
+    for (auto& ft : ctx->freq_tables)
+        if (ft.rot == rot && memcmp(&ft.theta, &theta, sizeof theta) == 0) {
+            *out = ft.dev;
+            return G4A_OK;
+        }
+    g4a_ctx::FreqTable ft{theta, rot, std::vector<float>(std::max<uint32_t>(rot / 2, 1)), nullptr};
+    for (uint32_t j = 0; j < rot / 2; ++j) ft.host[j] = powf(theta, -(2.0f * (float)j) / (float)rot);
+    if (hipMalloc(reinterpret_cast<void**>(&ft.dev), ft.host.size() * sizeof(float)) != hipSuccess)
+        return fail(ctx, G4A_E_NOMEM, "RoPE frequency table");
+    ctx->freq_tables.push_back(std::move(ft));
+    auto& t = ctx->freq_tables.back();
+    HIP_TRY(ctx, hipMemcpyAsync(t.dev, t.host.data(), t.host.size() * sizeof(float), hipMemcpyHostToDevice,
+                                ctx->stream));
+    *out = t.dev;
+    return G4A_OK;
+}
+
+// One g4a_norm_rope launch over up to three row segments.
+int norm_rope_launch(g4a_ctx* ctx, G4aNormRopeSeg* segs, uint32_t nseg, uint32_t T, uint32_t Dh, uint32_t rot,
+                     const uint32_t* positions, uint32_t pos0, float theta, float eps, uint32_t cache_row,
+                     uint32_t ring_cap) {
+    if (Dh == 0 || Dh % 4 != 0 || Dh > 1024)
+        return fail(ctx, G4A_E_UNSUPPORTED, "head_dim %u: RMSNorm/RoPE rows need head_dim %% 4 == 0 and <= 1024", Dh);
+    if (rot % 2 != 0 || rot > Dh) return fail(ctx, G4A_E_ARG, "rotary_dim %u must be even and <= head_dim %u", rot, Dh);
+    uint64_t rows = 0;
+    for (uint32_t i = 0; i < nseg; ++i) {
+        if (!segs[i].x || !segs[i].y) return fail(ctx, G4A_E_ARG, "null input/output rows");
+        rows += uint64_t(T) * segs[i].heads;
+    }
+    if (rows == 0) return G4A_OK;
+    if (rows >= (uint64_t(1) << 32)) return fail(ctx, G4A_E_SHAPE, "too many rows (%llu)", (unsigned long long)rows);
+    G4aNormRopeParams p{};
+    for (uint32_t i = 0; i < nseg; ++i) p.seg[i] = segs[i];
+    p.nseg = nseg;
+    p.total_rows = uint32_t(rows);
+    p.T = T;
+    p.Dh = Dh;
+    p.rotary_dim = rot;
+    p.eps = eps;
+    p.cache_row = cache_row;
+    p.ring_cap = ring_cap;
+    p.pos0 = pos0;
+    bool needs_rope = false;
+    for (uint32_t i = 0; i < nseg; ++i) needs_rope |= segs[i].rope != 0;
+    if (needs_rope && rot) {
+        if (int rc = freq_table(ctx, theta, rot, &p.freq)) return rc;
+        if (positions) {
+            bool contig = true;
+            for (uint32_t i = 0; i < T; ++i) contig &= positions[i] == positions[0] + i;
+            if (contig) p.pos0 = positions[0];
+            else if (int rc = upload_positions(ctx, positions, T, nullptr, 0, &p.pos, nullptr)) return rc;
+        }
+    }
+    const uint32_t blocks = uint32_t((rows + 3) / 4);
+    return launch(ctx, ctx->norm_rope, dim3(blocks, 1, 1), dim3(256, 1, 1), p, "norm/rope rows", true);
+}
+
+}  // namespace
+
+int g4a_head_norm_rope(g4a_ctx* ctx, const float* x, const float* w, float* y, uint32_t T, uint32_t heads,
+                       uint32_t head_dim, uint32_t rotary_dim, const uint32_t* positions, uint32_t pos0, float theta,
+                       float eps) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    G4aNormRopeSeg seg{x, w, y, heads, 1u, 1u, 0u, 0u};
+    return norm_rope_launch(ctx, &seg, 1, T, head_dim, rotary_dim, positions, pos0, theta, eps, 0, 0);
+}
+
+int g4a_rms_norm(g4a_ctx* ctx, const float* x, const float* w, float* y, uint32_t rows, uint32_t dim, float eps) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    G4aNormRopeSeg seg{x, w, y, rows, 1u, 0u, 0u, 0u};
+    return norm_rope_launch(ctx, &seg, 1, 1, dim, 0, nullptr, 0, 0.0f, eps, 0, 0);
+}
+
+int g4a_rope(g4a_ctx* ctx, const float* x, float* y, uint32_t T, uint32_t heads, uint32_t head_dim,
+             uint32_t rotary_dim, const uint32_t* positions, uint32_t pos0, float theta) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    G4aNormRopeSeg seg{x, nullptr, y, heads, 0u, 1u, 0u, 0u};
+    return norm_rope_launch(ctx, &seg, 1, T, head_dim, rotary_dim, positions, pos0, theta, 0.0f, 0, 0);
+}
+
+int g4a_attn_producer(g4a_ctx* ctx, const g4a_producer_args* a) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (!a) return fail(ctx, G4A_E_ARG, "null args");
+    if (!a->q || !a->q_out) return fail(ctx, G4A_E_ARG, "null q / q_out");
+    if ((a->k == nullptr) != (a->v == nullptr)) return fail(ctx, G4A_E_ARG, "k and v come together");
+    if (a->k && (!a->k_cache || !a->v_cache)) return fail(ctx, G4A_E_ARG, "null k_cache / v_cache");
+    G4aNormRopeSeg segs[3];
+    uint32_t n = 0;
+    // q: weighted norm + RoPE, or RoPE only without a q_norm weight (rust/src/model.rs:258-261)
+    segs[n++] = G4aNormRopeSeg{a->q, a->q_norm, a->q_out, a->Hq, a->q_norm ? 1u : 0u, 1u, 0u, 0u};
+    if (a->k) {
+        // a ring keeps only the last kv_ring_cap of the call's rows
+        const uint32_t first = a->kv_ring_cap && a->T > a->kv_ring_cap ? a->T - a->kv_ring_cap : 0;
+        // k like q (rust/src/model.rs:270-273); v: unweighted norm, no rotation (:275)
+        segs[n++] = G4aNormRopeSeg{a->k, a->k_norm, a->k_cache, a->Hkv, a->k_norm ? 1u : 0u, 1u, 1u, first};
+        segs[n++] = G4aNormRopeSeg{a->v, nullptr, a->v_cache, a->Hkv, 1u, 0u, 1u, first};
+    }
+    return norm_rope_launch(ctx, segs, n, a->T, a->Dh, a->rotary_dim, a->positions, a->pos0, a->theta, a->eps,
+                            a->cache_row, a->kv_ring_cap);
 }
 
 int g4a_timer_start(g4a_ctx* ctx) {

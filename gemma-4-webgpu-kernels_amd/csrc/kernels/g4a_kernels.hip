@@ -2,3 +2,4 @@
 // every kernel of the attention path, compiled as one translation unit.
 #include "attn_decode.hip"
 #include "attn_prefill.hip"
+#include "norm_rope.hip"

@@ -93,3 +93,28 @@ struct G4aSplitParams {
     uint32_t k0, nkeys, S, Hkv, Dh;
     uint32_t ring_cap, epoch;
 };
+
+// Per-head RMSNorm + half-split partial RoPE over rows of Dh values (the
+// attention producer, g4a_norm_rope). Up to three segments (q, k, v) run in
+// one launch; segment s covers T * heads_s rows, segment-major.
+struct G4aNormRopeSeg {
+    const float* x;     // [T, heads, Dh]
+    const float* w;     // [Dh] RMSNorm weight, or null (unweighted)
+    float* y;           // [T, heads, Dh], or a KV cache [rows, heads, Dh] when `cache`
+    uint32_t heads;
+    uint32_t norm;      // 1: RMSNorm the row
+    uint32_t rope;      // 1: rotate its first rotary_dim dims
+    uint32_t cache;     // 1: token t goes to logical cache row cache_row + t (slot % ring_cap)
+    uint32_t first_t;   // tokens below it are skipped (their ring slots are rewritten by later tokens)
+};
+
+struct G4aNormRopeParams {
+    G4aNormRopeSeg seg[3];
+    const float* freq;      // [rotary_dim / 2]: theta^(-2j/rotary_dim), computed on the host
+    const uint32_t* pos;    // device [T], or null: position pos0 + t
+    uint32_t pos0;
+    uint32_t T, Dh, rotary_dim;
+    uint32_t nseg, total_rows;
+    uint32_t cache_row, ring_cap;
+    float eps;
+};

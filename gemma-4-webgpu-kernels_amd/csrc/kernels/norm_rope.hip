@@ -1,0 +1,135 @@
+// The attention producer for gfx950: per-head RMSNorm and half-split partial
+// RoPE of the q/k projections, the unweighted per-head RMSNorm of v, and the
+// write of the new K/V rows into the layer's cache (linear or ring), in one
+// launch.
+//
+// Replaces, behind the backend trait, the WGSL RMSNORM_ROPE kernel
+// (rust/src/kernels/rmsnorm_rope.wgsl, dispatched by
+// rust/src/backend_wgpu.rs:877-893) and the COPY of the KV append
+// (rust/src/backend_wgpu.rs:1014-1055); the semantics are the CPU
+// composition the trait defines (rust/src/backend.rs:146-154):
+//   rms_norm (rust/src/backend_cpu.rs:149-172): inv = 1/sqrt(ss/Dh + eps),
+//            y = x*inv*w (w optional),
+//   rope     (rust/src/backend_cpu.rs:248-268): for j < rot/2,
+//            freq = theta^(-2j/rot), ang = pos*freq,
+//            out[j] = a*cos - b*sin, out[j + rot/2] = b*cos + a*sin
+//            (a = y[j], b = y[j + rot/2]); dims >= rot pass through,
+// as the model applies them to one attention block (rust/src/model.rs:256-281).
+//
+// One wave per row (token, head) of Dh values; lane l owns dims 4l..4l+3
+// (+256, +512, +768). The sum of squares reduces across the wave (a different
+// order from the reference's sequential sum: a few ulps in inv). Every other
+// operation is the reference's, separately rounded (this file is built with
+// -ffp-contract=off). The frequencies come from the host (libm powf, as Rust's
+// f32::powf on the same platform): a one-ulp difference in freq would move the
+// angle by pos * ulp, i.e. by ~2e-3 rad at position 32768.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "g4a_params.h"
+
+namespace {
+
+constexpr int NR_WAVES = 4;    // rows per workgroup
+constexpr int NR_MAXE = 4;     // float4 groups per lane: Dh <= 1024
+
+__device__ __forceinline__ float nr_wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+
+__device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
+    __shared__ __attribute__((aligned(16))) float stage[NR_WAVES][NR_MAXE * 256];
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const uint32_t row = blockIdx.x * NR_WAVES + w;
+    if (row >= p.total_rows) return;
+    // segment of this row (rows are segment-major: seg s covers T * heads_s rows)
+    int si = 0;
+    uint32_t r = row;
+    while (si + 1 < (int)p.nseg && r >= p.T * p.seg[si].heads) {
+        r -= p.T * p.seg[si].heads;
+        ++si;
+    }
+    const G4aNormRopeSeg& S = p.seg[si];
+    const uint32_t t = r / S.heads, h = r % S.heads;
+    if (t < S.first_t) return;  // its ring slot is taken by a later token of this call
+    const uint32_t Dh = p.Dh;
+    const float* __restrict__ xr = S.x + ((size_t)t * S.heads + h) * Dh;
+    float4 v[NR_MAXE];
+#pragma unroll
+    for (int e = 0; e < NR_MAXE; ++e) {
+        const uint32_t d = 4 * lane + 256 * e;
+        v[e] = d < Dh ? *reinterpret_cast<const float4*>(xr + d) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    if (S.norm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < NR_MAXE; ++e) ss += v[e].x * v[e].x + v[e].y * v[e].y + v[e].z * v[e].z + v[e].w * v[e].w;
+        ss = nr_wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)Dh + p.eps);
+#pragma unroll
+        for (int e = 0; e < NR_MAXE; ++e) {
+            const uint32_t d = 4 * lane + 256 * e;
+            if (d >= Dh) continue;
+            v[e].x = v[e].x * inv;
+            v[e].y = v[e].y * inv;
+            v[e].z = v[e].z * inv;
+            v[e].w = v[e].w * inv;
+            if (S.w) {
+                const float4 wv = *reinterpret_cast<const float4*>(S.w + d);
+                v[e].x = v[e].x * wv.x;
+                v[e].y = v[e].y * wv.y;
+                v[e].z = v[e].z * wv.z;
+                v[e].w = v[e].w * wv.w;
+            }
+        }
+    }
+    if (S.rope && p.rotary_dim) {
+        float* const ys = stage[w];
+#pragma unroll
+        for (int e = 0; e < NR_MAXE; ++e) {
+            const uint32_t d = 4 * lane + 256 * e;
+            if (d < Dh) *reinterpret_cast<float4*>(ys + d) = v[e];
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const uint32_t rot = p.rotary_dim, half = rot / 2;
+        const float pos = (float)(p.pos ? p.pos[t] : p.pos0 + t);
+#pragma unroll
+        for (int e = 0; e < NR_MAXE; ++e) {
+            const uint32_t d0 = 4 * lane + 256 * e;
+            if (d0 >= rot) continue;
+            float o[4] = {v[e].x, v[e].y, v[e].z, v[e].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t d = d0 + i;
+                if (d >= rot) continue;  // pass-through tail
+                const uint32_t j = d < half ? d : d - half;
+                const float a = ys[j], b = ys[j + half];
+                const float ang = pos * p.freq[j];
+                float sn, cs;
+                sincosf(ang, &sn, &cs);
+                o[i] = d < half ? a * cs - b * sn : b * cs + a * sn;
+            }
+            v[e] = make_float4(o[0], o[1], o[2], o[3]);
+        }
+    }
+    size_t orow = (size_t)t;
+    if (S.cache) {
+        const uint64_t lr = (uint64_t)p.cache_row + t;
+        orow = p.ring_cap ? (size_t)(lr % p.ring_cap) : (size_t)lr;
+    }
+    float* const yr = S.y + (orow * S.heads + h) * Dh;
+#pragma unroll
+    for (int e = 0; e < NR_MAXE; ++e) {
+        const uint32_t d = 4 * lane + 256 * e;
+        if (d < Dh) *reinterpret_cast<float4*>(yr + d) = v[e];
+    }
+}
+
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void g4a_norm_rope(G4aNormRopeParams p) { norm_rope_rows(p); }

@@ -46,6 +46,18 @@ class AttnPlan(ctypes.Structure):
     ]
 
 
+class ProducerArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p), ("q_out", ctypes.c_void_p),
+        ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
+        ("T", ctypes.c_uint32), ("Hq", ctypes.c_uint32), ("Hkv", ctypes.c_uint32), ("Dh", ctypes.c_uint32),
+        ("rotary_dim", ctypes.c_uint32), ("positions", _u32p), ("pos0", ctypes.c_uint32),
+        ("cache_row", ctypes.c_uint32), ("kv_ring_cap", ctypes.c_uint32),
+        ("theta", ctypes.c_float), ("eps", ctypes.c_float),
+    ]
+
+
 class DeviceInfo(ctypes.Structure):
     _fields_ = [
         ("device", ctypes.c_int), ("compute_units", ctypes.c_int), ("clock_khz", ctypes.c_int),
@@ -87,6 +99,11 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "g4a_attention_batch": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.c_uint32]),
         "g4a_attention_plan": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.POINTER(AttnPlan)]),
         "g4a_kv_write": (c_int, [ctxp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32]),
+        "g4a_head_norm_rope": (c_int, [ctxp, vp, vp, vp] + [ctypes.c_uint32] * 4 + [_u32p, ctypes.c_uint32,
+                                                                                    ctypes.c_float, ctypes.c_float]),
+        "g4a_rms_norm": (c_int, [ctxp, vp, vp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float]),
+        "g4a_rope": (c_int, [ctxp, vp, vp] + [ctypes.c_uint32] * 4 + [_u32p, ctypes.c_uint32, ctypes.c_float]),
+        "g4a_attn_producer": (c_int, [ctxp, ctypes.POINTER(ProducerArgs)]),
         "g4a_timer_start": (c_int, [ctxp]),
         "g4a_timer_stop": (c_int, [ctxp, ctypes.POINTER(ctypes.c_float)]),
         "g4a_get_device_info": (c_int, [ctxp, ctypes.POINTER(DeviceInfo)]),
@@ -245,6 +262,27 @@ class Context:
 
     def kv_write(self, cache: int, ring_cap: int, row_elems: int, dst_row: int, src: int, n_rows: int) -> None:
         self._check(self.lib.g4a_kv_write(self.handle, cache, ring_cap, row_elems, dst_row, src, n_rows))
+
+    # ---- the attention producer (per-head RMSNorm, partial RoPE, KV write) ----
+    def head_norm_rope(self, x: int, w: int, y: int, *, T, heads, head_dim, rotary_dim, positions=None, pos0=0,
+                       theta, eps) -> None:
+        pa, pp = _u32_array(positions)
+        self._check(self.lib.g4a_head_norm_rope(self.handle, x, w or None, y, T, heads, head_dim, rotary_dim, pp,
+                                                pos0, theta, eps))
+
+    def rope(self, x: int, y: int, *, T, heads, head_dim, rotary_dim, positions=None, pos0=0, theta) -> None:
+        pa, pp = _u32_array(positions)
+        self._check(self.lib.g4a_rope(self.handle, x, y, T, heads, head_dim, rotary_dim, pp, pos0, theta))
+
+    def rms_norm(self, x: int, w: int, y: int, *, rows, dim, eps) -> None:
+        self._check(self.lib.g4a_rms_norm(self.handle, x, w or None, y, rows, dim, eps))
+
+    def attn_producer(self, *, q, k=0, v=0, q_norm=0, k_norm=0, q_out, k_cache=0, v_cache=0, T, Hq, Hkv, Dh,
+                      rotary_dim, positions=None, pos0=0, cache_row=0, ring_cap=0, theta, eps) -> None:
+        pa, pp = _u32_array(positions)
+        a = ProducerArgs(q, k or None, v or None, q_norm or None, k_norm or None, q_out, k_cache or None,
+                         v_cache or None, T, Hq, Hkv, Dh, rotary_dim, pp, pos0, cache_row, ring_cap, theta, eps)
+        self._check(self.lib.g4a_attn_producer(self.handle, ctypes.byref(a)))
 
     def timer_start(self) -> None:
         self._check(self.lib.g4a_timer_start(self.handle))

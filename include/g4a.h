@@ -149,6 +149,60 @@ int g4a_attention_plan(g4a_ctx *ctx, const g4a_attn_args *args, g4a_attn_plan *p
 int g4a_kv_write(g4a_ctx *ctx, float *cache, uint32_t ring_cap, uint32_t row_elems, uint32_t dst_row,
                  const float *src, uint32_t n_rows);
 
+/* ---- the attention producer: per-head RMSNorm, partial RoPE, KV write ----
+ * Rows are (token, head) vectors of head_dim f32 values in [T, heads, head_dim]
+ * layout. positions: host [T] or NULL (then token i has position pos0 + i).
+ * RoPE is the reference's half-split partial rotation of the first rotary_dim
+ * dims (rotary_dim even, <= head_dim; rust/src/backend_cpu.rs:248-268):
+ * freq_j = theta^(-2j/rotary_dim) (libm powf, as the reference), ang = pos*freq_j,
+ * y[j] = a*cos - b*sin, y[j + rotary_dim/2] = b*cos + a*sin. head_dim must be a
+ * multiple of 4, at most 1024. Stream-ordered, like every op. */
+
+/* Backend::head_norm_rope (rust/src/backend.rs:146-154; the wgpu backend's
+ * RMSNORM_ROPE dispatch, rust/src/backend_wgpu.rs:877-893): y = rope(x * inv * w)
+ * per row, inv = 1/sqrt(mean(x^2) + eps) (rust/src/backend_cpu.rs:149-172).
+ * w NULL: unweighted norm. y may alias x. */
+int g4a_head_norm_rope(g4a_ctx *ctx, const float *x, const float *w, float *y, uint32_t T, uint32_t heads,
+                       uint32_t head_dim, uint32_t rotary_dim, const uint32_t *positions, uint32_t pos0,
+                       float theta, float eps);
+/* Backend::rms_norm (rust/src/backend.rs:103-104; rust/src/backend_cpu.rs:149-172) over
+ * `rows` rows of `dim` values (dim % 4 == 0, <= 1024): y = x * inv (* w), w NULL
+ * for the unweighted variant (the per-head V norm, rust/src/model.rs:274-275). */
+int g4a_rms_norm(g4a_ctx *ctx, const float *x, const float *w, float *y, uint32_t rows, uint32_t dim, float eps);
+/* Backend::rope (rust/src/backend.rs:117-118; rust/src/backend_cpu.rs:248-268). */
+int g4a_rope(g4a_ctx *ctx, const float *x, float *y, uint32_t T, uint32_t heads, uint32_t head_dim,
+             uint32_t rotary_dim, const uint32_t *positions, uint32_t pos0, float theta);
+
+/* The attention block's producer in ONE launch (the q/k/v steps of
+ * Gemma4Model::attention, rust/src/model.rs:256-281, followed by the KV append
+ * of KVCache::append_and_read, rust/src/kvcache.rs:49-62):
+ *   q_out = head_norm_rope(q, q_norm)   (rope only when q_norm is NULL);
+ *   K rows = head_norm_rope(k, k_norm)  (rope only when k_norm is NULL) and
+ *   V rows = unweighted per-head RMSNorm of v, written into k_cache / v_cache at
+ *   logical rows cache_row + t: slot (cache_row + t) % kv_ring_cap for a ring,
+ *   row cache_row + t for a linear cache (its capacity is the caller's, as for
+ *   g4a_kv_write; a ring keeps only the call's last kv_ring_cap rows).
+ * k = v = NULL for a layer that reads another layer's cache (rust/src/config.rs:152-159):
+ * then only q is produced. */
+typedef struct g4a_producer_args {
+    const float *q;       /* [T, Hq, Dh] q projection */
+    const float *k;       /* [T, Hkv, Dh] k projection, or NULL */
+    const float *v;       /* [T, Hkv, Dh] v projection, or NULL */
+    const float *q_norm;  /* [Dh] or NULL */
+    const float *k_norm;  /* [Dh] or NULL */
+    float *q_out;         /* [T, Hq, Dh] */
+    float *k_cache;       /* [rows, Hkv, Dh] */
+    float *v_cache;       /* [rows, Hkv, Dh] */
+    uint32_t T, Hq, Hkv, Dh, rotary_dim;
+    const uint32_t *positions; /* host [T] or NULL */
+    uint32_t pos0;
+    uint32_t cache_row;   /* logical cache row of token 0 */
+    uint32_t kv_ring_cap; /* 0: linear cache */
+    float theta, eps;
+} g4a_producer_args;
+
+int g4a_attn_producer(g4a_ctx *ctx, const g4a_producer_args *args);
+
 /* ---- timing (HIP events on the context's stream) ----------------------- */
 int g4a_timer_start(g4a_ctx *ctx);
 /* Records the stop event, waits for it and returns the elapsed milliseconds. */
@@ -156,7 +210,8 @@ int g4a_timer_stop(g4a_ctx *ctx, float *ms);
 
 /* Per-kernel timing: while enabled, every g4a_attention call records a HIP
  * event pair on the context's stream around its main kernel (decode, prefill
- * or generic; not the LSE combine). g4a_kernel_timing_read waits for the
+ * or generic; not the LSE combine), and so does every norm/RoPE/producer
+ * launch. g4a_kernel_timing_read waits for the
  * recorded pairs and returns their summed milliseconds and count, then clears
  * them. At most 4096 pairs are kept per read. Enabling clears old pairs. */
 int g4a_kernel_timing(g4a_ctx *ctx, int enable);

@@ -15,6 +15,9 @@
  *                                                          GEMMA_CPU_THREADS, PAR_MIN_WORK)
  *   oracle_rms_norm    <- rust/src/backend_cpu.rs:149-172 (CpuBackend::rms_norm)
  *   oracle_concat_rows <- rust/src/backend_cpu.rs:352-364 (concat_rows / kv_append)
+ *   oracle_rope        <- rust/src/backend_cpu.rs:248-268 (CpuBackend::rope: half-split
+ *                                                          partial RoPE; libm powf/sinf/cosf
+ *                                                          as Rust's f32::powf / sin_cos)
  *
  * Arithmetic contract (what makes it bit-identical to the Rust oracle):
  *   - every f32 op is a separately rounded IEEE single op: this file must be
@@ -184,6 +187,31 @@ void oracle_rms_norm(const float *x, const float *w, float *y, size_t rows, size
             for (size_t j = 0; j < d; ++j) o[j] = xr[j] * inv * w[j];
         } else {
             for (size_t j = 0; j < d; ++j) o[j] = xr[j] * inv;
+        }
+    }
+}
+
+/* CpuBackend::rope (rust/src/backend_cpu.rs:248-268): x, y [T, heads, head_dim];
+ * for each row and j < rotary_dim/2: freq = theta^(-(2j)/rotary_dim) (powf),
+ * ang = pos * freq, a = x[j], b = x[j + half]: y[j] = a*cos - b*sin,
+ * y[j + half] = b*cos + a*sin; every other dim is copied. */
+void oracle_rope(const float *x, float *y, size_t T, size_t heads, size_t head_dim, size_t rotary_dim,
+                 const uint32_t *positions, float theta) {
+    memcpy(y, x, T * heads * head_dim * sizeof(float));
+    const size_t half = rotary_dim / 2;
+    for (size_t i = 0; i < T; ++i) {
+        const float pos = (float)positions[i];
+        for (size_t h = 0; h < heads; ++h) {
+            const size_t base = (i * heads + h) * head_dim;
+            for (size_t j = 0; j < half; ++j) {
+                const float freq = powf(theta, -(2.0f * (float)j) / (float)rotary_dim);
+                const float ang = pos * freq;
+                const float sn = sinf(ang), cs = cosf(ang);
+                const float a = x[base + j];
+                const float b = x[base + j + half];
+                y[base + j] = a * cs - b * sn;
+                y[base + j + half] = b * cs + a * sn;
+            }
         }
     }
 }

@@ -2,7 +2,10 @@
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
 this module. It restates rust/src/backend_cpu.rs:270-336 (attention),
-:63-91 (par_ranges) and :149-172 (rms_norm); see attn_oracle.c.
+:63-91 (par_ranges), :149-172 (rms_norm) and :248-268 (rope); see
+attn_oracle.c. head_norm_rope and producer are the compositions the reference
+defines on top of them (rust/src/backend.rs:146-154, rust/src/model.rs:256-281,
+rust/src/kvcache.rs:49-62).
 """
 from __future__ import annotations
 
@@ -30,6 +33,8 @@ def lib() -> ctypes.CDLL:
                                            ctypes.c_uint32, ctypes.c_double]
         L.oracle_rms_norm.restype = None
         L.oracle_rms_norm.argtypes = [vp, vp, vp, sz, sz, ctypes.c_float]
+        L.oracle_rope.restype = None
+        L.oracle_rope.argtypes = [vp, vp, sz, sz, sz, sz, vp, ctypes.c_float]
         L.oracle_thread_count.restype = ctypes.c_size_t
         L.oracle_thread_count.argtypes = [sz, ctypes.c_int]
         _lib = L
@@ -85,3 +90,38 @@ def rms_norm(x, w=None, eps=1e-6):
 
 def thread_count(rows: int, requested: int = 0) -> int:
     return int(lib().oracle_thread_count(rows, requested))
+
+
+def rope(x, positions, theta, rotary_dim):
+    """CpuBackend::rope on x [T, heads, head_dim] -> same shape (rust/src/backend_cpu.rs:248-268)."""
+    x = np.ascontiguousarray(x, np.float32)
+    T, heads, dh = x.shape
+    pos = np.ascontiguousarray(positions, np.uint32)
+    assert pos.shape == (T,)
+    y = np.empty_like(x)
+    lib().oracle_rope(x.ctypes.data, y.ctypes.data, T, heads, dh, rotary_dim, pos.ctypes.data, theta)
+    return y
+
+
+def head_norm_rope(x, w, eps, positions, theta, rotary_dim):
+    """Backend::head_norm_rope's default (rust/src/backend.rs:146-154): per-row
+    rms_norm over head_dim (weighted when w is given), then rope."""
+    x = np.ascontiguousarray(x, np.float32)
+    T, heads, dh = x.shape
+    normed = rms_norm(x.reshape(T * heads, dh), w, eps).reshape(T, heads, dh)
+    return rope(normed, positions, theta, rotary_dim)
+
+
+def producer(q, k, v, q_norm, k_norm, positions, theta, rotary_dim, eps):
+    """The q/k/v steps of Gemma4Model::attention (rust/src/model.rs:256-281):
+    q and k through head_norm_rope (rope only without a norm weight), v through
+    the unweighted per-head rms_norm. Returns (q_out, k_rows, v_rows)."""
+    def qk(x, w):
+        return head_norm_rope(x, w, eps, positions, theta, rotary_dim) if w is not None else \
+            rope(x, positions, theta, rotary_dim)
+    q_out = qk(q, q_norm)
+    if k is None:
+        return q_out, None, None
+    T, hkv, dh = k.shape
+    v_rows = rms_norm(np.ascontiguousarray(v, np.float32).reshape(T * hkv, dh), None, eps).reshape(T, hkv, dh)
+    return q_out, qk(k, k_norm), v_rows

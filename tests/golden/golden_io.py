@@ -21,6 +21,7 @@ import numpy as np
 import g4a.synth as synth
 
 GOLDEN_PATH = Path(__file__).resolve().parent / "attention_golden.npz"
+NORM_ROPE_GOLDEN_PATH = Path(__file__).resolve().parent / "norm_rope_golden.npz"
 
 
 @dataclass
@@ -68,5 +69,89 @@ def load_golden() -> dict[str, Case]:
     cases = recipes()
     for name, c in cases.items():
         assert str(data[name + "__hash"]) == input_hash(c), f"{name}: regenerated inputs differ from the fixture's"
+        c.out = data[name + "__out"]
+    return cases
+
+
+# ---- the attention producer: rms_norm, rope, head_norm_rope ----------------
+
+@dataclass
+class NormRopeCase:
+    """op in {"rms_norm", "rope", "head_norm_rope"}; x [T, heads, Dh] (rms_norm: [rows, 1, d])."""
+    op: str
+    x: np.ndarray
+    w: np.ndarray | None
+    positions: np.ndarray
+    theta: float
+    rotary_dim: int
+    eps: float
+    out: np.ndarray | None = None
+
+
+def norm_rope_hash(c: NormRopeCase) -> str:
+    h = hashlib.sha256(c.op.encode())
+    for a in (c.x, c.w if c.w is not None else np.zeros(0, np.float32), c.positions):
+        h.update(np.ascontiguousarray(a).tobytes())
+    h.update(np.array([c.theta, c.rotary_dim, c.eps], np.float64).tobytes())
+    return h.hexdigest()
+
+
+def norm_rope_recipes() -> dict[str, NormRopeCase]:
+    """The reference's own cases, regenerated from its Lcg (rust/tests/common/mod.rs:29-42):
+      - kernel_parity's rmsNorm and rope(partial) (rust/tests/gpu.rs:53-59, :84-90; seed 7,
+        earlier draws skipped by count: linear 17*40 + 23*40 + 40, then rmsNorm 5*48 + 48,
+        elementwise 100 + 100, embed 30*16);
+      - fused_op_parity's head_norm_rope cases (rust/tests/gpu.rs:322-334; seed 33 after
+        add_rms_norm's 5*48 + 5*48 + 48 draws), positions i*7 + 3, theta 1e4, eps 1e-6;
+    and seeded Gaussian Gemma-4 shapes: the sliding layer (Dh 256, theta 1e4, full
+    rotation) and the global layer (Dh 512, theta 1e6, partial_rotary_factor 0.25 -> 128
+    dims, rust/assets/config.json) at positions up to 131071, where the angle is large."""
+    cases: dict[str, NormRopeCase] = {}
+    r = synth.Lcg(7)
+    r.skip(17 * 40 + 23 * 40 + 40)
+    x = r.rand(5 * 48, 1.0).reshape(5, 1, 48)
+    w = r.rand(48, 0.1)
+    cases["kernel_parity_rmsNorm"] = NormRopeCase("rms_norm", x, w, np.zeros(0, np.uint32), 0.0, 0, 1e-6)
+    cases["kernel_parity_rmsNorm_unweighted"] = NormRopeCase("rms_norm", x, None, np.zeros(0, np.uint32), 0.0, 0,
+                                                             1e-6)
+    r.skip(100 + 100 + 30 * 16)
+    x = r.rand(4 * 2 * 16, 1.0).reshape(4, 2, 16)
+    cases["kernel_parity_rope_partial"] = NormRopeCase("rope", x, None, np.array([0, 1, 5, 9], np.uint32), 1e4, 8,
+                                                       0.0)
+    r = synth.Lcg(33)
+    r.skip(5 * 48 + 5 * 48 + 48)
+    for t, heads, dh, rot in [(3, 4, 16, 8), (2, 8, 256, 256), (2, 1, 512, 128)]:
+        x = r.rand(t * heads * dh, 1.0).reshape(t, heads, dh)
+        w = r.rand(dh, 0.1)
+        pos = (np.arange(t, dtype=np.uint32) * 7 + 3).astype(np.uint32)
+        cases[f"fused_op_head_norm_rope_h{heads}_d{dh}_r{rot}"] = NormRopeCase("head_norm_rope", x, w, pos, 1e4, rot,
+                                                                               1e-6)
+    for name, t, heads, dh, theta, rot, p0, seed in [
+        ("gemma_sliding_q_T1_pos32767", 1, 8, 256, 1e4, 256, 32767, 40),
+        ("gemma_global_q_T1_pos32767", 1, 8, 512, 1e6, 128, 32767, 41),
+        ("gemma_global_k_T3_pos131069", 3, 1, 512, 1e6, 128, 131069, 42),
+        ("gemma_sliding_k_T6_pos1000", 6, 1, 256, 1e4, 256, 1000, 43),
+    ]:
+        x = (synth.normal_f32(seed, 0, t * heads * dh) * np.float32(2.0)).reshape(t, heads, dh)
+        w = (np.float32(1.0) + np.float32(0.1) * synth.normal_f32(seed, 1, dh)).astype(np.float32)
+        pos = np.arange(p0, p0 + t, dtype=np.uint32)
+        cases[name] = NormRopeCase("head_norm_rope", x, w, pos, theta, rot, 1e-6)
+    return cases
+
+
+def norm_rope_eval(c: NormRopeCase, oracle) -> np.ndarray:
+    """The oracle's output for a recipe."""
+    if c.op == "rms_norm":
+        return oracle.rms_norm(c.x.reshape(c.x.shape[0], -1), c.w, c.eps).reshape(c.x.shape)
+    if c.op == "rope":
+        return oracle.rope(c.x, c.positions, c.theta, c.rotary_dim)
+    return oracle.head_norm_rope(c.x, c.w, c.eps, c.positions, c.theta, c.rotary_dim)
+
+
+def load_norm_rope_golden() -> dict[str, NormRopeCase]:
+    data = np.load(NORM_ROPE_GOLDEN_PATH, allow_pickle=False)
+    cases = norm_rope_recipes()
+    for name, c in cases.items():
+        assert str(data[name + "__hash"]) == norm_rope_hash(c), f"{name}: regenerated inputs differ from the fixture's"
         c.out = data[name + "__out"]
     return cases

@@ -1,5 +1,6 @@
-"""Writes tests/golden/attention_golden.npz: for every recipe in golden_io, the
-sha256 of its regenerated inputs and the CPU oracle's output on them.
+"""Writes tests/golden/attention_golden.npz and norm_rope_golden.npz: for every
+recipe in golden_io, the sha256 of its regenerated inputs and the CPU oracle's
+output on them.
 
 Run from the repository root after building the oracle:
     python tests/golden/make_golden.py
@@ -14,7 +15,8 @@ sys.path[:0] = [str(HERE), str(REPO / "gemma-4-webgpu-kernels_amd"), str(REPO / 
 import numpy as np  # noqa: E402
 
 import oracle  # noqa: E402
-from golden_io import GOLDEN_PATH, input_hash, recipes  # noqa: E402
+from golden_io import (GOLDEN_PATH, NORM_ROPE_GOLDEN_PATH, input_hash, norm_rope_eval,  # noqa: E402
+                       norm_rope_hash, norm_rope_recipes, recipes)
 
 
 def main():
@@ -26,6 +28,14 @@ def main():
         print(f"{name}: out {out.shape}")
     np.savez_compressed(GOLDEN_PATH, **arrays)
     print("wrote", GOLDEN_PATH, GOLDEN_PATH.stat().st_size, "bytes")
+    arrays = {}
+    for name, c in norm_rope_recipes().items():
+        out = norm_rope_eval(c, oracle)
+        arrays[name + "__out"] = out
+        arrays[name + "__hash"] = np.array(norm_rope_hash(c))
+        print(f"{name}: out {out.shape}")
+    np.savez_compressed(NORM_ROPE_GOLDEN_PATH, **arrays)
+    print("wrote", NORM_ROPE_GOLDEN_PATH, NORM_ROPE_GOLDEN_PATH.stat().st_size, "bytes")
 
 
 if __name__ == "__main__":
