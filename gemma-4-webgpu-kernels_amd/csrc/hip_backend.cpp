@@ -154,6 +154,47 @@ HipTensor HipBackend::attention(const HipTensor& q, const HipTensor& k, const Hi
     return out;
 }
 
+HipTensor HipBackend::rms_norm(const HipTensor& x, const HipTensor* w, float eps) {
+    if (x.shape.empty() || x.ring_cap) bad("rms_norm wants a plain tensor");
+    const size_t d = x.shape.back(), rows = x.size() / std::max<size_t>(d, 1);
+    if (w && w->size() != d) bad("rms_norm: weight of " + std::to_string(w->size()) + " for rows of " + std::to_string(d));
+    HipTensor out = alloc_tensor(x.shape);
+    check(g4a_rms_norm(ctx_, x.data(), w ? w->data() : nullptr, out.data(), uint32_t(rows), uint32_t(d), eps),
+          "g4a_rms_norm");
+    return out;
+}
+
+namespace {
+void check_rows(const HipTensor& x, size_t n_positions, size_t head_dim, size_t heads, const char* op) {
+    if (x.shape.size() != 3 || x.shape[1] != heads || x.shape[2] != head_dim)
+        bad(std::string(op) + " wants x [T, heads, head_dim]; got " + shape_str(x.shape));
+    if (n_positions != x.shape[0]) bad(std::string(op) + ": one position per token");
+}
+}  // namespace
+
+HipTensor HipBackend::rope(const HipTensor& x, const uint32_t* positions, size_t n_positions, float theta,
+                           size_t head_dim, size_t heads, size_t rotary_dim) {
+    check_rows(x, n_positions, head_dim, heads, "rope");
+    HipTensor out = alloc_tensor(x.shape);
+    check(g4a_rope(ctx_, x.data(), out.data(), uint32_t(x.shape[0]), uint32_t(heads), uint32_t(head_dim),
+                   uint32_t(rotary_dim), positions, 0, theta),
+          "g4a_rope");
+    return out;
+}
+
+HipTensor HipBackend::head_norm_rope(const HipTensor& x, const HipTensor& w, float eps, const uint32_t* positions,
+                                     size_t n_positions, float theta, size_t head_dim, size_t heads,
+                                     size_t rotary_dim) {
+    check_rows(x, n_positions, head_dim, heads, "head_norm_rope");
+    if (w.size() != head_dim) bad("head_norm_rope: weight of " + std::to_string(w.size()) + " for head_dim " +
+                                  std::to_string(head_dim));
+    HipTensor out = alloc_tensor(x.shape);
+    check(g4a_head_norm_rope(ctx_, x.data(), w.data(), out.data(), uint32_t(x.shape[0]), uint32_t(heads),
+                             uint32_t(head_dim), uint32_t(rotary_dim), positions, 0, theta, eps),
+          "g4a_head_norm_rope");
+    return out;
+}
+
 HipTensor HipBackend::slice_rows(const HipTensor& x, size_t start, size_t count) {
     if (x.ring_cap) bad("slice_rows of a KV ring");
     if (x.shape.empty() || start + count > x.shape[0]) bad("slice_rows out of range");

@@ -106,6 +106,16 @@ public:
     // --- ops ---
     // q [T,Hq,Dh], k [S,Hkv,Dh], v [S,Hkv,Dv] -> [T, Hq*Dv] (rust/src/backend.rs:119-120)
     HipTensor attention(const HipTensor& q, const HipTensor& k, const HipTensor& v, const AttnOpts& o);
+    // y = x / sqrt(mean(x^2) + eps) * w per row of the last dim; w == nullptr for the
+    // unweighted variant (rust/src/backend.rs:103-104)
+    HipTensor rms_norm(const HipTensor& x, const HipTensor* w, float eps);
+    // half-split partial RoPE on [T, heads, head_dim], rotating the first rotary_dim
+    // dims (rust/src/backend.rs:117-118)
+    HipTensor rope(const HipTensor& x, const uint32_t* positions, size_t n_positions, float theta, size_t head_dim,
+                   size_t heads, size_t rotary_dim);
+    // per-head weighted RMSNorm then RoPE, one launch (rust/src/backend.rs:146-154)
+    HipTensor head_norm_rope(const HipTensor& x, const HipTensor& w, float eps, const uint32_t* positions,
+                             size_t n_positions, float theta, size_t head_dim, size_t heads, size_t rotary_dim);
     // rows [start, start+count) of a [rows, dim] tensor (rust/src/backend.rs:122)
     HipTensor slice_rows(const HipTensor& x, size_t start, size_t count);
     // concatenate along dim 0; a == nullptr copies b (rust/src/backend.rs:125-126)

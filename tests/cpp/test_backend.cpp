@@ -5,6 +5,9 @@
 //
 //   grouped_attention_parity   rust/tests/gpu.rs:262-293 (same cases, Lcg seed 21)
 //   slice/concat/kv_append     rust/tests/gpu.rs:96-120 (three 200-row appends: growth)
+//   norm_rope_parity           kernel_parity's rmsNorm and rope(partial) (rust/tests/gpu.rs:53-59,
+//                              :84-90, Lcg seed 7) and fused_op_parity's head_norm_rope cases
+//                              (rust/tests/gpu.rs:322-334, Lcg seed 33)
 //   kv_cache_decode            prefill chunks + decode steps through KvCache, with a
 //                              sliding layer on a ring (incl. regrowth and wrap-around)
 //                              and a global layer on the growing buffer, every step
@@ -25,6 +28,10 @@ extern "C" int oracle_attention(const float* q, const float* k, const float* v, 
                                 size_t Hq, size_t Hkv, size_t Dh, size_t Dv, const uint32_t* q_pos,
                                 const uint32_t* k_pos, float scale, uint32_t window, float softcap,
                                 int requested_threads);
+
+extern "C" void oracle_rms_norm(const float* x, const float* w, float* y, size_t rows, size_t d, float eps);
+extern "C" void oracle_rope(const float* x, float* y, size_t T, size_t heads, size_t head_dim, size_t rotary_dim,
+                            const uint32_t* positions, float theta);
 
 namespace {
 
@@ -235,6 +242,49 @@ void kv_cache_decode(g4a::HipBackend& b) {
     cache.reset(b);
 }
 
+void norm_rope_parity(g4a::HipBackend& b) {
+    std::printf("norm_rope_parity\n");
+    {
+        Lcg r(7);
+        r.rand(17 * 40 + 23 * 40 + 40, 1.0f);  // kernel_parity's linear draws
+        const size_t t = 5, d = 48;
+        const auto x = r.rand(t * d, 1.0f);
+        const auto w = r.rand(d, 0.1f);
+        std::vector<float> want(t * d);
+        oracle_rms_norm(x.data(), w.data(), want.data(), t, d, 1e-6f);
+        auto gx = b.tensor(x.data(), {t, d});
+        auto gw = b.tensor(w.data(), {d});
+        close("rmsNorm", b.readback(b.rms_norm(gx, &gw, 1e-6f)), want);
+        oracle_rms_norm(x.data(), nullptr, want.data(), t, d, 1e-6f);
+        close("rmsNorm (unweighted)", b.readback(b.rms_norm(gx, nullptr, 1e-6f)), want);
+        r.rand(100 + 100 + 30 * 16, 1.0f);  // elementwise and embed draws
+        const size_t T = 4, heads = 2, dh = 16, rot = 8;
+        const uint32_t pos[4] = {0, 1, 5, 9};
+        const auto xr = r.rand(T * heads * dh, 1.0f);
+        std::vector<float> wr(T * heads * dh);
+        oracle_rope(xr.data(), wr.data(), T, heads, dh, rot, pos, 1e4f);
+        close("rope(partial)", b.readback(b.rope(b.tensor(xr.data(), {T, heads, dh}), pos, T, 1e4f, dh, heads, rot)), wr);
+    }
+    Lcg r(33);
+    r.rand(5 * 48 + 5 * 48 + 48, 1.0f);  // fused_op_parity's add_rms_norm draws
+    const size_t cases[3][4] = {{3, 4, 16, 8}, {2, 8, 256, 256}, {2, 1, 512, 128}};
+    for (const auto& c : cases) {
+        const size_t t = c[0], heads = c[1], dh = c[2], rot = c[3];
+        const auto x = r.rand(t * heads * dh, 1.0f);
+        const auto w = r.rand(dh, 0.1f);
+        std::vector<uint32_t> pos(t);
+        for (size_t i = 0; i < t; ++i) pos[i] = uint32_t(i * 7 + 3);
+        std::vector<float> normed(x.size()), want(x.size());
+        oracle_rms_norm(x.data(), w.data(), normed.data(), t * heads, dh, 1e-6f);
+        oracle_rope(normed.data(), want.data(), t, heads, dh, rot, pos.data(), 1e4f);
+        auto got = b.head_norm_rope(b.tensor(x.data(), {t, heads, dh}), b.tensor(w.data(), {dh}), 1e-6f, pos.data(),
+                                    t, 1e4f, dh, heads, rot);
+        close("head_norm_rope (heads=" + std::to_string(heads) + ", Dh=" + std::to_string(dh) + ", rot=" +
+                  std::to_string(rot) + ")",
+              b.readback(got), want);
+    }
+}
+
 }  // namespace
 
 int main() {
@@ -248,6 +298,7 @@ int main() {
     try {
         grouped_attention_parity(*b);
         copies_and_kv_append(*b);
+        norm_rope_parity(*b);
         kv_cache_decode(*b);
     } catch (const std::exception& e) {
         std::fprintf(stderr, "test_backend: exception: %s\n", e.what());
