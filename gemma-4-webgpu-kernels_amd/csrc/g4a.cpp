@@ -365,7 +365,7 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->combine[1], "g4a_combine_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->generic, "g4a_generic_attention")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->prefill[0], "g4a_prefill2_d256")) return bail(rc);
-    if (int rc = get_fn(ctx, &ctx->prefill[1], "g4a_prefill_d512")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->prefill[1], "g4a_prefill2_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->split_kv, "g4a_split_kv")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->norm_rope, "g4a_norm_rope")) return bail(rc);
     if (hipMalloc(reinterpret_cast<void**>(&ctx->dummy), 4096) != hipSuccess ||
@@ -504,10 +504,12 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
         pp.ring_cap = a->kv_ring_cap;
         pp.window = a->sliding_window;
         pp.scale = a->scale;
-        // head_dim 256: 8 waves (two key parities per 16-row block), scores estimated from
-        // bf16 hi/lo splits of K made by a pre-pass into the workspace; 512: 4 waves
+        // 8-wave workgroups over 8 queries; scores estimated from bf16 hi/lo splits of K,
+        // P.V from fp16 hi/lo splits of V, both made by a pre-pass into the workspace.
+        // head_dim 256: two waves per 16-row block take the even / odd key tiles;
+        // 512: two waves per 16-row block split the head dim
         const bool d512 = a->Dh == 512;
-        if (!d512) {
+        {
             // keys [k_start, k_end) widened to multiples of 16 (the kernel's tile grid);
             // workspace: the V range flag (first 256 bytes), then the K and V splits
             const uint32_t k0 = pl.k_start & ~15u, nkeys = ((pl.k_end + 15u) & ~15u) - k0;
@@ -539,8 +541,8 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
             pp.split_n = nkeys;
             pp.epoch = sp.epoch;
         }
-        return launch(ctx, ctx->prefill[d512 ? 1 : 0], dim3((a->T + 7) / 8, a->Hkv, 1), dim3(d512 ? 256 : 512, 1, 1),
-                      pp, "prefill", true);
+        return launch(ctx, ctx->prefill[d512 ? 1 : 0], dim3((a->T + 7) / 8, a->Hkv, 1), dim3(512, 1, 1), pp, "prefill",
+                      true);
     }
     // split-K flash-decode (+ combine)
     const uint32_t *qd = nullptr, *kd = nullptr;

@@ -8,11 +8,10 @@
 // Per tile a wave computes S^T = K Q^T on the matrix cores (A = K from LDS,
 // B = Q held in registers), so the scores land as lane = row, 4 keys per lane:
 // exactly the A-operand layout of the following P.V product (B = V from LDS),
-// with no transpose. Two kernels:
-//   prefill<DH>       4 waves per workgroup, f32 MFMAs (head_dim 512);
-//   prefill_pair<256> 8 waves, two per row block taking even / odd tiles; scores
-//                     from bf16 hi/lo splits and P.V from fp16 hi/lo splits
-//                     (head_dim 256; K and V pre-split by split_kv).
+// with no transpose. Two 8-wave kernels, both on K and V pre-split by
+// split_kv, scores from bf16 hi/lo splits, P.V from fp16 hi/lo splits:
+//   prefill_pair<256>   two waves per row block take the even / odd key tiles;
+//   prefill_dsplit<512> two waves per row block split the head dim.
 //
 // Exactness. The matrix cores sum the 256/512-term dots in their own order
 // (and the split forms round their inputs), up to ~5e-4 away from the CPU
@@ -31,23 +30,8 @@
 
 namespace {
 
-constexpr float PF_TAU = 6.0f;     // rescoring band of the f32 matrix-core scores (head_dim 512)
-constexpr float PF_TAU_BF = 7.0f;  // rescoring band of the split-bf16 scores (head_dim 256)
+constexpr float PF_TAU_BF = 7.0f;  // rescoring band of the split-bf16 scores
 constexpr float PF_RESCALE = 8.0f;  // e^8 ~ 3e3: probability headroom before O and l are rescaled
-
-template <int DH>
-struct PrefillCfg {
-    static constexpr int BK = 16;                        // keys per tile (one MFMA K-block)
-    static constexpr int KRS = DH + 4;                   // padded K row stride in LDS
-    static constexpr int TILE = BK * KRS + BK * DH;      // floats per tile buffer: K then V
-    static constexpr int LPT = (2 * BK * DH / 4) / 256;  // float4 loads per thread per tile
-    static constexpr int NC = DH / 64;                   // O column groups (x4 MFMA blocks)
-    static constexpr int QT = DH / 16;                   // Q float4 per lane
-    static constexpr int CAP = DH == 256 ? 2048 : 640;   // candidate entries per wave
-    static constexpr int STAGE = (64 + 16) * 36;         // per-wave staging floats at the end (in the tile buffers)
-    static constexpr int SMEM = 2 * TILE + 4 * 2 * CAP + 4 * 16;
-    static_assert(4 * STAGE <= 2 * TILE, "the end-of-kernel staging areas fit in the tile buffers");
-};
 
 __device__ __forceinline__ uint64_t ballot(bool b) { return __ballot(b); }
 __device__ __forceinline__ int lanes_below(uint64_t m) {
@@ -58,479 +42,6 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
-
-template <int DH>
-__device__ __forceinline__ void prefill(const G4aPrefillParams& p) {
-    using C = PrefillCfg<DH>;
-    constexpr int BK = C::BK, KRS = C::KRS, LPT = C::LPT, NC = C::NC, QT = C::QT, CAP = C::CAP;
-    __shared__ __attribute__((aligned(16))) float smem[C::SMEM];
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = lane >> 4, rl = lane & 15;
-    const uint32_t kvh = blockIdx.y;
-    const uint32_t qb = blockIdx.x * 8;
-    const uint32_t qw = qb + 2 * w;
-    const uint32_t h0 = kvh * 8;
-    const size_t row_stride = (size_t)p.Hkv * DH;
-    const float* __restrict__ kbase = p.k + (size_t)kvh * DH;
-    const float* __restrict__ vbase = p.v + (size_t)kvh * DH;
-    uint32_t* const my_keys = reinterpret_cast<uint32_t*>(smem + 2 * C::TILE + w * 2 * CAP);
-    float* const my_s = smem + 2 * C::TILE + w * 2 * CAP + CAP;
-    float* const my_m = smem + 2 * C::TILE + 4 * 2 * CAP + w * 16;
-
-    // visible key-index range [lo, hi) of query i, clamped to [0, S] (S < 2^28)
-    auto key_hi = [&](int64_t i) -> int32_t {
-        const int64_t lim = (int64_t)p.q_pos0 + i - (int64_t)p.k_pos0 + 1;
-        return (int32_t)(lim <= 0 ? 0 : (lim < (int64_t)p.S ? lim : (int64_t)p.S));
-    };
-    auto key_lo = [&](int64_t i) -> int32_t {
-        if (p.window == 0) return 0;
-        const int64_t lo = (int64_t)p.q_pos0 + i - (int64_t)p.k_pos0 - (int64_t)p.window + 1;
-        return (int32_t)(lo <= 0 ? 0 : (lo < (int64_t)p.S ? lo : (int64_t)p.S));
-    };
-    auto prow = [&](uint32_t j) -> size_t { return p.ring_cap ? j % p.ring_cap : j; };
-
-    const uint32_t qlast = min(qb + 7, p.T - 1);
-    const int32_t wg_lo = key_lo(qb), wg_hi = key_hi(qlast);
-    const uint32_t nt = wg_hi > wg_lo ? (uint32_t)((wg_hi - wg_lo + BK - 1) / BK) : 0;
-    const bool wave_valid = qw < p.T;
-    const int32_t w_lo = wave_valid ? key_lo(qw) : 0;
-    const int32_t w_hi = wave_valid ? key_hi(min(qw + 1, p.T - 1)) : 0;
-
-    // this lane's softmax row: query qw + rl/8, head h0 + rl%8
-    const uint32_t myq = qw + (rl >> 3);
-    const bool qvalid = myq < p.T;
-    const int32_t my_lo = key_lo(myq), my_hi = qvalid ? key_hi(myq) : 0;
-    float4 qr[QT];
-    {
-        const float* qrow = p.q + ((size_t)min(myq, p.T - 1) * p.Hq + h0 + (rl & 7)) * DH + 4 * g;
-#pragma unroll
-        for (int t = 0; t < QT; ++t) qr[t] = ld4(qrow + 16 * t);
-    }
-
-    // Tile t holds keys t0 .. t0+BK-1, t0 = wg_lo + t*BK. Thread tid loads, for
-    // i < LPT, the float4 at key t0 + kf(i) and dims df(i) of K (i < LPT/2) or V,
-    // clamped to the last visible key. Physical rows follow the ring
-    // incrementally: ring_base = t0 % ring_cap is advanced per tile, and
-    // t0 + kf - t0 < BK <= ring_cap needs at most one wrap.
-    uint32_t ring_base = p.ring_cap ? (uint32_t)wg_lo % p.ring_cap : 0u;
-    // Thread tid's loads all sit at dims 4*(tid % (DH/4)) of keys
-    // tid/(DH/4) + i*KSTEP: one constant per-lane offset plus a uniform
-    // (scalar) tile base on the common path.
-    constexpr int KSTEP = 1024 / DH;
-    const uint32_t lane_off = (uint32_t)(tid / (DH / 4)) * (uint32_t)row_stride + 4u * (uint32_t)(tid % (DH / 4));
-    auto load_tile = [&](uint32_t t0, uint32_t rbase, float4 (&r)[LPT]) {
-        if (p.ring_cap == 0 && t0 + BK <= (uint32_t)wg_hi) {
-            const float* kt = kbase + (size_t)t0 * row_stride;
-            const float* vt = vbase + (size_t)t0 * row_stride;
-#pragma unroll
-            for (int i = 0; i < LPT / 2; ++i) r[i] = ld4(kt + (size_t)(i * KSTEP) * row_stride + lane_off);
-#pragma unroll
-            for (int i = 0; i < LPT / 2; ++i) r[LPT / 2 + i] = ld4(vt + (size_t)(i * KSTEP) * row_stride + lane_off);
-            return;
-        }
-#pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int f = (tid + 256 * i) % (BK * DH / 4);
-            const uint32_t kc = min(t0 + (uint32_t)(f / (DH / 4)), (uint32_t)wg_hi - 1u);
-            uint32_t row = kc;
-            if (p.ring_cap) {
-                row = rbase + (kc - t0);
-                if (row >= p.ring_cap) row -= p.ring_cap;
-            }
-            const float* base = i < LPT / 2 ? kbase : vbase;
-            r[i] = ld4(base + (size_t)row * row_stride + 4 * (f % (DH / 4)));
-        }
-    };
-    auto store_tile = [&](float* buf, const float4 (&r)[LPT]) {
-#pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int f = (tid + 256 * i) % (BK * DH / 4);
-            float* dst = i < LPT / 2 ? buf + (f / (DH / 4)) * KRS + 4 * (f % (DH / 4))
-                                     : buf + BK * KRS + (f / (DH / 4)) * DH + 4 * (f % (DH / 4));
-            *reinterpret_cast<float4*>(dst) = r[i];
-        }
-    };
-
-    // m_run: the row's running maximum (candidate threshold). m_ref: the
-    // maximum O and l are currently scaled to; it only moves when m_run gets
-    // more than RESCALE above it (a wave-uniform, rare rescale), so the
-    // probabilities e^{s - m_ref} stay below e^RESCALE.
-    float m_run = NEG_INF, m_ref = NEG_INF, l_part = 0.0f;
-    f4v O[NC][4];
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) O[c][e] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-    int cnt = 0;  // wave-uniform number of recorded candidates
-
-    // Publish every row's reference maximum to the wave's m table.
-    auto publish_m = [&](float mref) {
-        if (g == 0) my_m[rl] = mref;
-        wave_sync();
-    };
-    // Drop recorded candidates more than TAU below their row's published maximum.
-    auto compact = [&]() {
-        int nc = 0;
-        for (int base = 0; base < cnt; base += 64) {
-            const int e = base + lane;
-            const bool has = e < cnt;
-            const uint32_t pk = has ? my_keys[e] : 0u;
-            const float sa = has ? my_s[e] : 0.0f;
-            const bool keep = has && sa > my_m[pk >> 28] - PF_TAU;
-            wave_sync();
-            const uint64_t b = ballot(keep);
-            if (keep) {
-                const int pos = nc + lanes_below(b);
-                my_keys[pos] = pk;
-                my_s[pos] = sa;
-            }
-            nc += __builtin_popcountll(b);
-            wave_sync();
-        }
-        cnt = nc;
-    };
-    // Exact rescoring of every recorded candidate and correction of O and l,
-    // against the published maxima (the scale O and l are currently held at).
-    // 64 candidates per pass, lane = candidate:
-    //   1. exact dot in the reference's order (q and k rows from global memory,
-    //      64 dims of both in flight per step);
-    //   2. delta = e^{s_exact - m} - e^{s_approx - m} added to l of its row;
-    //   3. O += Delta V on the matrix cores, Delta[row][cand] = delta if the
-    //      candidate belongs to the row, else 0: K-step s of the 16x16x4 chain
-    //      takes candidates 4s..4s+3 (lane l: A = Delta[l%16][4s + l/16],
-    //      B = V[key(4s + l/16)][64c + 4(l%16) + e]), so each lane loads the V
-    //      float4s it feeds straight from memory.
-    auto flush = [&]() {
-        for (int base = 0; base < cnt; base += 64) {
-            const int e = base + lane;
-            const bool has = e < cnt;
-            const uint32_t pk = has ? my_keys[e] : 0u;
-            const uint32_t rho = pk >> 28, kap = has ? (pk & 0x0fffffffu) : (uint32_t)wg_lo;
-            float delta = 0.0f;
-            {
-                const float* qrow = p.q + ((size_t)min(qw + (rho >> 3), p.T - 1) * p.Hq + h0 + (rho & 7)) * DH;
-                const float* krow = kbase + prow(kap) * row_stride;
-                float dot = 0.0f;
-                for (int d = 0; d < DH; d += 64) {
-                    float4 qa[16], ka[16];
-#pragma unroll
-                    for (int u = 0; u < 16; ++u) {
-                        qa[u] = ld4(qrow + d + 4 * u);
-                        ka[u] = ld4(krow + d + 4 * u);
-                    }
-#pragma unroll
-                    for (int u = 0; u < 16; ++u) {
-                        dot = dot + qa[u].x * ka[u].x;
-                        dot = dot + qa[u].y * ka[u].y;
-                        dot = dot + qa[u].z * ka[u].z;
-                        dot = dot + qa[u].w * ka[u].w;
-                    }
-                }
-                if (has) {
-                    const float m = my_m[rho];
-                    delta = expf(dot * p.scale - m) - expf(my_s[e] - m);
-                }
-            }
-            const int nb = min(64, cnt - base);
-            // l of row rho (lanes with rl == rho hold partial sums of that row)
-            for (int i = 0; i < nb; ++i) {
-                const float di = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(delta), i));
-                const uint32_t ri = __builtin_amdgcn_readlane(rho, i);
-                if (lane == (int)ri) l_part += di;
-            }
-            for (int s4 = 0; s4 < nb; s4 += 4) {
-                const int src = s4 + g;
-                const float dl = __shfl(delta, src, 64);
-                const uint32_t rr = (uint32_t)__shfl((int)rho, src, 64);
-                const uint32_t kk = (uint32_t)__shfl((int)kap, src, 64);
-                const float a = rr == (uint32_t)rl ? dl : 0.0f;
-                const float* vrow = vbase + prow(kk) * row_stride + 4 * rl;
-                float4 vb[NC];
-#pragma unroll
-                for (int c = 0; c < NC; ++c) vb[c] = ld4(vrow + 64 * c);
-#pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].x, O[c][0], 0, 0, 0);
-                    O[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].y, O[c][1], 0, 0, 0);
-                    O[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].z, O[c][2], 0, 0, 0);
-                    O[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].w, O[c][3], 0, 0, 0);
-                }
-            }
-        }
-        cnt = 0;
-    };
-
-    // The same correction at the end of the kernel, when the tile buffers are
-    // free: instead of each lane streaming its own q and k rows (64 scattered
-    // rows per load instruction), the wave stages 32-dim segments of its 16 q
-    // rows and of the 64 candidates' k rows in its LDS area with coalesced
-    // 128-byte reads (8 rows per instruction, two segments in flight), and
-    // each lane runs its sequential dot from LDS. The Delta V products take
-    // their V rows two K-steps ahead.
-    auto flush_staged = [&](float* stage) {
-        constexpr int SR = 36;                 // staged row stride (floats)
-        constexpr int NSEG = DH / 32;
-        float* const kst = stage;              // [64 candidates][SR]
-        float* const qst = stage + 64 * SR;    // [16 rows][SR]
-        const int seg = lane >> 3, part = lane & 7;
-        const float* const q0 = p.q + ((size_t)min(qw, p.T - 1) * p.Hq + h0 + seg) * DH + 4 * part;
-        const float* const q1 = p.q + ((size_t)min(qw + 1, p.T - 1) * p.Hq + h0 + seg) * DH + 4 * part;
-        for (int base = 0; base < cnt; base += 64) {
-            const int e = base + lane;
-            const bool has = e < cnt;
-            const uint32_t pk = has ? my_keys[e] : 0u;
-            const uint32_t rho = pk >> 28, kap = has ? (pk & 0x0fffffffu) : (uint32_t)wg_lo;
-            const float* krow[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t ki = (uint32_t)__shfl((int)kap, 8 * i + seg, 64);
-                krow[i] = kbase + prow(ki) * row_stride + 4 * part;
-            }
-            // two register buffers (A, B) for alternate segments, no runtime indexing
-            float4 kA[8], qA[2], kB[8], qB[2];
-            auto load_seg = [&](int sg, float4 (&kk)[8], float4 (&qq)[2]) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) kk[i] = ld4(krow[i] + 32 * sg);
-                qq[0] = ld4(q0 + 32 * sg);
-                qq[1] = ld4(q1 + 32 * sg);
-            };
-            float dot = 0.0f;
-            auto consume = [&](int sg, float4 (&kk)[8], float4 (&qq)[2]) {
-                wave_sync();  // the previous segment's reads are done
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    *reinterpret_cast<float4*>(kst + (8 * i + seg) * SR + 4 * part) = kk[i];
-                *reinterpret_cast<float4*>(qst + seg * SR + 4 * part) = qq[0];
-                *reinterpret_cast<float4*>(qst + (8 + seg) * SR + 4 * part) = qq[1];
-                if (sg + 2 < NSEG) load_seg(sg + 2, kk, qq);
-                wave_sync();
-                const float* kr = kst + lane * SR;
-                const float* qv = qst + rho * SR;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * u);
-                    const float4 q4 = *reinterpret_cast<const float4*>(qv + 4 * u);
-                    dot = dot + q4.x * k4.x;
-                    dot = dot + q4.y * k4.y;
-                    dot = dot + q4.z * k4.z;
-                    dot = dot + q4.w * k4.w;
-                }
-            };
-            static_assert(NSEG % 2 == 0, "segments are consumed in pairs");
-            load_seg(0, kA, qA);
-            load_seg(1, kB, qB);
-            // not unrolled: the loads of later segments must not be hoisted (registers)
-#pragma unroll 1
-            for (int sg = 0; sg < NSEG; sg += 2) {
-                consume(sg, kA, qA);
-                consume(sg + 1, kB, qB);
-            }
-            float delta = 0.0f;
-            if (has) {
-                const float m = my_m[rho];
-                delta = expf(dot * p.scale - m) - expf(my_s[e] - m);
-            }
-            const int nb = min(64, cnt - base);
-            for (int i = 0; i < nb; ++i) {
-                const float di = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(delta), i));
-                const uint32_t ri = __builtin_amdgcn_readlane(rho, i);
-                if (lane == (int)ri) l_part += di;
-            }
-            float4 vA[NC], vB[NC];
-            auto load_v = [&](int s4, float4 (&vb)[NC]) {
-                const uint32_t kk = (uint32_t)__shfl((int)kap, s4 + g, 64);
-                const float* vrow = vbase + prow(kk) * row_stride + 4 * rl;
-#pragma unroll
-                for (int c = 0; c < NC; ++c) vb[c] = ld4(vrow + 64 * c);
-            };
-            auto apply_v = [&](int s4, const float4 (&vb)[NC]) {
-                const float dl = __shfl(delta, s4 + g, 64);
-                const uint32_t rr = (uint32_t)__shfl((int)rho, s4 + g, 64);
-                const float a = rr == (uint32_t)rl ? dl : 0.0f;
-#pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].x, O[c][0], 0, 0, 0);
-                    O[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].y, O[c][1], 0, 0, 0);
-                    O[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].z, O[c][2], 0, 0, 0);
-                    O[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].w, O[c][3], 0, 0, 0);
-                }
-            };
-            load_v(0, vA);
-            if (4 < nb) load_v(4, vB);
-            for (int s4 = 0; s4 < nb; s4 += 8) {
-                apply_v(s4, vA);
-                if (s4 + 8 < nb) load_v(s4 + 8, vA);
-                if (s4 + 4 < nb) {
-                    apply_v(s4 + 4, vB);
-                    if (s4 + 12 < nb) load_v(s4 + 12, vB);
-                }
-            }
-        }
-        cnt = 0;
-    };
-
-    // ---- software-pipelined tile loop ----
-    // Iteration t holds tiles t and t+1 in the two LDS buffers and tile t+2 in
-    // registers. It issues the score MFMAs of tile t+1 first, so the matrix
-    // cores are busy while the VALU runs tile t's softmax and candidate
-    // bookkeeping (scores of tile t come from the previous iteration), then
-    // the P.V MFMAs of tile t. Two barriers per tile: one before a buffer is
-    // refilled, one after.
-    auto tile_active = [&](uint32_t t) -> bool {
-        const int32_t t0 = wg_lo + (int32_t)(t * BK);
-        return wave_valid && t < nt && t0 < w_hi && t0 + BK > w_lo;
-    };
-    auto tile_rbase = [&](uint32_t rb) -> uint32_t {  // ring base of the next tile
-        if (!p.ring_cap) return 0u;
-        rb += BK;
-        return rb >= p.ring_cap ? rb - p.ring_cap : rb;
-    };
-    auto qk = [&](const float* Kt) -> f4v {
-        f4v S = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-        const float* kr = Kt + rl * KRS + 4 * g;
-#pragma unroll
-        for (int tt = 0; tt < QT; ++tt) {
-            const float4 kk = *reinterpret_cast<const float4*>(kr + 16 * tt);
-            S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.x, qr[tt].x, S, 0, 0, 0);
-            S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.y, qr[tt].y, S, 0, 0, 0);
-            S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, qr[tt].z, S, 0, 0, 0);
-            S = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, qr[tt].w, S, 0, 0, 0);
-        }
-        return S;
-    };
-
-    float4 pre[LPT];
-    f4v Scur = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-    if (nt > 0) {
-        load_tile((uint32_t)wg_lo, ring_base, pre);
-        store_tile(smem, pre);
-        __syncthreads();
-        // registers: tile 1 (tile 0 again when there is no tile 1)
-        const uint32_t rb1 = nt > 1 ? tile_rbase(ring_base) : ring_base;
-        load_tile(nt > 1 ? (uint32_t)wg_lo + BK : (uint32_t)wg_lo, rb1, pre);
-        ring_base = rb1;
-        if (tile_active(0)) Scur = qk(smem);
-    }
-    for (uint32_t t = 0; t < nt; ++t) {
-        const uint32_t t0 = (uint32_t)wg_lo + t * BK;
-        float* const cur = smem + (t & 1) * C::TILE;
-        float* const nxt = smem + ((t + 1) & 1) * C::TILE;
-        // tile t+1 into the other buffer (its previous tile t-1 is done: barrier at the end of t-1)
-        store_tile(nxt, pre);
-        __syncthreads();
-        {
-            // registers: tile t+2 (always issued; past the end it re-reads the last tile)
-            const bool more = t + 2 < nt;
-            const uint32_t rb2 = more ? tile_rbase(ring_base) : ring_base;
-            load_tile(more ? t0 + 2 * BK : (uint32_t)wg_lo + (nt - 1) * BK, rb2, pre);
-            if (more) ring_base = rb2;
-        }
-        const bool act = tile_active(t);
-        const bool act_next = tile_active(t + 1);
-        f4v Snext = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-        if (act_next) Snext = qk(nxt);
-        if (act) {
-            float s[4];
-            bool vis[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int32_t j = (int32_t)t0 + 4 * g + r;
-                vis[r] = j >= my_lo && j < my_hi;
-                s[r] = vis[r] ? Scur[r] * p.scale : NEG_INF;
-            }
-            float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-            tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
-            tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
-            const float mn = fmaxf(m_run, tm);
-
-            // ---- record the keys within TAU of the running maximum ----
-            if (cnt + 4 * 64 > CAP) {
-                publish_m(mn);
-                compact();
-                if (cnt + 4 * 64 > CAP) {
-                    publish_m(m_ref);  // O and l are held at m_ref
-                    flush();
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const bool cand = vis[r] && s[r] > mn - PF_TAU;
-                const uint64_t b = ballot(cand);
-                if (cand) {
-                    const int pos = cnt + lanes_below(b);
-                    my_keys[pos] = ((uint32_t)rl << 28) | (uint32_t)(t0 + 4 * g + r);
-                    my_s[pos] = s[r];
-                }
-                cnt += __builtin_popcountll(b);
-            }
-            m_run = mn;
-
-            // ---- rescale O and l when some row's maximum moved RESCALE above its reference ----
-            if (ballot(mn > m_ref + PF_RESCALE) != 0) {
-                const float corr = (m_ref == NEG_INF) ? 0.0f : expf(m_ref - mn);
-                l_part *= corr;
-                m_ref = mn;
-                // O rows are 4g + r'; their correction factors live in lanes 4g + r'
-                const f4v cr = f4v{__shfl(corr, 4 * g + 0, 64), __shfl(corr, 4 * g + 1, 64),
-                                   __shfl(corr, 4 * g + 2, 64), __shfl(corr, 4 * g + 3, 64)};
-#pragma unroll
-                for (int c = 0; c < NC; ++c)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) O[c][e] *= cr;
-            }
-
-            // ---- probabilities against m_ref and P.V on the matrix cores ----
-            float pr[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? expf(s[r] - m_ref) : 0.0f;
-            l_part += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-            const float* Vt = cur + BK * KRS;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float* vr = Vt + (4 * g + r) * DH + 4 * rl;
-#pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    const float4 vv = *reinterpret_cast<const float4*>(vr + 64 * c);
-                    O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.x, O[c][0], 0, 0, 0);
-                    O[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.y, O[c][1], 0, 0, 0);
-                    O[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.z, O[c][2], 0, 0, 0);
-                    O[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.w, O[c][3], 0, 0, 0);
-                }
-            }
-        }
-        Scur = Snext;
-        __syncthreads();  // every wave is done with buffer t before it is refilled with tile t+2
-    }
-    __syncthreads();  // every wave is done with the tile buffers: they become the staging areas
-    if (!wave_valid) return;  // no barrier follows
-
-    // ---- exact corrections for the keys still within TAU of the final maxima ----
-    publish_m(m_run);
-    compact();
-    publish_m(m_ref);
-    flush_staged(smem + w * (C::STAGE));
-
-    // ---- normalise and write: O row 4g + r' is query qw + row/8, head h0 + row%8 ----
-    float l = l_part;
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = 4 * g + r;
-        const float lr = __shfl(l, row, 64);
-        const float inv = lr > 0.0f ? 1.0f / lr : 0.0f;
-        const uint32_t qi = qw + (row >> 3);
-        if (qi >= p.T) continue;
-        float* orow = p.out + ((size_t)qi * p.Hq + h0 + (row & 7)) * DH + 4 * rl;
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-            *reinterpret_cast<float4*>(orow + 64 * c) =
-                make_float4(O[c][0][r] * inv, O[c][1][r] * inv, O[c][2][r] * inv, O[c][3][r] * inv);
-    }
-}
-
 
 // ---------------------------------------------------------------------------
 // Head-dim 256 prefill with two waves per SIMD. A workgroup is 8 waves over the
@@ -758,9 +269,12 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         cnt = nc;
     };
     // Exact correction of the recorded candidates against the published
-    // maxima (the scale O and l are held at); see prefill<>::flush. The
-    // in-loop form reads q and k rows straight from memory 16 dims at a time
-    // (few registers; it only runs when a list overflows).
+    // maxima (the scale O and l are held at), 64 candidates per pass, lane =
+    // candidate: its exact dot in the reference's order, then
+    // delta = e^{s_exact - m} - e^{s_approx - m} added to its row's l, then
+    // O += Delta V on the matrix cores. The in-loop form reads q and k rows
+    // straight from memory 16 dims at a time (few registers; it only runs when
+    // a list overflows).
     auto delta_and_l = [&](int base, bool has, uint32_t rho, float dot, int e) -> float {
         float delta = 0.0f;
         if (has) {
@@ -775,8 +289,11 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         }
         return delta;
     };
-    // O += Delta V (see prefill<>::flush), V rows DEPTH K-steps ahead
-    // (DEPTH 4 at the end of the kernel, 2 in the loop where registers are short).
+    // O += Delta V with Delta[row][cand] = delta if the candidate belongs to the
+    // row, else 0: K-step s of the 16x16x4 chain takes candidates 4s .. 4s+3
+    // (lane l: A = Delta[l%16][4s + l/16], B = V[key(4s + l/16)][64c + 4(l%16) + e]),
+    // V rows DEPTH K-steps ahead (DEPTH 4 at the end of the kernel, 2 in the
+    // loop where registers are short).
     auto load_v = [&](int s4, uint32_t kap, float4 (&vb)[NC]) {
         const uint32_t kk = (uint32_t)__shfl((int)kap, s4 + g, 64);
         const float* vrow = vbase + prow(kk) * row_stride + 4 * rl;
@@ -1122,11 +639,472 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Head-dim 512 prefill with two waves per SIMD. The split q rows and the O
+// accumulator of a 16-row block take 128 registers each at head_dim 512, more
+// than two waves per SIMD can hold, so a row block is shared by two waves that
+// split the head dim: wave w owns rows 16*(w%4) .. +15 (2 queries x 8 heads)
+// and dims 256*(w/4) .. +255. Per 16-key tile each wave computes its half of
+// the score estimate (bf16 hi/lo splits), the pair adds the halves through LDS
+// in a fixed order (both waves then hold bit-identical scores, maxima,
+// candidate lists and l), and each wave runs P.V (fp16 hi/lo splits) and the
+// exact corrections for its own 256 output columns. Tiles stream into a 2-slot
+// LDS ring with global->LDS copies, one tile ahead.
+template <int DH>
+struct DsplitCfg {
+    static constexpr int BK = 16;
+    static constexpr int HD = DH / 2;                 // dims per wave
+    static constexpr int KRS = DH + 4;                // K split row stride in LDS (4-byte slots)
+    static constexpr int TILE = BK * KRS + BK * DH;   // K rows then V (4 split key quads, or 16 rows)
+    static constexpr int NPR = DH / 256;              // 1 KiB pieces per row
+    static constexpr int NCH = HD / 64;               // O column groups per wave (x4 MFMA blocks)
+    static constexpr int QBH = HD / 32;               // 32-dim K-blocks of a wave's partial score
+    static constexpr int CAP = 256;                   // candidate entries per wave
+    static constexpr int XS = 8 * 64 * 4;             // partial-score exchange [wave][lane][4]
+    static constexpr int STAGE = (64 + 16) * 36;      // per-wave staging floats at the end (in the tile buffers)
+    static constexpr int SMEM = 2 * TILE + XS + 8 * 2 * CAP + 8 * 16;
+    static_assert(8 * STAGE <= 2 * TILE, "the end-of-kernel staging areas fit in the tile buffers");
+    static_assert(BK * NPR == 8 * 4, "a tile is 64 pieces of 1 KiB: 8 per wave");
+    static_assert(SMEM * 4 <= 160 * 1024, "LDS budget of a CU");
+};
+
+template <int DH>
+__device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
+    using C = DsplitCfg<DH>;
+    constexpr int BK = C::BK, HD = C::HD, KRS = C::KRS, NPR = C::NPR, NCH = C::NCH, QBH = C::QBH, CAP = C::CAP;
+    __shared__ __attribute__((aligned(16))) float smem[C::SMEM];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rb = w & 3, dhf = w >> 2;
+    const int g = lane >> 4, rl = lane & 15;
+    const uint32_t kvh = blockIdx.y;
+    const uint32_t qb = blockIdx.x * 8;
+    const uint32_t qw = qb + 2 * rb;
+    const uint32_t h0 = kvh * 8;
+    const size_t row_stride = (size_t)p.Hkv * DH;
+    const float* __restrict__ kbase = p.k + (size_t)kvh * DH;
+    const float* __restrict__ vbase = p.v + (size_t)kvh * DH;
+    float4* const xs = reinterpret_cast<float4*>(smem + 2 * C::TILE);            // [8 waves][64 lanes]
+    uint32_t* const my_keys = reinterpret_cast<uint32_t*>(smem + 2 * C::TILE + C::XS + w * 2 * CAP);
+    float* const my_s = smem + 2 * C::TILE + C::XS + w * 2 * CAP + CAP;
+    float* const my_m = smem + 2 * C::TILE + C::XS + 8 * 2 * CAP + w * 16;
+
+    auto key_hi = [&](int64_t i) -> int32_t {
+        const int64_t lim = (int64_t)p.q_pos0 + i - (int64_t)p.k_pos0 + 1;
+        return (int32_t)(lim <= 0 ? 0 : (lim < (int64_t)p.S ? lim : (int64_t)p.S));
+    };
+    auto key_lo = [&](int64_t i) -> int32_t {
+        if (p.window == 0) return 0;
+        const int64_t lo = (int64_t)p.q_pos0 + i - (int64_t)p.k_pos0 - (int64_t)p.window + 1;
+        return (int32_t)(lo <= 0 ? 0 : (lo < (int64_t)p.S ? lo : (int64_t)p.S));
+    };
+    auto prow = [&](uint32_t j) -> size_t { return p.ring_cap ? j % p.ring_cap : j; };
+
+    const uint32_t qlast = min(qb + 7, p.T - 1);
+    const int32_t wg_lo = key_lo(qb), wg_hi = key_hi(qlast);
+    // tiles start on multiples of BK (the pre-split V quads are aligned to them);
+    // keys of the first tile before wg_lo are masked like any invisible key
+    const int32_t wg_base = wg_lo & ~(BK - 1);
+    const uint32_t nt = wg_hi > wg_lo ? (uint32_t)((wg_hi - wg_base + BK - 1) / BK) : 0;
+    const bool v16 = __builtin_amdgcn_readfirstlane(*p.vflag) != p.epoch;
+    const bool wave_valid = qw < p.T;
+    const int32_t w_lo = wave_valid ? key_lo(qw) : 0;
+    const int32_t w_hi = wave_valid ? key_hi(min(qw + 1, p.T - 1)) : 0;
+    const uint32_t myq = qw + (rl >> 3);
+    const bool qvalid = myq < p.T;
+    const int32_t my_lo = key_lo(myq), my_hi = qvalid ? key_hi(myq) : 0;
+    // this wave's half of the q rows in the B layout of v_mfma_f32_16x16x32_bf16,
+    // split into bf16 hi/lo: lane (g, rl) holds row rl's dims HD*dhf + 32kb + 8g .. +7
+    bf8v qh[QBH], ql[QBH];
+    {
+        const float* qrow = p.q + ((size_t)min(myq, p.T - 1) * p.Hq + h0 + (rl & 7)) * DH + HD * dhf + 8 * g;
+#pragma unroll
+        for (int kb = 0; kb < QBH; ++kb) split8(ld4(qrow + 32 * kb), ld4(qrow + 32 * kb + 4), qh[kb], ql[kb]);
+    }
+    const float* __restrict__ ksbase = p.ksplit + (size_t)kvh * DH;
+
+    // Tile t (keys tile0 .. tile0+BK-1, tile0 = wg_base + t*BK) into buffer t&1:
+    // waves 0-3 copy K split rows 4w .. 4w+3, waves 4-7 V (key quad w-4, or raw
+    // rows 4(w-4) .. +3). K rows past the last visible key re-read it.
+    auto issue_tile = [&](uint32_t t) {
+        float* const buf = smem + (t & 1) * C::TILE;
+        const uint32_t tile0 = (uint32_t)wg_base + t * BK;
+        const uint32_t last = (uint32_t)wg_hi - 1u;
+        if (w < 4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int kf = 4 * w + i;
+                const uint32_t key = min(tile0 + kf, last);
+                const uint32_t ks = min(key - min(key, p.split0), p.split_n - 1u);
+                const float* src = ksbase + (size_t)ks * row_stride + 4 * lane;
+#pragma unroll
+                for (int pc = 0; pc < NPR; ++pc) copy16_to_lds(src + 256 * pc, buf + kf * KRS + 256 * pc);
+            }
+        } else if (v16) {
+            const uint32_t qd = min(tile0 - min(tile0, p.split0), p.split_n - (uint32_t)BK) / 4 + (w - 4);
+            const float* src = p.vsplit + ((size_t)qd * p.Hkv + kvh) * 4 * DH + 4 * lane;
+            float* const dst = buf + BK * KRS + (w - 4) * 4 * DH;
+#pragma unroll
+            for (int pc = 0; pc < 4 * NPR; ++pc) copy16_to_lds(src + 256 * pc, dst + 256 * pc);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int kf = 4 * (w - 4) + i;
+                const float* src = vbase + prow(min(tile0 + kf, last)) * row_stride + 4 * lane;
+#pragma unroll
+                for (int pc = 0; pc < NPR; ++pc) copy16_to_lds(src + 256 * pc, buf + BK * KRS + kf * DH + 256 * pc);
+            }
+        }
+    };
+
+    float m_run = NEG_INF, m_ref = NEG_INF, l_part = 0.0f;
+    f4v O[NCH][4];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) O[c][e] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    int cnt = 0;  // wave-uniform number of recorded candidates (the same in both waves of a pair)
+
+    auto publish_m = [&](float mref) {
+        if (g == 0) my_m[rl] = mref;
+        wave_sync();
+    };
+    // Drop recorded candidates more than TAU below their row's published maximum.
+    auto compact = [&]() {
+        int nc = 0;
+        for (int base = 0; base < cnt; base += 64) {
+            const int e = base + lane;
+            const bool has = e < cnt;
+            const uint32_t pk = has ? my_keys[e] : 0u;
+            const float sa = has ? my_s[e] : 0.0f;
+            const bool keep = has && sa > my_m[pk >> 28] - PF_TAU_BF;
+            wave_sync();
+            const uint64_t b = ballot(keep);
+            if (keep) {
+                const int pos = nc + lanes_below(b);
+                my_keys[pos] = pk;
+                my_s[pos] = sa;
+            }
+            nc += __builtin_popcountll(b);
+            wave_sync();
+        }
+        cnt = nc;
+    };
+    // delta = e^{s_exact - m} - e^{s_approx - m} of candidate e against its row's
+    // published maximum, added to that row's l.
+    auto delta_and_l = [&](int base, bool has, uint32_t rho, float dot, int e) -> float {
+        float delta = 0.0f;
+        if (has) {
+            const float m = my_m[rho];
+            delta = expf(dot * p.scale - m) - expf(my_s[e] - m);
+        }
+        const int nb = min(64, cnt - base);
+        for (int i = 0; i < nb; ++i) {
+            const float di = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(delta), i));
+            const uint32_t ri = __builtin_amdgcn_readlane(rho, i);
+            if (lane == (int)ri) l_part += di;
+        }
+        return delta;
+    };
+    // O += Delta V for this wave's columns: K-step s of the 16x16x4 chain takes
+    // candidates 4s .. 4s+3 (lane l: A = Delta[l%16][4s + l/16], B = V[key(4s + l/16)]
+    // [HD*dhf + 64c + 4(l%16) + e]); V rows straight from memory, two K-steps ahead.
+    auto correct_o = [&](int base, float delta, uint32_t rho, uint32_t kap) {
+        const int nb = min(64, cnt - base);
+        auto load_v = [&](int s4, float4 (&vb)[NCH]) {
+            const uint32_t kk = (uint32_t)__shfl((int)kap, s4 + g, 64);
+            const float* vrow = vbase + prow(kk) * row_stride + HD * dhf + 4 * rl;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) vb[c] = ld4(vrow + 64 * c);
+        };
+        auto apply_v = [&](int s4, const float4 (&vb)[NCH]) {
+            const float dl = __shfl(delta, s4 + g, 64);
+            const uint32_t rr = (uint32_t)__shfl((int)rho, s4 + g, 64);
+            const float a = rr == (uint32_t)rl ? dl : 0.0f;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].x, O[c][0], 0, 0, 0);
+                O[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].y, O[c][1], 0, 0, 0);
+                O[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].z, O[c][2], 0, 0, 0);
+                O[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[c].w, O[c][3], 0, 0, 0);
+            }
+        };
+        float4 vA[NCH], vB[NCH];
+        load_v(0, vA);
+        if (4 < nb) load_v(4, vB);
+        for (int s4 = 0; s4 < nb; s4 += 8) {
+            apply_v(s4, vA);
+            if (s4 + 8 < nb) load_v(s4 + 8, vA);
+            if (s4 + 4 < nb) {
+                apply_v(s4 + 4, vB);
+                if (s4 + 12 < nb) load_v(s4 + 12, vB);
+            }
+        }
+    };
+    // In-loop correction (a list overflowed): exact dots with q and k rows straight
+    // from memory, 16 dims per step (the split q rows stay live in registers).
+    auto flush_light = [&]() {
+        for (int base = 0; base < cnt; base += 64) {
+            const int e = base + lane;
+            const bool has = e < cnt;
+            const uint32_t pk = has ? my_keys[e] : 0u;
+            const uint32_t rho = pk >> 28, kap = has ? (pk & 0x0fffffffu) : (uint32_t)wg_lo;
+            const float* qrow = p.q + ((size_t)min(qw + (rho >> 3), p.T - 1) * p.Hq + h0 + (rho & 7)) * DH;
+            const float* krow = kbase + prow(kap) * row_stride;
+            float dot = 0.0f;
+#pragma unroll 1
+            for (int d = 0; d < DH; d += 16) {
+                float4 qa[4], ka[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    qa[u] = ld4(qrow + d + 4 * u);
+                    ka[u] = ld4(krow + d + 4 * u);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    dot = dot + qa[u].x * ka[u].x;
+                    dot = dot + qa[u].y * ka[u].y;
+                    dot = dot + qa[u].z * ka[u].z;
+                    dot = dot + qa[u].w * ka[u].w;
+                }
+            }
+            const float delta = delta_and_l(base, has, rho, dot, e);
+            correct_o(base, delta, rho, kap);
+        }
+        cnt = 0;
+    };
+    // End-of-kernel correction: 32-dim segments of the wave's 16 q rows and of 64
+    // candidates' k rows are staged in its LDS area with coalesced reads (two
+    // segments in flight), each lane runs its candidate's sequential dot from LDS.
+    auto flush_staged = [&](float* stage) {
+        constexpr int SR = 36;
+        constexpr int NSEG = DH / 32;
+        float* const kst = stage;              // [64 candidates][SR]
+        float* const qst = stage + 64 * SR;    // [16 rows][SR]
+        const int seg = lane >> 3, part = lane & 7;
+        const float* const q0 = p.q + ((size_t)min(qw, p.T - 1) * p.Hq + h0 + seg) * DH + 4 * part;
+        const float* const q1 = p.q + ((size_t)min(qw + 1, p.T - 1) * p.Hq + h0 + seg) * DH + 4 * part;
+        for (int base = 0; base < cnt; base += 64) {
+            const int e = base + lane;
+            const bool has = e < cnt;
+            const uint32_t pk = has ? my_keys[e] : 0u;
+            const uint32_t rho = pk >> 28, kap = has ? (pk & 0x0fffffffu) : (uint32_t)wg_lo;
+            const float* krow[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t ki = (uint32_t)__shfl((int)kap, 8 * i + seg, 64);
+                krow[i] = kbase + prow(ki) * row_stride + 4 * part;
+            }
+            float4 kA[8], qA[2], kB[8], qB[2];
+            auto load_seg = [&](int sg, float4 (&kk)[8], float4 (&qq)[2]) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) kk[i] = ld4(krow[i] + 32 * sg);
+                qq[0] = ld4(q0 + 32 * sg);
+                qq[1] = ld4(q1 + 32 * sg);
+            };
+            float dot = 0.0f;
+            auto consume = [&](int sg, float4 (&kk)[8], float4 (&qq)[2]) {
+                wave_sync();  // the previous segment's reads are done
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    *reinterpret_cast<float4*>(kst + (8 * i + seg) * SR + 4 * part) = kk[i];
+                *reinterpret_cast<float4*>(qst + seg * SR + 4 * part) = qq[0];
+                *reinterpret_cast<float4*>(qst + (8 + seg) * SR + 4 * part) = qq[1];
+                if (sg + 2 < NSEG) load_seg(sg + 2, kk, qq);
+                wave_sync();
+                const float* kr = kst + lane * SR;
+                const float* qv = qst + rho * SR;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * u);
+                    const float4 q4 = *reinterpret_cast<const float4*>(qv + 4 * u);
+                    dot = dot + q4.x * k4.x;
+                    dot = dot + q4.y * k4.y;
+                    dot = dot + q4.z * k4.z;
+                    dot = dot + q4.w * k4.w;
+                }
+            };
+            static_assert(NSEG % 2 == 0, "segments are consumed in pairs");
+            load_seg(0, kA, qA);
+            load_seg(1, kB, qB);
+#pragma unroll 1
+            for (int sg = 0; sg < NSEG; sg += 2) {
+                consume(sg, kA, qA);
+                consume(sg + 1, kB, qB);
+            }
+            const float delta = delta_and_l(base, has, rho, dot, e);
+            correct_o(base, delta, rho, kap);
+        }
+        cnt = 0;
+    };
+
+    auto tile_active = [&](uint32_t t) -> bool {
+        const int32_t t0 = wg_base + (int32_t)(t * BK);
+        return wave_valid && t < nt && t0 < w_hi && t0 + BK > w_lo;
+    };
+    if (nt > 0) issue_tile(0);
+    for (uint32_t t = 0; t < nt; ++t) {
+        wait_vm<0>();   // this wave's copies of tile t have landed (nothing else is in flight)
+        barrier_lds();  // every wave's have; buffer (t+1)&1 and the exchange slots are free
+        if (t + 1 < nt) issue_tile(t + 1);
+        // both waves of a pair share the row block, hence the activity of a tile
+        const bool act = tile_active(t);
+        const int32_t t0 = wg_base + (int32_t)(t * BK);
+        const float* const Kt = smem + (t & 1) * C::TILE;
+        const float* const Vt = Kt + BK * KRS;
+        f4v Sp = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+        if (act) {
+            // this wave's half of S^T = K Q^T from the bf16 splits: Khi Qhi + Klo Qhi + Khi Qlo
+            f4v SA[3];
+#pragma unroll
+            for (int a = 0; a < 3; ++a) SA[a] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+            const float* kr = Kt + rl * KRS + HD * dhf + 8 * g;
+#pragma unroll
+            for (int kb = 0; kb < QBH; ++kb) {
+                const bf8v khi = *reinterpret_cast<const bf8v*>(kr + 32 * kb);
+                const bf8v klo = *reinterpret_cast<const bf8v*>(kr + 32 * kb + 4);
+                SA[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qh[kb], SA[0], 0, 0, 0);
+                SA[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, qh[kb], SA[1], 0, 0, 0);
+                SA[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, ql[kb], SA[2], 0, 0, 0);
+            }
+            Sp = (SA[0] + SA[1]) + SA[2];
+            xs[w * 64 + lane] = make_float4(Sp[0], Sp[1], Sp[2], Sp[3]);
+        }
+        barrier_lds();  // both halves of every active pair are in the exchange slots
+        if (!act) continue;
+        const float4 o4 = xs[(w ^ 4) * 64 + lane];
+        const f4v So = f4v{o4.x, o4.y, o4.z, o4.w};
+        const f4v S = dhf == 0 ? Sp + So : So + Sp;  // the low half first in both waves
+        float s[4];
+        bool vis[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int32_t j = t0 + 4 * g + r;
+            vis[r] = j >= my_lo && j < my_hi;
+            s[r] = vis[r] ? S[r] * p.scale : NEG_INF;
+        }
+        float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
+        tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+        const float mn = fmaxf(m_run, tm);
+
+        // ---- record the keys within TAU of the running maximum ----
+        bool cand[4];
+        uint64_t bal[4];
+        int nnew = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            cand[r] = vis[r] && s[r] > mn - PF_TAU_BF;
+            bal[r] = ballot(cand[r]);
+            nnew += __builtin_popcountll(bal[r]);
+        }
+        if (cnt + nnew > CAP) {
+            publish_m(mn);
+            compact();
+            if (cnt + nnew > CAP) {
+                publish_m(m_ref);  // O and l are held at m_ref
+                flush_light();
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (cand[r]) {
+                const int pos = cnt + lanes_below(bal[r]);
+                my_keys[pos] = ((uint32_t)rl << 28) | (uint32_t)(t0 + 4 * g + r);
+                my_s[pos] = s[r];
+            }
+            cnt += __builtin_popcountll(bal[r]);
+        }
+        m_run = mn;
+
+        // ---- rescale O and l when some row's maximum moved RESCALE above its reference ----
+        if (ballot(mn > m_ref + PF_RESCALE) != 0) {
+            const float corr = (m_ref == NEG_INF) ? 0.0f : expf(m_ref - mn);
+            l_part *= corr;
+            m_ref = mn;
+            const f4v cr = f4v{__shfl(corr, 4 * g + 0, 64), __shfl(corr, 4 * g + 1, 64),
+                               __shfl(corr, 4 * g + 2, 64), __shfl(corr, 4 * g + 3, 64)};
+#pragma unroll
+            for (int c = 0; c < NCH; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) O[c][e] *= cr;
+        }
+
+        // ---- probabilities against m_ref and P.V for this wave's columns ----
+        float pr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? expf(s[r] - m_ref) : 0.0f;
+        l_part += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+        if (v16) {
+            // O += P V on v_mfma_f32_16x16x16_f16: Phi Vhi + Phi Vlo + Plo Vhi. Lane (g, rl)
+            // gives A = P[row rl][keys 4g .. 4g+3] and B = V[keys 4g .. 4g+3][dim
+            // 64 cg + 4rl + e] (cg = NCH*dhf + c): quad g's 16 bytes (4 hi, 4 lo).
+            h4v ah, al;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) split16(pr[r], ah, al, r);
+            const float* const vq = Vt + g * 4 * DH + 4 * rl;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int cg = NCH * dhf + c;
+                    const float4 raw = *reinterpret_cast<const float4*>(vq + 4 * 16 * (4 * cg + e));
+                    h4v bh, bl;
+                    __builtin_memcpy(&bh, &raw.x, 8);
+                    __builtin_memcpy(&bl, &raw.z, 8);
+                    O[c][e] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, O[c][e], 0, 0, 0);
+                    O[c][e] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, O[c][e], 0, 0, 0);
+                    O[c][e] = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, O[c][e], 0, 0, 0);
+                }
+            continue;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float* vr = Vt + (4 * g + r) * DH + HD * dhf + 4 * rl;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const float4 vv = *reinterpret_cast<const float4*>(vr + 64 * c);
+                O[c][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.x, O[c][0], 0, 0, 0);
+                O[c][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.y, O[c][1], 0, 0, 0);
+                O[c][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.z, O[c][2], 0, 0, 0);
+                O[c][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[r], vv.w, O[c][3], 0, 0, 0);
+            }
+        }
+    }
+    wait_vm<0>();
+    __syncthreads();  // every wave is done with the tile buffers: they become the staging areas
+    if (!wave_valid) return;  // no barrier follows
+
+    // ---- exact corrections for the keys still within TAU of the final maxima ----
+    publish_m(m_run);
+    compact();
+    publish_m(m_ref);
+    flush_staged(smem + w * C::STAGE);
+
+    // ---- normalise and write this wave's columns: O row 4g + r' is query qw + row/8, head h0 + row%8 ----
+    float l = l_part;
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = 4 * g + r;
+        const float lr = __shfl(l, row, 64);
+        const float inv = lr > 0.0f ? 1.0f / lr : 0.0f;
+        const uint32_t qi = qw + (row >> 3);
+        if (qi >= p.T) continue;
+        float* orow = p.out + ((size_t)qi * p.Hq + h0 + (row & 7)) * DH + HD * dhf + 4 * rl;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+            *reinterpret_cast<float4*>(orow + 64 * c) =
+                make_float4(O[c][0][r] * inv, O[c][1][r] * inv, O[c][2][r] * inv, O[c][3][r] * inv);
+    }
+}
+
 }  // namespace
 
 extern "C" {
-__global__ __launch_bounds__(256) void g4a_prefill_d256(G4aPrefillParams p) { prefill<256>(p); }
-__global__ __launch_bounds__(256) void g4a_prefill_d512(G4aPrefillParams p) { prefill<512>(p); }
 __global__ __launch_bounds__(512) void g4a_prefill2_d256(G4aPrefillParams p) { prefill_pair<256>(p); }
+__global__ __launch_bounds__(512) void g4a_prefill2_d512(G4aPrefillParams p) { prefill_dsplit<512>(p); }
 __global__ __launch_bounds__(256) void g4a_split_kv(G4aSplitParams p) { split_kv(p); }
 }
