@@ -60,6 +60,7 @@ struct g4a_ctx {
     hipEvent_t ev_staging = nullptr;  // last use of the pinned staging buffer
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
+    hipFunction_t prefill_merge = nullptr;  // merge of the split hd512 prefill blocks
     float* dummy = nullptr;  // 4 KiB of zeros: the load target of idle decode tiles
     uint32_t* pos_dev = nullptr;  // device copies of non-contiguous positions
     size_t pos_dev_cap = 0;       // in u32
@@ -123,6 +124,35 @@ int ensure_workspace(g4a_ctx* ctx, size_t bytes) {
     if (e != hipSuccess) return fail(ctx, G4A_E_NOMEM, "workspace of %zu bytes: %s", want, hipGetErrorString(e));
     ctx->workspace_bytes = want;
     return G4A_OK;
+}
+
+// Query blocks of the head_dim 512 prefill that run as two workgroups, one per
+// half of their key tiles: the trailing blocks (causal masks give later queries
+// more keys) whose tile count exceeds the average over all blocks. Mirrors the
+// kernel's tile range of a block of 8 queries (prefill_dsplit).
+uint32_t prefill_split_blocks(const g4a_attn_args* a, uint32_t q_pos0, uint32_t k_pos0) {
+    const uint32_t NB = (a->T + 7) / 8;
+    if (NB == 0) return 0;
+    auto key_hi = [&](int64_t i) -> int64_t {
+        const int64_t lim = (int64_t)q_pos0 + i - (int64_t)k_pos0 + 1;
+        return lim <= 0 ? 0 : std::min<int64_t>(lim, a->S);
+    };
+    auto key_lo = [&](int64_t i) -> int64_t {
+        if (a->sliding_window == 0) return 0;
+        const int64_t lo = (int64_t)q_pos0 + i - (int64_t)k_pos0 - (int64_t)a->sliding_window + 1;
+        return lo <= 0 ? 0 : std::min<int64_t>(lo, a->S);
+    };
+    std::vector<int64_t> nt(NB);
+    int64_t total = 0;
+    for (uint32_t b = 0; b < NB; ++b) {
+        const int64_t lo = key_lo(8 * int64_t(b)), hi = key_hi(std::min<int64_t>(8 * int64_t(b) + 7, a->T - 1));
+        const int64_t base = lo & ~int64_t(15);
+        nt[b] = hi > lo ? (hi - base + 15) / 16 : 0;
+        total += nt[b];
+    }
+    uint32_t nbig = 0;
+    while (nbig < NB && nt[NB - 1 - nbig] * int64_t(NB) > total) ++nbig;
+    return nbig;
 }
 
 // Stages up to two host position arrays into device memory (stream-ordered).
@@ -366,6 +396,7 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->generic, "g4a_generic_attention")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->prefill[0], "g4a_prefill2_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->prefill[1], "g4a_prefill2_d512")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->prefill_merge, "g4a_prefill_merge_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->split_kv, "g4a_split_kv")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->norm_rope, "g4a_norm_rope")) return bail(rc);
     if (hipMalloc(reinterpret_cast<void**>(&ctx->dummy), 4096) != hipSuccess ||
@@ -511,10 +542,15 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
         const bool d512 = a->Dh == 512;
         {
             // keys [k_start, k_end) widened to multiples of 16 (the kernel's tile grid);
-            // workspace: the V range flag (first 256 bytes), then the K and V splits
+            // workspace: the V range flag (first 256 bytes), then the K and V splits,
+            // then (head_dim 512) the partials of the split query blocks
             const uint32_t k0 = pl.k_start & ~15u, nkeys = ((pl.k_end + 15u) & ~15u) - k0;
             const size_t half = size_t(nkeys) * a->Hkv * a->Dh * sizeof(float);
-            if (int rc = ensure_workspace(ctx, 256 + 2 * half)) return rc;
+            if (d512) pp.nbig = prefill_split_blocks(a, pp.q_pos0, pp.k_pos0);
+            // a split block's partial: 8 waves x (O of 16 rows x 256 dims, then l and m of the rows)
+            const size_t part_bytes = size_t(pp.nbig) * a->Hkv * 2 * 8 * (4 * 16 * 64 + 32) * sizeof(float);
+            const size_t part_off = (256 + 2 * half + 255) & ~size_t(255);
+            if (int rc = ensure_workspace(ctx, part_off + part_bytes)) return rc;
             char* const ws = static_cast<char*>(ctx->workspace);
             if (++ctx->split_epoch == 0) ctx->split_epoch = 1;
             G4aSplitParams sp{};
@@ -540,9 +576,13 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
             pp.split0 = k0;
             pp.split_n = nkeys;
             pp.epoch = sp.epoch;
+            pp.part = reinterpret_cast<float*>(ws + part_off);
         }
-        return launch(ctx, ctx->prefill[d512 ? 1 : 0], dim3((a->T + 7) / 8, a->Hkv, 1), dim3(512, 1, 1), pp, "prefill",
-                      true);
+        if (int rc = launch(ctx, ctx->prefill[d512 ? 1 : 0], dim3((a->T + 7) / 8 + pp.nbig, a->Hkv, 1),
+                            dim3(512, 1, 1), pp, "prefill", true))
+            return rc;
+        if (pp.nbig == 0) return G4A_OK;
+        return launch(ctx, ctx->prefill_merge, dim3(pp.nbig, a->Hkv, 1), dim3(512, 1, 1), pp, "prefill merge");
     }
     // split-K flash-decode (+ combine)
     const uint32_t *qd = nullptr, *kd = nullptr;

@@ -650,6 +650,9 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
 // candidate lists and l), and each wave runs P.V (fp16 hi/lo splits) and the
 // exact corrections for its own 256 output columns. Tiles stream into a 2-slot
 // LDS ring with global->LDS copies, one tile ahead.
+// Causal balance: a query block with more key tiles than the average runs as
+// two workgroups over the two halves of its tiles (p.nbig, see G4aPrefillParams);
+// each writes its partial (O, l, m) and prefill_merge combines them.
 template <int DH>
 struct DsplitCfg {
     static constexpr int BK = 16;
@@ -663,6 +666,7 @@ struct DsplitCfg {
     static constexpr int XS = 8 * 64 * 4;             // partial-score exchange [wave][lane][4]
     static constexpr int STAGE = (64 + 16) * 36;      // per-wave staging floats at the end (in the tile buffers)
     static constexpr int SMEM = 2 * TILE + XS + 8 * 2 * CAP + 8 * 16;
+    static constexpr int PART_WAVE = NCH * 16 * 64 + 2 * 16;  // a wave's partial: O, then l and m of its rows
     static_assert(8 * STAGE <= 2 * TILE, "the end-of-kernel staging areas fit in the tile buffers");
     static_assert(BK * NPR == 8 * 4, "a tile is 64 pieces of 1 KiB: 8 per wave");
     static_assert(SMEM * 4 <= 160 * 1024, "LDS budget of a CU");
@@ -679,7 +683,14 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
     const int rb = w & 3, dhf = w >> 2;
     const int g = lane >> 4, rl = lane & 15;
     const uint32_t kvh = blockIdx.y;
-    const uint32_t qb = blockIdx.x * 8;
+    // work item: the two halves of each of the last nbig query blocks, then the
+    // other blocks, heaviest (latest queries) first
+    const uint32_t NB = (p.T + 7) / 8;
+    const uint32_t item = blockIdx.x;
+    const bool split = item < 2 * p.nbig;
+    const uint32_t half_id = split ? (item & 1u) : 0u;
+    const uint32_t blk = split ? NB - 1 - item / 2 : NB - 1 - p.nbig - (item - 2 * p.nbig);
+    const uint32_t qb = blk * 8;
     const uint32_t qw = qb + 2 * rb;
     const uint32_t h0 = kvh * 8;
     const size_t row_stride = (size_t)p.Hkv * DH;
@@ -707,6 +718,9 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
     // keys of the first tile before wg_lo are masked like any invisible key
     const int32_t wg_base = wg_lo & ~(BK - 1);
     const uint32_t nt = wg_hi > wg_lo ? (uint32_t)((wg_hi - wg_base + BK - 1) / BK) : 0;
+    // this workgroup's tiles [t_begin, t_end): all of them, or one half of a split block
+    const uint32_t t_begin = split && half_id ? nt / 2 : 0u;
+    const uint32_t t_end = split && !half_id ? nt / 2 : nt;
     const bool v16 = __builtin_amdgcn_readfirstlane(*p.vflag) != p.epoch;
     const bool wave_valid = qw < p.T;
     const int32_t w_lo = wave_valid ? key_lo(qw) : 0;
@@ -943,11 +957,11 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
         const int32_t t0 = wg_base + (int32_t)(t * BK);
         return wave_valid && t < nt && t0 < w_hi && t0 + BK > w_lo;
     };
-    if (nt > 0) issue_tile(0);
-    for (uint32_t t = 0; t < nt; ++t) {
+    if (t_begin < t_end) issue_tile(t_begin);
+    for (uint32_t t = t_begin; t < t_end; ++t) {
         wait_vm<0>();   // this wave's copies of tile t have landed (nothing else is in flight)
         barrier_lds();  // every wave's have; buffer (t+1)&1 and the exchange slots are free
-        if (t + 1 < nt) issue_tile(t + 1);
+        if (t + 1 < t_end) issue_tile(t + 1);
         // both waves of a pair share the row block, hence the activity of a tile
         const bool act = tile_active(t);
         const int32_t t0 = wg_base + (int32_t)(t * BK);
@@ -1074,30 +1088,93 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
     }
     wait_vm<0>();
     __syncthreads();  // every wave is done with the tile buffers: they become the staging areas
-    if (!wave_valid) return;  // no barrier follows
 
     // ---- exact corrections for the keys still within TAU of the final maxima ----
-    publish_m(m_run);
-    compact();
-    publish_m(m_ref);
-    flush_staged(smem + w * C::STAGE);
-
-    // ---- normalise and write this wave's columns: O row 4g + r' is query qw + row/8, head h0 + row%8 ----
+    if (wave_valid) {
+        publish_m(m_run);
+        compact();
+        publish_m(m_ref);
+        flush_staged(smem + w * C::STAGE);
+    }
     float l = l_part;
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
+    // O row 4g + r' is query qw + row/8, head h0 + row%8; this wave's columns HD*dhf + 64c + 4rl + e
+    if (!split) {
+        if (!wave_valid) return;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 4 * g + r;
+            const float lr = __shfl(l, row, 64);
+            const float inv = lr > 0.0f ? 1.0f / lr : 0.0f;
+            const uint32_t qi = qw + (row >> 3);
+            if (qi >= p.T) continue;
+            float* orow = p.out + ((size_t)qi * p.Hq + h0 + (row & 7)) * DH + HD * dhf + 4 * rl;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c)
+                *reinterpret_cast<float4*>(orow + 64 * c) =
+                    make_float4(O[c][0][r] * inv, O[c][1][r] * inv, O[c][2][r] * inv, O[c][3][r] * inv);
+        }
+        return;
+    }
+    // ---- one half of a split block: its partial, in the wave's register layout ----
+    const uint32_t bi = kvh * p.nbig + (blk - (NB - p.nbig));  // split block of this kv head
+    float* const mine = p.part + ((size_t)(bi * 2 + half_id) * 8 + w) * C::PART_WAVE;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mine[((c * 4 + e) * 4 + r) * 64 + lane] = O[c][e][r];
+    if (g == 0) {
+        mine[NCH * 16 * 64 + rl] = l;
+        mine[NCH * 16 * 64 + 16 + rl] = m_ref;
+    }
+}
+
+// Merge of the two halves of each split query block of prefill_dsplit:
+// workgroup = (split block, kv head), wave w = the producing waves' (row block,
+// dim half); out = (O0 e^{m0-M} + O1 e^{m1-M}) / (l0 e^{m0-M} + l1 e^{m1-M}).
+template <int DH>
+__device__ __forceinline__ void prefill_merge(const G4aPrefillParams& p) {
+    using C = DsplitCfg<DH>;
+    constexpr int HD = C::HD, NCH = C::NCH;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = tid >> 6;
+    const int rb = w & 3, dhf = w >> 2;
+    const int g = lane >> 4, rl = lane & 15;
+    const uint32_t kvh = blockIdx.y;
+    const uint32_t NB = (p.T + 7) / 8;
+    const uint32_t blk = NB - p.nbig + blockIdx.x;
+    const uint32_t qw = blk * 8 + 2 * rb;
+    const uint32_t h0 = kvh * 8;
+    const uint32_t bi = kvh * p.nbig + blockIdx.x;
+    const float* const p0 = p.part + ((size_t)(bi * 2 + 0) * 8 + w) * C::PART_WAVE;
+    const float* const p1 = p.part + ((size_t)(bi * 2 + 1) * 8 + w) * C::PART_WAVE;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int row = 4 * g + r;
-        const float lr = __shfl(l, row, 64);
-        const float inv = lr > 0.0f ? 1.0f / lr : 0.0f;
         const uint32_t qi = qw + (row >> 3);
         if (qi >= p.T) continue;
+        const float l0 = p0[NCH * 16 * 64 + row], m0 = p0[NCH * 16 * 64 + 16 + row];
+        const float l1 = p1[NCH * 16 * 64 + row], m1 = p1[NCH * 16 * 64 + 16 + row];
+        const float M = fmaxf(m0, m1);
+        const float e0 = (m0 == NEG_INF) ? 0.0f : expf(m0 - M);
+        const float e1 = (m1 == NEG_INF) ? 0.0f : expf(m1 - M);
+        const float L = l0 * e0 + l1 * e1;
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        const float a0 = e0 * inv, a1 = e1 * inv;
         float* orow = p.out + ((size_t)qi * p.Hq + h0 + (row & 7)) * DH + HD * dhf + 4 * rl;
 #pragma unroll
-        for (int c = 0; c < NCH; ++c)
-            *reinterpret_cast<float4*>(orow + 64 * c) =
-                make_float4(O[c][0][r] * inv, O[c][1][r] * inv, O[c][2][r] * inv, O[c][3][r] * inv);
+        for (int c = 0; c < NCH; ++c) {
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int idx = ((c * 4 + e) * 4 + r) * 64 + lane;
+                o[e] = p0[idx] * a0 + p1[idx] * a1;
+            }
+            *reinterpret_cast<float4*>(orow + 64 * c) = make_float4(o[0], o[1], o[2], o[3]);
+        }
     }
 }
 
@@ -1106,5 +1183,6 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
 extern "C" {
 __global__ __launch_bounds__(512) void g4a_prefill2_d256(G4aPrefillParams p) { prefill_pair<256>(p); }
 __global__ __launch_bounds__(512) void g4a_prefill2_d512(G4aPrefillParams p) { prefill_dsplit<512>(p); }
+__global__ __launch_bounds__(512) void g4a_prefill_merge_d512(G4aPrefillParams p) { prefill_merge<512>(p); }
 __global__ __launch_bounds__(256) void g4a_split_kv(G4aSplitParams p) { split_kv(p); }
 }

@@ -71,6 +71,13 @@ struct G4aPrefillParams {
     uint32_t ring_cap, window;
     uint32_t split0, split_n, epoch;
     float scale;
+    // head_dim 512 causal balance: the last `nbig` query blocks (8 queries each)
+    // run as two workgroups over the two halves of their key tiles; each half
+    // writes its partial (O, l, m) to `part` and g4a_prefill_merge_d512 merges
+    // them. Workgroup i runs the split halves first, then the other blocks,
+    // heaviest first (so heavy work starts first).
+    float* part;
+    uint32_t nbig;
 };
 
 // Pre-split keys for the head_dim 256 prefill: keys [k0, k0 + nkeys) (logical,
