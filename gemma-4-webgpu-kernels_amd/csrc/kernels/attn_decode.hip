@@ -65,6 +65,15 @@ __device__ __forceinline__ float score_epilogue(float dot, float scale, float so
 
 typedef float f4v __attribute__((ext_vector_type(4)));  // MFMA accumulator (4 VGPRs)
 
+// Split partials: the acc value of row ih (= query * Hq + head), split s, dim d
+// sits at ((ih * (DH/16) + d/16) * nsplit + s) * 16 + d%16, so the combine
+// block of 16 dims reads one contiguous run over all splits. The (m, l) pairs
+// follow all acc values: [ih][s][2].
+template <int DH>
+__device__ __forceinline__ size_t part_index(size_t ih, uint32_t nsplit, uint32_t s, uint32_t d) {
+    return ((ih * (DH / 16) + d / 16) * nsplit + s) * 16 + (d & 15);
+}
+
 // Sixteen dims (16B .. 16B+15 of a 64-dim stage) of the exact dots of the two
 // heads of a wave, lane = key: dot = ((dot + q[d]*k[d]) + q[d+1]*k[d+1]) + ...,
 // every multiply and add rounded separately, in the CPU reference's order.
@@ -489,7 +498,7 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
                 const float o = merged(NDG * hq + dg, r, es);
                 const int d = g * WD + 64 * dg + lane;
                 if (p.nsplit == 1) p.out[ih * DH + d] = o * inv;
-                else p.part[(ih * p.nsplit + split) * DH + d] = o;
+                else p.part[part_index<DH>(ih, p.nsplit, split, d)] = o;
             }
             if (p.nsplit > 1 && g == 0 && lane == 0) write_ml(ih, M, L);
         }
@@ -779,7 +788,6 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p) {
     }
     const size_t ih = (size_t)qi * p.Hq + h0 + h;
     const float sc = p.nsplit == 1 ? (L > 0.0f ? 1.0f / L : 0.0f) : 1.0f;
-    float* const dst = p.nsplit == 1 ? p.out + ih * DH : p.part + (ih * p.nsplit + split) * DH;
 #pragma unroll
     for (int e = 0; e < ND; ++e) {
         float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -795,7 +803,9 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p) {
         o.y *= sc;
         o.z *= sc;
         o.w *= sc;
-        *reinterpret_cast<float4*>(dst + 256 * e + 4 * lane) = o;
+        const uint32_t d = 256 * e + 4 * lane;
+        float* const dst = p.nsplit == 1 ? p.out + ih * DH + d : p.part + part_index<DH>(ih, p.nsplit, split, d);
+        *reinterpret_cast<float4*>(dst) = o;
     }
     if (p.nsplit > 1 && lane == 0) {
         float* ml = p.part + (size_t)p.T * p.Hq * p.nsplit * DH + (ih * p.nsplit + split) * 2;
@@ -1052,7 +1062,6 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p) {
         const float L = l0 * e0 + l1 * e1;
         const size_t ih = (size_t)qi * p.Hq + h0 + h;
         const float sc = p.nsplit == 1 ? (L > 0.0f ? 1.0f / L : 0.0f) : 1.0f;
-        float* const dst = p.nsplit == 1 ? p.out + ih * DH : p.part + (ih * p.nsplit + split) * DH;
 #pragma unroll
         for (int e = 0; e < ND; ++e) {
             float4 o;
@@ -1060,7 +1069,9 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p) {
             o.y = (a0[e].y * e0 + a1[e].y * e1) * sc;
             o.z = (a0[e].z * e0 + a1[e].z * e1) * sc;
             o.w = (a0[e].w * e0 + a1[e].w * e1) * sc;
-            *reinterpret_cast<float4*>(dst + 256 * e + 4 * lane) = o;
+            const uint32_t d = 256 * e + 4 * lane;
+            float* const dst = p.nsplit == 1 ? p.out + ih * DH + d : p.part + part_index<DH>(ih, p.nsplit, split, d);
+            *reinterpret_cast<float4*>(dst) = o;
         }
         if (p.nsplit > 1 && lane == 0) {
             float* const ml = mlp + (ih * p.nsplit + split) * 2;
@@ -1073,7 +1084,8 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p) {
 // out = sum_s acc_s * e^(m_s - M) / sum_s l_s * e^(m_s - M), M = max_s m_s; 0 when the
 // denominator is 0 (the semantics of rust/src/kernels/attention_combine.wgsl:1-28).
 // One block per (16 output dims, head, query): wide enough that a decode
-// step's partials are read by the whole GPU. The split weights e^(m_s - M) are
+// step's partials are read by the whole GPU; the block's acc values are one
+// contiguous run (part_index). The split weights e^(m_s - M) are
 // computed once per block into LDS; thread (group g, dim i) then sums splits
 // s = g, g + 16, ... with several loads in flight, and the 16 groups reduce
 // through LDS.
@@ -1091,7 +1103,8 @@ __device__ __forceinline__ void combine(const G4aCombineParams& p) {
     const size_t ih = (size_t)blockIdx.z * p.Hq + blockIdx.y;
     const uint32_t d = blockIdx.x * 16 + i;
     const float* __restrict__ ml = p.part + (size_t)p.T * p.Hq * p.nsplit * DH + ih * p.nsplit * 2;
-    const float* __restrict__ acc = p.part + ih * p.nsplit * DH + d;
+    // this block's 16 dims: a contiguous [split][16] run
+    const float* __restrict__ acc = p.part + part_index<DH>(ih, p.nsplit, 0, blockIdx.x * 16) + i;
     const uint32_t ns = p.nsplit;
     float M = NEG_INF;
     for (uint32_t s = tid; s < ns; s += 256) M = fmaxf(M, ml[2 * s]);
@@ -1116,11 +1129,11 @@ __device__ __forceinline__ void combine(const G4aCombineParams& p) {
     for (; s + 16 * (U - 1) < ns; s += 16 * U) {
         float x[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) x[u] = acc[(size_t)(s + 16 * u) * DH];
+        for (int u = 0; u < U; ++u) x[u] = acc[(size_t)(s + 16 * u) * 16];
 #pragma unroll
         for (int u = 0; u < U; ++u) A += x[u] * wgt[s + 16 * u];
     }
-    for (; s < ns; s += 16) A += acc[(size_t)s * DH] * wgt[s];
+    for (; s < ns; s += 16) A += acc[(size_t)s * 16] * wgt[s];
     red[grp][i] = A;
     __syncthreads();
     if (tid < 16) {
