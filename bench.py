@@ -252,6 +252,70 @@ def prefill(ctx, T, Dh, window, steps, warmup):
             "frac_fp32_mfma_peak": fl / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
 
 
+BATCH_CONFIGS = [
+    # name, sequences, context length, head dim, window, ring capacity (0: linear cache)
+    ("batch 64 sliding hd256 ring512 @32768", 64, 32768, 256, 512, 512),
+    ("batch 16 sliding hd256 ring512 @32768", 16, 32768, 256, 512, 512),
+    ("batch 32 global hd512 @4096", 32, 4096, 512, 0, 0),
+    ("batch 8 global hd512 @8192", 8, 8192, 512, 0, 0),
+]
+BATCH_BUST_BYTES = 512 << 20  # K/V copies rotated until a step's working set is this big (past the 256 MB MALL)
+
+
+def batched_decode(ctx, n, L, Dh, window, ring_cap, steps, warmup):
+    """One decode step of n independent sequences (a serving batch at one layer),
+    each a query at position L-1 over its own K/V cache: the batched entry point
+    (g4a_attention_decode_batch, one call per step) against the same n calls
+    issued as single g4a_attention calls (one g4a_attention_batch crossing per
+    step). Wall time per step from HIP events around the steps; kernel time per
+    step = the summed durations of the step's decode and combine launches."""
+    rows = ring_cap or L
+    kv_bytes = 2 * rows * Dh * 4
+    copies = int(min(16, max(2, -(-BATCH_BUST_BYTES // (n * kv_bytes)))))
+    q = ctx.upload(synth.rms_norm_rows(synth.normal_f32(11, 0, n * HQ * Dh).reshape(n, HQ, Dh)))
+    k0 = ctx.upload(synth.rms_norm_rows(synth.normal_f32(11, 1, rows * Dh).reshape(rows, 1, Dh)))
+    v0 = ctx.upload(synth.normal_f32(11, 2, rows * Dh).reshape(rows, 1, Dh))
+    kv = []
+    for _ in range(copies * n):
+        k, v = ctx.malloc(kv_bytes // 2), ctx.malloc(kv_bytes // 2)
+        ctx.d2d(k, k0.ptr, kv_bytes // 2)
+        ctx.d2d(v, v0.ptr, kv_bytes // 2)
+        kv.append((k, v))
+    out = ctx.empty((n, HQ * Dh))
+    qb, ob = HQ * Dh * 4, HQ * Dh * 4
+    steps_calls = []
+    for c in range(copies):
+        steps_calls.append([dict(q=q.ptr + i * qb, k=kv[c * n + i][0], v=kv[c * n + i][1], out=out.ptr + i * ob, T=1,
+                                 S=L, Hq=HQ, Hkv=1, Dh=Dh, Dv=Dh, q_pos0=L - 1, k_pos0=0, window=window,
+                                 ring_cap=ring_cap) for i in range(n)])
+    prepared = [ctx.prepare_batch(c) for c in steps_calls]
+    for i in range(warmup):
+        assert ctx.attention_decode_batch(prepared[i % copies]) == n
+    ctx.sync()
+    ctx.timer_start()
+    for i in range(steps):
+        ctx.attention_decode_batch(prepared[i % copies])
+    ms = ctx.timer_stop() / steps
+    ctx.kernel_timing(True)
+    for i in range(steps):
+        ctx.attention_decode_batch(prepared[i % copies])
+    ctx.sync()
+    kms, _ = ctx.kernel_timing_read()
+    ctx.kernel_timing(False)
+    kms /= steps
+    seq_ms, seq_kms = time_steps(ctx, steps_calls, max(10, steps // 4), min(warmup, 5))
+    for a in (q, k0, v0, out):
+        a.free()
+    for k, v in kv:
+        ctx.free(k)
+        ctx.free(v)
+    b = n * decode_bytes(min(L, window) if window else L, Dh)
+    return {"us_per_step": ms * 1e3, "kernel_us_per_step": kms * 1e3, "GB_s": b / (ms * 1e-3) / 1e9,
+            "kernel_GB_s": b / (kms * 1e-3) / 1e9, "frac_hbm_peak": b / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "bytes_per_step": b, "kv_copies_rotated": copies,
+            "single_calls_us_per_step": seq_ms * 1e3, "speedup_vs_single_calls": seq_ms / ms}
+
+
 def load_traffic():
     p = REPO / "profiles" / "decode_hd512_s32768_traffic.json"
     if p.exists():
@@ -269,7 +333,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="headline decode only (no extras, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "schedule", "producer"], default=None,
+    ap.add_argument("--only", choices=["prefill", "schedule", "producer", "batch"], default=None,
                     help="run only these extra workloads (for profiling) and print their JSON line")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="first run 3 device-to-device copies of MIB MiB (the reference dispatch for "
@@ -289,6 +353,10 @@ def main(argv=None):
         if args.only == "prefill":
             for name, T, Dh, W in PREFILL_CONFIGS:
                 out[name] = prefill(ctx, T, Dh, W, steps=args.steps, warmup=args.warmup)
+                print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
+        elif args.only == "batch":
+            for name, n, L, Dh, W, cap in BATCH_CONFIGS:
+                out[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=args.steps, warmup=args.warmup)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         elif args.only == "producer":
             for name, T, Dh, theta, rot, pos0, cap in PRODUCER_CONFIGS:
@@ -380,6 +448,9 @@ def main(argv=None):
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
         for name, T, Dh, theta, rot, pos0, cap in PRODUCER_CONFIGS:
             extras[name] = producer(ctx, T, Dh, theta, rot, pos0, cap, steps=50)
+            print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
+        for name, n, L, Dh, W, cap in BATCH_CONFIGS:
+            extras[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=50, warmup=10)
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
         extras["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=20, warmup=3)
         print(f"[bench] schedule: {extras['configs[4] 35-layer schedule @32768']}", file=sys.stderr, flush=True)

@@ -28,8 +28,12 @@ constexpr uint32_t TILE = 64;
 constexpr uint32_t PREFILL_MIN_T = 16;
 // Largest split-K count the LSE combine kernel takes (its LDS weight table).
 constexpr uint32_t MAX_SPLITS = 1024;
+// Split counts merged by the one-block-per-head combine kernel (combine_rows).
+constexpr uint32_t COMBINE_ROW_SPLITS = 64;
 // Keys per 4-wave workgroup of the short-context decode kernel (two 16-key tiles).
 constexpr uint32_t SHORT_KEYS = 32;
+// Most visible keys of a batched decode step (1024 splits of the short kernel).
+constexpr uint32_t BATCH_MAX_KEYS = SHORT_KEYS * MAX_SPLITS;
 
 std::string g_create_error;
 
@@ -42,6 +46,14 @@ struct g4a_ctx {
     hipFunction_t decode[2][2][2] = {};  // [dh512][group8][explicit key positions]
     hipFunction_t combine[2] = {nullptr, nullptr};                          // [dh512]
     hipFunction_t decode_short[2] = {nullptr, nullptr};  // [dh512]
+    hipFunction_t decode_batch[2] = {nullptr, nullptr};   // [dh512] short decode over many sequences
+    hipFunction_t decode_wave_batch[2] = {nullptr, nullptr};  // [dh512] streaming decode over many sequences
+    hipFunction_t combine_batch[2] = {nullptr, nullptr};  // [dh512]
+    hipFunction_t combine_rows[2] = {nullptr, nullptr};        // [dh512] combine of <= 64 splits
+    hipFunction_t combine_rows_batch[2] = {nullptr, nullptr};  // [dh512]
+    // batched decode tuning (G4A_BATCH_KERNEL=short|wave, G4A_BATCH_KEYS_PER_SPLIT=n): for comparisons
+    int batch_kernel = 0;  // 0 auto, 1 short, 2 streaming
+    uint32_t batch_kps = 0;  // streaming split size; 0 auto
     bool short_decode = true;  // G4A_DECODE_SHORT=0 turns the short-context kernel off (for comparisons)
     hipFunction_t generic = nullptr;
     hipFunction_t prefill[2] = {nullptr, nullptr};                          // [dh512]
@@ -391,6 +403,19 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->decode_short[0], "g4a_decode_short_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_short[1], "g4a_decode_short_d512")) return bail(rc);
     if (const char* env = getenv("G4A_DECODE_SHORT")) ctx->short_decode = atoi(env) != 0;
+    if (int rc = get_fn(ctx, &ctx->decode_batch[0], "g4a_decode_short_batch_d256")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->decode_batch[1], "g4a_decode_short_batch_d512")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->decode_wave_batch[0], "g4a_decode_wave_batch_d256")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->decode_wave_batch[1], "g4a_decode_wave_batch_d512")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->combine_batch[0], "g4a_combine_batch_d256")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->combine_batch[1], "g4a_combine_batch_d512")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->combine_rows[0], "g4a_combine_rows_d256")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->combine_rows[1], "g4a_combine_rows_d512")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->combine_rows_batch[0], "g4a_combine_rows_batch_d256")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->combine_rows_batch[1], "g4a_combine_rows_batch_d512")) return bail(rc);
+    if (const char* env = getenv("G4A_BATCH_KERNEL"))
+        ctx->batch_kernel = !strcmp(env, "short") ? 1 : !strcmp(env, "wave") ? 2 : 0;
+    if (const char* env = getenv("G4A_BATCH_KEYS_PER_SPLIT")) ctx->batch_kps = uint32_t(strtoul(env, nullptr, 10));
     if (int rc = get_fn(ctx, &ctx->combine[0], "g4a_combine_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->combine[1], "g4a_combine_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->generic, "g4a_generic_attention")) return bail(rc);
@@ -627,8 +652,13 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
     }
     if (pl.splits > 1) {
         G4aCombineParams cp{dp.part, a->out, a->T, a->Hq, pl.splits, a->Dh};
-        if (int rc = launch(ctx, ctx->combine[d512], dim3(a->Dh / 16, a->Hq, a->T), dim3(256, 1, 1), cp, "combine"))
+        if (pl.splits <= COMBINE_ROW_SPLITS) {
+            if (int rc = launch(ctx, ctx->combine_rows[d512], dim3(a->Hq, a->T, 1), dim3(256, 1, 1), cp, "combine"))
+                return rc;
+        } else if (int rc = launch(ctx, ctx->combine[d512], dim3(a->Dh / 16, a->Hq, a->T), dim3(256, 1, 1), cp,
+                                   "combine")) {
             return rc;
+        }
     }
     return G4A_OK;
 }
@@ -638,6 +668,127 @@ int g4a_attention_batch(g4a_ctx* ctx, const g4a_attn_args* args, uint32_t n) {
     if (n && !args) return fail(ctx, G4A_E_ARG, "null args");
     for (uint32_t i = 0; i < n; ++i)
         if (int rc = g4a_attention(ctx, &args[i])) return rc;
+    return G4A_OK;
+}
+
+int g4a_attention_decode_batch(g4a_ctx* ctx, const g4a_attn_args* args, uint32_t n, uint32_t* n_batched) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (n_batched) *n_batched = 0;
+    if (n == 0) return G4A_OK;
+    if (!args) return fail(ctx, G4A_E_ARG, "null args");
+    // every call is checked before anything is enqueued
+    std::vector<Analysis> an(n);
+    for (uint32_t i = 0; i < n; ++i)
+        if (int rc = analyse(ctx, &args[i], &an[i], true)) return fail(ctx, rc, "call %u: %s", i, ctx->err.c_str());
+    // the batched calls: single-query decode steps of the first such call's shape
+    const g4a_attn_args* ref = nullptr;
+    std::vector<uint32_t> batch;
+    for (uint32_t i = 0; i < n; ++i) {
+        const g4a_attn_args& a = args[i];
+        const Analysis& r = an[i];
+        if (a.T != 1 || !r.fast_shape || !r.k_contig || a.splits != 0 || a.Hq != 8 * a.Hkv) continue;
+        if (r.plan.kernel != G4A_KERNEL_DECODE && r.plan.kernel != G4A_KERNEL_DECODE_SHORT) continue;
+        if (r.plan.k_end - r.plan.k_start > BATCH_MAX_KEYS) continue;
+        if (!ref) ref = &a;
+        if (a.Hq != ref->Hq || a.Hkv != ref->Hkv || a.Dh != ref->Dh || a.sliding_window != ref->sliding_window ||
+            a.kv_ring_cap != ref->kv_ring_cap || memcmp(&a.scale, &ref->scale, sizeof(float)) != 0 ||
+            memcmp(&a.attn_softcap, &ref->attn_softcap, sizeof(float)) != 0)
+            continue;
+        batch.push_back(i);
+    }
+    const uint64_t cus = uint64_t(std::max(ctx->cu_count, 1));
+    // Launches of up to G4A_BATCH_SEQ sequences. A launch whose 32-key splits fit
+    // one short-kernel workgroup per CU runs the short kernel; otherwise the
+    // streaming kernel with 64-key-multiple splits sized for one 8-wave
+    // workgroup per CU over the launch's keys.
+    struct Launch {
+        uint32_t first, count, kps, max_split;
+        bool wave, rows, wide;  // streaming kernel; combines of <= 64 / more splits
+        size_t part;  // floats
+    };
+    std::vector<Launch> launches;
+    size_t part_floats = 0;
+    for (uint32_t c0 = 0; c0 < batch.size(); c0 += G4A_BATCH_SEQ) {
+        Launch L{c0, std::min<uint32_t>(G4A_BATCH_SEQ, uint32_t(batch.size()) - c0), SHORT_KEYS, 0, false, false,
+                 false, part_floats};
+        uint64_t short_wgs = 0, keys = 0;
+        uint32_t max_keys = 0;
+        for (uint32_t j = L.first; j < L.first + L.count; ++j) {
+            const uint32_t nk = an[batch[j]].plan.k_end - an[batch[j]].plan.k_start;
+            short_wgs += (nk + SHORT_KEYS - 1) / SHORT_KEYS;
+            keys += nk;
+            max_keys = std::max(max_keys, nk);
+        }
+        if (ctx->batch_kernel == 2 || (ctx->batch_kernel == 0 && short_wgs * ref->Hkv > cus)) {
+            L.wave = true;
+            uint64_t kps = ctx->batch_kps ? ctx->batch_kps : (keys * ref->Hkv + cus - 1) / cus;
+            kps = std::max<uint64_t>(kps, (max_keys + MAX_SPLITS - 1) / MAX_SPLITS);
+            L.kps = uint32_t((std::max<uint64_t>(kps, 1) + TILE - 1) / TILE * TILE);
+        }
+        for (uint32_t j = L.first; j < L.first + L.count; ++j) {
+            const uint32_t nk = an[batch[j]].plan.k_end - an[batch[j]].plan.k_start;
+            const uint32_t ns = (nk + L.kps - 1) / L.kps;
+            L.max_split = std::max(L.max_split, ns);
+            if (ns > 1) {
+                (ns <= COMBINE_ROW_SPLITS ? L.rows : L.wide) = true;
+                part_floats += (size_t(ref->Hq) * ns * (ref->Dh + 2) + 63) & ~size_t(63);
+            }
+        }
+        launches.push_back(L);
+    }
+    if (part_floats > 0xFFFFFFFFull) return fail(ctx, G4A_E_SHAPE, "batched decode partials exceed 2^32 floats");
+    if (part_floats)
+        if (int rc = ensure_workspace(ctx, part_floats * sizeof(float))) return rc;
+    const int d512 = ref && ref->Dh == 512 ? 1 : 0;
+    for (const Launch& L : launches) {
+        G4aBatchParams bp{};
+        bp.part = static_cast<float*>(ctx->workspace);
+        bp.dummy = ctx->dummy;
+        bp.Hq = ref->Hq;
+        bp.Hkv = ref->Hkv;
+        bp.keys_per_split = L.kps;
+        bp.ring_cap = ref->kv_ring_cap;
+        bp.window = ref->sliding_window;
+        bp.scale = ref->scale;
+        bp.softcap = ref->attn_softcap;
+        size_t off = L.part;
+        for (uint32_t j = 0; j < L.count; ++j) {
+            const g4a_attn_args& a = args[batch[L.first + j]];
+            const g4a_attn_plan& pl = an[batch[L.first + j]].plan;
+            G4aSeqDesc& d = bp.seq[j];
+            d.q = a.q;
+            d.k = a.k;
+            d.v = a.v;
+            d.out = a.out;
+            d.k_start = pl.k_start;
+            d.k_end = pl.k_end;
+            // key j sits at position k_pos0 + j; the kernel takes positions relative to k_pos0
+            // (the visible keys end at or before the query, so q_pos >= k_pos0)
+            d.q_pos = (a.q_pos ? a.q_pos[0] : a.q_pos0) - (a.k_pos ? a.k_pos[0] : a.k_pos0);
+            const uint32_t ns = (pl.k_end - pl.k_start + L.kps - 1) / L.kps;
+            d.part = uint32_t(ns > 1 ? off : 0);
+            if (ns > 1) off += (size_t(ref->Hq) * ns * (ref->Dh + 2) + 63) & ~size_t(63);
+        }
+        hipFunction_t f = L.wave ? ctx->decode_wave_batch[d512] : ctx->decode_batch[d512];
+        if (int rc = launch(ctx, f, dim3(L.max_split, L.count, bp.Hkv), dim3(L.wave ? 512 : 256, 1, 1), bp,
+                            "batched decode", true))
+            return rc;
+        if (L.rows)
+            if (int rc = launch(ctx, ctx->combine_rows_batch[d512], dim3(bp.Hq, L.count, 1), dim3(256, 1, 1), bp,
+                                "batched combine", true))
+                return rc;
+        if (L.wide)
+            if (int rc = launch(ctx, ctx->combine_batch[d512], dim3(ref->Dh / 16, bp.Hq, L.count), dim3(256, 1, 1), bp,
+                                "batched combine", true))
+                return rc;
+    }
+    // the rest, one call at a time
+    std::vector<bool> in_batch(n, false);
+    for (uint32_t i : batch) in_batch[i] = true;
+    for (uint32_t i = 0; i < n; ++i)
+        if (!in_batch[i])
+            if (int rc = g4a_attention(ctx, &args[i])) return rc;
+    if (n_batched) *n_batched = uint32_t(batch.size());
     return G4A_OK;
 }
 

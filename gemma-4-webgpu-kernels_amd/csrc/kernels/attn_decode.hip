@@ -547,7 +547,7 @@ struct WaveCfg {
 };
 
 template <int DH, bool KPOS>
-__device__ __forceinline__ void decode_wave(const G4aDecodeParams& p) {
+__device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t split, uint32_t qi) {
     using C = WaveCfg<DH>;
     constexpr int GROUP = C::GROUP, KEYS = C::KEYS, BUF = C::BUF, NB = C::NB, AHEAD = C::AHEAD, LPT = C::LPT,
                   NKS = C::NKS, KPC = C::KPC, NCH = C::NCH, ND = C::ND;
@@ -565,7 +565,7 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int key = lane & 15;  // score phase: key of the wave tile
     const int hp = lane >> 4;   // score phase: heads 2hp, 2hp+1
-    const uint32_t split = blockIdx.x, qi = blockIdx.y, kvh = blockIdx.z;
+    const uint32_t kvh = blockIdx.z;
     const uint32_t qpos = p.q_pos ? p.q_pos[qi] : p.q_pos0 + qi;
     const uint32_t ks = p.k_start + split * p.keys_per_split;
     const uint32_t ke = min(ks + p.keys_per_split, p.k_end);
@@ -903,7 +903,7 @@ struct ShortCfg {
 };
 
 template <int DH>
-__device__ __forceinline__ void decode_short(const G4aDecodeParams& p) {
+__device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t split, uint32_t qi) {
     using C = ShortCfg<DH>;
     constexpr int GROUP = C::GROUP, KEYS = C::KEYS, RS = C::RS, QRS = C::QRS, NRC = C::NRC, ND = C::ND, NB = C::NB;
 
@@ -919,7 +919,7 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p) {
     const int tile = w >> 1, half = w & 1;
     const int r = lane >> 4;     // score phase: head 4 * half + r
     const int key = lane & 15;   // score phase: key of the tile
-    const uint32_t split = blockIdx.x, qi = blockIdx.y, kvh = blockIdx.z;
+    const uint32_t kvh = blockIdx.z;
     const uint32_t qpos = p.q_pos ? p.q_pos[qi] : p.q_pos0 + qi;
     const uint32_t t0 = p.k_start + split * p.keys_per_split + tile * KEYS;
     const uint32_t nk = t0 < p.k_end ? min((uint32_t)KEYS, p.k_end - t0) : 0u;
@@ -1092,7 +1092,7 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p) {
 constexpr int COMBINE_MAX_SPLITS = 1024;
 
 template <int DH>
-__device__ __forceinline__ void combine(const G4aCombineParams& p) {
+__device__ __forceinline__ void combine(const G4aCombineParams& p, uint32_t qi) {
     __shared__ float wgt[COMBINE_MAX_SPLITS];
     __shared__ float red[16][17];
     __shared__ float redm[4], redl[4];
@@ -1100,7 +1100,7 @@ __device__ __forceinline__ void combine(const G4aCombineParams& p) {
     const int lane = tid & 63;
     const int w = tid >> 6;
     const int i = tid & 15, grp = tid >> 4;
-    const size_t ih = (size_t)blockIdx.z * p.Hq + blockIdx.y;
+    const size_t ih = (size_t)qi * p.Hq + blockIdx.y;
     const uint32_t d = blockIdx.x * 16 + i;
     const float* __restrict__ ml = p.part + (size_t)p.T * p.Hq * p.nsplit * DH + ih * p.nsplit * 2;
     // this block's 16 dims: a contiguous [split][16] run
@@ -1142,6 +1142,113 @@ __device__ __forceinline__ void combine(const G4aCombineParams& p) {
         for (int g = 0; g < 16; ++g) A += red[g][tid];
         p.out[ih * DH + d] = L > 0.0f ? A / L : 0.0f;
     }
+}
+
+// The same merge for up to COMBINE_ROW_SPLITS splits, one block per (head,
+// query): wave 0 computes the split weights into LDS, then thread t sums dims
+// t (+256) over the splits in split order, 8 loads in flight. A block per 16
+// dims would leave most of its threads idle at these split counts.
+constexpr uint32_t COMBINE_ROW_SPLITS = 64;
+
+template <int DH>
+__device__ __forceinline__ void combine_rows(const G4aCombineParams& p, uint32_t h, uint32_t qi) {
+    __shared__ float wgt[COMBINE_ROW_SPLITS];
+    __shared__ float lsum;
+    const int tid = threadIdx.x;
+    const size_t ih = (size_t)qi * p.Hq + h;
+    const uint32_t ns = p.nsplit;
+    if (tid < 64) {
+        const float* __restrict__ ml = p.part + (size_t)p.T * p.Hq * ns * DH + ih * ns * 2;
+        const bool on = (uint32_t)tid < ns;
+        const float ms = on ? ml[2 * tid] : NEG_INF;
+        const float M = wave_max(ms);
+        const float e = (ms == NEG_INF) ? 0.0f : expf(ms - M);
+        if (on) wgt[tid] = e;
+        const float L = wave_sum(on ? ml[2 * tid + 1] * e : 0.0f);
+        if (tid == 0) lsum = L;
+    }
+    __syncthreads();
+    const float L = lsum;
+#pragma unroll
+    for (int e = 0; e < DH / 256; ++e) {
+        const uint32_t d = 256 * e + tid;
+        const float* __restrict__ acc = p.part + part_index<DH>(ih, ns, 0, d);  // split s at acc[16 s]
+        float A = 0.0f;
+        uint32_t s = 0;
+        for (; s + 8 <= ns; s += 8) {
+            float x[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) x[u] = acc[(size_t)(s + u) * 16];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) A += x[u] * wgt[s + u];
+        }
+        for (; s < ns; ++s) A += acc[(size_t)s * 16] * wgt[s];
+        p.out[ih * DH + d] = L > 0.0f ? A / L : 0.0f;
+    }
+}
+
+// Batched decode: one launch over the independent single-query steps of
+// b.seq[]; grid (largest split count, sequences, Hkv). The decode parameters of
+// sequence blockIdx.y are rebuilt from its descriptor (T = 1, key positions
+// relative to its first cache key); a workgroup past the sequence's split count
+// exits at once.
+__device__ __forceinline__ bool batch_params(const G4aBatchParams& b, uint32_t si, G4aDecodeParams& p) {
+    const G4aSeqDesc& sd = b.seq[si];
+    p = G4aDecodeParams{};
+    p.nsplit = (sd.k_end - sd.k_start + b.keys_per_split - 1) / b.keys_per_split;
+    p.q = sd.q;
+    p.k = sd.k;
+    p.v = sd.v;
+    p.out = sd.out;
+    p.part = b.part + sd.part;
+    p.dummy = b.dummy;
+    p.q_pos0 = sd.q_pos;
+    p.k_pos0 = 0;
+    p.T = 1;
+    p.Hq = b.Hq;
+    p.Hkv = b.Hkv;
+    p.k_start = sd.k_start;
+    p.k_end = sd.k_end;
+    p.keys_per_split = b.keys_per_split;
+    p.ring_cap = b.ring_cap;
+    p.window = b.window;
+    p.scale = b.scale;
+    p.softcap = b.softcap;
+    return p.nsplit > 0;
+}
+
+template <int DH>
+__device__ __forceinline__ void decode_short_batch(const G4aBatchParams& b) {
+    G4aDecodeParams p;
+    if (!batch_params(b, blockIdx.y, p) || blockIdx.x >= p.nsplit) return;
+    decode_short<DH>(p, blockIdx.x, 0u);
+}
+
+template <int DH>
+__device__ __forceinline__ void decode_wave_batch(const G4aBatchParams& b) {
+    G4aDecodeParams p;
+    if (!batch_params(b, blockIdx.y, p) || blockIdx.x >= p.nsplit) return;
+    decode_wave<DH, false>(p, blockIdx.x, 0u);
+}
+
+// The LSE combines of a batched decode, each sequence merged by the kernel a
+// single call with its split count uses: more than COMBINE_ROW_SPLITS splits
+// here, grid (DH/16, Hq, sequences) ...
+template <int DH>
+__device__ __forceinline__ void combine_batch(const G4aBatchParams& b) {
+    G4aDecodeParams p;
+    if (!batch_params(b, blockIdx.z, p) || p.nsplit <= COMBINE_ROW_SPLITS) return;
+    const G4aCombineParams cp{p.part, p.out, 1u, b.Hq, p.nsplit, (uint32_t)DH};
+    combine<DH>(cp, 0u);
+}
+
+// ... and 2 .. COMBINE_ROW_SPLITS splits here, grid (Hq, sequences).
+template <int DH>
+__device__ __forceinline__ void combine_rows_batch(const G4aBatchParams& b) {
+    G4aDecodeParams p;
+    if (!batch_params(b, blockIdx.y, p) || p.nsplit < 2 || p.nsplit > COMBINE_ROW_SPLITS) return;
+    const G4aCombineParams cp{p.part, p.out, 1u, b.Hq, p.nsplit, (uint32_t)DH};
+    combine_rows<DH>(cp, blockIdx.x, 0u);
 }
 
 // Generic masked online-softmax attention, one wave per (query, head), for any
@@ -1207,17 +1314,43 @@ __device__ __forceinline__ void generic_attention(const G4aGenericParams& p) {
 }  // namespace
 
 extern "C" {
-__global__ __launch_bounds__(512) void g4a_decode_d256_g8(G4aDecodeParams p) { decode_wave<256, false>(p); }
-__global__ __launch_bounds__(512) void g4a_decode_d512_g8(G4aDecodeParams p) { decode_wave<512, false>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d256_g8(G4aDecodeParams p) {
+    decode_wave<256, false>(p, blockIdx.x, blockIdx.y);
+}
+__global__ __launch_bounds__(512) void g4a_decode_d512_g8(G4aDecodeParams p) {
+    decode_wave<512, false>(p, blockIdx.x, blockIdx.y);
+}
 __global__ __launch_bounds__(512) void g4a_decode_d256_g4(G4aDecodeParams p) { decode_split<256, 4, false>(p); }
 __global__ __launch_bounds__(512) void g4a_decode_d512_g4(G4aDecodeParams p) { decode_split<512, 4, false>(p); }
-__global__ __launch_bounds__(512) void g4a_decode_d256_g8_kpos(G4aDecodeParams p) { decode_wave<256, true>(p); }
-__global__ __launch_bounds__(512) void g4a_decode_d512_g8_kpos(G4aDecodeParams p) { decode_wave<512, true>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d256_g8_kpos(G4aDecodeParams p) {
+    decode_wave<256, true>(p, blockIdx.x, blockIdx.y);
+}
+__global__ __launch_bounds__(512) void g4a_decode_d512_g8_kpos(G4aDecodeParams p) {
+    decode_wave<512, true>(p, blockIdx.x, blockIdx.y);
+}
 __global__ __launch_bounds__(512) void g4a_decode_d256_g4_kpos(G4aDecodeParams p) { decode_split<256, 4, true>(p); }
 __global__ __launch_bounds__(512) void g4a_decode_d512_g4_kpos(G4aDecodeParams p) { decode_split<512, 4, true>(p); }
-__global__ __launch_bounds__(256) void g4a_decode_short_d256(G4aDecodeParams p) { decode_short<256>(p); }
-__global__ __launch_bounds__(256) void g4a_decode_short_d512(G4aDecodeParams p) { decode_short<512>(p); }
-__global__ __launch_bounds__(256) void g4a_combine_d256(G4aCombineParams p) { combine<256>(p); }
-__global__ __launch_bounds__(256) void g4a_combine_d512(G4aCombineParams p) { combine<512>(p); }
+__global__ __launch_bounds__(256) void g4a_decode_short_d256(G4aDecodeParams p) {
+    decode_short<256>(p, blockIdx.x, blockIdx.y);
+}
+__global__ __launch_bounds__(256) void g4a_decode_short_d512(G4aDecodeParams p) {
+    decode_short<512>(p, blockIdx.x, blockIdx.y);
+}
+__global__ __launch_bounds__(256) void g4a_decode_short_batch_d256(G4aBatchParams b) { decode_short_batch<256>(b); }
+__global__ __launch_bounds__(256) void g4a_decode_short_batch_d512(G4aBatchParams b) { decode_short_batch<512>(b); }
+__global__ __launch_bounds__(512) void g4a_decode_wave_batch_d256(G4aBatchParams b) { decode_wave_batch<256>(b); }
+__global__ __launch_bounds__(512) void g4a_decode_wave_batch_d512(G4aBatchParams b) { decode_wave_batch<512>(b); }
+__global__ __launch_bounds__(256) void g4a_combine_batch_d256(G4aBatchParams b) { combine_batch<256>(b); }
+__global__ __launch_bounds__(256) void g4a_combine_batch_d512(G4aBatchParams b) { combine_batch<512>(b); }
+__global__ __launch_bounds__(256) void g4a_combine_rows_batch_d256(G4aBatchParams b) { combine_rows_batch<256>(b); }
+__global__ __launch_bounds__(256) void g4a_combine_rows_batch_d512(G4aBatchParams b) { combine_rows_batch<512>(b); }
+__global__ __launch_bounds__(256) void g4a_combine_rows_d256(G4aCombineParams p) {
+    combine_rows<256>(p, blockIdx.x, blockIdx.y);
+}
+__global__ __launch_bounds__(256) void g4a_combine_rows_d512(G4aCombineParams p) {
+    combine_rows<512>(p, blockIdx.x, blockIdx.y);
+}
+__global__ __launch_bounds__(256) void g4a_combine_d256(G4aCombineParams p) { combine<256>(p, blockIdx.z); }
+__global__ __launch_bounds__(256) void g4a_combine_d512(G4aCombineParams p) { combine<512>(p, blockIdx.z); }
 __global__ __launch_bounds__(64) void g4a_generic_attention(G4aGenericParams p) { generic_attention(p); }
 }

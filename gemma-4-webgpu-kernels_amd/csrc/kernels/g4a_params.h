@@ -31,6 +31,39 @@ struct G4aDecodeParams {
     float scale, softcap;
 };
 
+// One sequence of a batched decode launch (g4a_decode_*_batch_*,
+// g4a_combine_batch_*): a single query over the cache rows k / v, keys
+// [k_start, k_end) in splits of G4aBatchParams::keys_per_split. Positions are
+// relative to the sequence's first cache key: key j sits at position j
+// (physical row j % ring_cap for a ring), the query at q_pos.
+struct G4aSeqDesc {
+    const float* q;        // [1, Hq, Dh]
+    const float* k;        // [rows, Hkv, Dh]
+    const float* v;        // [rows, Hkv, Dh]
+    float* out;            // [1, Hq*Dh]
+    uint32_t k_start, k_end;
+    uint32_t q_pos;
+    uint32_t part;         // offset of its partials in G4aBatchParams::part, in floats
+};
+
+// Sequences per batched decode launch: their descriptors travel in the kernel
+// arguments (48 bytes each), so a launch needs no upload of its own.
+constexpr uint32_t G4A_BATCH_SEQ = 64;
+
+// Arguments of a batched decode launch: sequences seq[0 .. gridDim.y) (decode)
+// or seq[0 .. gridDim.z) (combine) and the shape they share. A sequence's
+// partials are laid out as G4aDecodeParams::part for T = 1 and its split count.
+struct G4aBatchParams {
+    G4aSeqDesc seq[G4A_BATCH_SEQ];
+    float* part;
+    const float* dummy;
+    uint32_t Hq, Hkv;
+    uint32_t keys_per_split;
+    uint32_t ring_cap;
+    uint32_t window;
+    float scale, softcap;
+};
+
 // Log-sum-exp merge of the split partials written by the decode kernel.
 struct G4aCombineParams {
     const float* part;

@@ -97,6 +97,7 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "g4a_sync": (c_int, [ctxp]),
         "g4a_attention": (c_int, [ctxp, ctypes.POINTER(AttnArgs)]),
         "g4a_attention_batch": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.c_uint32]),
+        "g4a_attention_decode_batch": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.c_uint32, _u32p]),
         "g4a_attention_plan": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.POINTER(AttnPlan)]),
         "g4a_kv_write": (c_int, [ctxp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32]),
         "g4a_head_norm_rope": (c_int, [ctxp, vp, vp, vp] + [ctypes.c_uint32] * 4 + [_u32p, ctypes.c_uint32,
@@ -256,6 +257,15 @@ class Context:
         sets or the result of prepare_batch()."""
         arr, n, _keep = calls if isinstance(calls, tuple) else self.prepare_batch(calls)
         self._check(self.lib.g4a_attention_batch(self.handle, arr, n))
+
+    def attention_decode_batch(self, calls) -> int:
+        """One g4a_attention_decode_batch call over independent decode steps
+        (attention() keyword sets, or the result of prepare_batch()); returns how
+        many of them ran in the batched launches."""
+        arr, n, _keep = calls if isinstance(calls, tuple) else self.prepare_batch(calls)
+        done = ctypes.c_uint32(0)
+        self._check(self.lib.g4a_attention_decode_batch(self.handle, arr, n, ctypes.byref(done)))
+        return done.value
 
     def plan(self, **kw) -> AttnPlan:
         return plan(self, **kw)

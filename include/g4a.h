@@ -118,6 +118,26 @@ int g4a_attention(g4a_ctx *ctx, const g4a_attn_args *args);
  * crossing for all of them. */
 int g4a_attention_batch(g4a_ctx *ctx, const g4a_attn_args *args, uint32_t n);
 
+/* n independent single-query decode steps, e.g. one layer's attention for
+ * every sequence of a serving batch, in one decode launch per 64 sequences
+ * (plus one LSE-combine launch for the sequences with more than one split)
+ * instead of up to two launches per sequence. A launch whose 32-key splits
+ * fit one workgroup per CU runs the short-context kernel; a larger one runs
+ * the streaming kernel with splits sized for one workgroup per CU over all its
+ * keys. args[i] is exactly as for g4a_attention and gives its result within
+ * the same tolerance (bit-identical where g4a_attention would run the short
+ * kernel with the same splits). A call runs in the batched launches when
+ * T = 1, Hq = 8 * Hkv, Dh = Dv in {256, 512}, its key positions are
+ * contiguous, `splits` is 0, it sees at most 32768 keys and its Hq, Hkv, Dh,
+ * sliding_window, kv_ring_cap, scale and attn_softcap equal those of the first
+ * such call; every other call runs afterwards as g4a_attention. Every call is
+ * validated before any work is enqueued. The calls must be independent: no
+ * call's out may overlap another call's q, k, v or out. *n_batched (may be
+ * NULL) receives the number of calls that ran batched. No counterpart in the
+ * reference, which decodes one sequence (rust/src/engine.rs:202-238): the
+ * multi-sequence step a server runs. */
+int g4a_attention_decode_batch(g4a_ctx *ctx, const g4a_attn_args *args, uint32_t n, uint32_t *n_batched);
+
 /* The launch plan g4a_attention would use for `args` (no GPU work): the
  * trimmed key range [k_start, k_end) (rust/src/backend_wgpu.rs:929-936), the
  * kernel family and the split-K decomposition. */
@@ -211,7 +231,8 @@ int g4a_timer_stop(g4a_ctx *ctx, float *ms);
 /* Per-kernel timing: while enabled, every g4a_attention call records a HIP
  * event pair on the context's stream around its main kernel (decode, prefill
  * or generic; not the LSE combine), and so does every norm/RoPE/producer
- * launch. g4a_kernel_timing_read waits for the
+ * launch and every decode and combine launch of g4a_attention_decode_batch.
+ * g4a_kernel_timing_read waits for the
  * recorded pairs and returns their summed milliseconds and count, then clears
  * them. At most 4096 pairs are kept per read. Enabling clears old pairs. */
 int g4a_kernel_timing(g4a_ctx *ctx, int enable);
