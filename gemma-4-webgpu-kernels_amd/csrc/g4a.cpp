@@ -59,6 +59,9 @@ struct g4a_ctx {
     hipFunction_t prefill[2] = {nullptr, nullptr};                          // [dh512]
     hipFunction_t split_kv = nullptr;  // K/V pre-split for the head_dim 256 prefill
     hipFunction_t norm_rope = nullptr;  // the attention producer (RMSNorm + RoPE + KV write)
+    hipFunction_t linear_words[3][3][3] = {};  // [bits 2/4/8][(MT, RU) = (1, 2), (1, 8), (4, 4)][mode]
+    hipFunction_t linear_elem[3] = {};         // [mode]
+    hipFunction_t embed_q = nullptr;
     // RoPE frequency tables theta^(-2j/rot), one per (theta, rotary_dim) seen
     struct FreqTable {
         float theta;
@@ -208,7 +211,7 @@ constexpr uint32_t kMaxTimed = 4096;
 // timing is on (the main kernel of an attention call).
 template <typename P>
 int launch(g4a_ctx* ctx, hipFunction_t f, dim3 grid, dim3 block, const P& params, const char* what,
-           bool timed = false) {
+           bool timed = false, unsigned lds_bytes = 0) {
     P copy = params;
     void* args[] = {&copy};
     const bool rec = timed && ctx->timing && ctx->kev_used < kMaxTimed;
@@ -217,11 +220,12 @@ int launch(g4a_ctx* ctx, hipFunction_t f, dim3 grid, dim3 block, const P& params
         // events attached to the dispatch itself: they bracket the kernel's execution,
         // not the host-side enqueue, so they agree with a profiler's kernel duration
         e = hipExtModuleLaunchKernel(f, grid.x * block.x, grid.y * block.y, grid.z * block.z, block.x, block.y,
-                                     block.z, 0, ctx->stream, args, nullptr, ctx->kev[2 * ctx->kev_used],
+                                     block.z, lds_bytes, ctx->stream, args, nullptr, ctx->kev[2 * ctx->kev_used],
                                      ctx->kev[2 * ctx->kev_used + 1], 0);
         if (e == hipSuccess) ++ctx->kev_used;
     } else {
-        e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, ctx->stream, args, nullptr);
+        e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, lds_bytes, ctx->stream, args,
+                                  nullptr);
     }
     if (e != hipSuccess) return fail(ctx, G4A_E_HIP, "launch %s: %s", what, hipGetErrorString(e));
     return G4A_OK;
@@ -424,6 +428,23 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->prefill_merge, "g4a_prefill_merge_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->split_kv, "g4a_split_kv")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->norm_rope, "g4a_norm_rope")) return bail(rc);
+    {
+        static const int bits[3] = {2, 4, 8};
+        static const int mt_ru[3][2] = {{1, 2}, {1, 8}, {4, 4}};
+        for (int b = 0; b < 3; ++b)
+            for (int v = 0; v < 3; ++v)
+                for (int m = 0; m < 3; ++m) {
+                    char name[64];
+                    snprintf(name, sizeof name, "g4a_linear_q_b%d_m%d_r%d_mode%d", bits[b], mt_ru[v][0], mt_ru[v][1], m);
+                    if (int rc = get_fn(ctx, &ctx->linear_words[b][v][m], name)) return bail(rc);
+                }
+        for (int m = 0; m < 3; ++m) {
+            char name[64];
+            snprintf(name, sizeof name, "g4a_linear_q_elem_mode%d", m);
+            if (int rc = get_fn(ctx, &ctx->linear_elem[m], name)) return bail(rc);
+        }
+        if (int rc = get_fn(ctx, &ctx->embed_q, "g4a_embed_rows_q")) return bail(rc);
+    }
     if (hipMalloc(reinterpret_cast<void**>(&ctx->dummy), 4096) != hipSuccess ||
         hipMemset(ctx->dummy, 0, 4096) != hipSuccess) {
         fail(ctx, G4A_E_NOMEM, "dummy buffer allocation failed");
@@ -880,7 +901,159 @@ int norm_rope_launch(g4a_ctx* ctx, G4aNormRopeSeg* segs, uint32_t nseg, uint32_t
     return launch(ctx, ctx->norm_rope, dim3(blocks, 1, 1), dim3(256, 1, 1), p, "norm/rope rows", true);
 }
 
+// ---- quantised projections -------------------------------------------------
+
+// Activation rows of the word-parallel kernel kept in LDS per workgroup.
+constexpr size_t LINEAR_LDS_BYTES = 64 << 10;
+
+int check_qweight(g4a_ctx* ctx, const g4a_qweight* w, const char* what) {
+    if (!w) return fail(ctx, G4A_E_ARG, "%s: null weight", what);
+    if (!w->qbytes || !w->scales) return fail(ctx, G4A_E_ARG, "%s: null qbytes/scales", what);
+    if (w->N == 0 || w->K == 0) return fail(ctx, G4A_E_SHAPE, "%s: empty weight [%u, %u]", what, w->N, w->K);
+    if (w->bits != 2 && w->bits != 4 && w->bits != 8)
+        return fail(ctx, G4A_E_ARG, "%s: bits must be 2, 4 or 8 (got %u)", what, w->bits);
+    if (w->signed_i8 && w->bits != 8) return fail(ctx, G4A_E_ARG, "%s: signed_i8 needs bits = 8", what);
+    if (w->group_size == 0) return fail(ctx, G4A_E_ARG, "%s: group_size must be > 0", what);
+    const uint32_t per_byte = w->signed_i8 ? 1 : 8 / w->bits;
+    if (w->K % per_byte != 0)
+        return fail(ctx, G4A_E_UNSUPPORTED, "%s: K = %u is not a whole number of bytes at %u bits", what, w->K, w->bits);
+    return G4A_OK;
+}
+
+// y[M, N] = epilogue(x . W^T); mode 0 plain, 1 GeGLU with w2, 2 gelu times b's columns.
+int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qweight* w2, const float* x,
+                    const float* b, uint32_t b_stride, uint32_t b_off, float* y, uint32_t M) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (int rc = check_qweight(ctx, w, "weight")) return rc;
+    if (mode == 1) {
+        if (int rc = check_qweight(ctx, w2, "up weight")) return rc;
+        if (w2->N != w->N || w2->K != w->K || w2->bits != w->bits || w2->signed_i8 != w->signed_i8 ||
+            w2->group_size != w->group_size)
+            return fail(ctx, G4A_E_UNSUPPORTED, "gate and up weights differ in shape or format");
+    }
+    if (mode == 2) {
+        if (!b) return fail(ctx, G4A_E_ARG, "null column source");
+        if (uint64_t(b_off) + w->N > b_stride)
+            return fail(ctx, G4A_E_SHAPE, "columns [%u, %u) exceed the row stride %u", b_off, b_off + w->N, b_stride);
+    }
+    if (M == 0) return G4A_OK;
+    if (!x || !y) return fail(ctx, G4A_E_ARG, "null x/y");
+    G4aLinearParams p{};
+    p.s = w->scales;
+    p.s2 = mode == 1 ? w2->scales : nullptr;
+    p.b = b;
+    p.x = x;
+    p.y = y;
+    p.M = M;
+    p.N = w->N;
+    p.K = w->K;
+    p.b_stride = b_stride;
+    p.b_off = b_off;
+    p.bits = w->bits;
+    p.signed_i8 = w->signed_i8 ? 1 : 0;
+    p.row_bytes = w->signed_i8 ? w->K : w->K / (8 / w->bits);
+    p.group_size = w->group_size;
+    p.scale_stride = (w->K + w->group_size - 1) / w->group_size;
+    const bool aligned = (reinterpret_cast<uintptr_t>(w->qbytes) & 3) == 0 &&
+                         (mode != 1 || (reinterpret_cast<uintptr_t>(w2->qbytes) & 3) == 0) &&
+                         (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    const bool words = (uint64_t(w->K) * w->bits) % 32 == 0 && p.scale_stride == 1 && aligned &&
+                       size_t(w->K) * 4 <= LINEAR_LDS_BYTES;
+    if (!words) {
+        // one thread per output in the CPU's order: any K, grouped scales
+        p.wb = static_cast<const uint8_t*>(w->qbytes);
+        p.wb2 = mode == 1 ? static_cast<const uint8_t*>(w2->qbytes) : nullptr;
+        for (uint32_t m0 = 0; m0 < M; m0 += 65535) {
+            G4aLinearParams q = p;
+            q.x = x + size_t(m0) * w->K;
+            q.y = y + size_t(m0) * w->N;
+            q.b = b ? b + size_t(m0) * b_stride : nullptr;
+            q.M = std::min<uint32_t>(65535, M - m0);
+            if (int rc = launch(ctx, ctx->linear_elem[mode], dim3((w->N + 63) / 64, q.M, 1), dim3(64, 1, 1), q,
+                                "quantised linear (element)", true))
+                return rc;
+        }
+        return G4A_OK;
+    }
+    p.w = static_cast<const uint32_t*>(w->qbytes);
+    p.w2 = mode == 1 ? static_cast<const uint32_t*>(w2->qbytes) : nullptr;
+    p.W = uint32_t(uint64_t(w->K) * w->bits / 32);
+    // sub-byte fields are offset binary: flipping each field's top bit makes it two's complement
+    p.xm = w->signed_i8 ? 0u : w->bits == 4 ? 0x88888888u : w->bits == 2 ? 0xAAAAAAAAu : 0x80808080u;
+    const int bi = w->bits == 2 ? 0 : w->bits == 4 ? 1 : 2;
+    const uint64_t cus = uint64_t(std::max(ctx->cu_count, 1));
+    // 4 activation rows per workgroup when they fit its LDS share, else 1; 8 weight
+    // rows in flight per wave for tall weights, 2 for short ones (more waves)
+    int variant, MT, RU;
+    if (M >= 2 && size_t(4) * w->K * 4 <= LINEAR_LDS_BYTES) {
+        variant = 2, MT = 4, RU = 4;
+    } else if (w->N >= cus * 64) {
+        variant = 1, MT = 1, RU = 8;
+    } else {
+        variant = 0, MT = 1, RU = 2;
+    }
+    // about 8 waves per CU over the rows (two 4-wave workgroups)
+    const uint64_t target = cus * 8;
+    uint64_t rpw = (w->N + target - 1) / target;
+    rpw = std::max<uint64_t>(RU, (rpw + RU - 1) / RU * RU);
+    p.rows_per_wave = uint32_t(rpw);
+    const uint32_t gx = uint32_t((w->N + 4 * rpw - 1) / (4 * rpw));
+    const unsigned lds = unsigned(size_t(MT) * w->K * 4);
+    for (uint32_t m0 = 0; m0 < M; m0 += 65535u * MT) {
+        G4aLinearParams q = p;
+        q.x = x + size_t(m0) * w->K;
+        q.y = y + size_t(m0) * w->N;
+        q.b = b ? b + size_t(m0) * b_stride : nullptr;
+        q.M = std::min<uint32_t>(65535u * MT, M - m0);
+        if (int rc = launch(ctx, ctx->linear_words[bi][variant][mode], dim3(gx, (q.M + MT - 1) / MT, 1),
+                            dim3(256, 1, 1), q, "quantised linear", true, lds))
+            return rc;
+    }
+    return G4A_OK;
+}
+
 }  // namespace
+
+int g4a_linear_q(g4a_ctx* ctx, const g4a_qweight* w, const float* x, float* y, uint32_t M) {
+    return linear_q_launch(ctx, 0, w, nullptr, x, nullptr, 0, 0, y, M);
+}
+
+int g4a_linear_q_geglu(g4a_ctx* ctx, const g4a_qweight* w_gate, const g4a_qweight* w_up, const float* x, float* y,
+                       uint32_t M) {
+    return linear_q_launch(ctx, 1, w_gate, w_up, x, nullptr, 0, 0, y, M);
+}
+
+int g4a_linear_q_gelu_mul_cols(g4a_ctx* ctx, const g4a_qweight* w, const float* x, const float* b, uint32_t b_stride,
+                               uint32_t b_off, float* y, uint32_t M) {
+    return linear_q_launch(ctx, 2, w, nullptr, x, b, b_stride, b_off, y, M);
+}
+
+int g4a_embed_rows_q(g4a_ctx* ctx, const g4a_qweight* table, const uint32_t* ids, uint32_t T, float scale,
+                     float* out) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (int rc = check_qweight(ctx, table, "table")) return rc;
+    if (T == 0) return G4A_OK;
+    if (!ids || !out) return fail(ctx, G4A_E_ARG, "null ids/out");
+    for (uint32_t i = 0; i < T; ++i)
+        if (ids[i] >= table->N) return fail(ctx, G4A_E_ARG, "id %u at %u is outside the table's %u rows", ids[i], i, table->N);
+    if (uint64_t(T) * table->K >= (uint64_t(1) << 32)) return fail(ctx, G4A_E_SHAPE, "embedding output too large");
+    G4aEmbedParams p{};
+    p.wb = static_cast<const uint8_t*>(table->qbytes);
+    p.s = table->scales;
+    p.out = out;
+    p.T = T;
+    p.D = table->K;
+    p.bits = table->bits;
+    p.signed_i8 = table->signed_i8 ? 1 : 0;
+    p.row_bytes = table->signed_i8 ? table->K : table->K / (8 / table->bits);
+    p.group_size = table->group_size;
+    p.scale_stride = (table->K + table->group_size - 1) / table->group_size;
+    p.scale = scale;
+    if (int rc = upload_positions(ctx, ids, T, nullptr, 0, &p.ids, nullptr)) return rc;
+    const uint64_t n = uint64_t(T) * table->K;
+    return launch(ctx, ctx->embed_q, dim3(uint32_t((n + 255) / 256), 1, 1), dim3(256, 1, 1), p,
+                  "quantised embedding", true);
+}
 
 int g4a_head_norm_rope(g4a_ctx* ctx, const float* x, const float* w, float* y, uint32_t T, uint32_t heads,
                        uint32_t head_dim, uint32_t rotary_dim, const uint32_t* positions, uint32_t pos0, float theta,

@@ -158,3 +158,38 @@ struct G4aNormRopeParams {
     uint32_t cache_row, ring_cap;
     float eps;
 };
+
+// Quantised projection y[M, N] = epilogue(x[M, K] . W^T) (g4a_linear_q_*).
+// W rows are packed fields of `bits` bits, LSB-first (offset binary, or native
+// I8 when bits = 8 and xm = 0), each row starting on a 32-bit word for the
+// word-parallel kernel. mode 0: y = acc * s[n]; mode 1: gelu(acc * s[n]) *
+// (acc2 * s2[n]) with the second weight w2/s2; mode 2: gelu(acc * s[n]) *
+// b[m * b_stride + b_off + n].
+struct G4aLinearParams {
+    const uint32_t* w;      // word-parallel kernel: [N, W] words
+    const uint8_t* wb;      // element kernel: [N, row_bytes] bytes
+    const float* s;         // [N, scale_stride]
+    const uint32_t* w2;     // mode 1
+    const uint8_t* wb2;
+    const float* s2;
+    const float* b;         // mode 2: [M, b_stride]
+    const float* x;         // [M, K]
+    float* y;               // [M, N]
+    uint32_t M, N, K, W;
+    uint32_t rows_per_wave;
+    uint32_t b_stride, b_off;
+    uint32_t xm;            // word mask turning each field into two's complement
+    uint32_t bits, row_bytes, group_size, scale_stride, signed_i8;
+};
+
+// Quantised embedding rows: out[i, d] = deq(ids[i], d) * scale.
+struct G4aEmbedParams {
+    const uint8_t* wb;      // [V, row_bytes]
+    const float* s;         // [V, scale_stride]
+    const uint32_t* ids;    // [T]
+    float* out;             // [T, D]
+    uint32_t T, D;
+    uint32_t bits, row_bytes, group_size, scale_stride, signed_i8;
+    float scale;
+};
+

@@ -1,0 +1,284 @@
+// Quantised projections for gfx950: y = x . W^T with W packed 2/4/8-bit
+// (offset-binary sub-byte fields LSB-first, or native I8) and f32 scales, plus
+// the two epilogues Gemma-4 fuses into a projection (GeGLU of gate and up, and
+// the per-layer-input gate times a column slice), and the quantised embedding
+// gather.
+//
+// Replaces, behind the backend trait, the WGSL MATMUL_Q / MATMUL_Q_SCALAR /
+// EMBED_Q kernels (rust/src/kernels/matmul_q.wgsl, matmul_q_scalar.wgsl,
+// embed_q.wgsl, dispatched by rust/src/backend_wgpu.rs:624-832); the semantics
+// are the CPU backend's (rust/src/backend.rs:44-58 QuantWeight::deq,
+// rust/src/backend_cpu.rs:127-145 embed_rows, :174-222 linear, :55-58
+// gelu_tanh, and the trait's compositions rust/src/backend.rs:156-168).
+//
+// Two linear kernels:
+//  * linear_q_words (rows whose packed bytes are whole 32-bit words, one scale
+//    per row): decode projections are weight-streaming (HBM-bound). Lane l of a
+//    wave owns words l, l + 64, ... of every row, so each wave load reads 256
+//    contiguous bytes of a row; a wave keeps RU rows' words in flight. The
+//    activations sit in LDS (MT rows of K floats) and are read once per word
+//    for all RU rows. Each field is turned into a sign-extended byte holding
+//    value * F (F = 16 for 4-bit, 64 for 2-bit, 1 for 8-bit: an exact power of
+//    two) by one mask, so one SDWA convert and one FMA handle a value; the
+//    final scale is s / F. Per lane the sum runs over its words in order (an
+//    FMA chain within a word), then a transposed butterfly reduces the MT*RU
+//    sums across the wave. Not the CPU's summation order: results agree within
+//    f32 reordering error.
+//  * linear_q_elem (any K, grouped scales): one thread per output, the CPU's
+//    exact order (acc += x[k] * (q * s) for k in order, separately rounded), so
+//    plain projections are bit-identical to the reference.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "g4a_params.h"
+
+namespace {
+
+// sqrt(2 / pi) rounded to f32, as (2.0f32 / PI).sqrt() in rust/src/backend_cpu.rs:56
+constexpr float GELU_C = 0x1.988452p-1f;
+
+__device__ __forceinline__ float gelu_tanh(float v) {
+    return 0.5f * v * (1.0f + tanhf(GELU_C * (v + 0.044715f * v * v * v)));
+}
+
+template <int BITS>
+struct QFmt {
+    static constexpr int VPW = 32 / BITS;  // values per word
+    static constexpr float INV_F = BITS == 4 ? 0.0625f : BITS == 2 ? 0.015625f : 1.0f;
+};
+
+__device__ __forceinline__ float sbyte(uint32_t v, int j) { return (float)(int8_t)(v >> (8 * j)); }
+
+// The VPW values of a word whose fields are two's complement, each as value * F,
+// in k order.
+template <int BITS>
+__device__ __forceinline__ void unpack(uint32_t v, float (&q)[QFmt<BITS>::VPW]) {
+    if constexpr (BITS == 8) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = sbyte(v, j);
+    } else if constexpr (BITS == 4) {
+        const uint32_t a = (v << 4) & 0xF0F0F0F0u;  // field 2j at the top of byte j
+        const uint32_t b = v & 0xF0F0F0F0u;         // field 2j + 1
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            q[2 * j] = sbyte(a, j);
+            q[2 * j + 1] = sbyte(b, j);
+        }
+    } else {
+        const uint32_t a0 = (v << 6) & 0xC0C0C0C0u, a1 = (v << 4) & 0xC0C0C0C0u;
+        const uint32_t a2 = (v << 2) & 0xC0C0C0C0u, a3 = v & 0xC0C0C0C0u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            q[4 * j] = sbyte(a0, j);
+            q[4 * j + 1] = sbyte(a1, j);
+            q[4 * j + 2] = sbyte(a2, j);
+            q[4 * j + 3] = sbyte(a3, j);
+        }
+    }
+}
+
+// Sums v[i] over the 64 lanes for all V (a power of two <= 64) values at once:
+// each butterfly step hands half of the remaining values to the partner lane,
+// so log2(V) steps leave one value per lane, then plain xor steps finish it.
+// Returns the total of value `idx` (set here from the lane's bits); every lane
+// whose low 6 - log2(V) bits are zero holds a distinct idx.
+template <int V>
+__device__ __forceinline__ float wave_reduce_many(float (&v)[V], int lane, int& idx) {
+    idx = 0;
+    int o = 32;
+#pragma unroll
+    for (int n = V; n > 1; n >>= 1, o >>= 1) {
+        const int half = n / 2;
+        const bool hi = (lane & o) != 0;
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+            const float send = hi ? v[i] : v[i + half];
+            const float keep = hi ? v[i + half] : v[i];
+            v[i] = keep + __shfl_xor(send, o, 64);
+        }
+        idx = 2 * idx + (hi ? 1 : 0);
+    }
+    float s = v[0];
+#pragma unroll
+    for (; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    return s;
+}
+
+template <int BITS, int MT, int RU, int MODE>
+__device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
+    using F = QFmt<BITS>;
+    constexpr int VPW = F::VPW;
+    constexpr int V = MT * RU;
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // [MT][K]
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const uint32_t K = p.K, W = p.W, N = p.N;
+    const uint32_t m0 = blockIdx.y * MT;
+
+    // activation rows m0 .. m0 + MT - 1 (rows past M read as zeros)
+    for (uint32_t i = threadIdx.x; i < MT * K / 4; i += blockDim.x) {
+        const uint32_t e = 4 * i, mt = e / K, k = e - mt * K;
+        float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (m0 + mt < p.M) xv = *reinterpret_cast<const float4*>(p.x + (size_t)(m0 + mt) * K + k);
+        *reinterpret_cast<float4*>(xs + e) = xv;
+    }
+    __syncthreads();
+
+    const uint32_t first = (blockIdx.x * (blockDim.x / 64) + wv) * p.rows_per_wave;
+    const uint32_t last = min(first + p.rows_per_wave, N);
+    for (uint32_t r0 = first; r0 < last; r0 += RU) {
+        const uint32_t* wr[RU];
+        const uint32_t* wr2[RU];
+#pragma unroll
+        for (int r = 0; r < RU; ++r) {
+            const size_t row = min(r0 + r, N - 1);  // rows past N: re-read the last, not stored
+            wr[r] = p.w + row * W;
+            wr2[r] = MODE == 1 ? p.w2 + row * W : nullptr;
+        }
+        float acc[V], acc2[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = acc2[i] = 0.0f;
+        uint32_t cur[RU], cur2[RU];
+        uint32_t w = lane;
+        if (w < W) {
+#pragma unroll
+            for (int r = 0; r < RU; ++r) {
+                cur[r] = wr[r][w];
+                if (MODE == 1) cur2[r] = wr2[r][w];
+            }
+        }
+        for (; w < W; w += 64) {
+            // next words in flight while this one is used
+            uint32_t nxt[RU], nxt2[RU];
+            const uint32_t wn = w + 64;
+            if (wn < W) {
+#pragma unroll
+                for (int r = 0; r < RU; ++r) {
+                    nxt[r] = wr[r][wn];
+                    if (MODE == 1) nxt2[r] = wr2[r][wn];
+                }
+            }
+            float xv[MT][VPW];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < VPW; i += 4) {
+                    const float4 t = *reinterpret_cast<const float4*>(xs + mt * K + w * VPW + i);
+                    xv[mt][i] = t.x;
+                    xv[mt][i + 1] = t.y;
+                    xv[mt][i + 2] = t.z;
+                    xv[mt][i + 3] = t.w;
+                }
+#pragma unroll
+            for (int r = 0; r < RU; ++r) {
+                float q[VPW];
+                unpack<BITS>(cur[r] ^ p.xm, q);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int i = 0; i < VPW; ++i) acc[mt * RU + r] = __builtin_fmaf(xv[mt][i], q[i], acc[mt * RU + r]);
+                if (MODE == 1) {
+                    float q2[VPW];
+                    unpack<BITS>(cur2[r] ^ p.xm, q2);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int i = 0; i < VPW; ++i)
+                            acc2[mt * RU + r] = __builtin_fmaf(xv[mt][i], q2[i], acc2[mt * RU + r]);
+                }
+            }
+            if (wn < W) {
+#pragma unroll
+                for (int r = 0; r < RU; ++r) {
+                    cur[r] = nxt[r];
+                    if (MODE == 1) cur2[r] = nxt2[r];
+                }
+            }
+        }
+        int idx;
+        const float a = wave_reduce_many<V>(acc, lane, idx);
+        float a2 = 0.0f;
+        if (MODE == 1) {
+            int idx2;
+            a2 = wave_reduce_many<V>(acc2, lane, idx2);
+        }
+        if ((lane & (64 / V - 1)) == 0) {
+            const uint32_t mt = idx / RU, r = idx % RU;
+            const uint32_t n = r0 + r, m = m0 + mt;
+            if (n < last && m < p.M) {
+                const float v = a * (p.s[n] * F::INV_F);
+                float o = v;
+                if (MODE == 1) o = gelu_tanh(v) * (a2 * (p.s2[n] * F::INV_F));
+                if (MODE == 2) o = gelu_tanh(v) * p.b[(size_t)m * p.b_stride + p.b_off + n];
+                p.y[(size_t)m * N + n] = o;
+            }
+        }
+    }
+}
+
+// QuantWeight::deq (rust/src/backend.rs:44-58) of element (n, k).
+__device__ __forceinline__ float deq(const uint8_t* __restrict__ wb, const float* __restrict__ s, uint32_t bits,
+                                     uint32_t row_bytes, uint32_t group, uint32_t sstride, uint32_t signed_i8,
+                                     uint32_t n, uint32_t k) {
+    int32_t qv;
+    if (signed_i8) {
+        qv = (int32_t)(int8_t)wb[(size_t)n * row_bytes + k];
+    } else {
+        const uint32_t per_byte = 8 / bits;
+        const uint32_t b = wb[(size_t)n * row_bytes + k / per_byte];
+        const uint32_t shift = (k % per_byte) * bits;
+        qv = (int32_t)((b >> shift) & ((1u << bits) - 1u)) - (int32_t)(1u << (bits - 1));
+    }
+    return (float)qv * s[(size_t)n * sstride + k / group];
+}
+
+template <int MODE>
+__device__ __forceinline__ void linear_q_elem(const G4aLinearParams& p) {
+    const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
+    if (n >= p.N) return;
+    const float* __restrict__ xr = p.x + (size_t)m * p.K;
+    float acc = 0.0f, acc2 = 0.0f;
+    for (uint32_t k = 0; k < p.K; ++k) {
+        acc += xr[k] * deq(p.wb, p.s, p.bits, p.row_bytes, p.group_size, p.scale_stride, p.signed_i8, n, k);
+        if (MODE == 1)
+            acc2 += xr[k] * deq(p.wb2, p.s2, p.bits, p.row_bytes, p.group_size, p.scale_stride, p.signed_i8, n, k);
+    }
+    float o = acc;
+    if (MODE == 1) o = gelu_tanh(acc) * acc2;
+    if (MODE == 2) o = gelu_tanh(acc) * p.b[(size_t)m * p.b_stride + p.b_off + n];
+    p.y[(size_t)m * p.N + n] = o;
+}
+
+// embed_rows on a quantised table (rust/src/backend_cpu.rs:127-137): one thread
+// per output element.
+__device__ __forceinline__ void embed_rows_q(const G4aEmbedParams& p) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (size_t)p.T * p.D) return;
+    const uint32_t i = (uint32_t)(e / p.D), d = (uint32_t)(e % p.D);
+    p.out[e] = deq(p.wb, p.s, p.bits, p.row_bytes, p.group_size, p.scale_stride, p.signed_i8, p.ids[i], d) * p.scale;
+}
+
+}  // namespace
+
+#define G4A_LINEAR_WORDS(B, MT, RU, MODE)                                                               \
+    extern "C" __global__ __launch_bounds__(256) void g4a_linear_q_b##B##_m##MT##_r##RU##_mode##MODE( \
+        G4aLinearParams p) {                                                                           \
+        linear_q_words<B, MT, RU, MODE>(p);                                                            \
+    }
+#define G4A_LINEAR_SET(B, MODE) \
+    G4A_LINEAR_WORDS(B, 1, 2, MODE) G4A_LINEAR_WORDS(B, 1, 8, MODE) G4A_LINEAR_WORDS(B, 4, 4, MODE)
+G4A_LINEAR_SET(2, 0)
+G4A_LINEAR_SET(2, 1)
+G4A_LINEAR_SET(2, 2)
+G4A_LINEAR_SET(4, 0)
+G4A_LINEAR_SET(4, 1)
+G4A_LINEAR_SET(4, 2)
+G4A_LINEAR_SET(8, 0)
+G4A_LINEAR_SET(8, 1)
+G4A_LINEAR_SET(8, 2)
+
+extern "C" __global__ __launch_bounds__(64) void g4a_linear_q_elem_mode0(G4aLinearParams p) { linear_q_elem<0>(p); }
+extern "C" __global__ __launch_bounds__(64) void g4a_linear_q_elem_mode1(G4aLinearParams p) { linear_q_elem<1>(p); }
+extern "C" __global__ __launch_bounds__(64) void g4a_linear_q_elem_mode2(G4aLinearParams p) { linear_q_elem<2>(p); }
+extern "C" __global__ __launch_bounds__(256) void g4a_embed_rows_q(G4aEmbedParams p) { embed_rows_q(p); }

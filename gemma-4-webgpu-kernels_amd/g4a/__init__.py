@@ -58,6 +58,14 @@ class ProducerArgs(ctypes.Structure):
     ]
 
 
+class QWeightArgs(ctypes.Structure):
+    """g4a_qweight: a quantised weight [N, K] in device memory."""
+    _fields_ = [
+        ("qbytes", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("N", ctypes.c_uint32), ("K", ctypes.c_uint32),
+        ("bits", ctypes.c_uint32), ("signed_i8", ctypes.c_uint32), ("group_size", ctypes.c_uint32),
+    ]
+
+
 class DeviceInfo(ctypes.Structure):
     _fields_ = [
         ("device", ctypes.c_int), ("compute_units", ctypes.c_int), ("clock_khz", ctypes.c_int),
@@ -105,6 +113,12 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "g4a_rms_norm": (c_int, [ctxp, vp, vp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float]),
         "g4a_rope": (c_int, [ctxp, vp, vp] + [ctypes.c_uint32] * 4 + [_u32p, ctypes.c_uint32, ctypes.c_float]),
         "g4a_attn_producer": (c_int, [ctxp, ctypes.POINTER(ProducerArgs)]),
+        "g4a_linear_q": (c_int, [ctxp, ctypes.POINTER(QWeightArgs), vp, vp, ctypes.c_uint32]),
+        "g4a_linear_q_geglu": (c_int, [ctxp, ctypes.POINTER(QWeightArgs), ctypes.POINTER(QWeightArgs), vp, vp,
+                                       ctypes.c_uint32]),
+        "g4a_linear_q_gelu_mul_cols": (c_int, [ctxp, ctypes.POINTER(QWeightArgs), vp, vp, ctypes.c_uint32,
+                                               ctypes.c_uint32, vp, ctypes.c_uint32]),
+        "g4a_embed_rows_q": (c_int, [ctxp, ctypes.POINTER(QWeightArgs), _u32p, ctypes.c_uint32, ctypes.c_float, vp]),
         "g4a_timer_start": (c_int, [ctxp]),
         "g4a_timer_stop": (c_int, [ctxp, ctypes.POINTER(ctypes.c_float)]),
         "g4a_get_device_info": (c_int, [ctxp, ctypes.POINTER(DeviceInfo)]),
@@ -174,6 +188,18 @@ class DeviceArray:
         if self.ptr:
             self.ctx.free(self.ptr)
             self.ptr = 0
+
+
+@dataclass
+class DeviceQWeight:
+    """A quantised weight uploaded by Context.upload_qweight (owns its buffers)."""
+    args: QWeightArgs
+    qbytes: "DeviceArray"
+    scales: "DeviceArray"
+
+    def free(self) -> None:
+        self.qbytes.free()
+        self.scales.free()
 
 
 class Context:
@@ -293,6 +319,31 @@ class Context:
         a = ProducerArgs(q, k or None, v or None, q_norm or None, k_norm or None, q_out, k_cache or None,
                          v_cache or None, T, Hq, Hkv, Dh, rotary_dim, pp, pos0, cache_row, ring_cap, theta, eps)
         self._check(self.lib.g4a_attn_producer(self.handle, ctypes.byref(a)))
+
+    # ---- quantised projections ----
+    def upload_qweight(self, qbytes: np.ndarray, scales: np.ndarray, N: int, K: int, bits: int,
+                       signed_i8: bool = False, group_size: Optional[int] = None) -> "DeviceQWeight":
+        qb = self.upload(np.ascontiguousarray(qbytes, np.uint8))
+        sc = self.upload(np.ascontiguousarray(scales, np.float32))
+        args = QWeightArgs(qb.ptr, sc.ptr, N, K, bits, 1 if signed_i8 else 0, group_size or K)
+        return DeviceQWeight(args, qb, sc)
+
+    def linear_q(self, w: "DeviceQWeight", x: int, y: int, M: int) -> None:
+        self._check(self.lib.g4a_linear_q(self.handle, ctypes.byref(w.args), x, y, M))
+
+    def linear_q_geglu(self, w_gate: "DeviceQWeight", w_up: "DeviceQWeight", x: int, y: int, M: int) -> None:
+        self._check(self.lib.g4a_linear_q_geglu(self.handle, ctypes.byref(w_gate.args), ctypes.byref(w_up.args), x,
+                                                y, M))
+
+    def linear_q_gelu_mul_cols(self, w: "DeviceQWeight", x: int, b: int, b_stride: int, b_off: int, y: int,
+                               M: int) -> None:
+        self._check(self.lib.g4a_linear_q_gelu_mul_cols(self.handle, ctypes.byref(w.args), x, b, b_stride, b_off, y,
+                                                        M))
+
+    def embed_rows_q(self, table: "DeviceQWeight", ids, scale: float, out: int) -> None:
+        arr, ptr = _u32_array(ids)
+        n = 0 if arr is None else arr.size
+        self._check(self.lib.g4a_embed_rows_q(self.handle, ctypes.byref(table.args), ptr, n, scale, out))
 
     def timer_start(self) -> None:
         self._check(self.lib.g4a_timer_start(self.handle))

@@ -90,7 +90,7 @@ def build_oracle(verbose: bool = False) -> Path:
     ORACLE_OUT.mkdir(parents=True, exist_ok=True)
     tmp = LIBORACLE.with_suffix(".so.tmp")
     _run(["gcc", "-O2", "-std=gnu11", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
-          ORACLE_DIR / "attn_oracle.c", "-o", tmp, "-lm", "-lpthread"], verbose)
+          ORACLE_DIR / "attn_oracle.c", ORACLE_DIR / "linear_oracle.c", "-o", tmp, "-lm", "-lpthread"], verbose)
     tmp.replace(LIBORACLE)
     return LIBORACLE
 

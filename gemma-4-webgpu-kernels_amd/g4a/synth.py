@@ -112,6 +112,10 @@ class Lcg:
         self.s = s
         return out
 
+    def next(self, n: int) -> np.ndarray:
+        """n draws of Lcg::next: (s as f32) / (0x7fffffff as f32)."""
+        return (self.states(n).astype(np.float32) / self._DEN).astype(np.float32)
+
     def rand(self, n: int, scale: float) -> np.ndarray:
         f = self.states(n).astype(np.float32) / self._DEN
         return ((f * np.float32(2.0) - np.float32(1.0)) * np.float32(scale)).astype(np.float32)
@@ -172,3 +176,83 @@ def kernel_parity_attention_inputs():
     qpos = np.array([297, 298, 299], dtype=np.uint32)
     for window in (0, 150):
         yield f"attention(S=300, window={window})", q, k, v, qpos, kpos, 1.0, window
+
+
+# ---- quantised weights --------------------------------------------------------
+
+def pack_unsigned(values, bits: int) -> np.ndarray:
+    """Raw unsigned fields of `bits` bits packed LSB-first into bytes (the
+    reference's test helper rust/src/dequant.rs:53-63)."""
+    v = np.asarray(values, np.uint32).ravel()
+    per_byte = 8 // bits
+    n = -(-v.size // per_byte)
+    padded = np.zeros(n * per_byte, np.uint32)
+    padded[:v.size] = v & ((1 << bits) - 1)
+    fields = padded.reshape(n, per_byte)
+    shifts = (np.arange(per_byte, dtype=np.uint32) * bits)[None, :]
+    return (fields << shifts).sum(axis=1).astype(np.uint8)
+
+
+def pack_int(values, bits: int) -> np.ndarray:
+    """Signed values as stored by the checkpoint (rust/src/dequant.rs:37-51):
+    offset binary (raw = value + 2^(bits-1)) for sub-byte, two's complement I8."""
+    v = np.asarray(values, np.int64).ravel()
+    if bits == 8:
+        return (v & 0xFF).astype(np.uint8)
+    return pack_unsigned((v + (1 << (bits - 1))) & ((1 << bits) - 1), bits)
+
+
+def quant_weight(seed: int, N: int, K: int, bits: int, signed_i8: bool = False, group_size: int | None = None,
+                 scale_lo: float = 0.01, scale_span: float = 0.05):
+    """A random quantised weight [N, K]: uniform raw fields (or I8 bytes) and
+    scales in [scale_lo, scale_lo + scale_span). Returns (qbytes [N, row_bytes],
+    scales [N, ceil(K / group)], group_size)."""
+    g = group_size or K
+    rng = np.random.default_rng(seed)
+    if signed_i8:
+        qbytes = rng.integers(0, 256, size=(N, K), dtype=np.uint8)
+    else:
+        raw = rng.integers(0, 1 << bits, size=(N, K), dtype=np.uint32)
+        qbytes = pack_unsigned(raw, bits).reshape(N, K * bits // 8)
+    stride = -(-K // g)
+    scales = (np.float32(scale_lo) + rng.random((N, stride), dtype=np.float32) * np.float32(scale_span))
+    return qbytes, scales.astype(np.float32), g
+
+
+def quant_parity_inputs():
+    """The inputs of the reference's quantized_kernel_parity (rust/tests/gpu.rs:146-190),
+    regenerated with its Lcg(9) stream in the same draw order. Yields dicts with
+    name, qbytes, scales, N, K, bits, signed_i8, group_size and either x (linear)
+    or ids + scale (embedding)."""
+    r = Lcg(9)
+
+    def scales(n):  # 0.01 + r.next() * 0.05
+        return (r.next(n) * np.float32(0.05) + np.float32(0.01)).astype(np.float32)
+
+    def randu(n, bits):  # (r.next() * (1 << bits) as f32).floor() as u32 % (1 << bits)
+        return (np.floor(r.next(n) * np.float32(1 << bits)).astype(np.uint32) % (1 << bits)).astype(np.uint32)
+
+    for bits in (4, 2):
+        n, k = 40, 64
+        vals = randu(n * k, bits)
+        qb, sc = pack_unsigned(vals, bits), scales(n)
+        for m in (5, 1):
+            x = r.rand(m * k, 1.0).reshape(m, k)
+            yield dict(name=f"linear_q{bits}_M{m}", qbytes=qb, scales=sc, N=n, K=k, bits=bits, signed_i8=False,
+                       group_size=k, x=x)
+    bits, n, k, m = 4, 21, 52, 3
+    vals = randu(n * k, bits)
+    qb, sc = pack_unsigned(vals, bits), scales(n)
+    x = r.rand(m * k, 1.0).reshape(m, k)
+    yield dict(name="linear_q4_oddK", qbytes=qb, scales=sc, N=n, K=k, bits=bits, signed_i8=False, group_size=k, x=x)
+    n, k, m = 30, 48, 4
+    qb = np.floor(r.next(n * k) * np.float32(256.0)).astype(np.uint32).astype(np.uint8)
+    sc = (r.next(n) * np.float32(0.03) + np.float32(0.01)).astype(np.float32)
+    x = r.rand(m * k, 1.0).reshape(m, k)
+    yield dict(name="linear_i8", qbytes=qb, scales=sc, N=n, K=k, bits=8, signed_i8=True, group_size=k, x=x)
+    v, d, bits, group = 50, 32, 4, 16
+    vals = randu(v * d, bits)
+    qb = pack_unsigned(vals, bits)
+    sc = (r.next(v * (d // group)) * np.float32(0.04) + np.float32(0.02)).astype(np.float32)
+    yield dict(name="embed_q4_grouped", qbytes=qb, scales=sc, N=v, K=d, bits=bits, signed_i8=False,
+               group_size=group, ids=np.array([3, 7, 49, 0, 21], np.uint32), scale=float(np.sqrt(np.float32(d))))

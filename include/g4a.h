@@ -223,6 +223,51 @@ typedef struct g4a_producer_args {
 
 int g4a_attn_producer(g4a_ctx *ctx, const g4a_producer_args *args);
 
+/* ---- quantised projections (the calls on either side of attention) --------
+ * A weight as the reference's QuantWeight (rust/src/backend.rs:12-58), in
+ * device memory: logical shape [N, K]; row n's packed bytes start at
+ * qbytes + n * row_bytes with row_bytes = K (signed_i8) or K / (8 / bits);
+ * sub-byte fields are offset binary (value = raw - 2^(bits-1)) packed
+ * LSB-first, signed_i8 rows are two's complement bytes (bits = 8, signed_i8
+ * = 0 reads 8-bit offset binary); element (n, k) is multiplied by
+ * scales[n * ceil(K / group_size) + k / group_size]. K must be a whole number
+ * of bytes per row.
+ *
+ * Rows that are whole 32-bit words (K * bits % 32 == 0) with one scale per row
+ * (group_size >= K), a 4-byte aligned qbytes, 16-byte aligned x and K <= 16384
+ * run the word-parallel kernel (HBM-bound, f32 sums in another order than the
+ * reference's, within f32 reordering error); every other weight runs one
+ * thread per output in the reference CPU's order (bit-identical for
+ * g4a_linear_q). */
+typedef struct {
+    const void *qbytes;
+    const float *scales;
+    uint32_t N, K;
+    uint32_t bits;       /* 2, 4 or 8 */
+    uint32_t signed_i8;  /* 1: I8 rows */
+    uint32_t group_size; /* K (or more): one scale per row */
+} g4a_qweight;
+
+/* Backend::linear on a quantised weight (rust/src/backend.rs:105-106;
+ * rust/src/backend_cpu.rs:174-222; the reference GPU's MATMUL_Q mode 0,
+ * rust/src/backend_wgpu.rs:768-806): y[M, N] = x[M, K] . W^T (device x, y). */
+int g4a_linear_q(g4a_ctx *ctx, const g4a_qweight *w, const float *x, float *y, uint32_t M);
+/* Backend::linear_geglu (rust/src/backend.rs:156-161; MATMUL_Q mode 1,
+ * rust/src/backend_wgpu.rs:808-821): y = gelu_tanh(x . Wg^T) * (x . Wu^T), both
+ * weights of one shape and format. */
+int g4a_linear_q_geglu(g4a_ctx *ctx, const g4a_qweight *w_gate, const g4a_qweight *w_up, const float *x, float *y,
+                       uint32_t M);
+/* Backend::linear_gelu_mul_cols (rust/src/backend.rs:162-168; MATMUL_Q mode 2,
+ * rust/src/backend_wgpu.rs:823-832): y[m, n] = gelu_tanh((x . W^T)[m, n]) *
+ * b[m * b_stride + b_off + n], b_off + N <= b_stride. */
+int g4a_linear_q_gelu_mul_cols(g4a_ctx *ctx, const g4a_qweight *w, const float *x, const float *b, uint32_t b_stride,
+                               uint32_t b_off, float *y, uint32_t M);
+/* Backend::embed_rows on a quantised table [V, D] = [N, K] (rust/src/backend.rs:101-102;
+ * rust/src/backend_cpu.rs:127-137; EMBED_Q, rust/src/backend_wgpu.rs:734-760):
+ * out[i, d] = deq(ids[i], d) * scale, ids a host array of T values < N. */
+int g4a_embed_rows_q(g4a_ctx *ctx, const g4a_qweight *table, const uint32_t *ids, uint32_t T, float scale,
+                     float *out);
+
 /* ---- timing (HIP events on the context's stream) ----------------------- */
 int g4a_timer_start(g4a_ctx *ctx);
 /* Records the stop event, waits for it and returns the elapsed milliseconds. */
@@ -231,7 +276,8 @@ int g4a_timer_stop(g4a_ctx *ctx, float *ms);
 /* Per-kernel timing: while enabled, every g4a_attention call records a HIP
  * event pair on the context's stream around its main kernel (decode, prefill
  * or generic; not the LSE combine), and so does every norm/RoPE/producer
- * launch and every decode and combine launch of g4a_attention_decode_batch.
+ * launch, every decode and combine launch of g4a_attention_decode_batch and
+ * every quantised projection / embedding launch.
  * g4a_kernel_timing_read waits for the
  * recorded pairs and returns their summed milliseconds and count, then clears
  * them. At most 4096 pairs are kept per read. Enabling clears old pairs. */

@@ -5,7 +5,11 @@ this module. It restates rust/src/backend_cpu.rs:270-336 (attention),
 :63-91 (par_ranges), :149-172 (rms_norm) and :248-268 (rope); see
 attn_oracle.c. head_norm_rope and producer are the compositions the reference
 defines on top of them (rust/src/backend.rs:146-154, rust/src/model.rs:256-281,
-rust/src/kvcache.rs:49-62).
+rust/src/kvcache.rs:49-62). The quantised projections restate
+rust/src/backend.rs:44-58 (QuantWeight::deq), rust/src/backend_cpu.rs:174-222
+(linear), :55-58 (gelu_tanh) and :127-145 (embed_rows); linear_q_geglu and
+linear_q_gelu_mul_cols are the trait's default compositions
+(rust/src/backend.rs:156-168); see linear_oracle.c.
 """
 from __future__ import annotations
 
@@ -35,6 +39,17 @@ def lib() -> ctypes.CDLL:
         L.oracle_rms_norm.argtypes = [vp, vp, vp, sz, sz, ctypes.c_float]
         L.oracle_rope.restype = None
         L.oracle_rope.argtypes = [vp, vp, sz, sz, sz, sz, vp, ctypes.c_float]
+        L.oracle_deq.restype = ctypes.c_float
+        L.oracle_deq.argtypes = [vp, vp, sz, ctypes.c_uint32, ctypes.c_int, sz, sz, sz]
+        L.oracle_linear_q.restype = None
+        L.oracle_linear_q.argtypes = [vp, vp, sz, sz, ctypes.c_uint32, ctypes.c_int, sz, vp, sz, vp]
+        L.oracle_gelu_tanh.restype = ctypes.c_float
+        L.oracle_gelu_tanh.argtypes = [ctypes.c_float]
+        L.oracle_gelu_tanh_n.restype = None
+        L.oracle_gelu_tanh_n.argtypes = [vp, vp, sz]
+        L.oracle_embed_rows_q.restype = None
+        L.oracle_embed_rows_q.argtypes = [vp, vp, sz, sz, ctypes.c_uint32, ctypes.c_int, sz, vp, sz,
+                                          ctypes.c_float, vp]
         L.oracle_thread_count.restype = ctypes.c_size_t
         L.oracle_thread_count.argtypes = [sz, ctypes.c_int]
         _lib = L
@@ -125,3 +140,58 @@ def producer(q, k, v, q_norm, k_norm, positions, theta, rotary_dim, eps):
     T, hkv, dh = k.shape
     v_rows = rms_norm(np.ascontiguousarray(v, np.float32).reshape(T * hkv, dh), None, eps).reshape(T, hkv, dh)
     return q_out, qk(k, k_norm), v_rows
+
+
+class QWeight:
+    """A quantised weight as the reference's QuantWeight (rust/src/backend.rs:12-25):
+    qbytes [N, row_bytes] u8 (sub-byte offset-binary fields packed LSB-first, or
+    I8), scales [N, ceil(K / group_size)] f32, logical shape [N, K]."""
+
+    def __init__(self, qbytes, scales, N, K, bits, signed_i8=False, group_size=None):
+        self.qbytes = np.ascontiguousarray(qbytes, np.uint8)
+        self.scales = np.ascontiguousarray(scales, np.float32)
+        self.N, self.K, self.bits, self.signed_i8 = int(N), int(K), int(bits), bool(signed_i8)
+        self.group_size = int(group_size or K)
+
+
+def deq(w: QWeight, n: int, k: int) -> float:
+    return float(lib().oracle_deq(w.qbytes.ctypes.data, w.scales.ctypes.data, w.K, w.bits, int(w.signed_i8),
+                                  w.group_size, n, k))
+
+
+def linear_q(x, w: QWeight):
+    """CpuBackend::linear on a quantised weight: x [M, K] -> [M, N] f32."""
+    x = np.ascontiguousarray(x, np.float32)
+    M = x.shape[0]
+    assert x.shape == (M, w.K)
+    y = np.empty((M, w.N), np.float32)
+    lib().oracle_linear_q(w.qbytes.ctypes.data, w.scales.ctypes.data, w.N, w.K, w.bits, int(w.signed_i8),
+                          w.group_size, x.ctypes.data, M, y.ctypes.data)
+    return y
+
+
+def gelu_tanh(x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().oracle_gelu_tanh_n(x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
+def linear_q_geglu(x, w_gate: QWeight, w_up: QWeight):
+    """Backend::linear_geglu's default: gelu(x Wg^T) * (x Wu^T)."""
+    return gelu_tanh(linear_q(x, w_gate)) * linear_q(x, w_up)
+
+
+def linear_q_gelu_mul_cols(x, w: QWeight, b, offset):
+    """Backend::linear_gelu_mul_cols's default: gelu(x W^T) * b[:, offset:offset+N]."""
+    b = np.ascontiguousarray(b, np.float32)
+    return gelu_tanh(linear_q(x, w)) * b[:, offset:offset + w.N]
+
+
+def embed_rows_q(w: QWeight, ids, scale):
+    """CpuBackend::embed_rows on a quantised table [V, D]: [T, D] f32."""
+    ids = np.ascontiguousarray(ids, np.uint32)
+    out = np.empty((ids.size, w.K), np.float32)
+    lib().oracle_embed_rows_q(w.qbytes.ctypes.data, w.scales.ctypes.data, w.N, w.K, w.bits, int(w.signed_i8),
+                              w.group_size, ids.ctypes.data, ids.size, scale, out.ctypes.data)
+    return out

@@ -155,3 +155,100 @@ def load_norm_rope_golden() -> dict[str, NormRopeCase]:
         assert str(data[name + "__hash"]) == norm_rope_hash(c), f"{name}: regenerated inputs differ from the fixture's"
         c.out = data[name + "__out"]
     return cases
+
+
+# ---- quantised projections ----------------------------------------------------
+
+LINEAR_GOLDEN_PATH = Path(__file__).resolve().parent / "linear_golden.npz"
+
+
+@dataclass
+class LinearCase:
+    op: str                  # linear | geglu | gelu_mul_cols | embed
+    w: dict                  # qbytes, scales, N, K, bits, signed_i8, group_size
+    x: np.ndarray | None     # [M, K] (linear ops)
+    w2: dict | None = None   # geglu: the up weight
+    b: np.ndarray | None = None
+    b_off: int = 0
+    ids: np.ndarray | None = None
+    scale: float = 1.0
+    out: np.ndarray | None = None
+
+
+def _qw_bytes(h, w: dict) -> None:
+    h.update(np.ascontiguousarray(w["qbytes"], np.uint8).tobytes())
+    h.update(np.ascontiguousarray(w["scales"], np.float32).tobytes())
+    h.update(np.array([w["N"], w["K"], w["bits"], int(w["signed_i8"]), w["group_size"]], np.int64).tobytes())
+
+
+def linear_hash(c: LinearCase) -> str:
+    h = hashlib.sha256(c.op.encode())
+    _qw_bytes(h, c.w)
+    if c.w2 is not None:
+        _qw_bytes(h, c.w2)
+    for a in (c.x, c.b, c.ids):
+        if a is not None:
+            h.update(np.ascontiguousarray(a).tobytes())
+    h.update(np.array([c.b_off, c.scale], np.float64).tobytes())
+    return h.hexdigest()
+
+
+def _qw(qbytes, scales, N, K, bits, signed_i8=False, group_size=None) -> dict:
+    return dict(qbytes=np.ascontiguousarray(qbytes, np.uint8).ravel(), scales=np.ascontiguousarray(scales, np.float32),
+                N=N, K=K, bits=bits, signed_i8=signed_i8, group_size=group_size or K)
+
+
+def linear_recipes() -> dict[str, LinearCase]:
+    """The reference's quantized_kernel_parity inputs (rust/tests/gpu.rs:146-190),
+    regenerated from its Lcg(9) stream: q4 and q2 linear at M = 5 and 1, q4 with
+    K = 52 (not whole words), I8, and the grouped-scale q4 embedding. Then seeded
+    cases of this build for the fused epilogues and Gemma-4 shapes (q_proj 4-bit
+    [2048, 1536] at M = 1, a 2-bit GeGLU [256, 1536] pair at M = 3, the per-layer
+    gate [256, 1536] times a column slice at M = 2, grouped-scale linear)."""
+    cases: dict[str, LinearCase] = {}
+    for c in synth.quant_parity_inputs():
+        w = _qw(c["qbytes"], c["scales"], c["N"], c["K"], c["bits"], c["signed_i8"], c["group_size"])
+        if "ids" in c:
+            cases["ref_" + c["name"]] = LinearCase("embed", w, None, ids=c["ids"], scale=c["scale"])
+        else:
+            cases["ref_" + c["name"]] = LinearCase("linear", w, c["x"])
+    qb, sc, g = synth.quant_weight(51, 2048, 1536, 4)
+    cases["gemma_q_proj_q4_M1"] = LinearCase("linear", _qw(qb, sc, 2048, 1536, 4), synth.normal_f32(51, 9, 1536)
+                                             .reshape(1, 1536))
+    qg, sg, _ = synth.quant_weight(52, 256, 1536, 2)
+    qu, su, _ = synth.quant_weight(53, 256, 1536, 2)
+    cases["geglu_q2_M3"] = LinearCase("geglu", _qw(qg, sg, 256, 1536, 2), synth.normal_f32(52, 9, 3 * 1536)
+                                      .reshape(3, 1536), w2=_qw(qu, su, 256, 1536, 2))
+    qb, sc, _ = synth.quant_weight(54, 256, 1536, 4)
+    b = synth.normal_f32(54, 8, 2 * 35 * 256).reshape(2, 35 * 256)
+    cases["gelu_mul_cols_q4_M2"] = LinearCase("gelu_mul_cols", _qw(qb, sc, 256, 1536, 4),
+                                              synth.normal_f32(54, 9, 2 * 1536).reshape(2, 1536), b=b, b_off=7 * 256)
+    qb, sc, g = synth.quant_weight(55, 96, 256, 4, group_size=64)
+    cases["linear_q4_grouped64_M2"] = LinearCase("linear", _qw(qb, sc, 96, 256, 4, group_size=g),
+                                                 synth.normal_f32(55, 9, 2 * 256).reshape(2, 256))
+    return cases
+
+
+def oracle_qweight(oracle, w: dict):
+    return oracle.QWeight(w["qbytes"], w["scales"], w["N"], w["K"], w["bits"], w["signed_i8"], w["group_size"])
+
+
+def linear_eval(c: LinearCase, oracle) -> np.ndarray:
+    """The oracle's output for a recipe."""
+    w = oracle_qweight(oracle, c.w)
+    if c.op == "linear":
+        return oracle.linear_q(c.x, w)
+    if c.op == "geglu":
+        return oracle.linear_q_geglu(c.x, w, oracle_qweight(oracle, c.w2))
+    if c.op == "gelu_mul_cols":
+        return oracle.linear_q_gelu_mul_cols(c.x, w, c.b, c.b_off)
+    return oracle.embed_rows_q(w, c.ids, c.scale)
+
+
+def load_linear_golden() -> dict[str, LinearCase]:
+    data = np.load(LINEAR_GOLDEN_PATH, allow_pickle=False)
+    cases = linear_recipes()
+    for name, c in cases.items():
+        assert str(data[name + "__hash"]) == linear_hash(c), f"{name}: regenerated inputs differ from the fixture's"
+        c.out = data[name + "__out"]
+    return cases

@@ -1,4 +1,5 @@
-"""Writes tests/golden/attention_golden.npz and norm_rope_golden.npz: for every
+"""Writes tests/golden/attention_golden.npz, norm_rope_golden.npz and
+linear_golden.npz: for every
 recipe in golden_io, the sha256 of its regenerated inputs and the CPU oracle's
 output on them.
 
@@ -15,8 +16,9 @@ sys.path[:0] = [str(HERE), str(REPO / "gemma-4-webgpu-kernels_amd"), str(REPO / 
 import numpy as np  # noqa: E402
 
 import oracle  # noqa: E402
-from golden_io import (GOLDEN_PATH, NORM_ROPE_GOLDEN_PATH, input_hash, norm_rope_eval,  # noqa: E402
-                       norm_rope_hash, norm_rope_recipes, recipes)
+from golden_io import (GOLDEN_PATH, LINEAR_GOLDEN_PATH, NORM_ROPE_GOLDEN_PATH, input_hash,  # noqa: E402
+                       linear_eval, linear_hash, linear_recipes, norm_rope_eval, norm_rope_hash, norm_rope_recipes,
+                       recipes)
 
 
 def main():
@@ -36,6 +38,14 @@ def main():
         print(f"{name}: out {out.shape}")
     np.savez_compressed(NORM_ROPE_GOLDEN_PATH, **arrays)
     print("wrote", NORM_ROPE_GOLDEN_PATH, NORM_ROPE_GOLDEN_PATH.stat().st_size, "bytes")
+    arrays = {}
+    for name, c in linear_recipes().items():
+        out = linear_eval(c, oracle)
+        arrays[name + "__out"] = out
+        arrays[name + "__hash"] = np.array(linear_hash(c))
+        print(f"{name}: out {out.shape}")
+    np.savez_compressed(LINEAR_GOLDEN_PATH, **arrays)
+    print("wrote", LINEAR_GOLDEN_PATH, LINEAR_GOLDEN_PATH.stat().st_size, "bytes")
 
 
 if __name__ == "__main__":
