@@ -316,6 +316,88 @@ def batched_decode(ctx, n, L, Dh, window, ring_cap, steps, warmup):
             "single_calls_us_per_step": seq_ms * 1e3, "speedup_vs_single_calls": seq_ms / ms}
 
 
+LINEAR_CONFIGS = [
+    # name, op, N (output rows), K, bits, M (activation rows); Gemma-4 E2B shapes
+    ("linear q_proj sliding 4-bit [2048,1536] M=1", "linear", 2048, 1536, 4, 1),
+    ("linear q_proj global 4-bit [4096,1536] M=1", "linear", 4096, 1536, 4, 1),
+    ("linear o_proj global 4-bit [1536,4096] M=1", "linear", 1536, 4096, 4, 1),
+    ("linear gate+up GeGLU 4-bit 2x[6144,1536] M=1", "geglu", 6144, 1536, 4, 1),
+    ("linear down 4-bit [1536,6144] M=1", "linear", 1536, 6144, 4, 1),
+    ("linear lm_head 2-bit [262144,1536] M=1", "linear", 262144, 1536, 2, 1),
+    ("linear gate 2-bit [12288,1536] M=64", "linear", 12288, 1536, 2, 64),
+]
+
+
+def linear_bytes(op, N, K, bits, M):
+    """Algorithmic bytes of one projection: packed weights (two for GeGLU) and
+    their per-row scales read once, x read, y written."""
+    nw = 2 if op == "geglu" else 1
+    return nw * (N * K * bits // 8 + 4 * N) + 4 * M * K + 4 * M * N
+
+
+def linear_bench(ctx, op, N, K, bits, M, steps, cpu=True):
+    """Kernel µs per call from dispatch-attached events over `steps` calls, the
+    weights rotated over enough copies to pass the 256 MB MALL; and the CPU
+    oracle on the same call (1 thread)."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle
+    nw = 2 if op == "geglu" else 1
+    wbytes = N * K * bits // 8
+    copies = int(min(256, max(2, -(-BATCH_BUST_BYTES // (nw * wbytes)))))
+    qb, sc, _ = synth.quant_weight(21, N, K, bits)
+    qb2, sc2, _ = synth.quant_weight(22, N, K, bits)
+    base = [ctx.upload_qweight(qb, sc, N, K, bits), ctx.upload_qweight(qb2, sc2, N, K, bits)]
+    ws = []
+    for i in range(copies):
+        pair = []
+        for j in range(nw):
+            src = base[j]
+            qbuf = ctx.malloc(wbytes)
+            ctx.d2d(qbuf, src.qbytes.ptr, wbytes)
+            args = g4a.QWeightArgs(qbuf, src.scales.ptr, N, K, bits, 0, K)
+            pair.append(g4a.DeviceQWeight(args, None, None))
+        ws.append(pair)
+    x_h = synth.normal_f32(23, 0, M * K).reshape(M, K)
+    x, y = ctx.upload(x_h), ctx.empty((M, N))
+
+    def call(i):
+        pair = ws[i % copies]
+        if op == "geglu":
+            ctx.linear_q_geglu(pair[0], pair[1], x.ptr, y.ptr, M)
+        else:
+            ctx.linear_q(pair[0], x.ptr, y.ptr, M)
+    for i in range(min(copies, 20)):
+        call(i)
+    ctx.sync()
+    ctx.kernel_timing(True)
+    for i in range(steps):
+        call(i)
+    ctx.sync()
+    kms, n = ctx.kernel_timing_read()
+    ctx.kernel_timing(False)
+    for pair in ws:
+        for w in pair:
+            ctx.free(w.args.qbytes)
+    for w in base:
+        w.free()
+    x.free()
+    y.free()
+    us = kms / n * 1e3
+    b = linear_bytes(op, N, K, bits, M)
+    res = {"kernel_us": us, "GB_s": b / (us * 1e-6) / 1e9, "frac_hbm_peak": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+           "bytes": b, "weight_copies_rotated": copies}
+    if cpu:
+        w_o = oracle.QWeight(qb, sc, N, K, bits)
+        t0 = time.perf_counter()
+        if op == "geglu":
+            oracle.linear_q_geglu(x_h, w_o, oracle.QWeight(qb2, sc2, N, K, bits))
+        else:
+            oracle.linear_q(x_h, w_o)
+        res["cpu_oracle_us"] = (time.perf_counter() - t0) * 1e6
+        res["cpu_threads"] = 1
+    return res
+
+
 def load_traffic():
     p = REPO / "profiles" / "decode_hd512_s32768_traffic.json"
     if p.exists():
@@ -333,7 +415,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="headline decode only (no extras, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "schedule", "producer", "batch"], default=None,
+    ap.add_argument("--only", choices=["prefill", "schedule", "producer", "batch", "linear"], default=None,
                     help="run only these extra workloads (for profiling) and print their JSON line")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="first run 3 device-to-device copies of MIB MiB (the reference dispatch for "
@@ -353,6 +435,10 @@ def main(argv=None):
         if args.only == "prefill":
             for name, T, Dh, W in PREFILL_CONFIGS:
                 out[name] = prefill(ctx, T, Dh, W, steps=args.steps, warmup=args.warmup)
+                print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
+        elif args.only == "linear":
+            for name, op, N, K, bits, M in LINEAR_CONFIGS:
+                out[name] = linear_bench(ctx, op, N, K, bits, M, steps=args.steps)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         elif args.only == "batch":
             for name, n, L, Dh, W, cap in BATCH_CONFIGS:
@@ -448,6 +534,9 @@ def main(argv=None):
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
         for name, T, Dh, theta, rot, pos0, cap in PRODUCER_CONFIGS:
             extras[name] = producer(ctx, T, Dh, theta, rot, pos0, cap, steps=50)
+            print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
+        for name, op, N, K, bits, M in LINEAR_CONFIGS:
+            extras[name] = linear_bench(ctx, op, N, K, bits, M, steps=100)
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
         for name, n, L, Dh, W, cap in BATCH_CONFIGS:
             extras[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=50, warmup=10)

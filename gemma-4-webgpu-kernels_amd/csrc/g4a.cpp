@@ -957,8 +957,11 @@ int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qwei
     const bool aligned = (reinterpret_cast<uintptr_t>(w->qbytes) & 3) == 0 &&
                          (mode != 1 || (reinterpret_cast<uintptr_t>(w2->qbytes) & 3) == 0) &&
                          (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    // the word kernel's activation rows, zero-padded to whole wave strides of words
+    const uint64_t vpw = 32 / w->bits, words_per_row = uint64_t(w->K) * w->bits / 32;
+    const uint64_t kpad = (words_per_row + 63) / 64 * 64 * vpw;
     const bool words = (uint64_t(w->K) * w->bits) % 32 == 0 && p.scale_stride == 1 && aligned &&
-                       size_t(w->K) * 4 <= LINEAR_LDS_BYTES;
+                       kpad * 4 <= LINEAR_LDS_BYTES;
     if (!words) {
         // one thread per output in the CPU's order: any K, grouped scales
         p.wb = static_cast<const uint8_t*>(w->qbytes);
@@ -985,20 +988,21 @@ int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qwei
     // 4 activation rows per workgroup when they fit its LDS share, else 1; 8 weight
     // rows in flight per wave for tall weights, 2 for short ones (more waves)
     int variant, MT, RU;
-    if (M >= 2 && size_t(4) * w->K * 4 <= LINEAR_LDS_BYTES) {
+    if (M >= 2 && 4 * kpad * 4 <= LINEAR_LDS_BYTES) {
         variant = 2, MT = 4, RU = 4;
     } else if (w->N >= cus * 64) {
         variant = 1, MT = 1, RU = 8;
     } else {
         variant = 0, MT = 1, RU = 2;
     }
-    // about 8 waves per CU over the rows (two 4-wave workgroups)
-    const uint64_t target = cus * 8;
+    // about 16 waves per CU over the rows (four 4-wave workgroups): weight
+    // streaming needs many loads in flight
+    const uint64_t target = cus * 16;
     uint64_t rpw = (w->N + target - 1) / target;
     rpw = std::max<uint64_t>(RU, (rpw + RU - 1) / RU * RU);
     p.rows_per_wave = uint32_t(rpw);
     const uint32_t gx = uint32_t((w->N + 4 * rpw - 1) / (4 * rpw));
-    const unsigned lds = unsigned(size_t(MT) * w->K * 4);
+    const unsigned lds = unsigned(MT * kpad * 4);
     for (uint32_t m0 = 0; m0 < M; m0 += 65535u * MT) {
         G4aLinearParams q = p;
         q.x = x + size_t(m0) * w->K;

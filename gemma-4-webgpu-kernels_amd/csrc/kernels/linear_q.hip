@@ -15,9 +15,11 @@
 //  * linear_q_words (rows whose packed bytes are whole 32-bit words, one scale
 //    per row): decode projections are weight-streaming (HBM-bound). Lane l of a
 //    wave owns words l, l + 64, ... of every row, so each wave load reads 256
-//    contiguous bytes of a row; a wave keeps RU rows' words in flight. The
-//    activations sit in LDS (MT rows of K floats) and are read once per word
-//    for all RU rows. Each field is turned into a sign-extended byte holding
+//    contiguous bytes of a row. Every lane takes the same number of steps (a
+//    step: one word of each of RU rows); two register sets alternate so the
+//    next step's loads are in flight while a step computes. The activations
+//    sit in LDS (MT rows, zero-padded to whole wave strides) and are read once
+//    per word for all RU rows. Each field is turned into a sign-extended byte holding
 //    value * F (F = 16 for 4-bit, 64 for 2-bit, 1 for 8-bit: an exact power of
 //    two) by one mask, so one SDWA convert and one FMA handle a value; the
 //    final scale is s / F. Per lane the sum runs over its words in order (an
@@ -93,8 +95,9 @@ __device__ __forceinline__ float wave_reduce_many(float (&v)[V], int lane, int& 
         const bool hi = (lane & o) != 0;
 #pragma unroll
         for (int i = 0; i < half; ++i) {
-            const float send = hi ? v[i] : v[i + half];
-            const float keep = hi ? v[i + half] : v[i];
+            const float lo_v = v[i], hi_v = v[i + half];  // values first: a select of addresses would go to scratch
+            const float send = hi ? lo_v : hi_v;
+            const float keep = hi ? hi_v : lo_v;
             v[i] = keep + __shfl_xor(send, o, 64);
         }
         idx = 2 * idx + (hi ? 1 : 0);
@@ -105,113 +108,118 @@ __device__ __forceinline__ float wave_reduce_many(float (&v)[V], int lane, int& 
     return s;
 }
 
-template <int BITS, int MT, int RU, int MODE>
+template <int BITS, int MT, int RU, int D, int MODE>
 __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
     using F = QFmt<BITS>;
     constexpr int VPW = F::VPW;
     constexpr int V = MT * RU;
-    extern __shared__ __attribute__((aligned(16))) float xs[];  // [MT][K]
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // [MT][J * 64 * VPW], zeros past K
     const int lane = threadIdx.x & 63;
-    const int wv = threadIdx.x >> 6;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: rows in scalar registers
     const uint32_t K = p.K, W = p.W, N = p.N;
+    const uint32_t J = (W + 63) / 64;       // word steps per row chunk (lanes past W read zeros of x)
+    const uint32_t KP = J * 64 * VPW;       // padded activation row
     const uint32_t m0 = blockIdx.y * MT;
+    const uint32_t first = (blockIdx.x * (blockDim.x / 64) + wv) * p.rows_per_wave;
+    const uint32_t last = min(first + p.rows_per_wave, N);
+    const uint32_t nchunks = first < last ? (last - first + RU - 1) / RU : 0;
+    const uint32_t T = nchunks * J;         // the wave's steps: chunk t / J, word step t % J
 
-    // activation rows m0 .. m0 + MT - 1 (rows past M read as zeros)
-    for (uint32_t i = threadIdx.x; i < MT * K / 4; i += blockDim.x) {
-        const uint32_t e = 4 * i, mt = e / K, k = e - mt * K;
+    // Step t loads word lane + 64 (t % J) (clamped to the row) of the RU rows of
+    // chunk t / J (clamped to the matrix). D register sets form a ring, so the
+    // loads of steps t + 1 .. t + D - 1 are in flight while step t computes,
+    // with no register copies.
+    auto load = [&](uint32_t (&wd)[RU], uint32_t (&wd2)[RU], uint32_t t) {
+        const uint32_t c = t / J, j = t - c * J;
+        const uint32_t w = min(lane + 64 * j, W - 1);
+#pragma unroll
+        for (int r = 0; r < RU; ++r) {
+            const size_t row = min(first + c * RU + r, N - 1);
+            wd[r] = p.w[row * W + w];
+            if (MODE == 1) wd2[r] = p.w2[row * W + w];
+        }
+    };
+    uint32_t wd[D][RU], wd2[D][RU];
+    // the first steps' words are requested before the activations are staged
+#pragma unroll
+    for (int d = 0; d + 1 < D; ++d)
+        if (T) load(wd[d], wd2[d], min((uint32_t)d, T - 1));
+
+    for (uint32_t i = threadIdx.x; i < MT * KP / 4; i += blockDim.x) {
+        const uint32_t e = 4 * i, mt = e / KP, k = e - mt * KP;
         float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (m0 + mt < p.M) xv = *reinterpret_cast<const float4*>(p.x + (size_t)(m0 + mt) * K + k);
+        if (m0 + mt < p.M && k < K) xv = *reinterpret_cast<const float4*>(p.x + (size_t)(m0 + mt) * K + k);
         *reinterpret_cast<float4*>(xs + e) = xv;
     }
     __syncthreads();
 
-    const uint32_t first = (blockIdx.x * (blockDim.x / 64) + wv) * p.rows_per_wave;
-    const uint32_t last = min(first + p.rows_per_wave, N);
-    for (uint32_t r0 = first; r0 < last; r0 += RU) {
-        const uint32_t* wr[RU];
-        const uint32_t* wr2[RU];
+    float acc[V], acc2[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = acc2[i] = 0.0f;
+
+    auto step = [&](const uint32_t (&wd)[RU], const uint32_t (&wd2)[RU], uint32_t t) {
+        const uint32_t c = t / J, j = t - c * J;
+        const uint32_t w = lane + 64 * j;
+        float xv[MT][VPW];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < VPW; i += 4) {
+                const float4 v4 = *reinterpret_cast<const float4*>(xs + mt * KP + w * VPW + i);
+                xv[mt][i] = v4.x;
+                xv[mt][i + 1] = v4.y;
+                xv[mt][i + 2] = v4.z;
+                xv[mt][i + 3] = v4.w;
+            }
 #pragma unroll
         for (int r = 0; r < RU; ++r) {
-            const size_t row = min(r0 + r, N - 1);  // rows past N: re-read the last, not stored
-            wr[r] = p.w + row * W;
-            wr2[r] = MODE == 1 ? p.w2 + row * W : nullptr;
-        }
-        float acc[V], acc2[V];
-#pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] = acc2[i] = 0.0f;
-        uint32_t cur[RU], cur2[RU];
-        uint32_t w = lane;
-        if (w < W) {
-#pragma unroll
-            for (int r = 0; r < RU; ++r) {
-                cur[r] = wr[r][w];
-                if (MODE == 1) cur2[r] = wr2[r][w];
-            }
-        }
-        for (; w < W; w += 64) {
-            // next words in flight while this one is used
-            uint32_t nxt[RU], nxt2[RU];
-            const uint32_t wn = w + 64;
-            if (wn < W) {
-#pragma unroll
-                for (int r = 0; r < RU; ++r) {
-                    nxt[r] = wr[r][wn];
-                    if (MODE == 1) nxt2[r] = wr2[r][wn];
-                }
-            }
-            float xv[MT][VPW];
+            float q[VPW];
+            unpack<BITS>(wd[r] ^ p.xm, q);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int i = 0; i < VPW; i += 4) {
-                    const float4 t = *reinterpret_cast<const float4*>(xs + mt * K + w * VPW + i);
-                    xv[mt][i] = t.x;
-                    xv[mt][i + 1] = t.y;
-                    xv[mt][i + 2] = t.z;
-                    xv[mt][i + 3] = t.w;
-                }
-#pragma unroll
-            for (int r = 0; r < RU; ++r) {
-                float q[VPW];
-                unpack<BITS>(cur[r] ^ p.xm, q);
+                for (int i = 0; i < VPW; ++i) acc[mt * RU + r] = __builtin_fmaf(xv[mt][i], q[i], acc[mt * RU + r]);
+            if (MODE == 1) {
+                float q2[VPW];
+                unpack<BITS>(wd2[r] ^ p.xm, q2);
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                    for (int i = 0; i < VPW; ++i) acc[mt * RU + r] = __builtin_fmaf(xv[mt][i], q[i], acc[mt * RU + r]);
-                if (MODE == 1) {
-                    float q2[VPW];
-                    unpack<BITS>(cur2[r] ^ p.xm, q2);
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                        for (int i = 0; i < VPW; ++i)
-                            acc2[mt * RU + r] = __builtin_fmaf(xv[mt][i], q2[i], acc2[mt * RU + r]);
-                }
-            }
-            if (wn < W) {
-#pragma unroll
-                for (int r = 0; r < RU; ++r) {
-                    cur[r] = nxt[r];
-                    if (MODE == 1) cur2[r] = nxt2[r];
-                }
+                    for (int i = 0; i < VPW; ++i)
+                        acc2[mt * RU + r] = __builtin_fmaf(xv[mt][i], q2[i], acc2[mt * RU + r]);
             }
         }
-        int idx;
-        const float a = wave_reduce_many<V>(acc, lane, idx);
-        float a2 = 0.0f;
-        if (MODE == 1) {
-            int idx2;
-            a2 = wave_reduce_many<V>(acc2, lane, idx2);
+        if (j + 1 == J) {
+            // the chunk's sums are complete: reduce across the wave and store
+            int idx;
+            const float a = wave_reduce_many<V>(acc, lane, idx);
+            float a2 = 0.0f;
+            if (MODE == 1) {
+                int idx2;
+                a2 = wave_reduce_many<V>(acc2, lane, idx2);
+            }
+            if ((lane & (64 / V - 1)) == 0) {
+                const uint32_t mt = idx / RU, r = idx % RU;
+                const uint32_t n = first + c * RU + r, m = m0 + mt;
+                if (n < last && m < p.M) {
+                    const float v = a * (p.s[n] * F::INV_F);
+                    float o = v;
+                    if (MODE == 1) o = gelu_tanh(v) * (a2 * (p.s2[n] * F::INV_F));
+                    if (MODE == 2) o = gelu_tanh(v) * p.b[(size_t)m * p.b_stride + p.b_off + n];
+                    p.y[(size_t)m * N + n] = o;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < V; ++i) acc[i] = acc2[i] = 0.0f;
         }
-        if ((lane & (64 / V - 1)) == 0) {
-            const uint32_t mt = idx / RU, r = idx % RU;
-            const uint32_t n = r0 + r, m = m0 + mt;
-            if (n < last && m < p.M) {
-                const float v = a * (p.s[n] * F::INV_F);
-                float o = v;
-                if (MODE == 1) o = gelu_tanh(v) * (a2 * (p.s2[n] * F::INV_F));
-                if (MODE == 2) o = gelu_tanh(v) * p.b[(size_t)m * p.b_stride + p.b_off + n];
-                p.y[(size_t)m * N + n] = o;
+    };
+
+    for (uint32_t t = 0; t < T; t += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (t + d < T) {
+                load(wd[(d + D - 1) % D], wd2[(d + D - 1) % D], min(t + d + D - 1, T - 1));
+                step(wd[d], wd2[d], t + d);
             }
         }
     }
@@ -261,13 +269,15 @@ __device__ __forceinline__ void embed_rows_q(const G4aEmbedParams& p) {
 
 }  // namespace
 
-#define G4A_LINEAR_WORDS(B, MT, RU, MODE)                                                               \
+// Variants (activation rows MT, weight rows RU, loads in flight D steps):
+// (1, 2, 4) short weights at M = 1, (1, 8, 2) tall weights at M = 1, (4, 4, 2) M >= 2.
+#define G4A_LINEAR_WORDS(B, MT, RU, D, MODE)                                                            \
     extern "C" __global__ __launch_bounds__(256) void g4a_linear_q_b##B##_m##MT##_r##RU##_mode##MODE( \
         G4aLinearParams p) {                                                                           \
-        linear_q_words<B, MT, RU, MODE>(p);                                                            \
+        linear_q_words<B, MT, RU, D, MODE>(p);                                                         \
     }
 #define G4A_LINEAR_SET(B, MODE) \
-    G4A_LINEAR_WORDS(B, 1, 2, MODE) G4A_LINEAR_WORDS(B, 1, 8, MODE) G4A_LINEAR_WORDS(B, 4, 4, MODE)
+    G4A_LINEAR_WORDS(B, 1, 2, 4, MODE) G4A_LINEAR_WORDS(B, 1, 8, 2, MODE) G4A_LINEAR_WORDS(B, 4, 4, 2, MODE)
 G4A_LINEAR_SET(2, 0)
 G4A_LINEAR_SET(2, 1)
 G4A_LINEAR_SET(2, 2)

@@ -234,8 +234,9 @@ int g4a_attn_producer(g4a_ctx *ctx, const g4a_producer_args *args);
  * of bytes per row.
  *
  * Rows that are whole 32-bit words (K * bits % 32 == 0) with one scale per row
- * (group_size >= K), a 4-byte aligned qbytes, 16-byte aligned x and K <= 16384
- * run the word-parallel kernel (HBM-bound, f32 sums in another order than the
+ * (group_size >= K), a 4-byte aligned qbytes, 16-byte aligned x and at most
+ * 16384 activations per row once the row's words are padded to a multiple of
+ * 64 run the word-parallel kernel (HBM-bound, f32 sums in another order than the
  * reference's, within f32 reordering error); every other weight runs one
  * thread per output in the reference CPU's order (bit-identical for
  * g4a_linear_q). */

@@ -99,7 +99,9 @@ def _linear_gpu(c, w, x):
 
 
 def _words_path(w):
-    return (w.K * w.bits) % 32 == 0 and w.group_size >= w.K and w.K * 4 <= 65536
+    words = w.K * w.bits // 32
+    kpad = -(-words // 64) * 64 * (32 // w.bits)  # the row padded to whole 64-word strides
+    return (w.K * w.bits) % 32 == 0 and w.group_size >= w.K and kpad * 4 <= 65536
 
 
 def test_golden_fixtures(ctx):
