@@ -115,12 +115,82 @@ HipTensor HipBackend::reshape(const HipTensor& x, std::vector<size_t> shape) {
     HipTensor t;
     t.buffer = x.buffer;
     t.ring_cap = x.ring_cap;
+    t.scales = x.scales;
+    t.quant = x.quant;
     t.shape = std::move(shape);
     return t;
 }
 
 // rust/src/backend_wgpu.rs:895-969 (the attention dispatch) and
 // rust/src/backend.rs:119-120 (the contract).
+HipTensor HipBackend::quant_tensor(const QuantWeight& q) {
+    const size_t N = q.shape[0], K = q.shape[1];
+    const size_t group = q.group_size ? q.group_size : K;
+    const size_t per_byte = q.signed_i8 ? 1 : 8 / q.bits;
+    const size_t row_bytes = q.signed_i8 ? K : K / per_byte;
+    const size_t stride = (K + group - 1) / group;
+    if (q.qbytes.size() < N * row_bytes || q.scales.size() < N * stride)
+        throw std::runtime_error("quant_tensor: payload smaller than the shape needs");
+    HipTensor t;
+    t.shape = {N, K};
+    t.buffer = alloc(std::max<size_t>(q.qbytes.size(), 4));
+    check(g4a_h2d(ctx_, t.buffer->ptr(), q.qbytes.data(), q.qbytes.size()), "quant_tensor (bytes)");
+    t.scales = alloc(q.scales.size() * sizeof(float));
+    check(g4a_h2d(ctx_, t.scales->ptr(), q.scales.data(), q.scales.size() * sizeof(float)), "quant_tensor (scales)");
+    g4a_qweight d{};
+    d.qbytes = t.buffer->ptr();
+    d.scales = static_cast<const float*>(t.scales->ptr());
+    d.N = uint32_t(N);
+    d.K = uint32_t(K);
+    d.bits = q.signed_i8 ? 8 : q.bits;
+    d.signed_i8 = q.signed_i8 ? 1 : 0;
+    d.group_size = uint32_t(group);
+    t.quant = d;
+    return t;
+}
+
+namespace {
+const g4a_qweight& quant_of(const HipTensor& w, const char* op) {
+    if (!w.quant) throw std::runtime_error(std::string(op) + ": the weight is not quantised (f32 weights are not in this build)");
+    return *w.quant;
+}
+}  // namespace
+
+HipTensor HipBackend::embed_rows(const HipTensor& table, const uint32_t* ids, size_t n_ids, float scale) {
+    const g4a_qweight& q = quant_of(table, "embed_rows");
+    HipTensor out = alloc_tensor({n_ids, size_t(q.K)});
+    check(g4a_embed_rows_q(ctx_, &q, ids, uint32_t(n_ids), scale, out.data()), "embed_rows");
+    return out;
+}
+
+HipTensor HipBackend::linear(const HipTensor& x, const HipTensor& w) {
+    const g4a_qweight& q = quant_of(w, "linear");
+    if (x.shape.size() != 2 || x.shape[1] != q.K) throw std::runtime_error("linear: x must be [T, K]");
+    HipTensor y = alloc_tensor({x.shape[0], size_t(q.N)});
+    check(g4a_linear_q(ctx_, &q, x.data(), y.data(), uint32_t(x.shape[0])), "linear");
+    return y;
+}
+
+HipTensor HipBackend::linear_geglu(const HipTensor& x, const HipTensor& w_gate, const HipTensor& w_up) {
+    const g4a_qweight& g = quant_of(w_gate, "linear_geglu");
+    const g4a_qweight& u = quant_of(w_up, "linear_geglu");
+    if (x.shape.size() != 2 || x.shape[1] != g.K) throw std::runtime_error("linear_geglu: x must be [T, K]");
+    HipTensor y = alloc_tensor({x.shape[0], size_t(g.N)});
+    check(g4a_linear_q_geglu(ctx_, &g, &u, x.data(), y.data(), uint32_t(x.shape[0])), "linear_geglu");
+    return y;
+}
+
+HipTensor HipBackend::linear_gelu_mul_cols(const HipTensor& x, const HipTensor& w, const HipTensor& b, size_t offset) {
+    const g4a_qweight& q = quant_of(w, "linear_gelu_mul_cols");
+    if (x.shape.size() != 2 || x.shape[1] != q.K || b.shape.size() != 2 || b.shape[0] != x.shape[0])
+        throw std::runtime_error("linear_gelu_mul_cols: x must be [M, K] and b [M, stride]");
+    HipTensor y = alloc_tensor({x.shape[0], size_t(q.N)});
+    check(g4a_linear_q_gelu_mul_cols(ctx_, &q, x.data(), b.data(), uint32_t(b.shape[1]), uint32_t(offset), y.data(),
+                                     uint32_t(x.shape[0])),
+          "linear_gelu_mul_cols");
+    return y;
+}
+
 HipTensor HipBackend::attention(const HipTensor& q, const HipTensor& k, const HipTensor& v, const AttnOpts& o) {
     if (q.shape.size() != 3 || k.shape.size() != 3 || v.shape.size() != 3)
         bad("attention wants q [T,Hq,Dh], k [S,Hkv,Dh], v [S,Hkv,Dv]; got " + shape_str(q.shape) + " " +

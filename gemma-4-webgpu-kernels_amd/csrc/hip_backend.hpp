@@ -43,6 +43,17 @@ struct AttnOpts {
 
 class HipBackend;
 
+// rust/src/backend.rs:12-58 (QuantWeight): packed rows (sub-byte offset-binary
+// fields LSB-first, or I8), one scale per (row, group), logical shape [N, K].
+struct QuantWeight {
+    std::vector<uint8_t> qbytes;
+    std::vector<float> scales;
+    size_t shape[2] = {0, 0};
+    uint32_t bits = 4;
+    bool signed_i8 = false;
+    size_t group_size = 0;
+};
+
 // A pooled device allocation; released to its backend's pool when the last
 // handle drops. Reuse is safe without a sync: every op runs on the backend's
 // single stream, so a later op that reuses the memory runs after every earlier
@@ -70,6 +81,10 @@ struct HipTensor {
     std::vector<size_t> shape;
     size_t cap_rows = 0;
     uint32_t ring_cap = 0;
+    // a quantised weight (rust/src/backend_wgpu.rs:78-86, GpuQuant): `buffer` holds
+    // the packed rows, `scales` the per-(row, group) scales
+    std::shared_ptr<DeviceBuffer> scales;
+    std::optional<g4a_qweight> quant;
 
     const std::vector<size_t>& dims() const { return shape; }
     size_t size() const {
@@ -102,8 +117,18 @@ public:
     HipTensor tensor(const float* data, std::vector<size_t> shape);
     HipTensor zeros(std::vector<size_t> shape);
     HipTensor reshape(const HipTensor& x, std::vector<size_t> shape);
+    // the packed weight kept in its quantised form (rust/src/backend.rs:94)
+    HipTensor quant_tensor(const QuantWeight& q);
 
     // --- ops ---
+    // out[i, :] = table[ids[i], :] * scale on a quantised [V, D] table (rust/src/backend.rs:100-101)
+    HipTensor embed_rows(const HipTensor& table, const uint32_t* ids, size_t n_ids, float scale);
+    // y = x . W^T; x [T, K], W [N, K] quantised (rust/src/backend.rs:105-106)
+    HipTensor linear(const HipTensor& x, const HipTensor& w);
+    // gelu(x . Wg^T) * (x . Wu^T) in one launch (rust/src/backend.rs:156-161)
+    HipTensor linear_geglu(const HipTensor& x, const HipTensor& w_gate, const HipTensor& w_up);
+    // gelu(x . W^T) * b[:, offset : offset + N], b [M, stride] (rust/src/backend.rs:162-168)
+    HipTensor linear_gelu_mul_cols(const HipTensor& x, const HipTensor& w, const HipTensor& b, size_t offset);
     // q [T,Hq,Dh], k [S,Hkv,Dh], v [S,Hkv,Dv] -> [T, Hq*Dv] (rust/src/backend.rs:119-120)
     HipTensor attention(const HipTensor& q, const HipTensor& k, const HipTensor& v, const AttnOpts& o);
     // y = x / sqrt(mean(x^2) + eps) * w per row of the last dim; w == nullptr for the

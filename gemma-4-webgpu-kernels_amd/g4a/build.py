@@ -76,10 +76,13 @@ def build_backend(verbose: bool = False) -> Path:
     TEST_BACKEND.parent.mkdir(parents=True, exist_ok=True)
     tmp = TEST_BACKEND.with_suffix(".tmp")
     oracle_obj = TEST_BACKEND.parent / "attn_oracle.o"
+    linear_obj = TEST_BACKEND.parent / "linear_oracle.o"
     _run(["gcc", "-O2", "-std=gnu11", "-ffp-contract=off", "-fno-fast-math", "-c", ORACLE_DIR / "attn_oracle.c",
           "-o", oracle_obj], verbose)
+    _run(["gcc", "-O2", "-std=gnu11", "-ffp-contract=off", "-fno-fast-math", "-c", ORACLE_DIR / "linear_oracle.c",
+          "-o", linear_obj], verbose)
     _run(["g++", "-O2", "-std=c++17", f"-I{INCLUDE}", f"-I{CSRC}", REPO / "tests" / "cpp" / "test_backend.cpp",
-          oracle_obj, "-o", tmp, f"-L{OUT}", "-lg4a_backend", "-lg4a", "-Wl,-rpath,$ORIGIN/../../../gemma-4-webgpu-kernels_amd/_build", "-lpthread", "-lm"],
+          oracle_obj, linear_obj, "-o", tmp, f"-L{OUT}", "-lg4a_backend", "-lg4a", "-Wl,-rpath,$ORIGIN/../../../gemma-4-webgpu-kernels_amd/_build", "-lpthread", "-lm"],
          verbose)
     tmp.replace(TEST_BACKEND)
     return LIBBACKEND

@@ -8,6 +8,10 @@
 //   norm_rope_parity           kernel_parity's rmsNorm and rope(partial) (rust/tests/gpu.rs:53-59,
 //                              :84-90, Lcg seed 7) and fused_op_parity's head_norm_rope cases
 //                              (rust/tests/gpu.rs:322-334, Lcg seed 33)
+//   quantized_kernel_parity    rust/tests/gpu.rs:146-190 (Lcg seed 9): q4/q2 linear at M = 5
+//                              and 1, q4 with K = 52, I8, the grouped-scale q4 embedding,
+//                              plus the fused GeGLU and gelu-times-columns projections,
+//                              against oracle/linear_oracle.c
 //   kv_cache_decode            prefill chunks + decode steps through KvCache, with a
 //                              sliding layer on a ring (incl. regrowth and wrap-around)
 //                              and a global layer on the growing buffer, every step
@@ -15,6 +19,7 @@
 //
 // The bar is the north star's: max-abs <= 1e-5 and mean-abs <= 1e-6 (f32),
 // exact equality for the copies. Exit status 0 = all passed.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -29,6 +34,14 @@ extern "C" int oracle_attention(const float* q, const float* k, const float* v, 
                                 const uint32_t* k_pos, float scale, uint32_t window, float softcap,
                                 int requested_threads);
 
+extern "C" void oracle_linear_q(const uint8_t* qb, const float* scales, size_t N, size_t K, uint32_t bits,
+                                int signed_i8, size_t group, const float* x, size_t M, float* y);
+extern "C" float oracle_gelu_tanh(float v);
+extern "C" float oracle_deq(const uint8_t* qb, const float* scales, size_t K, uint32_t bits, int signed_i8,
+                            size_t group, size_t n, size_t k);
+extern "C" void oracle_embed_rows_q(const uint8_t* qb, const float* scales, size_t V, size_t D, uint32_t bits,
+                                    int signed_i8, size_t group, const uint32_t* ids, size_t T, float scale,
+                                    float* out);
 extern "C" void oracle_rms_norm(const float* x, const float* w, float* y, size_t rows, size_t d, float eps);
 extern "C" void oracle_rope(const float* x, float* y, size_t T, size_t heads, size_t head_dim, size_t rotary_dim,
                             const uint32_t* positions, float theta);
@@ -285,6 +298,191 @@ void norm_rope_parity(g4a::HipBackend& b) {
     }
 }
 
+// rust/src/dequant.rs:53-63 (pack_unsigned): raw fields LSB-first
+std::vector<uint8_t> pack_unsigned(const std::vector<uint32_t>& v, uint32_t bits) {
+    const size_t per = 8 / bits;
+    std::vector<uint8_t> out((v.size() + per - 1) / per, 0);
+    for (size_t i = 0; i < v.size(); ++i)
+        out[i / per] |= uint8_t((v[i] & ((1u << bits) - 1)) << ((i % per) * bits));
+    return out;
+}
+
+// The word-parallel kernel sums in another order than the CPU: per output
+// |gpu - oracle| <= 2e-6 * sum_k |x_k w_nk| + 1e-7 (the reference's own test
+// allows 2e-3 absolute, rust/tests/gpu.rs:156-190).
+void close_linear(const std::string& label, const std::vector<float>& got, const std::vector<float>& want,
+                  const g4a::QuantWeight& q, const std::vector<float>& x, size_t m) {
+    const size_t N = q.shape[0], K = q.shape[1];
+    double worst = 0.0, max_abs = 0.0;
+    bool ok = got.size() == want.size();
+    for (size_t i = 0; ok && i < m; ++i)
+        for (size_t n = 0; n < N; ++n) {
+            double bound = 0.0;
+            for (size_t k = 0; k < K; ++k)
+                bound += std::fabs(double(x[i * K + k])) *
+                         std::fabs(double(oracle_deq(q.qbytes.data(), q.scales.data(), K, q.bits, q.signed_i8 ? 1 : 0,
+                                                     q.group_size, n, k)));
+            const double err = std::fabs(double(got[i * N + n]) - double(want[i * N + n]));
+            const double tol = 2e-6 * bound + 1e-7;
+            worst = std::max(worst, err / tol);
+            max_abs = std::max(max_abs, err);
+        }
+    char buf[128];
+    std::snprintf(buf, sizeof buf, " (max-abs %.3e, worst err/tol %.3f)", max_abs, worst);
+    expect(ok && worst <= 1.0, label + buf);
+}
+
+// sum_k |x_ik w_nk| per output [m, N]
+std::vector<double> abs_bound(const g4a::QuantWeight& q, const std::vector<float>& x, size_t m) {
+    const size_t N = q.shape[0], K = q.shape[1];
+    std::vector<double> out(m * N, 0.0);
+    for (size_t i = 0; i < m; ++i)
+        for (size_t n = 0; n < N; ++n)
+            for (size_t k = 0; k < K; ++k)
+                out[i * N + n] += std::fabs(double(x[i * K + k])) *
+                                  std::fabs(double(oracle_deq(q.qbytes.data(), q.scales.data(), K, q.bits,
+                                                              q.signed_i8 ? 1 : 0, q.group_size, n, k)));
+    return out;
+}
+
+// gelu(g) * u with g, u reordered sums: the bound of each carried through
+// (|gelu'| < 1.13), plus 2e-6 relative for tanhf
+void close_fused(const std::string& label, const std::vector<float>& got, const std::vector<float>& want,
+                 const std::vector<float>& g, const std::vector<double>& bg, const std::vector<float>& u,
+                 const std::vector<double>* bu) {
+    double worst = 0.0, max_abs = 0.0;
+    bool ok = got.size() == want.size();
+    for (size_t i = 0; ok && i < want.size(); ++i) {
+        double tol = 1.13 * (2e-6 * bg[i] + 1e-7) * std::fabs(double(u[i]));
+        if (bu) tol += std::fabs(double(oracle_gelu_tanh(g[i]))) * (2e-6 * (*bu)[i] + 1e-7);
+        tol += 2e-6 * std::fabs(double(want[i])) + 1e-7;
+        const double err = std::fabs(double(got[i]) - double(want[i]));
+        worst = std::max(worst, err / tol);
+        max_abs = std::max(max_abs, err);
+    }
+    char buf[128];
+    std::snprintf(buf, sizeof buf, " (max-abs %.3e, worst err/tol %.3f)", max_abs, worst);
+    expect(ok && worst <= 1.0, label + buf);
+}
+
+std::vector<float> oracle_linear(const g4a::QuantWeight& q, const std::vector<float>& x, size_t m) {
+    std::vector<float> y(m * q.shape[0]);
+    oracle_linear_q(q.qbytes.data(), q.scales.data(), q.shape[0], q.shape[1], q.bits, q.signed_i8 ? 1 : 0,
+                    q.group_size, x.data(), m, y.data());
+    return y;
+}
+
+void quantized_kernel_parity(g4a::HipBackend& b) {
+    std::printf("quantized_kernel_parity\n");
+    Lcg r(9);
+    auto scales = [&](size_t n) {
+        std::vector<float> s(n);
+        for (auto& v : s) v = 0.01f + r.next() * 0.05f;
+        return s;
+    };
+    auto randu = [&](size_t n, uint32_t bits) {
+        std::vector<uint32_t> v(n);
+        for (auto& x : v) x = uint32_t(std::floor(r.next() * float(1u << bits))) % (1u << bits);
+        return v;
+    };
+    for (uint32_t bits : {4u, 2u}) {
+        const size_t n = 40, k = 64;
+        g4a::QuantWeight q;
+        q.qbytes = pack_unsigned(randu(n * k, bits), bits);
+        q.scales = scales(n);
+        q.shape[0] = n;
+        q.shape[1] = k;
+        q.bits = bits;
+        q.group_size = k;
+        const auto gw = b.quant_tensor(q);
+        for (size_t m : {size_t(5), size_t(1)}) {
+            const auto x = r.rand(m * k, 1.0f);
+            close_linear("linear q" + std::to_string(bits) + " M=" + std::to_string(m),
+                         b.readback(b.linear(b.tensor(x.data(), {m, k}), gw)), oracle_linear(q, x, m), q, x, m);
+        }
+    }
+    {
+        const uint32_t bits = 4;
+        const size_t n = 21, k = 52, m = 3;
+        g4a::QuantWeight q;
+        q.qbytes = pack_unsigned(randu(n * k, bits), bits);
+        q.scales = scales(n);
+        q.shape[0] = n;
+        q.shape[1] = k;
+        q.bits = bits;
+        q.group_size = k;
+        const auto x = r.rand(m * k, 1.0f);
+        const auto got = b.readback(b.linear(b.tensor(x.data(), {m, k}), b.quant_tensor(q)));
+        expect(got == oracle_linear(q, x, m), "linear q4 oddK (element kernel, bit-exact)");
+    }
+    {
+        const size_t n = 30, k = 48, m = 4;
+        g4a::QuantWeight q;
+        q.qbytes.resize(n * k);
+        for (auto& v : q.qbytes) v = uint8_t(uint32_t(std::floor(r.next() * 256.0f)));
+        q.scales.resize(n);
+        for (auto& v : q.scales) v = 0.01f + r.next() * 0.03f;
+        q.shape[0] = n;
+        q.shape[1] = k;
+        q.bits = 8;
+        q.signed_i8 = true;
+        q.group_size = k;
+        const auto x = r.rand(m * k, 1.0f);
+        close_linear("linear i8", b.readback(b.linear(b.tensor(x.data(), {m, k}), b.quant_tensor(q))),
+                     oracle_linear(q, x, m), q, x, m);
+    }
+    {
+        const size_t v = 50, d = 32, group = 16;
+        const uint32_t bits = 4;
+        g4a::QuantWeight q;
+        q.qbytes = pack_unsigned(randu(v * d, bits), bits);
+        q.scales.resize(v * (d / group));
+        for (auto& s : q.scales) s = 0.02f + r.next() * 0.04f;
+        q.shape[0] = v;
+        q.shape[1] = d;
+        q.bits = bits;
+        q.group_size = group;
+        const uint32_t ids[5] = {3, 7, 49, 0, 21};
+        const float sc = std::sqrt(float(d));
+        std::vector<float> want(5 * d);
+        oracle_embed_rows_q(q.qbytes.data(), q.scales.data(), v, d, bits, 0, group, ids, 5, sc, want.data());
+        expect(b.readback(b.embed_rows(b.quant_tensor(q), ids, 5, sc)) == want, "embed q4 grouped (bit-exact)");
+    }
+    // the fused projections (rust/src/backend.rs:156-168 compositions)
+    {
+        const size_t n = 96, k = 256, m = 3;
+        const uint32_t bits = 4;
+        g4a::QuantWeight qg, qu;
+        for (auto* q : {&qg, &qu}) {
+            q->qbytes = pack_unsigned(randu(n * k, bits), bits);
+            q->scales = scales(n);
+            q->shape[0] = n;
+            q->shape[1] = k;
+            q->bits = bits;
+            q->group_size = k;
+        }
+        const auto x = r.rand(m * k, 1.0f);
+        const auto g = oracle_linear(qg, x, m), u = oracle_linear(qu, x, m);
+        std::vector<float> want(m * n);
+        for (size_t i = 0; i < want.size(); ++i) want[i] = oracle_gelu_tanh(g[i]) * u[i];
+        const auto gx = b.tensor(x.data(), {m, k});
+        const auto bg = abs_bound(qg, x, m), bu = abs_bound(qu, x, m);
+        close_fused("linear_geglu q4", b.readback(b.linear_geglu(gx, b.quant_tensor(qg), b.quant_tensor(qu))), want,
+                    g, bg, u, &bu);
+        const size_t stride = 5 * n, off = 2 * n;
+        const auto bs = r.rand(m * stride, 1.0f);
+        std::vector<float> cols(m * n);
+        for (size_t i = 0; i < m; ++i)
+            for (size_t j = 0; j < n; ++j) {
+                cols[i * n + j] = bs[i * stride + off + j];
+                want[i * n + j] = oracle_gelu_tanh(g[i * n + j]) * cols[i * n + j];
+            }
+        close_fused("linear_gelu_mul_cols q4",
+                    b.readback(b.linear_gelu_mul_cols(gx, b.quant_tensor(qg), b.tensor(bs.data(), {m, stride}), off)),
+                    want, g, bg, cols, nullptr);
+    }
+}
+
 }  // namespace
 
 int main() {
@@ -299,6 +497,7 @@ int main() {
         grouped_attention_parity(*b);
         copies_and_kv_append(*b);
         norm_rope_parity(*b);
+        quantized_kernel_parity(*b);
         kv_cache_decode(*b);
     } catch (const std::exception& e) {
         std::fprintf(stderr, "test_backend: exception: %s\n", e.what());
