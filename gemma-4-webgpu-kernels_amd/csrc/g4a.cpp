@@ -61,6 +61,7 @@ struct g4a_ctx {
     hipFunction_t norm_rope = nullptr;  // the attention producer (RMSNorm + RoPE + KV write)
     hipFunction_t linear_words[3][3][3] = {};  // [bits 2/4/8][(MT, RU) = (1, 2), (1, 8), (4, 4)][mode]
     hipFunction_t linear_elem[3] = {};         // [mode]
+    hipFunction_t linear_mfma[3][3] = {};      // [bits 2/4/8][mode]: M >= 16 on the matrix cores
     hipFunction_t embed_q = nullptr;
     // RoPE frequency tables theta^(-2j/rot), one per (theta, rotary_dim) seen
     struct FreqTable {
@@ -442,6 +443,10 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
             char name[64];
             snprintf(name, sizeof name, "g4a_linear_q_elem_mode%d", m);
             if (int rc = get_fn(ctx, &ctx->linear_elem[m], name)) return bail(rc);
+            for (int b = 0; b < 3; ++b) {
+                snprintf(name, sizeof name, "g4a_linear_q_mfma_b%d_mode%d", bits[b], m);
+                if (int rc = get_fn(ctx, &ctx->linear_mfma[b][m], name)) return bail(rc);
+            }
         }
         if (int rc = get_fn(ctx, &ctx->embed_q, "g4a_embed_rows_q")) return bail(rc);
     }
@@ -905,6 +910,8 @@ int norm_rope_launch(g4a_ctx* ctx, G4aNormRopeSeg* segs, uint32_t nseg, uint32_t
 
 // Activation rows of the word-parallel kernel kept in LDS per workgroup.
 constexpr size_t LINEAR_LDS_BYTES = 64 << 10;
+// Activation rows from which a projection runs on the matrix cores.
+constexpr uint32_t LINEAR_MFMA_MIN_M = 16;
 
 int check_qweight(g4a_ctx* ctx, const g4a_qweight* w, const char* what) {
     if (!w) return fail(ctx, G4A_E_ARG, "%s: null weight", what);
@@ -957,6 +964,28 @@ int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qwei
     const bool aligned = (reinterpret_cast<uintptr_t>(w->qbytes) & 3) == 0 &&
                          (mode != 1 || (reinterpret_cast<uintptr_t>(w2->qbytes) & 3) == 0) &&
                          (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    const bool aligned8 = aligned && (reinterpret_cast<uintptr_t>(w->qbytes) & 7) == 0 &&
+                          (mode != 1 || (reinterpret_cast<uintptr_t>(w2->qbytes) & 7) == 0);
+    // sub-byte fields are offset binary: flipping each field's top bit makes it two's complement
+    p.xm = w->signed_i8 ? 0u : w->bits == 4 ? 0x88888888u : w->bits == 2 ? 0xAAAAAAAAu : 0x80808080u;
+    const int bi = w->bits == 2 ? 0 : w->bits == 4 ? 1 : 2;
+    if (M >= LINEAR_MFMA_MIN_M && w->K % 64 == 0 && p.scale_stride == 1 && aligned8) {
+        // 64 activation rows x 64 weight rows per workgroup on the matrix cores
+        p.wb = static_cast<const uint8_t*>(w->qbytes);
+        p.wb2 = mode == 1 ? static_cast<const uint8_t*>(w2->qbytes) : nullptr;
+        const uint32_t gx = (w->N + 63) / 64;
+        for (uint32_t m0 = 0; m0 < M; m0 += 65535u * 64) {
+            G4aLinearParams q = p;
+            q.x = x + size_t(m0) * w->K;
+            q.y = y + size_t(m0) * w->N;
+            q.b = b ? b + size_t(m0) * b_stride : nullptr;
+            q.M = std::min<uint32_t>(65535u * 64, M - m0);
+            if (int rc = launch(ctx, ctx->linear_mfma[bi][mode], dim3(gx, (q.M + 63) / 64, 1), dim3(256, 1, 1), q,
+                                "quantised linear (matrix cores)", true))
+                return rc;
+        }
+        return G4A_OK;
+    }
     // the word kernel's activation rows, zero-padded to whole wave strides of words
     const uint64_t vpw = 32 / w->bits, words_per_row = uint64_t(w->K) * w->bits / 32;
     const uint64_t kpad = (words_per_row + 63) / 64 * 64 * vpw;
@@ -980,10 +1009,7 @@ int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qwei
     }
     p.w = static_cast<const uint32_t*>(w->qbytes);
     p.w2 = mode == 1 ? static_cast<const uint32_t*>(w2->qbytes) : nullptr;
-    p.W = uint32_t(uint64_t(w->K) * w->bits / 32);
-    // sub-byte fields are offset binary: flipping each field's top bit makes it two's complement
-    p.xm = w->signed_i8 ? 0u : w->bits == 4 ? 0x88888888u : w->bits == 2 ? 0xAAAAAAAAu : 0x80808080u;
-    const int bi = w->bits == 2 ? 0 : w->bits == 4 ? 1 : 2;
+    p.W = uint32_t(words_per_row);
     const uint64_t cus = uint64_t(std::max(ctx->cu_count, 1));
     // 4 activation rows per workgroup when they fit its LDS share, else 1; 8 weight
     // rows in flight per wave for tall weights, 2 for short ones (more waves)

@@ -225,6 +225,172 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill projections (M >= 16) on the matrix cores: v_mfma_f32_16x16x32_bf16
+// with exact products. x = x0 + x1 + x2 exactly, each part a bf16 holding the
+// next 8 significant bits (rounded splits of an f32 leave at most 8 bits for
+// the last part); the quantised fields times F are small integers, exact in
+// bf16. So every product x_p * q is exact in f32 and the three partial sums
+// differ from the f32 sum only by accumulation rounding, like the VALU kernel.
+//
+// Workgroup: 64 activation rows (tokens) x 64 weight rows, 4 waves; wave w owns
+// weight rows 16w .. 16w + 15 (the MFMA's A operand, one 8-value fragment per
+// lane: row lane % 16, k 8 (lane / 16) .. + 7 of each 32-wide sub-step) and all
+// 64 tokens (four 16-token B blocks). Per 64-wide k step the workgroup stages
+// the three bf16 parts of its x tile in LDS (double-buffered); the next step's
+// x and weight fragments are loaded into registers before this step's MFMAs.
+// C lane layout: weight row 4 (lane / 16) + i, token lane % 16.
+typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr int LQ_BM = 64, LQ_BN = 64, LQ_BK = 64;
+constexpr int LQ_XS = LQ_BK + 8;  // bf16 per staged x row (+16 bytes: rows start on different banks)
+
+// The 8 fields of row `row` at k .. k + 7 as value * F.
+template <int BITS>
+__device__ __forceinline__ void frag8(const uint8_t* __restrict__ rowp, uint32_t k, uint32_t xm, float (&q)[8]) {
+    if constexpr (BITS == 4) {
+        float t[8];
+        unpack<4>(*reinterpret_cast<const uint32_t*>(rowp + k / 2) ^ xm, t);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = t[i];
+    } else if constexpr (BITS == 8) {
+        const uint2 w = *reinterpret_cast<const uint2*>(rowp + k);
+        float t0[4], t1[4];
+        unpack<8>(w.x ^ xm, t0);
+        unpack<8>(w.y ^ xm, t1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q[i] = t0[i];
+            q[4 + i] = t1[i];
+        }
+    } else {
+        const uint32_t h = *reinterpret_cast<const uint16_t*>(rowp + k / 4);
+        float t[16];
+        unpack<2>((h ^ xm) & 0xFFFFu, t);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = t[i];
+    }
+}
+
+template <int BITS, int MODE>
+__device__ __forceinline__ void linear_q_mfma(const G4aLinearParams& p) {
+    using F = QFmt<BITS>;
+    __shared__ __attribute__((aligned(16))) __bf16 xsp[2][3][LQ_BM * LQ_XS];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, rl = lane & 15;
+    const uint32_t K = p.K, N = p.N, M = p.M;
+    const uint32_t n0 = blockIdx.x * LQ_BN, m0 = blockIdx.y * LQ_BM;
+    const uint32_t nsteps = K / LQ_BK;
+    const uint32_t row = min(n0 + 16 * wv + rl, N - 1);  // this lane's A row (rows past N: re-read, not stored)
+    const uint8_t* __restrict__ wrow = p.wb + (size_t)row * p.row_bytes;
+    const uint8_t* __restrict__ wrow2 = MODE == 1 ? p.wb2 + (size_t)row * p.row_bytes : nullptr;
+
+    // x tile staging: thread tid splits tokens tid / 4 (16 values at 16 (tid % 4))
+    const uint32_t xt = tid >> 2, xk = 16 * (tid & 3);
+    const bool xin = m0 + xt < M;
+    const float* __restrict__ xrow = p.x + (size_t)min(m0 + xt, M - 1) * K;
+    float4 xr[4];
+    auto load_x = [&](uint32_t st) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            xr[i] = xin ? *reinterpret_cast<const float4*>(xrow + st * LQ_BK + xk + 4 * i)
+                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    };
+    auto stage_x = [&](int buf) {
+        const float v[16] = {xr[0].x, xr[0].y, xr[0].z, xr[0].w, xr[1].x, xr[1].y, xr[1].z, xr[1].w,
+                             xr[2].x, xr[2].y, xr[2].z, xr[2].w, xr[3].x, xr[3].y, xr[3].z, xr[3].w};
+        bf8v p0[2], p1[2], p2[2];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const __bf16 a = (__bf16)v[i];
+            const float r1 = v[i] - (float)a;
+            const __bf16 b = (__bf16)r1;
+            const __bf16 c = (__bf16)(r1 - (float)b);
+            p0[i / 8][i % 8] = a;
+            p1[i / 8][i % 8] = b;
+            p2[i / 8][i % 8] = c;
+        }
+        __bf16* d0 = &xsp[buf][0][xt * LQ_XS + xk];
+        __bf16* d1 = &xsp[buf][1][xt * LQ_XS + xk];
+        __bf16* d2 = &xsp[buf][2][xt * LQ_XS + xk];
+        *reinterpret_cast<bf8v*>(d0) = p0[0];
+        *reinterpret_cast<bf8v*>(d0 + 8) = p0[1];
+        *reinterpret_cast<bf8v*>(d1) = p1[0];
+        *reinterpret_cast<bf8v*>(d1 + 8) = p1[1];
+        *reinterpret_cast<bf8v*>(d2) = p2[0];
+        *reinterpret_cast<bf8v*>(d2 + 8) = p2[1];
+    };
+    // A fragments of one step: sub-step kk covers k 32 kk + 8 g .. + 7
+    float qa[2][8], qb2[2][8];
+    auto load_w = [&](uint32_t st) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const uint32_t k = st * LQ_BK + 32 * kk + 8 * g;
+            frag8<BITS>(wrow, k, p.xm, qa[kk]);
+            if (MODE == 1) frag8<BITS>(wrow2, k, p.xm, qb2[kk]);
+        }
+    };
+
+    f4v acc[4], acc2[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) acc[tb] = acc2[tb] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    if (nsteps) {
+        load_x(0);
+        load_w(0);
+        stage_x(0);
+    }
+    for (uint32_t st = 0; st < nsteps; ++st) {
+        __syncthreads();  // step st's x parts are staged; every wave is done with the other buffer
+        bf8v a[2], a2[2];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                a[kk][i] = (__bf16)qa[kk][i];
+                if (MODE == 1) a2[kk][i] = (__bf16)qb2[kk][i];
+            }
+        if (st + 1 < nsteps) {
+            load_x(st + 1);
+            load_w(st + 1);
+        }
+        const int buf = st & 1;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                const int off = (16 * tb + rl) * LQ_XS + 32 * kk + 8 * g;
+#pragma unroll
+                for (int part = 0; part < 3; ++part) {
+                    const bf8v bx = *reinterpret_cast<const bf8v*>(&xsp[buf][part][off]);
+                    acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kk], bx, acc[tb], 0, 0, 0);
+                    if (MODE == 1) acc2[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[kk], bx, acc2[tb], 0, 0, 0);
+                }
+            }
+        if (st + 1 < nsteps) stage_x(buf ^ 1);
+    }
+
+    // lane (g, rl) of block tb holds weight rows 16 wv + 4 g + i, token 16 tb + rl
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        const uint32_t m = m0 + 16 * tb + rl;
+        if (m >= M) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t n = n0 + 16 * wv + 4 * g + i;
+            if (n >= N) continue;
+            const float v = acc[tb][i] * (p.s[n] * F::INV_F);
+            float o = v;
+            if (MODE == 1) o = gelu_tanh(v) * (acc2[tb][i] * (p.s2[n] * F::INV_F));
+            if (MODE == 2) o = gelu_tanh(v) * p.b[(size_t)m * p.b_stride + p.b_off + n];
+            p.y[(size_t)m * N + n] = o;
+        }
+    }
+}
+
 // QuantWeight::deq (rust/src/backend.rs:44-58) of element (n, k).
 __device__ __forceinline__ float deq(const uint8_t* __restrict__ wb, const float* __restrict__ s, uint32_t bits,
                                      uint32_t row_bytes, uint32_t group, uint32_t sstride, uint32_t signed_i8,
@@ -287,6 +453,20 @@ G4A_LINEAR_SET(4, 2)
 G4A_LINEAR_SET(8, 0)
 G4A_LINEAR_SET(8, 1)
 G4A_LINEAR_SET(8, 2)
+
+#define G4A_LINEAR_MFMA(B, MODE)                                                                 \
+    extern "C" __global__ __launch_bounds__(256) void g4a_linear_q_mfma_b##B##_mode##MODE(G4aLinearParams p) { \
+        linear_q_mfma<B, MODE>(p);                                                               \
+    }
+G4A_LINEAR_MFMA(2, 0)
+G4A_LINEAR_MFMA(2, 1)
+G4A_LINEAR_MFMA(2, 2)
+G4A_LINEAR_MFMA(4, 0)
+G4A_LINEAR_MFMA(4, 1)
+G4A_LINEAR_MFMA(4, 2)
+G4A_LINEAR_MFMA(8, 0)
+G4A_LINEAR_MFMA(8, 1)
+G4A_LINEAR_MFMA(8, 2)
 
 extern "C" __global__ __launch_bounds__(64) void g4a_linear_q_elem_mode0(G4aLinearParams p) { linear_q_elem<0>(p); }
 extern "C" __global__ __launch_bounds__(64) void g4a_linear_q_elem_mode1(G4aLinearParams p) { linear_q_elem<1>(p); }

@@ -237,9 +237,10 @@ int g4a_attn_producer(g4a_ctx *ctx, const g4a_producer_args *args);
  * (group_size >= K), a 4-byte aligned qbytes, 16-byte aligned x and at most
  * 16384 activations per row once the row's words are padded to a multiple of
  * 64 run the word-parallel kernel (HBM-bound, f32 sums in another order than the
- * reference's, within f32 reordering error); every other weight runs one
- * thread per output in the reference CPU's order (bit-identical for
- * g4a_linear_q). */
+ * reference's, within f32 reordering error); with M >= 16, K % 64 == 0 and an
+ * 8-byte aligned qbytes they run on the matrix cores instead (exact products,
+ * f32 accumulation, the same error bound); every other weight runs one thread
+ * per output in the reference CPU's order (bit-identical for g4a_linear_q). */
 typedef struct {
     const void *qbytes;
     const float *scales;

@@ -252,3 +252,38 @@ def test_argument_errors(ctx):
         finally:
             bad.free()
         c.linear_q(dw, x.ptr, y.ptr, 0)  # M = 0: nothing to do
+
+
+@pytest.mark.parametrize("bits,signed", [(2, False), (4, False), (8, True)])
+def test_matrix_core_shapes(ctx, bits, signed):
+    """M >= 16 with K % 64 == 0 runs on the matrix cores (x split into three exact
+    bf16 parts, exact products, f32 accumulation): ragged token and weight-row
+    tiles, K past the word kernel's LDS limit, Gemma-4 prefill shapes."""
+    c = ctx
+    for N, K, M in [(40, 64, 17), (64, 1536, 16), (1536, 2048, 100), (256, 6144, 300), (12288, 1536, 64),
+                    (64, 20480, 16), (100, 4096, 65)]:
+        label = f"mfma b{bits}{'s' if signed else ''} N={N} K={K} M={M}"
+        step(label)
+        w = _qw(N * 3 + K + M, N, K, bits, signed)
+        x = synth.normal_f32(N + 2 * K, M, M * K).reshape(M, K)
+        _check_sum(_linear_gpu(c, w, x), oracle.linear_q(x, w), _bound(x, w), label)
+
+
+def test_matrix_core_fused_epilogues(ctx):
+    c = ctx
+    N, K, M = 2048, 1536, 64
+    wg, wu = _qw(91, N, K, 4), _qw(92, N, K, 4)
+    x = synth.normal_f32(93, M, M * K).reshape(M, K)
+    step("mfma geglu [2048, 1536] M=64")
+    with Dev(c) as d:
+        y = d.empty((M, N))
+        c.linear_q_geglu(d.w(wg), d.w(wu), d.arr(x).ptr, y.ptr, M)
+        _check_fused(y.to_host(), x, wg, wu, None, 0, "mfma geglu")
+    w = _qw(94, 256, 1536, 4)
+    x = synth.normal_f32(95, 33, 33 * 1536).reshape(33, 1536)
+    b = synth.normal_f32(96, 33, 33 * 35 * 256).reshape(33, 35 * 256)
+    step("mfma per-layer gate [256, 1536] M=33")
+    with Dev(c) as d:
+        y = d.empty((33, 256))
+        c.linear_q_gelu_mul_cols(d.w(w), d.arr(x).ptr, d.arr(b).ptr, 35 * 256, 20 * 256, y.ptr, 33)
+        _check_fused(y.to_host(), x, w, None, b, 20 * 256, "mfma per-layer gate")
