@@ -63,6 +63,12 @@ struct g4a_ctx {
     hipFunction_t linear_elem[3] = {};         // [mode]
     hipFunction_t linear_mfma[3][3] = {};      // [bits 2/4/8][mode]: M >= 16 on the matrix cores
     hipFunction_t embed_q = nullptr;
+    hipFunction_t linear_f32_words[3] = {};  // f32 weights: (MT, RU) = (1, 2), (1, 8), (4, 4)
+    hipFunction_t linear_f32_elem = nullptr;
+    hipFunction_t ew = nullptr;              // elementwise ops
+    hipFunction_t slice_cols = nullptr;
+    hipFunction_t rms_rows = nullptr;        // (residual +) RMSNorm (* scalar) over rows of any width
+    hipFunction_t embed_f32 = nullptr;
     // RoPE frequency tables theta^(-2j/rot), one per (theta, rotary_dim) seen
     struct FreqTable {
         float theta;
@@ -449,6 +455,15 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
             }
         }
         if (int rc = get_fn(ctx, &ctx->embed_q, "g4a_embed_rows_q")) return bail(rc);
+        static const char* f32_words[3] = {"g4a_linear_q_b32_m1_r2_mode0", "g4a_linear_q_b32_m1_r8_mode0",
+                                           "g4a_linear_q_b32_m4_r4_mode0"};
+        for (int v = 0; v < 3; ++v)
+            if (int rc = get_fn(ctx, &ctx->linear_f32_words[v], f32_words[v])) return bail(rc);
+        if (int rc = get_fn(ctx, &ctx->linear_f32_elem, "g4a_linear_f32_elem")) return bail(rc);
+        if (int rc = get_fn(ctx, &ctx->ew, "g4a_ew")) return bail(rc);
+        if (int rc = get_fn(ctx, &ctx->slice_cols, "g4a_slice_cols")) return bail(rc);
+        if (int rc = get_fn(ctx, &ctx->rms_rows, "g4a_rms_rows")) return bail(rc);
+        if (int rc = get_fn(ctx, &ctx->embed_f32, "g4a_embed_rows_f32")) return bail(rc);
     }
     if (hipMalloc(reinterpret_cast<void**>(&ctx->dummy), 4096) != hipSuccess ||
         hipMemset(ctx->dummy, 0, 4096) != hipSuccess) {
@@ -913,6 +928,30 @@ constexpr size_t LINEAR_LDS_BYTES = 64 << 10;
 // Activation rows from which a projection runs on the matrix cores.
 constexpr uint32_t LINEAR_MFMA_MIN_M = 16;
 
+// Grid of a grid-stride elementwise launch over n items.
+dim3 ew_grid(g4a_ctx* ctx, size_t n) {
+    const size_t want = (n + 255) / 256, cap = size_t(std::max(ctx->cu_count, 1)) * 16;
+    return dim3(uint32_t(std::max<size_t>(1, std::min(want, cap))), 1, 1);
+}
+
+int ew_launch(g4a_ctx* ctx, G4aEwOp op, const float* a, const float* b, const float* sp, float s, float* y, size_t n) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (n == 0) return G4A_OK;
+    const bool binary = op == G4A_EW_ADD || op == G4A_EW_MUL || op == G4A_EW_GEGLU;
+    if (!a || !y || (binary && !b) || (op == G4A_EW_SCALE_BY && !sp)) return fail(ctx, G4A_E_ARG, "null operand");
+    G4aEwParams p{a, b, sp, y, n, s, uint32_t(op)};
+    return launch(ctx, ctx->ew, ew_grid(ctx, n), dim3(256, 1, 1), p, "elementwise", true);
+}
+
+int rms_rows_launch(g4a_ctx* ctx, const float* res, const float* x, const float* w, const float* scale_by, float* y,
+                    uint32_t rows, uint32_t dim, float eps) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (rows == 0) return G4A_OK;
+    if (!x || !y || dim == 0) return fail(ctx, G4A_E_ARG, "null x/y or zero width");
+    G4aRmsRowsParams p{x, w, res, scale_by, y, rows, dim, eps};
+    return launch(ctx, ctx->rms_rows, dim3(rows, 1, 1), dim3(256, 1, 1), p, "rms rows", true);
+}
+
 int check_qweight(g4a_ctx* ctx, const g4a_qweight* w, const char* what) {
     if (!w) return fail(ctx, G4A_E_ARG, "%s: null weight", what);
     if (!w->qbytes || !w->scales) return fail(ctx, G4A_E_ARG, "%s: null qbytes/scales", what);
@@ -1095,8 +1134,112 @@ int g4a_head_norm_rope(g4a_ctx* ctx, const float* x, const float* w, float* y, u
 
 int g4a_rms_norm(g4a_ctx* ctx, const float* x, const float* w, float* y, uint32_t rows, uint32_t dim, float eps) {
     if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (dim % 4 != 0 || dim > 1024)  // wide or ragged rows: a workgroup per row
+        return rms_rows_launch(ctx, nullptr, x, w, nullptr, y, rows, dim, eps);
     G4aNormRopeSeg seg{x, w, y, rows, 1u, 0u, 0u, 0u};
     return norm_rope_launch(ctx, &seg, 1, 1, dim, 0, nullptr, 0, 0.0f, eps, 0, 0);
+}
+
+int g4a_add_rms_norm(g4a_ctx* ctx, const float* residual, const float* x, const float* w, const float* scale_by,
+                     float* y, uint32_t rows, uint32_t dim, float eps) {
+    if (!residual || !w) return fail(ctx, G4A_E_ARG, "null residual/weight");
+    return rms_rows_launch(ctx, residual, x, w, scale_by, y, rows, dim, eps);
+}
+
+int g4a_add(g4a_ctx* ctx, const float* a, const float* b, float* y, size_t n) {
+    return ew_launch(ctx, G4A_EW_ADD, a, b, nullptr, 0.0f, y, n);
+}
+int g4a_mul(g4a_ctx* ctx, const float* a, const float* b, float* y, size_t n) {
+    return ew_launch(ctx, G4A_EW_MUL, a, b, nullptr, 0.0f, y, n);
+}
+int g4a_scale(g4a_ctx* ctx, const float* a, float s, float* y, size_t n) {
+    return ew_launch(ctx, G4A_EW_SCALE, a, nullptr, nullptr, s, y, n);
+}
+int g4a_scale_by_tensor(g4a_ctx* ctx, const float* a, const float* s, float* y, size_t n) {
+    return ew_launch(ctx, G4A_EW_SCALE_BY, a, nullptr, s, 0.0f, y, n);
+}
+int g4a_gelu_tanh(g4a_ctx* ctx, const float* a, float* y, size_t n) {
+    return ew_launch(ctx, G4A_EW_GELU, a, nullptr, nullptr, 0.0f, y, n);
+}
+int g4a_geglu(g4a_ctx* ctx, const float* gate, const float* up, float* y, size_t n) {
+    return ew_launch(ctx, G4A_EW_GEGLU, gate, up, nullptr, 0.0f, y, n);
+}
+int g4a_softcap(g4a_ctx* ctx, const float* a, float cap, float* y, size_t n) {
+    return ew_launch(ctx, G4A_EW_SOFTCAP, a, nullptr, nullptr, cap, y, n);
+}
+
+int g4a_slice_cols(g4a_ctx* ctx, const float* x, uint32_t rows, uint32_t stride, uint32_t offset, uint32_t width,
+                   float* y) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (uint64_t(offset) + width > stride)
+        return fail(ctx, G4A_E_SHAPE, "columns [%u, %u) exceed the row stride %u", offset, offset + width, stride);
+    const size_t n = size_t(rows) * width;
+    if (n == 0) return G4A_OK;
+    if (!x || !y) return fail(ctx, G4A_E_ARG, "null x/y");
+    G4aSliceColsParams p{x, y, rows, stride, offset, width};
+    return launch(ctx, ctx->slice_cols, ew_grid(ctx, n), dim3(256, 1, 1), p, "slice cols", true);
+}
+
+int g4a_embed_rows(g4a_ctx* ctx, const float* table, uint32_t V, uint32_t D, const uint32_t* ids, uint32_t T,
+                   float scale, float* out) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (T == 0 || D == 0) return G4A_OK;
+    if (!table || !ids || !out) return fail(ctx, G4A_E_ARG, "null table/ids/out");
+    for (uint32_t i = 0; i < T; ++i)
+        if (ids[i] >= V) return fail(ctx, G4A_E_ARG, "id %u at %u is outside the table's %u rows", ids[i], i, V);
+    G4aEmbedF32Params p{table, nullptr, out, T, D, scale};
+    if (int rc = upload_positions(ctx, ids, T, nullptr, 0, &p.ids, nullptr)) return rc;
+    return launch(ctx, ctx->embed_f32, ew_grid(ctx, size_t(T) * D), dim3(256, 1, 1), p, "embedding", true);
+}
+
+int g4a_linear(g4a_ctx* ctx, const float* w, uint32_t N, uint32_t K, const float* x, float* y, uint32_t M) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (N == 0 || K == 0) return fail(ctx, G4A_E_SHAPE, "empty weight [%u, %u]", N, K);
+    if (M == 0) return G4A_OK;
+    if (!w || !x || !y) return fail(ctx, G4A_E_ARG, "null w/x/y");
+    G4aLinearParams p{};
+    p.w = reinterpret_cast<const uint32_t*>(w);
+    p.x = x;
+    p.y = y;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.W = K;
+    const uint64_t kpad = (uint64_t(K) + 63) / 64 * 64;
+    const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 3) == 0;
+    if (!aligned || K % 4 != 0 || kpad * 4 > LINEAR_LDS_BYTES) {
+        for (uint32_t m0 = 0; m0 < M; m0 += 65535) {
+            G4aLinearParams q = p;
+            q.x = x + size_t(m0) * K;
+            q.y = y + size_t(m0) * N;
+            q.M = std::min<uint32_t>(65535, M - m0);
+            if (int rc = launch(ctx, ctx->linear_f32_elem, dim3((N + 63) / 64, q.M, 1), dim3(64, 1, 1), q,
+                                "linear (element)", true))
+                return rc;
+        }
+        return G4A_OK;
+    }
+    const uint64_t cus = uint64_t(std::max(ctx->cu_count, 1));
+    int variant, MT, RU;
+    if (M >= 2 && 4 * kpad * 4 <= LINEAR_LDS_BYTES) variant = 2, MT = 4, RU = 4;
+    else if (N >= cus * 64) variant = 1, MT = 1, RU = 8;
+    else variant = 0, MT = 1, RU = 2;
+    const uint64_t target = cus * 16;
+    uint64_t rpw = (N + target - 1) / target;
+    rpw = std::max<uint64_t>(RU, (rpw + RU - 1) / RU * RU);
+    p.rows_per_wave = uint32_t(rpw);
+    const uint32_t gx = uint32_t((N + 4 * rpw - 1) / (4 * rpw));
+    const unsigned lds = unsigned(MT * kpad * 4);
+    for (uint32_t m0 = 0; m0 < M; m0 += 65535u * MT) {
+        G4aLinearParams q = p;
+        q.x = x + size_t(m0) * K;
+        q.y = y + size_t(m0) * N;
+        q.M = std::min<uint32_t>(65535u * MT, M - m0);
+        if (int rc = launch(ctx, ctx->linear_f32_words[variant], dim3(gx, (q.M + MT - 1) / MT, 1), dim3(256, 1, 1), q,
+                            "linear", true, lds))
+            return rc;
+    }
+    return G4A_OK;
 }
 
 int g4a_rope(g4a_ctx* ctx, const float* x, float* y, uint32_t T, uint32_t heads, uint32_t head_dim,

@@ -149,46 +149,122 @@ HipTensor HipBackend::quant_tensor(const QuantWeight& q) {
     return t;
 }
 
-namespace {
-const g4a_qweight& quant_of(const HipTensor& w, const char* op) {
-    if (!w.quant) throw std::runtime_error(std::string(op) + ": the weight is not quantised (f32 weights are not in this build)");
-    return *w.quant;
-}
-}  // namespace
-
 HipTensor HipBackend::embed_rows(const HipTensor& table, const uint32_t* ids, size_t n_ids, float scale) {
-    const g4a_qweight& q = quant_of(table, "embed_rows");
-    HipTensor out = alloc_tensor({n_ids, size_t(q.K)});
-    check(g4a_embed_rows_q(ctx_, &q, ids, uint32_t(n_ids), scale, out.data()), "embed_rows");
+    if (table.shape.size() != 2) throw std::runtime_error("embed_rows: the table must be [V, D]");
+    HipTensor out = alloc_tensor({n_ids, table.shape[1]});
+    if (table.quant)
+        check(g4a_embed_rows_q(ctx_, &*table.quant, ids, uint32_t(n_ids), scale, out.data()), "embed_rows");
+    else
+        check(g4a_embed_rows(ctx_, table.data(), uint32_t(table.shape[0]), uint32_t(table.shape[1]), ids,
+                             uint32_t(n_ids), scale, out.data()),
+              "embed_rows");
     return out;
 }
 
 HipTensor HipBackend::linear(const HipTensor& x, const HipTensor& w) {
-    const g4a_qweight& q = quant_of(w, "linear");
-    if (x.shape.size() != 2 || x.shape[1] != q.K) throw std::runtime_error("linear: x must be [T, K]");
-    HipTensor y = alloc_tensor({x.shape[0], size_t(q.N)});
-    check(g4a_linear_q(ctx_, &q, x.data(), y.data(), uint32_t(x.shape[0])), "linear");
+    if (x.shape.size() != 2 || w.shape.size() != 2 || x.shape[1] != w.shape[1])
+        throw std::runtime_error("linear: x [T, K] and W [N, K] required, got " + shape_str(x.shape) + " and " +
+                                 shape_str(w.shape));
+    HipTensor y = alloc_tensor({x.shape[0], w.shape[0]});
+    if (w.quant)
+        check(g4a_linear_q(ctx_, &*w.quant, x.data(), y.data(), uint32_t(x.shape[0])), "linear");
+    else
+        check(g4a_linear(ctx_, w.data(), uint32_t(w.shape[0]), uint32_t(w.shape[1]), x.data(), y.data(),
+                         uint32_t(x.shape[0])),
+              "linear");
+    return y;
+}
+
+namespace {
+void same_size(const HipTensor& a, const HipTensor& b, const char* op) {
+    if (a.size() != b.size()) throw std::runtime_error(std::string(op) + ": operands differ in size");
+}
+}  // namespace
+
+HipTensor HipBackend::add(const HipTensor& a, const HipTensor& b) {
+    same_size(a, b, "add");
+    HipTensor y = alloc_tensor(a.shape);
+    check(g4a_add(ctx_, a.data(), b.data(), y.data(), a.size()), "add");
+    return y;
+}
+HipTensor HipBackend::mul(const HipTensor& a, const HipTensor& b) {
+    same_size(a, b, "mul");
+    HipTensor y = alloc_tensor(a.shape);
+    check(g4a_mul(ctx_, a.data(), b.data(), y.data(), a.size()), "mul");
+    return y;
+}
+HipTensor HipBackend::scale(const HipTensor& a, float s) {
+    HipTensor y = alloc_tensor(a.shape);
+    check(g4a_scale(ctx_, a.data(), s, y.data(), a.size()), "scale");
+    return y;
+}
+HipTensor HipBackend::scale_by_tensor(const HipTensor& a, const HipTensor& s) {
+    HipTensor y = alloc_tensor(a.shape);
+    check(g4a_scale_by_tensor(ctx_, a.data(), s.data(), y.data(), a.size()), "scale_by_tensor");
+    return y;
+}
+HipTensor HipBackend::gelu_tanh(const HipTensor& a) {
+    HipTensor y = alloc_tensor(a.shape);
+    check(g4a_gelu_tanh(ctx_, a.data(), y.data(), a.size()), "gelu_tanh");
+    return y;
+}
+HipTensor HipBackend::geglu(const HipTensor& gate, const HipTensor& up) {
+    same_size(gate, up, "geglu");
+    HipTensor y = alloc_tensor(gate.shape);
+    check(g4a_geglu(ctx_, gate.data(), up.data(), y.data(), gate.size()), "geglu");
+    return y;
+}
+HipTensor HipBackend::softcap(const HipTensor& a, float cap) {
+    HipTensor y = alloc_tensor(a.shape);
+    check(g4a_softcap(ctx_, a.data(), cap, y.data(), a.size()), "softcap");
+    return y;
+}
+
+HipTensor HipBackend::slice_cols(const HipTensor& x, size_t offset, size_t width) {
+    if (x.shape.size() != 2) throw std::runtime_error("slice_cols: x must be [rows, stride]");
+    HipTensor y = alloc_tensor({x.shape[0], width});
+    check(g4a_slice_cols(ctx_, x.data(), uint32_t(x.shape[0]), uint32_t(x.shape[1]), uint32_t(offset),
+                         uint32_t(width), y.data()),
+          "slice_cols");
+    return y;
+}
+
+HipTensor HipBackend::add_rms_norm(const HipTensor& residual, const HipTensor& x, const HipTensor& w, float eps,
+                                   const HipTensor* scale_by) {
+    same_size(residual, x, "add_rms_norm");
+    const size_t d = x.shape.back();
+    HipTensor y = alloc_tensor(x.shape);
+    check(g4a_add_rms_norm(ctx_, residual.data(), x.data(), w.data(), scale_by ? scale_by->data() : nullptr, y.data(),
+                           uint32_t(x.size() / d), uint32_t(d), eps),
+          "add_rms_norm");
     return y;
 }
 
 HipTensor HipBackend::linear_geglu(const HipTensor& x, const HipTensor& w_gate, const HipTensor& w_up) {
-    const g4a_qweight& g = quant_of(w_gate, "linear_geglu");
-    const g4a_qweight& u = quant_of(w_up, "linear_geglu");
-    if (x.shape.size() != 2 || x.shape[1] != g.K) throw std::runtime_error("linear_geglu: x must be [T, K]");
-    HipTensor y = alloc_tensor({x.shape[0], size_t(g.N)});
-    check(g4a_linear_q_geglu(ctx_, &g, &u, x.data(), y.data(), uint32_t(x.shape[0])), "linear_geglu");
-    return y;
+    if (w_gate.quant && w_up.quant) {
+        const g4a_qweight &g = *w_gate.quant, &u = *w_up.quant;
+        if (g.N == u.N && g.K == u.K && g.bits == u.bits && g.signed_i8 == u.signed_i8 && g.group_size == u.group_size) {
+            if (x.shape.size() != 2 || x.shape[1] != g.K) throw std::runtime_error("linear_geglu: x must be [T, K]");
+            HipTensor y = alloc_tensor({x.shape[0], size_t(g.N)});
+            check(g4a_linear_q_geglu(ctx_, &g, &u, x.data(), y.data(), uint32_t(x.shape[0])), "linear_geglu");
+            return y;
+        }
+    }
+    return geglu(linear(x, w_gate), linear(x, w_up));
 }
 
 HipTensor HipBackend::linear_gelu_mul_cols(const HipTensor& x, const HipTensor& w, const HipTensor& b, size_t offset) {
-    const g4a_qweight& q = quant_of(w, "linear_gelu_mul_cols");
-    if (x.shape.size() != 2 || x.shape[1] != q.K || b.shape.size() != 2 || b.shape[0] != x.shape[0])
-        throw std::runtime_error("linear_gelu_mul_cols: x must be [M, K] and b [M, stride]");
-    HipTensor y = alloc_tensor({x.shape[0], size_t(q.N)});
-    check(g4a_linear_q_gelu_mul_cols(ctx_, &q, x.data(), b.data(), uint32_t(b.shape[1]), uint32_t(offset), y.data(),
-                                     uint32_t(x.shape[0])),
-          "linear_gelu_mul_cols");
-    return y;
+    if (w.quant && b.shape.size() == 2 && b.shape[0] == x.shape[0]) {
+        const g4a_qweight& q = *w.quant;
+        if (x.shape.size() != 2 || x.shape[1] != q.K)
+            throw std::runtime_error("linear_gelu_mul_cols: x must be [M, K]");
+        HipTensor y = alloc_tensor({x.shape[0], size_t(q.N)});
+        check(g4a_linear_q_gelu_mul_cols(ctx_, &q, x.data(), b.data(), uint32_t(b.shape[1]), uint32_t(offset),
+                                         y.data(), uint32_t(x.shape[0])),
+              "linear_gelu_mul_cols");
+        return y;
+    }
+    return geglu(linear(x, w), slice_cols(b, offset, w.shape[0]));
 }
 
 HipTensor HipBackend::attention(const HipTensor& q, const HipTensor& k, const HipTensor& v, const AttnOpts& o) {

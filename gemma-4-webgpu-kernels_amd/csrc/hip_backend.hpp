@@ -121,13 +121,28 @@ public:
     HipTensor quant_tensor(const QuantWeight& q);
 
     // --- ops ---
-    // out[i, :] = table[ids[i], :] * scale on a quantised [V, D] table (rust/src/backend.rs:100-101)
+    // out[i, :] = table[ids[i], :] * scale; table [V, D] f32 or quantised (rust/src/backend.rs:100-101)
     HipTensor embed_rows(const HipTensor& table, const uint32_t* ids, size_t n_ids, float scale);
-    // y = x . W^T; x [T, K], W [N, K] quantised (rust/src/backend.rs:105-106)
+    // y = x . W^T; x [T, K], W [N, K] f32 or quantised (rust/src/backend.rs:105-106)
     HipTensor linear(const HipTensor& x, const HipTensor& w);
-    // gelu(x . Wg^T) * (x . Wu^T) in one launch (rust/src/backend.rs:156-161)
+    // elementwise (rust/src/backend.rs:107-116)
+    HipTensor add(const HipTensor& a, const HipTensor& b);
+    HipTensor mul(const HipTensor& a, const HipTensor& b);
+    HipTensor scale(const HipTensor& a, float s);
+    HipTensor scale_by_tensor(const HipTensor& a, const HipTensor& s);  // a * s[0]
+    HipTensor gelu_tanh(const HipTensor& a);
+    HipTensor geglu(const HipTensor& gate, const HipTensor& up);  // gelu(gate) * up
+    HipTensor softcap(const HipTensor& a, float cap);              // cap * tanh(a / cap)
+    // [:, offset : offset + width] of a [rows, stride] tensor (rust/src/backend.rs:123-124)
+    HipTensor slice_cols(const HipTensor& x, size_t offset, size_t width);
+    // (residual + rms_norm(x, w)) * scale_by[0], one launch (rust/src/backend.rs:136-145)
+    HipTensor add_rms_norm(const HipTensor& residual, const HipTensor& x, const HipTensor& w, float eps,
+                           const HipTensor* scale_by);
+    // gelu(x . Wg^T) * (x . Wu^T): one launch for two quantised weights of one format,
+    // else the trait's composition (rust/src/backend.rs:156-161)
     HipTensor linear_geglu(const HipTensor& x, const HipTensor& w_gate, const HipTensor& w_up);
-    // gelu(x . W^T) * b[:, offset : offset + N], b [M, stride] (rust/src/backend.rs:162-168)
+    // gelu(x . W^T) * b[:, offset : offset + N], b [M, stride]: one launch for a quantised
+    // weight, else the trait's composition (rust/src/backend.rs:162-168)
     HipTensor linear_gelu_mul_cols(const HipTensor& x, const HipTensor& w, const HipTensor& b, size_t offset);
     // q [T,Hq,Dh], k [S,Hkv,Dh], v [S,Hkv,Dv] -> [T, Hq*Dv] (rust/src/backend.rs:119-120)
     HipTensor attention(const HipTensor& q, const HipTensor& k, const HipTensor& v, const AttnOpts& o);

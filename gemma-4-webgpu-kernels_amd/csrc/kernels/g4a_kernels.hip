@@ -5,3 +5,4 @@
 #include "attn_prefill.hip"
 #include "norm_rope.hip"
 #include "linear_q.hip"
+#include "elementwise.hip"

@@ -1,0 +1,14 @@
+// Scalar math shared by the gfx950 kernels, in the reference CPU backend's
+// operation order (each file is built with -ffp-contract=off).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+// sqrt(2 / pi) rounded to f32, as (2.0f32 / PI).sqrt() in rust/src/backend_cpu.rs:56
+constexpr float G4A_GELU_C = 0x1.988452p-1f;
+
+// gelu_tanh_scalar (rust/src/backend_cpu.rs:55-58):
+// 0.5 * v * (1 + tanh(c * (v + 0.044715 * v * v * v)))
+__device__ __forceinline__ float g4a_gelu_tanh(float v) {
+    return 0.5f * v * (1.0f + tanhf(G4A_GELU_C * (v + 0.044715f * v * v * v)));
+}

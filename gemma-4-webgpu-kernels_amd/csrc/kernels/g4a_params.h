@@ -193,3 +193,49 @@ struct G4aEmbedParams {
     float scale;
 };
 
+
+// Elementwise ops (g4a_ew): y = op(a, b) over n elements.
+enum G4aEwOp : uint32_t {
+    G4A_EW_ADD = 0,
+    G4A_EW_MUL = 1,
+    G4A_EW_SCALE = 2,     // a * s
+    G4A_EW_SCALE_BY = 3,  // a * sp[0]
+    G4A_EW_GELU = 4,
+    G4A_EW_GEGLU = 5,     // gelu(a) * b
+    G4A_EW_SOFTCAP = 6,   // s * tanh(a / s)
+};
+
+struct G4aEwParams {
+    const float* a;
+    const float* b;
+    const float* sp;
+    float* y;
+    size_t n;
+    float s;
+    uint32_t op;
+};
+
+struct G4aSliceColsParams {
+    const float* x;  // [rows, stride]
+    float* y;        // [rows, width]
+    uint32_t rows, stride, offset, width;
+};
+
+// y = (res + x * inv * w) * scale_by[0] per row of D values; res, w, scale_by optional.
+struct G4aRmsRowsParams {
+    const float* x;
+    const float* w;
+    const float* res;
+    const float* scale_by;
+    float* y;
+    uint32_t rows, D;
+    float eps;
+};
+
+struct G4aEmbedF32Params {
+    const float* table;     // [V, D]
+    const uint32_t* ids;    // [T]
+    float* out;             // [T, D]
+    uint32_t T, D;
+    float scale;
+};

@@ -33,17 +33,14 @@
 #include <math.h>
 #include <stdint.h>
 
+#include "g4a_math.h"
 #include "g4a_params.h"
 
 namespace {
 
-// sqrt(2 / pi) rounded to f32, as (2.0f32 / PI).sqrt() in rust/src/backend_cpu.rs:56
-constexpr float GELU_C = 0x1.988452p-1f;
+__device__ __forceinline__ float gelu_tanh(float v) { return g4a_gelu_tanh(v); }
 
-__device__ __forceinline__ float gelu_tanh(float v) {
-    return 0.5f * v * (1.0f + tanhf(GELU_C * (v + 0.044715f * v * v * v)));
-}
-
+// BITS = 32: an f32 weight per word (the unquantised linear).
 template <int BITS>
 struct QFmt {
     static constexpr int VPW = 32 / BITS;  // values per word
@@ -56,7 +53,9 @@ __device__ __forceinline__ float sbyte(uint32_t v, int j) { return (float)(int8_
 // in k order.
 template <int BITS>
 __device__ __forceinline__ void unpack(uint32_t v, float (&q)[QFmt<BITS>::VPW]) {
-    if constexpr (BITS == 8) {
+    if constexpr (BITS == 32) {
+        q[0] = __uint_as_float(v);
+    } else if constexpr (BITS == 8) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) q[j] = sbyte(v, j);
     } else if constexpr (BITS == 4) {
@@ -163,13 +162,17 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
         float xv[MT][VPW];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
+            if constexpr (VPW == 1) {
+                xv[mt][0] = xs[mt * KP + w];
+            } else {
 #pragma unroll
-            for (int i = 0; i < VPW; i += 4) {
-                const float4 v4 = *reinterpret_cast<const float4*>(xs + mt * KP + w * VPW + i);
-                xv[mt][i] = v4.x;
-                xv[mt][i + 1] = v4.y;
-                xv[mt][i + 2] = v4.z;
-                xv[mt][i + 3] = v4.w;
+                for (int i = 0; i < VPW; i += 4) {
+                    const float4 v4 = *reinterpret_cast<const float4*>(xs + mt * KP + w * VPW + i);
+                    xv[mt][i] = v4.x;
+                    xv[mt][i + 1] = v4.y;
+                    xv[mt][i + 2] = v4.z;
+                    xv[mt][i + 3] = v4.w;
+                }
             }
 #pragma unroll
         for (int r = 0; r < RU; ++r) {
@@ -202,7 +205,7 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
                 const uint32_t mt = idx / RU, r = idx % RU;
                 const uint32_t n = first + c * RU + r, m = m0 + mt;
                 if (n < last && m < p.M) {
-                    const float v = a * (p.s[n] * F::INV_F);
+                    const float v = BITS == 32 ? a : a * (p.s[n] * F::INV_F);  // f32 weights carry no scale
                     float o = v;
                     if (MODE == 1) o = gelu_tanh(v) * (a2 * (p.s2[n] * F::INV_F));
                     if (MODE == 2) o = gelu_tanh(v) * p.b[(size_t)m * p.b_stride + p.b_off + n];
@@ -407,6 +410,18 @@ __device__ __forceinline__ float deq(const uint8_t* __restrict__ wb, const float
     return (float)qv * s[(size_t)n * sstride + k / group];
 }
 
+// CpuBackend::linear with an f32 weight (rust/src/backend_cpu.rs:199-208), one
+// thread per output in the CPU's order: bit-identical.
+__device__ __forceinline__ void linear_f32_elem(const G4aLinearParams& p) {
+    const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
+    if (n >= p.N) return;
+    const float* __restrict__ xr = p.x + (size_t)m * p.K;
+    const float* __restrict__ wr = reinterpret_cast<const float*>(p.w) + (size_t)n * p.K;
+    float acc = 0.0f;
+    for (uint32_t k = 0; k < p.K; ++k) acc += xr[k] * wr[k];
+    p.y[(size_t)m * p.N + n] = acc;
+}
+
 template <int MODE>
 __device__ __forceinline__ void linear_q_elem(const G4aLinearParams& p) {
     const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
@@ -467,6 +482,11 @@ G4A_LINEAR_MFMA(4, 2)
 G4A_LINEAR_MFMA(8, 0)
 G4A_LINEAR_MFMA(8, 1)
 G4A_LINEAR_MFMA(8, 2)
+
+G4A_LINEAR_WORDS(32, 1, 2, 4, 0)
+G4A_LINEAR_WORDS(32, 1, 8, 2, 0)
+G4A_LINEAR_WORDS(32, 4, 4, 2, 0)
+extern "C" __global__ __launch_bounds__(64) void g4a_linear_f32_elem(G4aLinearParams p) { linear_f32_elem(p); }
 
 extern "C" __global__ __launch_bounds__(64) void g4a_linear_q_elem_mode0(G4aLinearParams p) { linear_q_elem<0>(p); }
 extern "C" __global__ __launch_bounds__(64) void g4a_linear_q_elem_mode1(G4aLinearParams p) { linear_q_elem<1>(p); }

@@ -113,6 +113,18 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "g4a_rms_norm": (c_int, [ctxp, vp, vp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float]),
         "g4a_rope": (c_int, [ctxp, vp, vp] + [ctypes.c_uint32] * 4 + [_u32p, ctypes.c_uint32, ctypes.c_float]),
         "g4a_attn_producer": (c_int, [ctxp, ctypes.POINTER(ProducerArgs)]),
+        "g4a_add": (c_int, [ctxp, vp, vp, vp, sz]),
+        "g4a_mul": (c_int, [ctxp, vp, vp, vp, sz]),
+        "g4a_scale": (c_int, [ctxp, vp, ctypes.c_float, vp, sz]),
+        "g4a_scale_by_tensor": (c_int, [ctxp, vp, vp, vp, sz]),
+        "g4a_gelu_tanh": (c_int, [ctxp, vp, vp, sz]),
+        "g4a_geglu": (c_int, [ctxp, vp, vp, vp, sz]),
+        "g4a_softcap": (c_int, [ctxp, vp, ctypes.c_float, vp, sz]),
+        "g4a_slice_cols": (c_int, [ctxp, vp] + [ctypes.c_uint32] * 4 + [vp]),
+        "g4a_add_rms_norm": (c_int, [ctxp, vp, vp, vp, vp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float]),
+        "g4a_embed_rows": (c_int, [ctxp, vp, ctypes.c_uint32, ctypes.c_uint32, _u32p, ctypes.c_uint32, ctypes.c_float,
+                                   vp]),
+        "g4a_linear": (c_int, [ctxp, vp, ctypes.c_uint32, ctypes.c_uint32, vp, vp, ctypes.c_uint32]),
         "g4a_linear_q": (c_int, [ctxp, ctypes.POINTER(QWeightArgs), vp, vp, ctypes.c_uint32]),
         "g4a_linear_q_geglu": (c_int, [ctxp, ctypes.POINTER(QWeightArgs), ctypes.POINTER(QWeightArgs), vp, vp,
                                        ctypes.c_uint32]),
@@ -319,6 +331,29 @@ class Context:
         a = ProducerArgs(q, k or None, v or None, q_norm or None, k_norm or None, q_out, k_cache or None,
                          v_cache or None, T, Hq, Hkv, Dh, rotary_dim, pp, pos0, cache_row, ring_cap, theta, eps)
         self._check(self.lib.g4a_attn_producer(self.handle, ctypes.byref(a)))
+
+    # ---- the rest of the backend trait (device pointers) ----
+    def ew(self, op: str, a: int, y: int, n: int, b: int = 0, s: float = 0.0) -> None:
+        """op in add, mul, scale, scale_by_tensor (b = device scalar), gelu_tanh, geglu, softcap (s = cap)."""
+        L, h = self.lib, self.handle
+        rc = {"add": lambda: L.g4a_add(h, a, b, y, n), "mul": lambda: L.g4a_mul(h, a, b, y, n),
+              "scale": lambda: L.g4a_scale(h, a, s, y, n), "scale_by_tensor": lambda: L.g4a_scale_by_tensor(h, a, b, y, n),
+              "gelu_tanh": lambda: L.g4a_gelu_tanh(h, a, y, n), "geglu": lambda: L.g4a_geglu(h, a, b, y, n),
+              "softcap": lambda: L.g4a_softcap(h, a, s, y, n)}[op]()
+        self._check(rc)
+
+    def slice_cols(self, x: int, rows: int, stride: int, offset: int, width: int, y: int) -> None:
+        self._check(self.lib.g4a_slice_cols(self.handle, x, rows, stride, offset, width, y))
+
+    def add_rms_norm(self, residual: int, x: int, w: int, scale_by: int, y: int, rows: int, dim: int, eps: float):
+        self._check(self.lib.g4a_add_rms_norm(self.handle, residual, x, w, scale_by or None, y, rows, dim, eps))
+
+    def embed_rows(self, table: int, V: int, D: int, ids, scale: float, out: int) -> None:
+        arr, ptr = _u32_array(ids)
+        self._check(self.lib.g4a_embed_rows(self.handle, table, V, D, ptr, 0 if arr is None else arr.size, scale, out))
+
+    def linear(self, w: int, N: int, K: int, x: int, y: int, M: int) -> None:
+        self._check(self.lib.g4a_linear(self.handle, w, N, K, x, y, M))
 
     # ---- quantised projections ----
     def upload_qweight(self, qbytes: np.ndarray, scales: np.ndarray, N: int, K: int, bits: int,

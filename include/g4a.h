@@ -186,8 +186,8 @@ int g4a_head_norm_rope(g4a_ctx *ctx, const float *x, const float *w, float *y, u
                        uint32_t head_dim, uint32_t rotary_dim, const uint32_t *positions, uint32_t pos0,
                        float theta, float eps);
 /* Backend::rms_norm (rust/src/backend.rs:103-104; rust/src/backend_cpu.rs:149-172) over
- * `rows` rows of `dim` values (dim % 4 == 0, <= 1024): y = x * inv (* w), w NULL
- * for the unweighted variant (the per-head V norm, rust/src/model.rs:274-275). */
+ * `rows` rows of `dim` values: y = x * inv (* w), w NULL for the unweighted
+ * variant (the per-head V norm, rust/src/model.rs:274-275). */
 int g4a_rms_norm(g4a_ctx *ctx, const float *x, const float *w, float *y, uint32_t rows, uint32_t dim, float eps);
 /* Backend::rope (rust/src/backend.rs:117-118; rust/src/backend_cpu.rs:248-268). */
 int g4a_rope(g4a_ctx *ctx, const float *x, float *y, uint32_t T, uint32_t heads, uint32_t head_dim,
@@ -222,6 +222,44 @@ typedef struct g4a_producer_args {
 } g4a_producer_args;
 
 int g4a_attn_producer(g4a_ctx *ctx, const g4a_producer_args *args);
+
+/* ---- the rest of the backend trait (rust/src/backend.rs:99-168) -----------
+ * Device pointers, n elements (or rows x dim); the same results as the
+ * reference CPU backend: add, mul, scale, scale_by_tensor, slice_cols and
+ * embed_rows bit-identical; gelu_tanh, geglu and softcap within the device
+ * tanhf's last-bit difference; add_rms_norm and wide rms_norm within the
+ * reordered sum of squares; g4a_linear as g4a_linear_q.
+ * Backend::add / mul / scale / scale_by_tensor / gelu_tanh / geglu / softcap
+ * (rust/src/backend.rs:107-116; rust/src/backend_cpu.rs:224-244): */
+int g4a_add(g4a_ctx *ctx, const float *a, const float *b, float *y, size_t n);
+int g4a_mul(g4a_ctx *ctx, const float *a, const float *b, float *y, size_t n);
+int g4a_scale(g4a_ctx *ctx, const float *a, float s, float *y, size_t n);
+/* y = a * s[0] with s a device scalar (the learned layer_scalar) */
+int g4a_scale_by_tensor(g4a_ctx *ctx, const float *a, const float *s, float *y, size_t n);
+int g4a_gelu_tanh(g4a_ctx *ctx, const float *a, float *y, size_t n);
+/* y = gelu_tanh(gate) * up */
+int g4a_geglu(g4a_ctx *ctx, const float *gate, const float *up, float *y, size_t n);
+/* y = cap * tanh(a / cap) */
+int g4a_softcap(g4a_ctx *ctx, const float *a, float cap, float *y, size_t n);
+/* Backend::slice_cols (rust/src/backend.rs:123-124; rust/src/backend_cpu.rs:343-350):
+ * y[r, c] = x[r * stride + offset + c] for c < width. */
+int g4a_slice_cols(g4a_ctx *ctx, const float *x, uint32_t rows, uint32_t stride, uint32_t offset, uint32_t width,
+                   float *y);
+/* Backend::add_rms_norm (rust/src/backend.rs:136-145; the reference GPU's fused
+ * RMSNORM, rust/src/kernels/rmsnorm.wgsl): y = (residual + rms_norm(x, w)) *
+ * scale_by[0], scale_by (a device scalar) may be NULL. */
+int g4a_add_rms_norm(g4a_ctx *ctx, const float *residual, const float *x, const float *w, const float *scale_by,
+                     float *y, uint32_t rows, uint32_t dim, float eps);
+/* Backend::embed_rows on an f32 table [V, D] (rust/src/backend_cpu.rs:138-144):
+ * out[i, d] = table[ids[i] * D + d] * scale, ids a host array of T values < V. */
+int g4a_embed_rows(g4a_ctx *ctx, const float *table, uint32_t V, uint32_t D, const uint32_t *ids, uint32_t T,
+                   float scale, float *out);
+/* Backend::linear with an f32 weight W [N, K] (rust/src/backend_cpu.rs:174-222;
+ * the reference GPU's GEMV / MATMUL, rust/src/backend_wgpu.rs:768-806):
+ * y[M, N] = x[M, K] . W^T; the word-parallel kernel when K % 4 == 0, x is
+ * 16-byte aligned and K <= 16384 (reordered f32 sum), else one thread per
+ * output in the CPU's order (bit-identical). */
+int g4a_linear(g4a_ctx *ctx, const float *w, uint32_t N, uint32_t K, const float *x, float *y, uint32_t M);
 
 /* ---- quantised projections (the calls on either side of attention) --------
  * A weight as the reference's QuantWeight (rust/src/backend.rs:12-58), in

@@ -21,6 +21,9 @@
  *                                                        Rust's f32::tanh)
  *   oracle_embed_rows_q <- rust/src/backend_cpu.rs:127-145 (embed_rows on a quantised
  *                                                        table: deq(id, d) * scale)
+ *   oracle_linear_f32   <- rust/src/backend_cpu.rs:174-222 (linear on an f32 weight)
+ *   oracle_softcap_n    <- rust/src/backend_cpu.rs:242-244 (cap * tanhf(v / cap))
+ *   oracle_embed_rows_f32 <- rust/src/backend_cpu.rs:138-144 (table[id, d] * scale)
  *
  * Build with -ffp-contract=off and without -ffast-math: every f32 operation is
  * a separately rounded IEEE single operation, as in the Rust code.
@@ -94,4 +97,29 @@ void oracle_embed_rows_q(const uint8_t *qb, const float *scales, size_t V, size_
     for (size_t i = 0; i < T; ++i)
         for (size_t d = 0; d < D; ++d)
             out[i * D + d] = oracle_deq(qb, scales, D, bits, signed_i8, group, ids[i], d) * scale;
+}
+
+/* CpuBackend::linear with an f32 weight (rust/src/backend_cpu.rs:174-222):
+ * y[i, n] = sum over k in order of x[i, k] * w[n, k]. */
+void oracle_linear_f32(const float *w, size_t N, size_t K, const float *x, size_t M, float *y) {
+    for (size_t n = 0; n < N; ++n) {
+        const float *wb = w + n * K;
+        for (size_t i = 0; i < M; ++i) {
+            const float *xb = x + i * K;
+            float acc = 0.0f;
+            for (size_t k = 0; k < K; ++k) acc += xb[k] * wb[k];
+            y[i * N + n] = acc;
+        }
+    }
+}
+
+/* CpuBackend::softcap (rust/src/backend_cpu.rs:242-244): cap * tanh(v / cap). */
+void oracle_softcap_n(const float *x, float cap, float *y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = cap * tanhf(x[i] / cap);
+}
+
+/* CpuBackend::embed_rows on an f32 table (rust/src/backend_cpu.rs:138-144). */
+void oracle_embed_rows_f32(const float *table, size_t D, const uint32_t *ids, size_t T, float scale, float *out) {
+    for (size_t i = 0; i < T; ++i)
+        for (size_t d = 0; d < D; ++d) out[i * D + d] = table[(size_t)ids[i] * D + d] * scale;
 }

@@ -50,6 +50,12 @@ def lib() -> ctypes.CDLL:
         L.oracle_embed_rows_q.restype = None
         L.oracle_embed_rows_q.argtypes = [vp, vp, sz, sz, ctypes.c_uint32, ctypes.c_int, sz, vp, sz,
                                           ctypes.c_float, vp]
+        L.oracle_linear_f32.restype = None
+        L.oracle_linear_f32.argtypes = [vp, sz, sz, vp, sz, vp]
+        L.oracle_softcap_n.restype = None
+        L.oracle_softcap_n.argtypes = [vp, ctypes.c_float, vp, sz]
+        L.oracle_embed_rows_f32.restype = None
+        L.oracle_embed_rows_f32.argtypes = [vp, sz, vp, sz, ctypes.c_float, vp]
         L.oracle_thread_count.restype = ctypes.c_size_t
         L.oracle_thread_count.argtypes = [sz, ctypes.c_int]
         _lib = L
@@ -194,4 +200,65 @@ def embed_rows_q(w: QWeight, ids, scale):
     out = np.empty((ids.size, w.K), np.float32)
     lib().oracle_embed_rows_q(w.qbytes.ctypes.data, w.scales.ctypes.data, w.N, w.K, w.bits, int(w.signed_i8),
                               w.group_size, ids.ctypes.data, ids.size, scale, out.ctypes.data)
+    return out
+
+
+# ---- the rest of the trait's ops (rust/src/backend_cpu.rs:127-145, :224-244, :343-350;
+# rust/src/backend.rs:136-145). add / mul / scale are single IEEE f32 operations per
+# element, exactly numpy's float32 arithmetic.
+
+def add(a, b):
+    return (np.asarray(a, np.float32) + np.asarray(b, np.float32)).astype(np.float32)
+
+
+def mul(a, b):
+    return (np.asarray(a, np.float32) * np.asarray(b, np.float32)).astype(np.float32)
+
+
+def scale(a, s):
+    return (np.asarray(a, np.float32) * np.float32(s)).astype(np.float32)
+
+
+def geglu(gate, up):
+    """CpuBackend::geglu: mul(gelu_tanh(gate), up)."""
+    return mul(gelu_tanh(gate), up)
+
+
+def softcap(a, cap):
+    a = np.ascontiguousarray(a, np.float32)
+    y = np.empty_like(a)
+    lib().oracle_softcap_n(a.ctypes.data, cap, y.ctypes.data, a.size)
+    return y
+
+
+def slice_cols(x, offset, width):
+    x = np.asarray(x, np.float32)
+    return np.ascontiguousarray(x[:, offset:offset + width])
+
+
+def add_rms_norm(residual, x, w, eps, scale_by=None):
+    """Backend::add_rms_norm's default (rust/src/backend.rs:136-145):
+    h = add(residual, rms_norm(x, w)); h * s[0] when scale_by is given."""
+    x = np.ascontiguousarray(x, np.float32)
+    h = add(residual, rms_norm(x.reshape(-1, x.shape[-1]), w, eps).reshape(x.shape))
+    return scale(h, np.float32(scale_by)) if scale_by is not None else h
+
+
+def linear_f32(x, w):
+    """CpuBackend::linear on an f32 weight: x [M, K], w [N, K] -> [M, N]."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.empty((M, N), np.float32)
+    lib().oracle_linear_f32(w.ctypes.data, N, K, x.ctypes.data, M, y.ctypes.data)
+    return y
+
+
+def embed_rows_f32(table, ids, scale_):
+    table = np.ascontiguousarray(table, np.float32)
+    ids = np.ascontiguousarray(ids, np.uint32)
+    out = np.empty((ids.size, table.shape[1]), np.float32)
+    lib().oracle_embed_rows_f32(table.ctypes.data, table.shape[1], ids.ctypes.data, ids.size, scale_,
+                                out.ctypes.data)
     return out

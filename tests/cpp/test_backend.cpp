@@ -12,6 +12,10 @@
 //                              and 1, q4 with K = 52, I8, the grouped-scale q4 embedding,
 //                              plus the fused GeGLU and gelu-times-columns projections,
 //                              against oracle/linear_oracle.c
+//   kernel_parity_ops          rust/tests/gpu.rs:37-100 (Lcg seed 7): f32 linear (tiled and
+//                              gemv), add, mul, scale, geluTanh, geglu, softcap,
+//                              scaleByTensor, embedRows, sliceCols; fused_op_parity's
+//                              add_rms_norm (rust/tests/gpu.rs:310-321, Lcg seed 33)
 //   kv_cache_decode            prefill chunks + decode steps through KvCache, with a
 //                              sliding layer on a ring (incl. regrowth and wrap-around)
 //                              and a global layer on the growing buffer, every step
@@ -37,6 +41,10 @@ extern "C" int oracle_attention(const float* q, const float* k, const float* v, 
 extern "C" void oracle_linear_q(const uint8_t* qb, const float* scales, size_t N, size_t K, uint32_t bits,
                                 int signed_i8, size_t group, const float* x, size_t M, float* y);
 extern "C" float oracle_gelu_tanh(float v);
+extern "C" void oracle_linear_f32(const float* w, size_t N, size_t K, const float* x, size_t M, float* y);
+extern "C" void oracle_softcap_n(const float* x, float cap, float* y, size_t n);
+extern "C" void oracle_embed_rows_f32(const float* table, size_t D, const uint32_t* ids, size_t T, float scale,
+                                      float* out);
 extern "C" float oracle_deq(const uint8_t* qb, const float* scales, size_t K, uint32_t bits, int signed_i8,
                             size_t group, size_t n, size_t k);
 extern "C" void oracle_embed_rows_q(const uint8_t* qb, const float* scales, size_t V, size_t D, uint32_t bits,
@@ -483,6 +491,84 @@ void quantized_kernel_parity(g4a::HipBackend& b) {
     }
 }
 
+void kernel_parity_ops(g4a::HipBackend& b) {
+    std::printf("kernel_parity_ops\n");
+    Lcg r(7);
+    {
+        const size_t m = 17, k = 40, n = 23;
+        const auto x = r.rand(m * k, 1.0f), w = r.rand(n * k, 1.0f);
+        std::vector<float> want(m * n);
+        oracle_linear_f32(w.data(), n, k, x.data(), m, want.data());
+        const auto gw = b.tensor(w.data(), {n, k});
+        close("linear (tiled)", b.readback(b.linear(b.tensor(x.data(), {m, k}), gw)), want);
+        const auto x1 = r.rand(k, 1.0f);
+        std::vector<float> want1(n);
+        oracle_linear_f32(w.data(), n, k, x1.data(), 1, want1.data());
+        close("linear (gemv)", b.readback(b.linear(b.tensor(x1.data(), {1, k}), gw)), want1);
+    }
+    r.rand(5 * 48 + 48, 1.0f);  // rmsNorm (norm_rope_parity covers it)
+    {
+        const size_t n = 100;
+        const auto a = r.rand(n, 1.0f), c = r.rand(n, 1.0f);
+        const auto ga = b.tensor(a.data(), {n}), gc = b.tensor(c.data(), {n});
+        std::vector<float> want(n);
+        for (size_t i = 0; i < n; ++i) want[i] = a[i] + c[i];
+        expect(b.readback(b.add(ga, gc)) == want, "add (bit-exact)");
+        for (size_t i = 0; i < n; ++i) want[i] = a[i] * c[i];
+        expect(b.readback(b.mul(ga, gc)) == want, "mul (bit-exact)");
+        for (size_t i = 0; i < n; ++i) want[i] = a[i] * 3.5f;
+        expect(b.readback(b.scale(ga, 3.5f)) == want, "scale (bit-exact)");
+        for (size_t i = 0; i < n; ++i) want[i] = oracle_gelu_tanh(a[i]);
+        close("geluTanh", b.readback(b.gelu_tanh(ga)), want);
+        for (size_t i = 0; i < n; ++i) want[i] = oracle_gelu_tanh(a[i]) * c[i];
+        close("geglu", b.readback(b.geglu(ga, gc)), want);
+        std::vector<float> a50(n);
+        for (size_t i = 0; i < n; ++i) a50[i] = a[i] * 50.0f;
+        oracle_softcap_n(a50.data(), 30.0f, want.data(), n);
+        close("softcap", b.readback(b.softcap(b.scale(ga, 50.0f), 30.0f)), want);
+        const float s = 0.37f;
+        for (size_t i = 0; i < n; ++i) want[i] = a[i] * s;
+        expect(b.readback(b.scale_by_tensor(ga, b.tensor(&s, {1}))) == want, "scaleByTensor (bit-exact)");
+        const float big[3] = {1000.0f, -1000.0f, 50.0f};
+        const auto gv = b.readback(b.gelu_tanh(b.tensor(big, {3})));
+        expect(std::isfinite(gv[0]) && std::isfinite(gv[1]) && std::isfinite(gv[2]), "gelu finite on large inputs");
+        const auto z = b.readback(b.zeros({37}));
+        bool zero = true;
+        for (float v : z) zero &= v == 0.0f;
+        expect(zero, "zeros");
+    }
+    {
+        const size_t v = 30, d = 16;
+        const auto table = r.rand(v * d, 1.0f);
+        const uint32_t ids[5] = {3, 7, 0, 29, 12};
+        std::vector<float> want(5 * d);
+        oracle_embed_rows_f32(table.data(), d, ids, 5, 4.0f, want.data());
+        expect(b.readback(b.embed_rows(b.tensor(table.data(), {v, d}), ids, 5, 4.0f)) == want, "embedRows (bit-exact)");
+    }
+    r.rand(4 * 2 * 16, 1.0f);  // rope(partial)
+    {
+        const size_t rows = 4, stride = 20;
+        const auto x = r.rand(rows * stride, 1.0f);
+        std::vector<float> want;
+        for (size_t i = 0; i < rows; ++i) want.insert(want.end(), x.begin() + i * stride + 5, x.begin() + i * stride + 12);
+        expect(b.readback(b.slice_cols(b.tensor(x.data(), {rows, stride}), 5, 7)) == want, "sliceCols (bit-exact)");
+    }
+    {
+        Lcg q(33);
+        const size_t t = 5, d = 48;
+        const auto x = q.rand(t * d, 1.0f), res = q.rand(t * d, 1.0f), w = q.rand(d, 0.1f);
+        const float s = 1.37f;
+        std::vector<float> normed(t * d), want(t * d);
+        oracle_rms_norm(x.data(), w.data(), normed.data(), t, d, 1e-6f);
+        for (size_t i = 0; i < t * d; ++i) want[i] = res[i] + normed[i];
+        const auto gx = b.tensor(x.data(), {t, d}), gr = b.tensor(res.data(), {t, d}), gw = b.tensor(w.data(), {d});
+        close("add_rms_norm", b.readback(b.add_rms_norm(gr, gx, gw, 1e-6f, nullptr)), want);
+        for (auto& v : want) v = v * s;
+        const auto gs = b.tensor(&s, {1});
+        close("add_rms_norm (layer_scalar)", b.readback(b.add_rms_norm(gr, gx, gw, 1e-6f, &gs)), want);
+    }
+}
+
 }  // namespace
 
 int main() {
@@ -498,6 +584,7 @@ int main() {
         copies_and_kv_append(*b);
         norm_rope_parity(*b);
         quantized_kernel_parity(*b);
+        kernel_parity_ops(*b);
         kv_cache_decode(*b);
     } catch (const std::exception& e) {
         std::fprintf(stderr, "test_backend: exception: %s\n", e.what());

@@ -252,3 +252,174 @@ def load_linear_golden() -> dict[str, LinearCase]:
         assert str(data[name + "__hash"]) == linear_hash(c), f"{name}: regenerated inputs differ from the fixture's"
         c.out = data[name + "__out"]
     return cases
+
+
+# ---- the rest of the trait's ops ----------------------------------------------
+
+OPS_GOLDEN_PATH = Path(__file__).resolve().parent / "backend_ops_golden.npz"
+
+
+@dataclass
+class OpCase:
+    op: str            # add mul scale scale_by_tensor gelu_tanh geglu softcap slice_cols rms_norm
+                       # add_rms_norm embed_rows linear_f32 | linear_q geglu_q gelu_mul_cols_q
+    arrays: dict       # named input arrays
+    params: dict       # named scalars
+    out: np.ndarray | None = None
+
+
+def op_hash(c: OpCase) -> str:
+    h = hashlib.sha256(c.op.encode())
+    for k in sorted(c.arrays):
+        h.update(k.encode())
+        h.update(np.ascontiguousarray(c.arrays[k]).tobytes())
+    for k in sorted(c.params):
+        h.update(f"{k}={c.params[k]!r}".encode())
+    return h.hexdigest()
+
+
+def _lcg_qw(r, n, k, bits):
+    """fused_op_parity's qw closure (rust/tests/gpu.rs:303-308)."""
+    vals = (np.floor(r.next(n * k) * np.float32(1 << bits)).astype(np.uint32) % (1 << bits)).astype(np.uint32)
+    scales = (r.next(n) * np.float32(0.05) + np.float32(0.01)).astype(np.float32)
+    return dict(qbytes=synth.pack_unsigned(vals, bits), scales=scales, N=n, K=k, bits=bits, signed_i8=False,
+                group_size=k)
+
+
+def _lcg_i8(r, n, k):
+    qbytes = np.floor(r.next(n * k) * np.float32(256.0)).astype(np.uint32).astype(np.uint8)
+    scales = (r.next(n) * np.float32(0.05) + np.float32(0.01)).astype(np.float32)
+    return dict(qbytes=qbytes, scales=scales, N=n, K=k, bits=8, signed_i8=True, group_size=k)
+
+
+def _qw_arrays(prefix, w):
+    return {prefix + "qbytes": w["qbytes"], prefix + "scales": w["scales"]}, \
+        {prefix + "N": w["N"], prefix + "K": w["K"], prefix + "bits": w["bits"], prefix + "signed_i8": w["signed_i8"]}
+
+
+def ops_recipes() -> dict[str, OpCase]:
+    """The reference's kernel_parity (rust/tests/gpu.rs:37-100, Lcg seed 7) and
+    fused_op_parity (rust/tests/gpu.rs:298-375, Lcg seed 33) cases for the
+    trait's remaining ops, regenerated in the same draw order, plus seeded
+    Gemma-4-width cases of this build (hidden 1536 post-norms, the per-layer
+    projection slice, an f32 projection)."""
+    cases: dict[str, OpCase] = {}
+    r = synth.Lcg(7)
+    m, k, n = 17, 40, 23
+    x, w = r.rand(m * k, 1.0).reshape(m, k), r.rand(n * k, 1.0).reshape(n, k)
+    cases["kp_linear_tiled"] = OpCase("linear_f32", {"x": x, "w": w}, {})
+    x1 = r.rand(k, 1.0).reshape(1, k)
+    cases["kp_linear_gemv"] = OpCase("linear_f32", {"x": x1, "w": w}, {})
+    t, d = 5, 48
+    x, w = r.rand(t * d, 1.0).reshape(t, d), r.rand(d, 0.1)
+    cases["kp_rmsNorm"] = OpCase("rms_norm", {"x": x, "w": w}, {"eps": 1e-6})
+    nn = 100
+    a, b = r.rand(nn, 1.0), r.rand(nn, 1.0)
+    cases["kp_add"] = OpCase("add", {"a": a, "b": b}, {})
+    cases["kp_mul"] = OpCase("mul", {"a": a, "b": b}, {})
+    cases["kp_scale"] = OpCase("scale", {"a": a}, {"s": 3.5})
+    cases["kp_geluTanh"] = OpCase("gelu_tanh", {"a": a}, {})
+    cases["kp_geglu"] = OpCase("geglu", {"a": a, "b": b}, {})
+    cases["kp_softcap"] = OpCase("softcap", {"a": (a * np.float32(50.0)).astype(np.float32)}, {"cap": 30.0})
+    cases["kp_scaleByTensor"] = OpCase("scale_by_tensor", {"a": a, "s": np.array([0.37], np.float32)}, {})
+    cases["kp_gelu_large"] = OpCase("gelu_tanh", {"a": np.array([1000.0, -1000.0, 50.0], np.float32)}, {})
+    v, d = 30, 16
+    table = r.rand(v * d, 1.0).reshape(v, d)
+    cases["kp_embedRows"] = OpCase("embed_rows", {"table": table, "ids": np.array([3, 7, 0, 29, 12], np.uint32)},
+                                   {"scale": 4.0})
+    r.skip(4 * 2 * 16)  # rope(partial)
+    rows, stride = 4, 20
+    x = r.rand(rows * stride, 1.0).reshape(rows, stride)
+    cases["kp_sliceCols"] = OpCase("slice_cols", {"x": x}, {"offset": 5, "width": 7})
+
+    r = synth.Lcg(33)
+    t, d = 5, 48
+    x, res, w = r.rand(t * d, 1.0).reshape(t, d), r.rand(t * d, 1.0).reshape(t, d), r.rand(d, 0.1)
+    cases["fo_add_rms_norm"] = OpCase("add_rms_norm", {"res": res, "x": x, "w": w}, {"eps": 1e-6})
+    cases["fo_add_rms_norm_scalar"] = OpCase("add_rms_norm", {"res": res, "x": x, "w": w,
+                                                              "s": np.array([1.37], np.float32)}, {"eps": 1e-6})
+    r.skip(3 * 4 * 16 + 16 + 2 * 8 * 256 + 256 + 2 * 1 * 512 + 512)  # head_norm_rope cases
+    for bits in (2, 4, 8):
+        qn, qk = 70, 96
+        wq = _lcg_i8(r, qn, qk) if bits == 8 else _lcg_qw(r, qn, qk, bits)
+        for mm in (8, 9, 64, 70):
+            x = r.rand(mm * qk, 1.0).reshape(mm, qk)
+            arr, par = _qw_arrays("w_", wq)
+            cases[f"fo_linear_q{bits}_M{mm}"] = OpCase("linear_q", dict(arr, x=x), par)
+    for bits in (2, 4):
+        qn, qk = 40, 64
+        wg, wu = _lcg_qw(r, qn, qk, bits), _lcg_qw(r, qn, qk, bits)
+        for mm in (1, 4, 9, 40):
+            x = r.rand(mm * qk, 1.0).reshape(mm, qk)
+            ag, pg = _qw_arrays("w_", wg)
+            au, pu = _qw_arrays("u_", wu)
+            cases[f"fo_linear_geglu_q{bits}_M{mm}"] = OpCase("geglu_q", dict(ag, **au, x=x), dict(pg, **pu))
+    qn, qk, stride, off = 24, 32, 96, 48
+    wi = _lcg_i8(r, qn, qk)
+    for mm in (1, 6, 33):
+        x = r.rand(mm * qk, 1.0).reshape(mm, qk)
+        bb = r.rand(mm * stride, 1.0).reshape(mm, stride)
+        arr, par = _qw_arrays("w_", wi)
+        cases[f"fo_linear_gelu_mul_cols_i8_M{mm}"] = OpCase("gelu_mul_cols_q", dict(arr, x=x, b=bb),
+                                                            dict(par, offset=off))
+
+    # Gemma-4 widths (hidden 1536, 35 layers x 256 per-layer inputs)
+    h = (synth.normal_f32(60, 0, 3 * 1536) * np.float32(4.0)).reshape(3, 1536)
+    res = synth.normal_f32(60, 1, 3 * 1536).reshape(3, 1536)
+    wn = (np.float32(1.0) + np.float32(0.1) * synth.normal_f32(60, 2, 1536)).astype(np.float32)
+    cases["gemma_post_norm_layer_scalar"] = OpCase("add_rms_norm", {"res": res, "x": h, "w": wn,
+                                                                    "s": np.array([0.71], np.float32)}, {"eps": 1e-6})
+    cases["gemma_final_norm"] = OpCase("rms_norm", {"x": h, "w": wn}, {"eps": 1e-6})
+    ple = synth.normal_f32(61, 0, 2 * 35 * 256).reshape(2, 35 * 256)
+    cases["gemma_ple_slice"] = OpCase("slice_cols", {"x": ple}, {"offset": 17 * 256, "width": 256})
+    wf = (synth.normal_f32(62, 0, 256 * 1536) * np.float32(0.03)).reshape(256, 1536)
+    cases["gemma_f32_projection_M2"] = OpCase("linear_f32", {"x": synth.normal_f32(62, 1, 2 * 1536).reshape(2, 1536),
+                                                             "w": wf}, {})
+    return cases
+
+
+def _qw_from(arrays, params, prefix, oracle):
+    return oracle.QWeight(arrays[prefix + "qbytes"], arrays[prefix + "scales"], params[prefix + "N"],
+                          params[prefix + "K"], params[prefix + "bits"], params[prefix + "signed_i8"])
+
+
+def ops_eval(c: OpCase, oracle) -> np.ndarray:
+    a, p = c.arrays, c.params
+    if c.op == "add":
+        return oracle.add(a["a"], a["b"])
+    if c.op == "mul":
+        return oracle.mul(a["a"], a["b"])
+    if c.op == "scale":
+        return oracle.scale(a["a"], p["s"])
+    if c.op == "scale_by_tensor":
+        return oracle.scale(a["a"], a["s"][0])
+    if c.op == "gelu_tanh":
+        return oracle.gelu_tanh(a["a"])
+    if c.op == "geglu":
+        return oracle.geglu(a["a"], a["b"])
+    if c.op == "softcap":
+        return oracle.softcap(a["a"], p["cap"])
+    if c.op == "slice_cols":
+        return oracle.slice_cols(a["x"], p["offset"], p["width"])
+    if c.op == "rms_norm":
+        return oracle.rms_norm(a["x"], a["w"], p["eps"])
+    if c.op == "add_rms_norm":
+        return oracle.add_rms_norm(a["res"], a["x"], a["w"], p["eps"], a["s"][0] if "s" in a else None)
+    if c.op == "embed_rows":
+        return oracle.embed_rows_f32(a["table"], a["ids"], p["scale"])
+    if c.op == "linear_f32":
+        return oracle.linear_f32(a["x"], a["w"])
+    if c.op == "linear_q":
+        return oracle.linear_q(a["x"], _qw_from(a, p, "w_", oracle))
+    if c.op == "geglu_q":
+        return oracle.linear_q_geglu(a["x"], _qw_from(a, p, "w_", oracle), _qw_from(a, p, "u_", oracle))
+    return oracle.linear_q_gelu_mul_cols(a["x"], _qw_from(a, p, "w_", oracle), a["b"], p["offset"])
+
+
+def load_ops_golden() -> dict[str, OpCase]:
+    data = np.load(OPS_GOLDEN_PATH, allow_pickle=False)
+    cases = ops_recipes()
+    for name, c in cases.items():
+        assert str(data[name + "__hash"]) == op_hash(c), f"{name}: regenerated inputs differ from the fixture's"
+        c.out = data[name + "__out"]
+    return cases

@@ -1,5 +1,5 @@
-"""Writes tests/golden/attention_golden.npz, norm_rope_golden.npz and
-linear_golden.npz: for every
+"""Writes tests/golden/attention_golden.npz, norm_rope_golden.npz,
+linear_golden.npz and backend_ops_golden.npz: for every
 recipe in golden_io, the sha256 of its regenerated inputs and the CPU oracle's
 output on them.
 
@@ -16,9 +16,9 @@ sys.path[:0] = [str(HERE), str(REPO / "gemma-4-webgpu-kernels_amd"), str(REPO / 
 import numpy as np  # noqa: E402
 
 import oracle  # noqa: E402
-from golden_io import (GOLDEN_PATH, LINEAR_GOLDEN_PATH, NORM_ROPE_GOLDEN_PATH, input_hash,  # noqa: E402
-                       linear_eval, linear_hash, linear_recipes, norm_rope_eval, norm_rope_hash, norm_rope_recipes,
-                       recipes)
+from golden_io import (GOLDEN_PATH, LINEAR_GOLDEN_PATH, NORM_ROPE_GOLDEN_PATH, OPS_GOLDEN_PATH,  # noqa: E402
+                       input_hash, linear_eval, linear_hash, linear_recipes, norm_rope_eval, norm_rope_hash,
+                       norm_rope_recipes, op_hash, ops_eval, ops_recipes, recipes)
 
 
 def main():
@@ -46,6 +46,13 @@ def main():
         print(f"{name}: out {out.shape}")
     np.savez_compressed(LINEAR_GOLDEN_PATH, **arrays)
     print("wrote", LINEAR_GOLDEN_PATH, LINEAR_GOLDEN_PATH.stat().st_size, "bytes")
+    arrays = {}
+    for name, c in ops_recipes().items():
+        out = ops_eval(c, oracle)
+        arrays[name + "__out"] = out
+        arrays[name + "__hash"] = np.array(op_hash(c))
+    np.savez_compressed(OPS_GOLDEN_PATH, **arrays)
+    print("wrote", OPS_GOLDEN_PATH, OPS_GOLDEN_PATH.stat().st_size, "bytes")
 
 
 if __name__ == "__main__":
