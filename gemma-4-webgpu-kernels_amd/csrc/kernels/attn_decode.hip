@@ -32,23 +32,15 @@
 #include <math.h>
 #include <stdint.h>
 
+#include "g4a_math.h"
 #include "g4a_params.h"
 
 namespace {
 
-constexpr float NEG_INF = -__builtin_huge_valf();
+constexpr float NEG_INF = G4A_NEG_INF;
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
-    return x;
-}
-
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-    return x;
-}
+__device__ __forceinline__ float wave_max(float x) { return g4a_wave_max(x); }
+__device__ __forceinline__ float wave_sum(float x) { return g4a_wave_sum(x); }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 

@@ -12,3 +12,18 @@ constexpr float G4A_GELU_C = 0x1.988452p-1f;
 __device__ __forceinline__ float g4a_gelu_tanh(float v) {
     return 0.5f * v * (1.0f + tanhf(G4A_GELU_C * (v + 0.044715f * v * v * v)));
 }
+
+constexpr float G4A_NEG_INF = -__builtin_huge_valf();
+
+// Butterfly max / sum over the 64 lanes of a wave (every lane gets the result).
+__device__ __forceinline__ float g4a_wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+
+__device__ __forceinline__ float g4a_wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
