@@ -398,58 +398,6 @@ def linear_bench(ctx, op, N, K, bits, M, steps, cpu=True):
     return res
 
 
-def fused_projection(ctx, steps, warmup=20, copies=64):
-    """A sliding layer's decode step and its output projection (4-bit o_proj
-    [1536, 2048]): g4a_attention_linear_q (the projection merges the 16 split
-    partials while staging x) against g4a_attention + g4a_linear_q (decode,
-    combine, projection). Wall µs per step from HIP events around a Python loop
-    of calls, and the summed kernel time of the launches the library times
-    (decode and projection; the separate path's combine is not among them, so
-    its kernel sum leaves that launch out)."""
-    S, Dh, W, cap, N = 32768, 256, 512, 512, 1536
-    K = 8 * Dh
-    ins_q = synth.rms_norm_rows(synth.normal_f32(31, 0, 8 * Dh).reshape(1, 8, Dh))
-    rk = synth.rms_norm_rows(synth.normal_f32(31, 1, cap * Dh).reshape(cap, 1, Dh))
-    rv = synth.normal_f32(31, 2, cap * Dh).reshape(cap, 1, Dh)
-    q = ctx.upload(ins_q)
-    kv = [(ctx.upload(rk), ctx.upload(rv)) for _ in range(copies)]
-    qb, sc, _ = synth.quant_weight(32, N, K, 4)
-    w = ctx.upload_qweight(qb, sc, N, K, 4)
-    out, y = ctx.empty((1, K)), ctx.empty((1, N))
-    kw = dict(T=1, S=S, Hq=HQ, Hkv=1, Dh=Dh, Dv=Dh, q_pos0=S - 1, k_pos0=0, window=W, ring_cap=cap)
-
-    def fused(i):
-        k, v = kv[i % copies]
-        ctx.attention_linear_q(q.ptr, k.ptr, v.ptr, out.ptr, w, y.ptr, **kw)
-
-    def separate(i):
-        k, v = kv[i % copies]
-        ctx.attention(q.ptr, k.ptr, v.ptr, out.ptr, **kw)
-        ctx.linear_q(w, out.ptr, y.ptr, 1)
-    res = {}
-    for name, fn in (("fused", fused), ("separate", separate)):
-        for i in range(warmup):
-            fn(i)
-        ctx.sync()
-        ctx.timer_start()
-        for i in range(steps):
-            fn(i)
-        wall = ctx.timer_stop() / steps
-        ctx.kernel_timing(True)
-        for i in range(steps):
-            fn(i)
-        ctx.sync()
-        kms, n = ctx.kernel_timing_read()
-        ctx.kernel_timing(False)
-        res[name] = {"us_per_step": wall * 1e3, "timed_kernels_us_per_step": kms / steps * 1e3,
-                     "launches_timed_per_step": n / steps}
-    for a in [q, out, y] + [x for pair in kv for x in pair]:
-        a.free()
-    w.free()
-    res["splits"] = ctx.plan(**kw).splits
-    return res
-
-
 def load_traffic():
     p = REPO / "profiles" / "decode_hd512_s32768_traffic.json"
     if p.exists():
@@ -467,7 +415,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="headline decode only (no extras, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "schedule", "producer", "batch", "linear", "fuse"], default=None,
+    ap.add_argument("--only", choices=["prefill", "schedule", "producer", "batch", "linear"], default=None,
                     help="run only these extra workloads (for profiling) and print their JSON line")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="first run 3 device-to-device copies of MIB MiB (the reference dispatch for "
@@ -488,9 +436,6 @@ def main(argv=None):
             for name, T, Dh, W in PREFILL_CONFIGS:
                 out[name] = prefill(ctx, T, Dh, W, steps=args.steps, warmup=args.warmup)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
-        elif args.only == "fuse":
-            out["sliding step + o_proj"] = fused_projection(ctx, steps=args.steps)
-            print(f"[bench] fuse: {out['sliding step + o_proj']}", file=sys.stderr, flush=True)
         elif args.only == "linear":
             for name, op, N, K, bits, M in LINEAR_CONFIGS:
                 out[name] = linear_bench(ctx, op, N, K, bits, M, steps=args.steps)

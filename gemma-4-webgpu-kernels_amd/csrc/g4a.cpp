@@ -62,7 +62,6 @@ struct g4a_ctx {
     hipFunction_t linear_words[3][3][3] = {};  // [bits 2/4/8][(MT, RU) = (1, 2), (1, 8), (4, 4)][mode]
     hipFunction_t linear_elem[3] = {};         // [mode]
     hipFunction_t linear_mfma[3][3] = {};      // [bits 2/4/8][mode]: M >= 16 on the matrix cores
-    hipFunction_t linear_fused[3] = {};        // [bits 2/4/8]: a decode step's split partials merged into x
     hipFunction_t embed_q = nullptr;
     hipFunction_t linear_f32_words[3] = {};  // f32 weights: (MT, RU) = (1, 2), (1, 8), (4, 4)
     hipFunction_t linear_f32_elem = nullptr;
@@ -456,11 +455,6 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
             }
         }
         if (int rc = get_fn(ctx, &ctx->embed_q, "g4a_embed_rows_q")) return bail(rc);
-        for (int b = 0; b < 3; ++b) {
-            char name[64];
-            snprintf(name, sizeof name, "g4a_linear_q_b%d_m1_r2_mode3", bits[b]);
-            if (int rc = get_fn(ctx, &ctx->linear_fused[b], name)) return bail(rc);
-        }
         static const char* f32_words[3] = {"g4a_linear_q_b32_m1_r2_mode0", "g4a_linear_q_b32_m1_r8_mode0",
                                            "g4a_linear_q_b32_m4_r4_mode0"};
         for (int v = 0; v < 3; ++v)
@@ -1115,52 +1109,6 @@ int g4a_linear_q_geglu(g4a_ctx* ctx, const g4a_qweight* w_gate, const g4a_qweigh
 int g4a_linear_q_gelu_mul_cols(g4a_ctx* ctx, const g4a_qweight* w, const float* x, const float* b, uint32_t b_stride,
                                uint32_t b_off, float* y, uint32_t M) {
     return linear_q_launch(ctx, 2, w, nullptr, x, b, b_stride, b_off, y, M);
-}
-
-int g4a_attention_linear_q(g4a_ctx* ctx, const g4a_attn_args* a, const g4a_qweight* w, float* y) {
-    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
-    if (!a) return fail(ctx, G4A_E_ARG, "null args");
-    if (int rc = check_qweight(ctx, w, "projection")) return rc;
-    if (uint64_t(a->Hq) * a->Dv != w->K)
-        return fail(ctx, G4A_E_SHAPE, "projection K = %u, attention rows are %u x %u", w->K, a->Hq, a->Dv);
-    Analysis an;
-    if (int rc = analyse(ctx, a, &an, true)) return rc;
-    if (a->T == 0) return G4A_OK;
-    if (!y) return fail(ctx, G4A_E_ARG, "null y");
-    const g4a_attn_plan& pl = an.plan;
-    const uint64_t vpw = 32 / w->bits, words = uint64_t(w->K) * w->bits / 32;
-    const uint64_t kpad = (words + 63) / 64 * 64 * vpw;
-    // one decode step with a few splits, a projection on the word kernel: the
-    // projection merges the partials while it stages its activation row
-    const bool fuse = a->T == 1 && (pl.kernel == G4A_KERNEL_DECODE || pl.kernel == G4A_KERNEL_DECODE_SHORT) &&
-                      pl.splits >= 2 && pl.splits <= G4A_FUSE_MAX_SPLITS && a->Hq <= G4A_FUSE_MAX_HEADS &&
-                      a->Dh == a->Dv && a->Dh % 16 == 0 && (uint64_t(w->K) * w->bits) % 32 == 0 &&
-                      (w->K + w->group_size - 1) / w->group_size == 1 &&
-                      (reinterpret_cast<uintptr_t>(w->qbytes) & 3) == 0 && kpad * 4 <= LINEAR_LDS_BYTES &&
-                      kpad <= 16 * 256;  // the merge's dims per thread
-    if (int rc = attention_run(ctx, a, an, !fuse)) return rc;
-    if (!fuse) return linear_q_launch(ctx, 0, w, nullptr, a->out, nullptr, 0, 0, y, a->T);
-    G4aLinearParams p{};
-    p.w = static_cast<const uint32_t*>(w->qbytes);
-    p.s = w->scales;
-    p.y = y;
-    p.M = 1;
-    p.N = w->N;
-    p.K = w->K;
-    p.W = uint32_t(words);
-    p.xm = w->signed_i8 ? 0u : w->bits == 4 ? 0x88888888u : w->bits == 2 ? 0xAAAAAAAAu : 0x80808080u;
-    p.part = static_cast<const float*>(ctx->workspace);
-    p.xout = a->out;
-    p.nsplit = pl.splits;
-    p.dh = a->Dh;
-    p.hq = a->Hq;
-    const uint64_t cus = uint64_t(std::max(ctx->cu_count, 1)), target = cus * 16;
-    uint64_t rpw = (w->N + target - 1) / target;
-    rpw = std::max<uint64_t>(2, (rpw + 1) / 2 * 2);
-    p.rows_per_wave = uint32_t(rpw);
-    const int bi = w->bits == 2 ? 0 : w->bits == 4 ? 1 : 2;
-    return launch(ctx, ctx->linear_fused[bi], dim3(uint32_t((w->N + 4 * rpw - 1) / (4 * rpw)), 1, 1),
-                  dim3(256, 1, 1), p, "attention row + projection", true, unsigned(kpad * 4));
 }
 
 int g4a_embed_rows_q(g4a_ctx* ctx, const g4a_qweight* table, const uint32_t* ids, uint32_t T, float scale,

@@ -144,69 +144,11 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
     for (int d = 0; d + 1 < D; ++d)
         if (T) load(wd[d], wd2[d], min((uint32_t)d, T - 1));
 
-    if constexpr (MODE == 3) {
-        // x = the attention row of one query, merged from the decode step's split
-        // partials exactly as the LSE combine kernel (combine_rows) merges them:
-        // per head, wave-wide max and sum of the split weights, then per dim the
-        // splits summed in order (8 loads in flight), divided by L.
-        __shared__ float cw[G4A_FUSE_MAX_HEADS][G4A_FUSE_MAX_SPLITS];
-        __shared__ float cl[G4A_FUSE_MAX_HEADS];
-        const uint32_t ns = p.nsplit, Dh = p.dh, Hq = p.hq;
-        const float* __restrict__ ml = p.part + (size_t)Hq * ns * Dh;
-        for (uint32_t h = wv; h < Hq; h += blockDim.x / 64) {
-            const bool on = (uint32_t)lane < ns;
-            const float ms = on ? ml[(h * ns + lane) * 2] : G4A_NEG_INF;
-            const float Mx = g4a_wave_max(ms);
-            const float e = (ms == G4A_NEG_INF) ? 0.0f : expf(ms - Mx);
-            if (on) cw[h][lane] = e;
-            const float L = g4a_wave_sum(on ? ml[(h * ns + lane) * 2 + 1] * e : 0.0f);
-            if (lane == 0) cl[h] = L;
-        }
-        __syncthreads();
-        // thread t merges dims t, t + 256, ... (up to FK of them) together: the
-        // splits are the outer loop, so each dim still sums them in order while
-        // every dim's load of a split is in flight at once
-        constexpr int FK = 16;  // dims per thread: K <= 4096
-        float A[FK];
-        const float* accp[FK];
-        uint32_t hk[FK];
-#pragma unroll
-        for (int j = 0; j < FK; ++j) {
-            const uint32_t k = threadIdx.x + 256 * j;
-            const uint32_t kk = k < K ? k : 0;
-            hk[j] = kk / Dh;
-            const uint32_t d = kk - hk[j] * Dh;
-            accp[j] = p.part + ((size_t)(hk[j] * (Dh / 16) + d / 16) * ns) * 16 + (d & 15);
-            A[j] = 0.0f;
-        }
-        for (uint32_t s = 0; s < ns; ++s) {
-            float xx[FK];
-#pragma unroll
-            for (int j = 0; j < FK; ++j)
-                if (threadIdx.x + 256 * j < K) xx[j] = accp[j][(size_t)s * 16];
-#pragma unroll
-            for (int j = 0; j < FK; ++j)
-                if (threadIdx.x + 256 * j < K) A[j] += xx[j] * cw[hk[j]][s];
-        }
-#pragma unroll
-        for (int j = 0; j < FK; ++j) {
-            const uint32_t k = threadIdx.x + 256 * j;
-            if (k >= KP) continue;
-            float o = 0.0f;
-            if (k < K) {
-                const float L = cl[hk[j]];
-                o = L > 0.0f ? A[j] / L : 0.0f;
-                if (blockIdx.x == 0 && p.xout) p.xout[k] = o;
-            }
-            xs[k] = o;
-        }
-    } else {
-        for (uint32_t i = threadIdx.x; i < MT * KP / 4; i += blockDim.x) {
-            const uint32_t e = 4 * i, mt = e / KP, k = e - mt * KP;
-            float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (m0 + mt < p.M && k < K) xv = *reinterpret_cast<const float4*>(p.x + (size_t)(m0 + mt) * K + k);
-            *reinterpret_cast<float4*>(xs + e) = xv;
-        }
+    for (uint32_t i = threadIdx.x; i < MT * KP / 4; i += blockDim.x) {
+        const uint32_t e = 4 * i, mt = e / KP, k = e - mt * KP;
+        float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (m0 + mt < p.M && k < K) xv = *reinterpret_cast<const float4*>(p.x + (size_t)(m0 + mt) * K + k);
+        *reinterpret_cast<float4*>(xs + e) = xv;
     }
     __syncthreads();
 
@@ -541,10 +483,6 @@ G4A_LINEAR_MFMA(8, 0)
 G4A_LINEAR_MFMA(8, 1)
 G4A_LINEAR_MFMA(8, 2)
 
-// mode 3: the projection after a decode step, merging its split partials while staging x
-G4A_LINEAR_WORDS(2, 1, 2, 4, 3)
-G4A_LINEAR_WORDS(4, 1, 2, 4, 3)
-G4A_LINEAR_WORDS(8, 1, 2, 4, 3)
 G4A_LINEAR_WORDS(32, 1, 2, 4, 0)
 G4A_LINEAR_WORDS(32, 1, 8, 2, 0)
 G4A_LINEAR_WORDS(32, 4, 4, 2, 0)

@@ -302,17 +302,6 @@ int g4a_linear_q_geglu(g4a_ctx *ctx, const g4a_qweight *w_gate, const g4a_qweigh
  * b[m * b_stride + b_off + n], b_off + N <= b_stride. */
 int g4a_linear_q_gelu_mul_cols(g4a_ctx *ctx, const g4a_qweight *w, const float *x, const float *b, uint32_t b_stride,
                                uint32_t b_off, float *y, uint32_t M);
-/* The attention block's output projection after its attention call
- * (Gemma4Model::attention, rust/src/model.rs:302-303: o_proj(attention(q, k, v))):
- * exactly g4a_attention(args) then g4a_linear_q(w, args->out, y, T), with
- * w->K = Hq * Dv; args->out receives the attention rows as usual. A decode
- * step (T = 1) that runs 2..16 splits on a projection the word-parallel kernel
- * takes skips the LSE-combine launch: the projection merges the split
- * partials while it stages its activation row, in the combine kernel's exact
- * order, so y and args->out are bit-identical to the two separate calls.
- * Sliding-window decode steps (512 keys, 16 splits) take this path. No
- * counterpart call in the reference, which dispatches the two separately. */
-int g4a_attention_linear_q(g4a_ctx *ctx, const g4a_attn_args *args, const g4a_qweight *w, float *y);
 /* Backend::embed_rows on a quantised table [V, D] = [N, K] (rust/src/backend.rs:101-102;
  * rust/src/backend_cpu.rs:127-137; EMBED_Q, rust/src/backend_wgpu.rs:734-760):
  * out[i, d] = deq(ids[i], d) * scale, ids a host array of T values < N. */
