@@ -544,7 +544,7 @@ def main(argv=None):
         extras["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=20, warmup=3)
         print(f"[bench] schedule: {extras['configs[4] 35-layer schedule @32768']}", file=sys.stderr, flush=True)
         result["extra"] = extras
-        result["prefill_TFLOP_s"] = {k: round(v["TFLOP_s"], 2) for k, v in extras.items() if "prefill" in k}
+        result["prefill_TFLOP_s"] = {k: round(v["TFLOP_s"], 2) for k, v in extras.items() if "TFLOP_s" in v}
     if not (args.quick or args.no_cpu):
         result["cpu_baseline"] = cpu_baseline()
         print(f"[bench] cpu baseline: {result['cpu_baseline']}", file=sys.stderr, flush=True)
