@@ -325,6 +325,8 @@ LINEAR_CONFIGS = [
     ("linear down 4-bit [1536,6144] M=1", "linear", 1536, 6144, 4, 1),
     ("linear lm_head 2-bit [262144,1536] M=1", "linear", 262144, 1536, 2, 1),
     ("linear gate 2-bit [12288,1536] M=64", "linear", 12288, 1536, 2, 64),
+    ("linear q_proj sliding 4-bit [2048,1536] M=2048 (prefill chunk)", "linear", 2048, 1536, 4, 2048),
+    ("linear gate+up GeGLU 4-bit 2x[6144,1536] M=2048 (prefill chunk)", "geglu", 6144, 1536, 4, 2048),
 ]
 
 
@@ -386,7 +388,13 @@ def linear_bench(ctx, op, N, K, bits, M, steps, cpu=True):
     b = linear_bytes(op, N, K, bits, M)
     res = {"kernel_us": us, "GB_s": b / (us * 1e-6) / 1e9, "frac_hbm_peak": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
            "bytes": b, "weight_copies_rotated": copies}
-    if cpu:
+    if M >= 16:
+        # 2 flops per multiply-add of the projection(s), against the dense bf16 matrix peak
+        # (the kernel issues three bf16 MFMAs per multiply-add: x split into three exact parts)
+        fl = 2 * nw * M * N * K
+        res["TFLOP_s_linear"] = fl / (us * 1e-6) / 1e12
+        res["frac_bf16_mfma_peak_x3"] = 3 * fl / (us * 1e-6) / 1e12 / 2500.0
+    if cpu and M * N * K <= 2e9:
         w_o = oracle.QWeight(qb, sc, N, K, bits)
         t0 = time.perf_counter()
         if op == "geglu":

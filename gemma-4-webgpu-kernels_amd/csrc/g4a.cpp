@@ -61,7 +61,7 @@ struct g4a_ctx {
     hipFunction_t norm_rope = nullptr;  // the attention producer (RMSNorm + RoPE + KV write)
     hipFunction_t linear_words[3][3][3] = {};  // [bits 2/4/8][(MT, RU) = (1, 2), (1, 8), (4, 4)][mode]
     hipFunction_t linear_elem[3] = {};         // [mode]
-    hipFunction_t linear_mfma[3][3] = {};      // [bits 2/4/8][mode]: M >= 16 on the matrix cores
+    hipFunction_t linear_mfma[3][2][3] = {};   // [bits 2/4/8][64 / 128 weight rows per tile][mode]: M >= 16
     hipFunction_t embed_q = nullptr;
     hipFunction_t linear_f32_words[3] = {};  // f32 weights: (MT, RU) = (1, 2), (1, 8), (4, 4)
     hipFunction_t linear_f32_elem = nullptr;
@@ -449,10 +449,11 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
             char name[64];
             snprintf(name, sizeof name, "g4a_linear_q_elem_mode%d", m);
             if (int rc = get_fn(ctx, &ctx->linear_elem[m], name)) return bail(rc);
-            for (int b = 0; b < 3; ++b) {
-                snprintf(name, sizeof name, "g4a_linear_q_mfma_b%d_mode%d", bits[b], m);
-                if (int rc = get_fn(ctx, &ctx->linear_mfma[b][m], name)) return bail(rc);
-            }
+            for (int b = 0; b < 3; ++b)
+                for (int t = 0; t < 2; ++t) {
+                    snprintf(name, sizeof name, "g4a_linear_q_mfma_b%d_n%d_mode%d", bits[b], t ? 128 : 64, m);
+                    if (int rc = get_fn(ctx, &ctx->linear_mfma[b][t][m], name)) return bail(rc);
+                }
         }
         if (int rc = get_fn(ctx, &ctx->embed_q, "g4a_embed_rows_q")) return bail(rc);
         static const char* f32_words[3] = {"g4a_linear_q_b32_m1_r2_mode0", "g4a_linear_q_b32_m1_r8_mode0",
@@ -1023,17 +1024,20 @@ int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qwei
     p.xm = w->signed_i8 ? 0u : w->bits == 4 ? 0x88888888u : w->bits == 2 ? 0xAAAAAAAAu : 0x80808080u;
     const int bi = w->bits == 2 ? 0 : w->bits == 4 ? 1 : 2;
     if (M >= LINEAR_MFMA_MIN_M && w->K % 64 == 0 && p.scale_stride == 1 && aligned8) {
-        // 64 activation rows x 64 weight rows per workgroup on the matrix cores
+        // 64 activation rows x 128 weight rows per workgroup on the matrix cores,
+        // or x 64 rows when the larger tile would leave fewer than 2 workgroups per CU
         p.wb = static_cast<const uint8_t*>(w->qbytes);
         p.wb2 = mode == 1 ? static_cast<const uint8_t*>(w2->qbytes) : nullptr;
-        const uint32_t gx = (w->N + 63) / 64;
+        const uint64_t tiles128 = uint64_t((w->N + 127) / 128) * ((M + 63) / 64);
+        const int wide = tiles128 >= 2 * uint64_t(std::max(ctx->cu_count, 1)) ? 1 : 0;
+        const uint32_t gx = wide ? (w->N + 127) / 128 : (w->N + 63) / 64;
         for (uint32_t m0 = 0; m0 < M; m0 += 65535u * 64) {
             G4aLinearParams q = p;
             q.x = x + size_t(m0) * w->K;
             q.y = y + size_t(m0) * w->N;
             q.b = b ? b + size_t(m0) * b_stride : nullptr;
             q.M = std::min<uint32_t>(65535u * 64, M - m0);
-            if (int rc = launch(ctx, ctx->linear_mfma[bi][mode], dim3(gx, (q.M + 63) / 64, 1), dim3(256, 1, 1), q,
+            if (int rc = launch(ctx, ctx->linear_mfma[bi][wide][mode], dim3(gx, (q.M + 63) / 64, 1), dim3(256, 1, 1), q,
                                 "quantised linear (matrix cores)", true))
                 return rc;
         }

@@ -236,17 +236,19 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
 // bf16. So every product x_p * q is exact in f32 and the three partial sums
 // differ from the f32 sum only by accumulation rounding, like the VALU kernel.
 //
-// Workgroup: 64 activation rows (tokens) x 64 weight rows, 4 waves; wave w owns
-// weight rows 16w .. 16w + 15 (the MFMA's A operand, one 8-value fragment per
-// lane: row lane % 16, k 8 (lane / 16) .. + 7 of each 32-wide sub-step) and all
-// 64 tokens (four 16-token B blocks). Per 64-wide k step the workgroup stages
+// Workgroup: 64 activation rows (tokens) x 64 AB weight rows, 4 waves; wave w
+// owns weight rows 16 AB w .. + 16 AB - 1 as AB 16-row A blocks (the MFMA's A
+// operand, one 8-value fragment per lane: row lane % 16, k 8 (lane / 16) .. + 7
+// of each 32-wide sub-step) and all 64 tokens (four 16-token B blocks), so
+// each B fragment read from LDS feeds AB MFMAs. AB = 2 for large M (more MFMA
+// work per staged x), 1 when the grid would otherwise be too small. Per 64-wide k step the workgroup stages
 // the three bf16 parts of its x tile in LDS (double-buffered); the next step's
 // x and weight fragments are loaded into registers before this step's MFMAs.
 // C lane layout: weight row 4 (lane / 16) + i, token lane % 16.
 typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-constexpr int LQ_BM = 64, LQ_BN = 64, LQ_BK = 64;
+constexpr int LQ_BM = 64, LQ_BK = 64;
 constexpr int LQ_XS = LQ_BK + 8;  // bf16 per staged x row (+16 bytes: rows start on different banks)
 
 // The 8 fields of row `row` at k .. k + 7 as value * F.
@@ -276,8 +278,9 @@ __device__ __forceinline__ void frag8(const uint8_t* __restrict__ rowp, uint32_t
     }
 }
 
-template <int BITS, int MODE>
+template <int BITS, int AB, int MODE>
 __device__ __forceinline__ void linear_q_mfma(const G4aLinearParams& p) {
+    constexpr int LQ_BN = 64 * AB;
     using F = QFmt<BITS>;
     __shared__ __attribute__((aligned(16))) __bf16 xsp[2][3][LQ_BM * LQ_XS];
     const int tid = threadIdx.x;
@@ -287,9 +290,15 @@ __device__ __forceinline__ void linear_q_mfma(const G4aLinearParams& p) {
     const uint32_t K = p.K, N = p.N, M = p.M;
     const uint32_t n0 = blockIdx.x * LQ_BN, m0 = blockIdx.y * LQ_BM;
     const uint32_t nsteps = K / LQ_BK;
-    const uint32_t row = min(n0 + 16 * wv + rl, N - 1);  // this lane's A row (rows past N: re-read, not stored)
-    const uint8_t* __restrict__ wrow = p.wb + (size_t)row * p.row_bytes;
-    const uint8_t* __restrict__ wrow2 = MODE == 1 ? p.wb2 + (size_t)row * p.row_bytes : nullptr;
+    // this lane's A rows, one per 16-row block (rows past N: re-read, not stored)
+    const uint8_t* wrow[AB];
+    const uint8_t* wrow2[AB];
+#pragma unroll
+    for (int ab = 0; ab < AB; ++ab) {
+        const uint32_t row = min(n0 + 16 * AB * wv + 16 * ab + rl, N - 1);
+        wrow[ab] = p.wb + (size_t)row * p.row_bytes;
+        wrow2[ab] = MODE == 1 ? p.wb2 + (size_t)row * p.row_bytes : nullptr;
+    }
 
     // x tile staging: thread tid splits tokens tid / 4 (16 values at 16 (tid % 4))
     const uint32_t xt = tid >> 2, xk = 16 * (tid & 3);
@@ -326,20 +335,24 @@ __device__ __forceinline__ void linear_q_mfma(const G4aLinearParams& p) {
         *reinterpret_cast<bf8v*>(d2) = p2[0];
         *reinterpret_cast<bf8v*>(d2 + 8) = p2[1];
     };
-    // A fragments of one step: sub-step kk covers k 32 kk + 8 g .. + 7
-    float qa[2][8], qb2[2][8];
+    // A fragments of one step: block ab, sub-step kk covers k 32 kk + 8 g .. + 7
+    float qa[AB][2][8], qb2[AB][2][8];
     auto load_w = [&](uint32_t st) {
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            const uint32_t k = st * LQ_BK + 32 * kk + 8 * g;
-            frag8<BITS>(wrow, k, p.xm, qa[kk]);
-            if (MODE == 1) frag8<BITS>(wrow2, k, p.xm, qb2[kk]);
-        }
+        for (int ab = 0; ab < AB; ++ab)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const uint32_t k = st * LQ_BK + 32 * kk + 8 * g;
+                frag8<BITS>(wrow[ab], k, p.xm, qa[ab][kk]);
+                if (MODE == 1) frag8<BITS>(wrow2[ab], k, p.xm, qb2[ab][kk]);
+            }
     };
 
-    f4v acc[4], acc2[4];
+    f4v acc[AB][4], acc2[AB][4];
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) acc[tb] = acc2[tb] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int ab = 0; ab < AB; ++ab)
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) acc[ab][tb] = acc2[ab][tb] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 
     if (nsteps) {
         load_x(0);
@@ -348,14 +361,16 @@ __device__ __forceinline__ void linear_q_mfma(const G4aLinearParams& p) {
     }
     for (uint32_t st = 0; st < nsteps; ++st) {
         __syncthreads();  // step st's x parts are staged; every wave is done with the other buffer
-        bf8v a[2], a2[2];
+        bf8v a[AB][2], a2[AB][2];
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
+        for (int ab = 0; ab < AB; ++ab)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                a[kk][i] = (__bf16)qa[kk][i];
-                if (MODE == 1) a2[kk][i] = (__bf16)qb2[kk][i];
-            }
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    a[ab][kk][i] = (__bf16)qa[ab][kk][i];
+                    if (MODE == 1) a2[ab][kk][i] = (__bf16)qb2[ab][kk][i];
+                }
         if (st + 1 < nsteps) {
             load_x(st + 1);
             load_w(st + 1);
@@ -369,29 +384,35 @@ __device__ __forceinline__ void linear_q_mfma(const G4aLinearParams& p) {
 #pragma unroll
                 for (int part = 0; part < 3; ++part) {
                     const bf8v bx = *reinterpret_cast<const bf8v*>(&xsp[buf][part][off]);
-                    acc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kk], bx, acc[tb], 0, 0, 0);
-                    if (MODE == 1) acc2[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[kk], bx, acc2[tb], 0, 0, 0);
+#pragma unroll
+                    for (int ab = 0; ab < AB; ++ab) {
+                        acc[ab][tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ab][kk], bx, acc[ab][tb], 0, 0, 0);
+                        if (MODE == 1)
+                            acc2[ab][tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[ab][kk], bx, acc2[ab][tb], 0, 0, 0);
+                    }
                 }
             }
         if (st + 1 < nsteps) stage_x(buf ^ 1);
     }
 
-    // lane (g, rl) of block tb holds weight rows 16 wv + 4 g + i, token 16 tb + rl
+    // lane (g, rl) of blocks (ab, tb) holds weight rows 16 AB wv + 16 ab + 4 g + i, token 16 tb + rl
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-        const uint32_t m = m0 + 16 * tb + rl;
-        if (m >= M) continue;
+    for (int ab = 0; ab < AB; ++ab)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t n = n0 + 16 * wv + 4 * g + i;
-            if (n >= N) continue;
-            const float v = acc[tb][i] * (p.s[n] * F::INV_F);
-            float o = v;
-            if (MODE == 1) o = gelu_tanh(v) * (acc2[tb][i] * (p.s2[n] * F::INV_F));
-            if (MODE == 2) o = gelu_tanh(v) * p.b[(size_t)m * p.b_stride + p.b_off + n];
-            p.y[(size_t)m * N + n] = o;
+        for (int tb = 0; tb < 4; ++tb) {
+            const uint32_t m = m0 + 16 * tb + rl;
+            if (m >= M) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t n = n0 + 16 * AB * wv + 16 * ab + 4 * g + i;
+                if (n >= N) continue;
+                const float v = acc[ab][tb][i] * (p.s[n] * F::INV_F);
+                float o = v;
+                if (MODE == 1) o = gelu_tanh(v) * (acc2[ab][tb][i] * (p.s2[n] * F::INV_F));
+                if (MODE == 2) o = gelu_tanh(v) * p.b[(size_t)m * p.b_stride + p.b_off + n];
+                p.y[(size_t)m * N + n] = o;
+            }
         }
-    }
 }
 
 // QuantWeight::deq (rust/src/backend.rs:44-58) of element (n, k).
@@ -469,9 +490,12 @@ G4A_LINEAR_SET(8, 0)
 G4A_LINEAR_SET(8, 1)
 G4A_LINEAR_SET(8, 2)
 
-#define G4A_LINEAR_MFMA(B, MODE)                                                                 \
-    extern "C" __global__ __launch_bounds__(256) void g4a_linear_q_mfma_b##B##_mode##MODE(G4aLinearParams p) { \
-        linear_q_mfma<B, MODE>(p);                                                               \
+#define G4A_LINEAR_MFMA(B, MODE)                                                                     \
+    extern "C" __global__ __launch_bounds__(256) void g4a_linear_q_mfma_b##B##_n64_mode##MODE(G4aLinearParams p) {  \
+        linear_q_mfma<B, 1, MODE>(p);                                                                \
+    }                                                                                                \
+    extern "C" __global__ __launch_bounds__(256) void g4a_linear_q_mfma_b##B##_n128_mode##MODE(G4aLinearParams p) { \
+        linear_q_mfma<B, 2, MODE>(p);                                                                \
     }
 G4A_LINEAR_MFMA(2, 0)
 G4A_LINEAR_MFMA(2, 1)
