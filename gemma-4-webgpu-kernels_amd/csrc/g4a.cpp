@@ -63,6 +63,7 @@ struct g4a_ctx {
     hipFunction_t linear_elem[3] = {};         // [mode]
     hipFunction_t linear_mfma[3][2][3] = {};   // [bits 2/4/8][64 / 128 weight rows per tile][mode]: M >= 16
     hipFunction_t embed_q = nullptr;
+    hipFunction_t linear_half[2][3] = {};       // 2-bit, M = 1, 32 lanes per row: [RU = 1, 4][mode]
     hipFunction_t linear_f32_words[3] = {};  // f32 weights: (MT, RU) = (1, 2), (1, 8), (4, 4)
     hipFunction_t linear_f32_elem = nullptr;
     hipFunction_t ew = nullptr;              // elementwise ops
@@ -447,6 +448,10 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
                 }
         for (int m = 0; m < 3; ++m) {
             char name[64];
+            for (int v = 0; v < 2; ++v) {
+                snprintf(name, sizeof name, "g4a_linear_q_b2_m1_r%d_h_mode%d", v ? 4 : 1, m);
+                if (int rc = get_fn(ctx, &ctx->linear_half[v][m], name)) return bail(rc);
+            }
             snprintf(name, sizeof name, "g4a_linear_q_elem_mode%d", m);
             if (int rc = get_fn(ctx, &ctx->linear_elem[m], name)) return bail(rc);
             for (int b = 0; b < 3; ++b)
@@ -1085,15 +1090,19 @@ int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qwei
     rpw = std::max<uint64_t>(RU, (rpw + RU - 1) / RU * RU);
     p.rows_per_wave = uint32_t(rpw);
     const uint32_t gx = uint32_t((w->N + 4 * rpw - 1) / (4 * rpw));
-    const unsigned lds = unsigned(MT * kpad * 4);
+    // 2-bit rows of an odd multiple of 32 words (K = 1536 is 96 words): half-waves
+    // walk two rows at once, so no lane idles on the row's last word step
+    const bool half = MT == 1 && w->bits == 2 && words_per_row % 64 == 32;
+    hipFunction_t fn = half ? ctx->linear_half[variant][mode] : ctx->linear_words[bi][variant][mode];
+    const unsigned lds = unsigned(MT * (half ? (words_per_row + 31) / 32 * 32 * vpw : kpad) * 4);
     for (uint32_t m0 = 0; m0 < M; m0 += 65535u * MT) {
         G4aLinearParams q = p;
         q.x = x + size_t(m0) * w->K;
         q.y = y + size_t(m0) * w->N;
         q.b = b ? b + size_t(m0) * b_stride : nullptr;
         q.M = std::min<uint32_t>(65535u * MT, M - m0);
-        if (int rc = launch(ctx, ctx->linear_words[bi][variant][mode], dim3(gx, (q.M + MT - 1) / MT, 1),
-                            dim3(256, 1, 1), q, "quantised linear", true, lds))
+        if (int rc = launch(ctx, fn, dim3(gx, (q.M + MT - 1) / MT, 1), dim3(256, 1, 1), q, "quantised linear", true,
+                            lds))
             return rc;
     }
     return G4A_OK;

@@ -84,10 +84,10 @@ __device__ __forceinline__ void unpack(uint32_t v, float (&q)[QFmt<BITS>::VPW]) 
 // so log2(V) steps leave one value per lane, then plain xor steps finish it.
 // Returns the total of value `idx` (set here from the lane's bits); every lane
 // whose low 6 - log2(V) bits are zero holds a distinct idx.
-template <int V>
+template <int V, int LANES = 64>
 __device__ __forceinline__ float wave_reduce_many(float (&v)[V], int lane, int& idx) {
     idx = 0;
-    int o = 32;
+    int o = LANES / 2;  // LANES = 32: each half-wave reduces on its own
 #pragma unroll
     for (int n = V; n > 1; n >>= 1, o >>= 1) {
         const int half = n / 2;
@@ -107,21 +107,27 @@ __device__ __forceinline__ float wave_reduce_many(float (&v)[V], int lane, int& 
     return s;
 }
 
-template <int BITS, int MT, int RU, int D, int MODE>
+// LPR (lanes per row) = 32 splits the wave into two halves that walk different
+// rows (RU each): for rows of an odd multiple of 32 words (2-bit rows of 1536
+// values are 96 words) every lane then has a word on every step.
+template <int BITS, int MT, int RU, int D, int MODE, int LPR = 64>
 __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
     using F = QFmt<BITS>;
     constexpr int VPW = F::VPW;
     constexpr int V = MT * RU;
-    extern __shared__ __attribute__((aligned(16))) float xs[];  // [MT][J * 64 * VPW], zeros past K
+    constexpr int RC = RU * (64 / LPR);  // rows per chunk (both halves)
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // [MT][J * LPR * VPW], zeros past K
     const int lane = threadIdx.x & 63;
+    const int ll = lane & (LPR - 1);        // lane within its row group
+    const int hf = lane / LPR;              // row group (0 for LPR = 64)
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: rows in scalar registers
     const uint32_t K = p.K, W = p.W, N = p.N;
-    const uint32_t J = (W + 63) / 64;       // word steps per row chunk (lanes past W read zeros of x)
-    const uint32_t KP = J * 64 * VPW;       // padded activation row
+    const uint32_t J = (W + LPR - 1) / LPR;  // word steps per row chunk (lanes past W read zeros of x)
+    const uint32_t KP = J * LPR * VPW;       // padded activation row
     const uint32_t m0 = blockIdx.y * MT;
     const uint32_t first = (blockIdx.x * (blockDim.x / 64) + wv) * p.rows_per_wave;
     const uint32_t last = min(first + p.rows_per_wave, N);
-    const uint32_t nchunks = first < last ? (last - first + RU - 1) / RU : 0;
+    const uint32_t nchunks = first < last ? (last - first + RC - 1) / RC : 0;
     const uint32_t T = nchunks * J;         // the wave's steps: chunk t / J, word step t % J
 
     // Step t loads word lane + 64 (t % J) (clamped to the row) of the RU rows of
@@ -130,10 +136,10 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
     // with no register copies.
     auto load = [&](uint32_t (&wd)[RU], uint32_t (&wd2)[RU], uint32_t t) {
         const uint32_t c = t / J, j = t - c * J;
-        const uint32_t w = min(lane + 64 * j, W - 1);
+        const uint32_t w = min(ll + LPR * j, W - 1);
 #pragma unroll
         for (int r = 0; r < RU; ++r) {
-            const size_t row = min(first + c * RU + r, N - 1);
+            const size_t row = min(first + c * RC + hf * RU + r, N - 1);
             wd[r] = p.w[row * W + w];
             if (MODE == 1) wd2[r] = p.w2[row * W + w];
         }
@@ -158,7 +164,7 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
 
     auto step = [&](const uint32_t (&wd)[RU], const uint32_t (&wd2)[RU], uint32_t t) {
         const uint32_t c = t / J, j = t - c * J;
-        const uint32_t w = lane + 64 * j;
+        const uint32_t w = ll + LPR * j;
         float xv[MT][VPW];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
@@ -195,15 +201,15 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
         if (j + 1 == J) {
             // the chunk's sums are complete: reduce across the wave and store
             int idx;
-            const float a = wave_reduce_many<V>(acc, lane, idx);
+            const float a = wave_reduce_many<V, LPR>(acc, ll, idx);
             float a2 = 0.0f;
             if (MODE == 1) {
                 int idx2;
-                a2 = wave_reduce_many<V>(acc2, lane, idx2);
+                a2 = wave_reduce_many<V, LPR>(acc2, ll, idx2);
             }
-            if ((lane & (64 / V - 1)) == 0) {
+            if ((ll & (LPR / V - 1)) == 0) {
                 const uint32_t mt = idx / RU, r = idx % RU;
-                const uint32_t n = first + c * RU + r, m = m0 + mt;
+                const uint32_t n = first + c * RC + hf * RU + r, m = m0 + mt;
                 if (n < last && m < p.M) {
                     const float v = BITS == 32 ? a : a * (p.s[n] * F::INV_F);  // f32 weights carry no scale
                     float o = v;
@@ -480,6 +486,18 @@ __device__ __forceinline__ void embed_rows_q(const G4aEmbedParams& p) {
     }
 #define G4A_LINEAR_SET(B, MODE) \
     G4A_LINEAR_WORDS(B, 1, 2, 4, MODE) G4A_LINEAR_WORDS(B, 1, 8, 2, MODE) G4A_LINEAR_WORDS(B, 4, 4, 2, MODE)
+// 32 lanes per row (two rows per wave step), M = 1, for rows of an odd multiple of 32 words
+#define G4A_LINEAR_HALF(B, RU, D, MODE)                                                                  \
+    extern "C" __global__ __launch_bounds__(256) void g4a_linear_q_b##B##_m1_r##RU##_h_mode##MODE(  \
+        G4aLinearParams p) {                                                                           \
+        linear_q_words<B, 1, RU, D, MODE, 32>(p);                                                      \
+    }
+G4A_LINEAR_HALF(2, 1, 4, 0)
+G4A_LINEAR_HALF(2, 4, 2, 0)
+G4A_LINEAR_HALF(2, 1, 4, 1)
+G4A_LINEAR_HALF(2, 4, 2, 1)
+G4A_LINEAR_HALF(2, 1, 4, 2)
+G4A_LINEAR_HALF(2, 4, 2, 2)
 G4A_LINEAR_SET(2, 0)
 G4A_LINEAR_SET(2, 1)
 G4A_LINEAR_SET(2, 2)

@@ -159,12 +159,16 @@ def _check_fused(got, x, w, w2, b, b_off, label):
 def test_word_kernel_shapes(ctx, bits, signed):
     """Every (activation rows, weight rows) variant: M = 1 with short and tall
     weights (2 or 8 rows in flight), M >= 2 in 4-row tiles with ragged M, N not a
-    multiple of the rows per wave, K from one word per lane to the LDS limit."""
+    multiple of the rows per wave, K from one word per lane to the LDS limit.
+    2-bit rows of an odd multiple of 32 words (K = 512, 1536, 3584, 4608) take
+    the half-wave kernels (two rows per wave step), also at M = 2 when four
+    activation rows do not fit the LDS share."""
     c = ctx
     cus = c.device_info().compute_units
     for N, K, M in [(1, 64, 1), (7, 128, 1), (255, 1536, 1), (2048, 1536, 1), (cus * 64 + 5, 1536, 1),
                     (1536, 2048, 1), (1536, 6144, 1), (1536, 16384, 1), (300, 1536, 2), (300, 1536, 3),
-                    (257, 2048, 5), (96, 4096, 8), (64, 6144, 3), (40, 64, 17)]:
+                    (257, 2048, 5), (96, 4096, 8), (64, 6144, 3), (40, 64, 17), (5, 512, 1),
+                    (cus * 64 + 3, 3584, 1), (41, 4608, 2)]:
         label = f"b{bits}{'s' if signed else ''} N={N} K={K} M={M}"
         step(label)
         w = _qw(N * 7 + K + M, N, K, bits, signed)
@@ -197,10 +201,10 @@ def test_geglu_and_gelu_mul_cols_at_gemma_shapes(ctx):
             y = d.empty((M, N))
             c.linear_q_geglu(d.w(wg), d.w(wu), d.arr(x).ptr, y.ptr, M)
             _check_fused(y.to_host(), x, wg, wu, None, 0, label)
-    for M, off in [(1, 0), (1, 34 * 256), (3, 11 * 256)]:
-        label = f"per-layer gate [256, 1536] M={M} cols {off}"
+    for M, off, bits in [(1, 0, 4), (1, 34 * 256, 4), (3, 11 * 256, 4), (1, 5 * 256, 2)]:
+        label = f"per-layer gate b{bits} [256, 1536] M={M} cols {off}"
         step(label)
-        w = _qw(77, 256, 1536, 4)
+        w = _qw(77, 256, 1536, bits)
         x = synth.normal_f32(78, M, M * 1536).reshape(M, 1536)
         b = synth.normal_f32(79, M, M * 35 * 256).reshape(M, 35 * 256)
         with Dev(c) as d:
