@@ -66,7 +66,9 @@ def test_benchmark_decode_configs(ctx, name, T, S, Dh, window, seed):
 
 
 def test_config2_long_context_split_sweep(ctx):
-    """hd512 global decode over 131072 keys, split count swept 8..512."""
+    """hd512 global decode over 131072 keys, split count swept 8..512,
+    plus counts that leave ragged 16-split groups in the merge (100, 300, and
+    1000, which the 192-key splits make 683)."""
     ins = synth.gemma_inputs(T=1, S=131072, Dh=512, seed=2)
     step("configs[2] oracle")
     want = oracle.attention(ins.q, ins.k, ins.v, ins.q_pos, ins.k_pos)
@@ -74,7 +76,7 @@ def test_config2_long_context_split_sweep(ctx):
     out = ctx.empty((1, 8 * 512))
     try:
         results = {}
-        for splits in (8, 16, 32, 64, 128, 256, 512, 0):
+        for splits in (8, 16, 32, 64, 100, 128, 256, 300, 512, 1000, 0):
             step(f"configs[2] splits={splits}")
             ctx.attention(dev[0].ptr, dev[1].ptr, dev[2].ptr, out.ptr, T=1, S=131072, Hq=8, Hkv=1, Dh=512,
                           Dv=512, q_pos0=131071, k_pos0=0, splits=splits)
