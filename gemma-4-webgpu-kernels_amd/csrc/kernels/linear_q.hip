@@ -107,6 +107,15 @@ __device__ __forceinline__ float wave_reduce_many(float (&v)[V], int lane, int& 
     return s;
 }
 
+// The value index wave_reduce_many<V, LANES> leaves in `lane`.
+template <int V, int LANES>
+__device__ __forceinline__ int reduce_slot(int lane) {
+    int idx = 0, o = LANES / 2;
+#pragma unroll
+    for (int n = V; n > 1; n >>= 1, o >>= 1) idx = 2 * idx + ((lane & o) ? 1 : 0);
+    return idx;
+}
+
 // LPR (lanes per row) = 32 splits the wave into two halves that walk different
 // rows (RU each): for rows of an odd multiple of 32 words (2-bit rows of 1536
 // values are 96 words) every lane then has a word on every step.
@@ -134,7 +143,13 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
     // chunk t / J (clamped to the matrix). D register sets form a ring, so the
     // loads of steps t + 1 .. t + D - 1 are in flight while step t computes,
     // with no register copies.
-    auto load = [&](uint32_t (&wd)[RU], uint32_t (&wd2)[RU], uint32_t t) {
+    // The output this lane stores after a chunk's reduction, and the epilogue
+    // operands of that output (scales, the gelu-times column), which each step
+    // loads with its words: a load issued at the store itself would wait for
+    // every word in flight.
+    const int oidx = reduce_slot<V, LPR>(ll);
+    const uint32_t omt = oidx / RU, orr = oidx % RU;
+    auto load = [&](uint32_t (&wd)[RU], uint32_t (&wd2)[RU], float (&ep)[2], uint32_t t) {
         const uint32_t c = t / J, j = t - c * J;
         const uint32_t w = min(ll + LPR * j, W - 1);
 #pragma unroll
@@ -143,12 +158,17 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
             wd[r] = p.w[row * W + w];
             if (MODE == 1) wd2[r] = p.w2[row * W + w];
         }
+        const uint32_t n = min(first + c * RC + hf * RU + orr, N - 1);
+        if (BITS != 32) ep[0] = p.s[n];
+        if (MODE == 1) ep[1] = p.s2[n];
+        if (MODE == 2) ep[1] = p.b[(size_t)min(m0 + omt, p.M - 1) * p.b_stride + p.b_off + n];
     };
     uint32_t wd[D][RU], wd2[D][RU];
+    float ep[D][2];
     // the first steps' words are requested before the activations are staged
 #pragma unroll
     for (int d = 0; d + 1 < D; ++d)
-        if (T) load(wd[d], wd2[d], min((uint32_t)d, T - 1));
+        if (T) load(wd[d], wd2[d], ep[d], min((uint32_t)d, T - 1));
 
     for (uint32_t i = threadIdx.x; i < MT * KP / 4; i += blockDim.x) {
         const uint32_t e = 4 * i, mt = e / KP, k = e - mt * KP;
@@ -162,7 +182,7 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = acc2[i] = 0.0f;
 
-    auto step = [&](const uint32_t (&wd)[RU], const uint32_t (&wd2)[RU], uint32_t t) {
+    auto step = [&](const uint32_t (&wd)[RU], const uint32_t (&wd2)[RU], const float (&ep)[2], uint32_t t) {
         const uint32_t c = t / J, j = t - c * J;
         const uint32_t w = ll + LPR * j;
         float xv[MT][VPW];
@@ -211,10 +231,10 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
                 const uint32_t mt = idx / RU, r = idx % RU;
                 const uint32_t n = first + c * RC + hf * RU + r, m = m0 + mt;
                 if (n < last && m < p.M) {
-                    const float v = BITS == 32 ? a : a * (p.s[n] * F::INV_F);  // f32 weights carry no scale
+                    const float v = BITS == 32 ? a : a * (ep[0] * F::INV_F);  // f32 weights carry no scale
                     float o = v;
-                    if (MODE == 1) o = gelu_tanh(v) * (a2 * (p.s2[n] * F::INV_F));
-                    if (MODE == 2) o = gelu_tanh(v) * p.b[(size_t)m * p.b_stride + p.b_off + n];
+                    if (MODE == 1) o = gelu_tanh(v) * (a2 * (ep[1] * F::INV_F));
+                    if (MODE == 2) o = gelu_tanh(v) * ep[1];
                     p.y[(size_t)m * N + n] = o;
                 }
             }
@@ -223,13 +243,17 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
         }
     };
 
+    // Whole groups of D steps, with no branch between them: the loads of a step
+    // never wait behind a path that skipped one. Steps past T (at most D - 1)
+    // re-read the last words and store nothing: their rows lie past `last`.
     for (uint32_t t = 0; t < T; t += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            if (t + d < T) {
-                load(wd[(d + D - 1) % D], wd2[(d + D - 1) % D], min(t + d + D - 1, T - 1));
-                step(wd[d], wd2[d], t + d);
-            }
+            load(wd[(d + D - 1) % D], wd2[(d + D - 1) % D], ep[(d + D - 1) % D], min(t + d + D - 1, T - 1));
+            // keep the loads ahead of this step's arithmetic: left alone, the
+            // scheduler sinks them below it, behind a wait for every load in flight
+            __builtin_amdgcn_sched_barrier(0);
+            step(wd[d], wd2[d], ep[d], t + d);
         }
     }
 }
