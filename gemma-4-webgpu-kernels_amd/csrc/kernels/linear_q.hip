@@ -281,16 +281,21 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 constexpr int LQ_BM = 64, LQ_BK = 64;
 constexpr int LQ_XS = LQ_BK + 8;  // bf16 per staged x row (+16 bytes: rows start on different banks)
 
-// The 8 fields of row `row` at k .. k + 7 as value * F.
+// The packed bytes of the 8 fields of a row at k .. k + 7 (8, 4 or 2 bytes).
 template <int BITS>
-__device__ __forceinline__ void frag8(const uint8_t* __restrict__ rowp, uint32_t k, uint32_t xm, float (&q)[8]) {
+__device__ __forceinline__ uint2 frag8_load(const uint8_t* __restrict__ rowp, uint32_t k) {
+    if constexpr (BITS == 8) return *reinterpret_cast<const uint2*>(rowp + k);
+    if constexpr (BITS == 4) return make_uint2(*reinterpret_cast<const uint32_t*>(rowp + k / 2), 0u);
+    return make_uint2(*reinterpret_cast<const uint16_t*>(rowp + k / 4), 0u);
+}
+
+// Those 8 fields as value * F in bf16 (small integers: exact).
+template <int BITS>
+__device__ __forceinline__ bf8v frag8_bf16(uint2 w, uint32_t xm) {
+    float q[8];
     if constexpr (BITS == 4) {
-        float t[8];
-        unpack<4>(*reinterpret_cast<const uint32_t*>(rowp + k / 2) ^ xm, t);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = t[i];
+        unpack<4>(w.x ^ xm, q);
     } else if constexpr (BITS == 8) {
-        const uint2 w = *reinterpret_cast<const uint2*>(rowp + k);
         float t0[4], t1[4];
         unpack<8>(w.x ^ xm, t0);
         unpack<8>(w.y ^ xm, t1);
@@ -300,12 +305,15 @@ __device__ __forceinline__ void frag8(const uint8_t* __restrict__ rowp, uint32_t
             q[4 + i] = t1[i];
         }
     } else {
-        const uint32_t h = *reinterpret_cast<const uint16_t*>(rowp + k / 4);
         float t[16];
-        unpack<2>((h ^ xm) & 0xFFFFu, t);
+        unpack<2>((w.x ^ xm) & 0xFFFFu, t);
 #pragma unroll
         for (int i = 0; i < 8; ++i) q[i] = t[i];
     }
+    bf8v a;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = (__bf16)q[i];
+    return a;
 }
 
 template <int BITS, int AB, int MODE>
@@ -365,16 +373,18 @@ __device__ __forceinline__ void linear_q_mfma(const G4aLinearParams& p) {
         *reinterpret_cast<bf8v*>(d2) = p2[0];
         *reinterpret_cast<bf8v*>(d2 + 8) = p2[1];
     };
-    // A fragments of one step: block ab, sub-step kk covers k 32 kk + 8 g .. + 7
-    float qa[AB][2][8], qb2[AB][2][8];
+    // A fragments of one step, packed: block ab, sub-step kk covers k 32 kk + 8 g .. + 7.
+    // They are unpacked only at the start of their step, so their loads stay in
+    // flight under the previous step's MFMAs.
+    uint2 wr[AB][2], wr2[AB][2];
     auto load_w = [&](uint32_t st) {
 #pragma unroll
         for (int ab = 0; ab < AB; ++ab)
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
                 const uint32_t k = st * LQ_BK + 32 * kk + 8 * g;
-                frag8<BITS>(wrow[ab], k, p.xm, qa[ab][kk]);
-                if (MODE == 1) frag8<BITS>(wrow2[ab], k, p.xm, qb2[ab][kk]);
+                wr[ab][kk] = frag8_load<BITS>(wrow[ab], k);
+                if (MODE == 1) wr2[ab][kk] = frag8_load<BITS>(wrow2[ab], k);
             }
     };
 
@@ -395,16 +405,16 @@ __device__ __forceinline__ void linear_q_mfma(const G4aLinearParams& p) {
 #pragma unroll
         for (int ab = 0; ab < AB; ++ab)
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    a[ab][kk][i] = (__bf16)qa[ab][kk][i];
-                    if (MODE == 1) a2[ab][kk][i] = (__bf16)qb2[ab][kk][i];
-                }
+            for (int kk = 0; kk < 2; ++kk) {
+                a[ab][kk] = frag8_bf16<BITS>(wr[ab][kk], p.xm);
+                if (MODE == 1) a2[ab][kk] = frag8_bf16<BITS>(wr2[ab][kk], p.xm);
+            }
         if (st + 1 < nsteps) {
             load_x(st + 1);
             load_w(st + 1);
         }
+        // the next step's loads go out before this step's MFMAs
+        __builtin_amdgcn_sched_barrier(0);
         const int buf = st & 1;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
