@@ -674,6 +674,9 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
                 const int other = __builtin_amdgcn_readfirstlane(progress[w ^ 4]);
                 if (other > done) __builtin_amdgcn_s_setprio(1);
                 else __builtin_amdgcn_s_setprio(0);
+                // left alone, the scheduler gathers the priority changes of all
+                // chunks after the last one, where they no longer steer anything
+                __builtin_amdgcn_sched_barrier(0);
             }
             if (!cur.active) continue;
             if (c < NKS) {
