@@ -2,14 +2,18 @@
 the C-ABI, as Gemma4Model composes them (rust/src/model.rs:142-206 forward,
 :207-245 decoder_layer, :247-304 attention), against the same composition
 through the CPU oracle. Layer 0 slides (Dh 256, window 512, full RoPE, a
-512-slot ring cache); layer 1 is global (Dh 512, partial RoPE 0.25, a linear
+520-slot ring cache: a T-token chunk needs window + T - 1 rows, which the
+library checks); layer 1 is global (Dh 512, partial RoPE 0.25, a linear
 cache). Gemma-4-E2B widths (hidden 1536, 8 query heads over 1 kv head, GeGLU
 6144, per-layer inputs 256), 4-bit projections and embeddings, a 2-bit lm_head,
 random weights.
 
 As the reference's full_model_parity (rust/tests/gpu.rs:190-227): a 5-token
 prefill, then decode steps that append to the caches, the logits of each pass
-compared. Bar: the reference's own, max |d| < 5e-3 (rust/tests/gpu.rs:200).
+compared. A second run starts the caches with 516 rows of history (the same
+random K/V on both sides), so the decode steps wrap the sliding layer's ring
+and its oldest keys leave the window.
+Bar: the reference's own, max |d| < 5e-3 (rust/tests/gpu.rs:200).
 The composition reorders no sum beyond the individual ops' (each pinned
 elsewhere), so the test also holds the logits to 1e-4 relative to their
 largest magnitude and prints the achieved difference."""
@@ -22,9 +26,8 @@ import oracle
 pytestmark = pytest.mark.gpu
 
 H, HQ, HKV, I, DPLE, L, V, EPS = 1536, 8, 1, 6144, 256, 2, 300, 1e-6
-LAYERS = [dict(dh=256, window=512, theta=10000.0, rot=256, ring=512),
+LAYERS = [dict(dh=256, window=512, theta=10000.0, rot=256, ring=520),
           dict(dh=512, window=0, theta=1000000.0, rot=128, ring=0)]
-CACHE_ROWS = 16  # the global layer's linear cache
 
 
 def step(msg):
@@ -57,12 +60,12 @@ def make_weights():
 class CpuModel:
     """The composition through the oracle (host arrays)."""
 
-    def __init__(self, w):
+    def __init__(self, w, hist):
         qw = lambda t: oracle.QWeight(t[0][0], t[0][1], t[1], t[2], t[3])  # noqa: E731
         self.w = {k: (qw(v) if isinstance(v, tuple) else v) for k, v in w.items() if k != "layers"}
         self.layers = [{k: (qw(v) if isinstance(v, tuple) else v) for k, v in lw.items()} for lw in w["layers"]]
-        self.k = [np.zeros((0, HKV, lc["dh"]), np.float32) for lc in LAYERS]
-        self.v = [np.zeros((0, HKV, lc["dh"]), np.float32) for lc in LAYERS]
+        self.k = [h[0] for h in hist]
+        self.v = [h[1] for h in hist]
 
     def attention(self, i, x, pos):
         lc, lw, T = LAYERS[i], self.layers[i], x.shape[0]
@@ -99,16 +102,24 @@ class CpuModel:
 class GpuModel:
     """The same composition on the GPU: every op a C-ABI call on device buffers."""
 
-    def __init__(self, c, w):
+    def __init__(self, c, w, hist):
         self.c, self.keep = c, []
         up = lambda t: self._keep(c.upload_qweight(t[0][0], t[0][1], t[1], t[2], t[3]))  # noqa: E731
         dev = lambda a: self._keep(c.upload(a))  # noqa: E731
         self.w = {k: (up(v) if isinstance(v, tuple) else dev(v)) for k, v in w.items() if k != "layers"}
         self.layers = [{k: (up(v) if isinstance(v, tuple) else dev(v)) for k, v in lw.items()} for lw in w["layers"]]
-        self.kc = [self._keep(c.empty((lc["ring"] or CACHE_ROWS, HKV, lc["dh"]))) for lc in LAYERS]
-        self.vc = [self._keep(c.empty((lc["ring"] or CACHE_ROWS, HKV, lc["dh"]))) for lc in LAYERS]
-        self.len = 0
+        n = hist[0][0].shape[0]
+        rows = [lc["ring"] or n + 16 for lc in LAYERS]
+        self.kc = [self._keep(c.empty((r, HKV, lc["dh"]))) for r, lc in zip(rows, LAYERS)]
+        self.vc = [self._keep(c.empty((r, HKV, lc["dh"]))) for r, lc in zip(rows, LAYERS)]
         self.tmp = []
+        for i, lc in enumerate(LAYERS):  # the history rows, through the cache write (ring slots wrap)
+            if n:
+                for cache, src in ((self.kc[i], hist[i][0]), (self.vc[i], hist[i][1])):
+                    d = self.buf(*src.shape)
+                    c.h2d(d.ptr, np.ascontiguousarray(src))
+                    c.kv_write(cache.ptr, lc["ring"], HKV * lc["dh"], 0, d.ptr, n)
+        self.len = n
 
     def _keep(self, d):
         self.keep.append(d)
@@ -194,16 +205,23 @@ def _check(got, want, label):
     assert d <= 1e-4 * max(top, 1.0), f"{label}: max diff {d:e} above 1e-4 of the largest logit"
 
 
-def test_two_layer_prefill_then_incremental_decode(ctx):
+@pytest.mark.parametrize("history", [0, 516])
+def test_two_layer_prefill_then_incremental_decode(ctx, history):
     w = make_weights()
-    cpu, gpu = CpuModel(w), GpuModel(ctx, w)
+    hist = []
+    for i, lc in enumerate(LAYERS):
+        n, dh = history * HKV * lc["dh"], lc["dh"]
+        hist.append((synth.normal_f32(3000 + i, 0, n).reshape(history, HKV, dh),
+                     synth.normal_f32(3000 + i, 1, n).reshape(history, HKV, dh)))
+    cpu, gpu = CpuModel(w, hist), GpuModel(ctx, w, hist)
     try:
         ids = [2, 5, 11, 19, 30]
-        step("prefill T=5")
-        _check(gpu.forward(ids, 0), cpu.forward(ids, np.arange(5, dtype=np.uint32)), "prefill logits")
+        step(f"history {history}: prefill T=5")
+        _check(gpu.forward(ids, history), cpu.forward(ids, np.arange(history, history + 5, dtype=np.uint32)),
+               f"history {history} prefill logits")
         for n, tok in enumerate([44, 7, 299]):
-            p = 5 + n
-            step(f"decode step at position {p}")
+            p = history + 5 + n
+            step(f"history {history}: decode step at position {p}")
             _check(gpu.forward([tok], p), cpu.forward([tok], np.array([p], np.uint32)), f"decode pos {p}")
     finally:
         gpu.free()
