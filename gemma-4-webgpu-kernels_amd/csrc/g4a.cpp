@@ -92,6 +92,7 @@ struct g4a_ctx {
     int cu_count = 0;
     // per-kernel event pairs (g4a_kernel_timing)
     bool timing = false;
+    bool capturing = false;  // between g4a_capture_begin and g4a_capture_end
     std::vector<hipEvent_t> kev;  // 2 * kMaxTimed
     uint32_t kev_used = 0;
     std::string err;
@@ -135,6 +136,9 @@ int get_fn(g4a_ctx* ctx, hipFunction_t* f, const char* name) {
 
 int ensure_workspace(g4a_ctx* ctx, size_t bytes) {
     if (bytes <= ctx->workspace_bytes) return G4A_OK;
+    if (ctx->capturing)
+        return fail(ctx, G4A_E_ARG, "the workspace must grow to %zu bytes, which a graph capture cannot do: "
+                    "run the calls once before capturing them", bytes);
     if (ctx->workspace) {
         // the old buffer may still be read by queued kernels
         HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
@@ -184,6 +188,9 @@ int upload_positions(g4a_ctx* ctx, const uint32_t* a, size_t na, const uint32_t*
                      const uint32_t** db) {
     const size_t n = na + nb;
     if (n == 0) return G4A_OK;
+    if (ctx->capturing)
+        return fail(ctx, G4A_E_ARG, "explicit positions or ids are staged from host memory, which a graph capture "
+                    "cannot hold: capture calls with contiguous positions (q_pos0 / k_pos0)");
     if (n > ctx->pos_dev_cap) {
         if (ctx->pos_dev) {
             HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
@@ -519,8 +526,15 @@ int g4a_free(g4a_ctx* ctx, void* dptr) {
     return G4A_OK;
 }
 
+namespace {
+int refuse_in_capture(g4a_ctx* ctx, const char* what) {
+    return ctx->capturing ? fail(ctx, G4A_E_ARG, "%s cannot be captured in a graph", what) : G4A_OK;
+}
+}  // namespace
+
 int g4a_h2d(g4a_ctx* ctx, void* dst, const void* src, size_t bytes) {
     if (!ctx || (bytes && (!dst || !src))) return fail(ctx, G4A_E_ARG, "null pointer");
+    if (int rc = refuse_in_capture(ctx, "g4a_h2d (a host copy)")) return rc;
     if (bytes) HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
     // the caller may reuse `src` on return: make the copy complete
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
@@ -529,6 +543,7 @@ int g4a_h2d(g4a_ctx* ctx, void* dst, const void* src, size_t bytes) {
 
 int g4a_d2h(g4a_ctx* ctx, void* dst, const void* src, size_t bytes) {
     if (!ctx || (bytes && (!dst || !src))) return fail(ctx, G4A_E_ARG, "null pointer");
+    if (int rc = refuse_in_capture(ctx, "g4a_d2h (a host copy)")) return rc;
     if (bytes) HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     return G4A_OK;
@@ -542,12 +557,14 @@ int g4a_d2d(g4a_ctx* ctx, void* dst, const void* src, size_t bytes) {
 
 int g4a_zero(g4a_ctx* ctx, void* dst, size_t bytes) {
     if (!ctx || (bytes && !dst)) return fail(ctx, G4A_E_ARG, "null pointer");
+    if (int rc = refuse_in_capture(ctx, "g4a_zero (a memset)")) return rc;
     if (bytes) HIP_TRY(ctx, hipMemsetAsync(dst, 0, bytes, ctx->stream));
     return G4A_OK;
 }
 
 int g4a_sync(g4a_ctx* ctx) {
     if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (int rc = refuse_in_capture(ctx, "g4a_sync")) return rc;
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     return G4A_OK;
 }
@@ -571,8 +588,12 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
     if (a->T == 0) return G4A_OK;
     const size_t out_bytes = size_t(a->T) * a->Hq * a->Dv * sizeof(float);
     if (pl.kernel == G4A_KERNEL_NONE) {
-        HIP_TRY(ctx, hipMemsetAsync(a->out, 0, out_bytes, ctx->stream));
-        return G4A_OK;
+        // no visible key: zero rows, written by a kernel (a memset node in a
+        // captured graph is not replayed reliably)
+        const size_t n = out_bytes / sizeof(float);
+        G4aEwParams p{a->out, nullptr, nullptr, a->out, n, 0.0f, uint32_t(G4A_EW_FILL)};
+        const uint32_t blocks = uint32_t(std::min<size_t>((n + 255) / 256, 4096));
+        return launch(ctx, ctx->ew, dim3(blocks, 1, 1), dim3(256, 1, 1), p, "zero rows");
     }
     const uint32_t group = a->Hq / a->Hkv;
     if (pl.kernel == G4A_KERNEL_GENERIC) {
@@ -889,6 +910,9 @@ int freq_table(g4a_ctx* ctx, float theta, uint32_t rot, const float** out) {
             *out = ft.dev;
             return G4A_OK;
         }
+    if (ctx->capturing)
+        return fail(ctx, G4A_E_ARG, "a RoPE table (theta %g, rotary_dim %u) is built on first use, which a graph "
+                    "capture cannot do: run the call once before capturing it", theta, rot);
     g4a_ctx::FreqTable ft{theta, rot, std::vector<float>(std::max<uint32_t>(rot / 2, 1)), nullptr};
     for (uint32_t j = 0; j < rot / 2; ++j) ft.host[j] = powf(theta, -(2.0f * (float)j) / (float)rot);
     if (hipMalloc(reinterpret_cast<void**>(&ft.dev), ft.host.size() * sizeof(float)) != hipSuccess)
@@ -1297,14 +1321,62 @@ int g4a_attn_producer(g4a_ctx* ctx, const g4a_producer_args* a) {
                             a->cache_row, a->kv_ring_cap);
 }
 
+struct g4a_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+int g4a_capture_begin(g4a_ctx* ctx) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (ctx->capturing) return fail(ctx, G4A_E_ARG, "a capture is already open on this context");
+    if (ctx->timing) return fail(ctx, G4A_E_ARG, "per-kernel timing is on: turn it off before capturing");
+    HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    return G4A_OK;
+}
+
+int g4a_capture_end(g4a_ctx* ctx, g4a_graph** graph) {
+    if (!ctx || !graph) return fail(ctx, G4A_E_ARG, "null ctx/graph");
+    *graph = nullptr;
+    if (!ctx->capturing) return fail(ctx, G4A_E_ARG, "no capture is open on this context");
+    ctx->capturing = false;
+    hipGraph_t g = nullptr;
+    HIP_TRY(ctx, hipStreamEndCapture(ctx->stream, &g));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        hipGraphDestroy(g);
+        return fail(ctx, G4A_E_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    }
+    *graph = new g4a_graph{g, exec};
+    return G4A_OK;
+}
+
+int g4a_graph_launch(g4a_ctx* ctx, g4a_graph* graph) {
+    if (!ctx || !graph) return fail(ctx, G4A_E_ARG, "null ctx/graph");
+    if (int rc = refuse_in_capture(ctx, "g4a_graph_launch")) return rc;
+    HIP_TRY(ctx, hipGraphLaunch(graph->exec, ctx->stream));
+    return G4A_OK;
+}
+
+int g4a_graph_destroy(g4a_graph* graph) {
+    if (!graph) return G4A_OK;
+    if (graph->exec) hipGraphExecDestroy(graph->exec);
+    if (graph->graph) hipGraphDestroy(graph->graph);
+    delete graph;
+    return G4A_OK;
+}
+
 int g4a_timer_start(g4a_ctx* ctx) {
     if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (int rc = refuse_in_capture(ctx, "g4a_timer_start")) return rc;
     HIP_TRY(ctx, hipEventRecord(ctx->ev_start, ctx->stream));
     return G4A_OK;
 }
 
 int g4a_timer_stop(g4a_ctx* ctx, float* ms) {
     if (!ctx || !ms) return fail(ctx, G4A_E_ARG, "null ctx/ms");
+    if (int rc = refuse_in_capture(ctx, "g4a_timer_stop")) return rc;
     HIP_TRY(ctx, hipEventRecord(ctx->ev_stop, ctx->stream));
     HIP_TRY(ctx, hipEventSynchronize(ctx->ev_stop));
     HIP_TRY(ctx, hipEventElapsedTime(ms, ctx->ev_start, ctx->ev_stop));
@@ -1313,6 +1385,7 @@ int g4a_timer_stop(g4a_ctx* ctx, float* ms) {
 
 int g4a_kernel_timing(g4a_ctx* ctx, int enable) {
     if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (int rc = refuse_in_capture(ctx, "g4a_kernel_timing")) return rc;
     if (enable && ctx->kev.empty()) {
         ctx->kev.resize(2 * kMaxTimed, nullptr);
         for (auto& ev : ctx->kev) HIP_TRY(ctx, hipEventCreate(&ev));

@@ -25,7 +25,7 @@ __device__ __forceinline__ void ew(const G4aEwParams& p) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     const float s = p.op == G4A_EW_SCALE_BY ? p.sp[0] : p.s;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < p.n; i += stride) {
-        const float v = p.a[i];
+        const float v = p.op == G4A_EW_FILL ? 0.0f : p.a[i];
         float o;
         switch (p.op) {
             case G4A_EW_ADD: o = v + p.b[i]; break;
@@ -34,6 +34,7 @@ __device__ __forceinline__ void ew(const G4aEwParams& p) {
             case G4A_EW_SCALE_BY: o = v * s; break;
             case G4A_EW_GELU: o = g4a_gelu_tanh(v); break;
             case G4A_EW_GEGLU: o = g4a_gelu_tanh(v) * p.b[i]; break;
+            case G4A_EW_FILL: o = s; break;
             default: o = s * tanhf(v / s); break;  // softcap: cap * tanh(v / cap)
         }
         p.y[i] = o;

@@ -203,6 +203,7 @@ enum G4aEwOp : uint32_t {
     G4A_EW_GELU = 4,
     G4A_EW_GEGLU = 5,     // gelu(a) * b
     G4A_EW_SOFTCAP = 6,   // s * tanh(a / s)
+    G4A_EW_FILL = 7,      // s (a is not read): the clear that graph capture can hold
 };
 
 struct G4aEwParams {

@@ -131,6 +131,10 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "g4a_linear_q_gelu_mul_cols": (c_int, [ctxp, ctypes.POINTER(QWeightArgs), vp, vp, ctypes.c_uint32,
                                                ctypes.c_uint32, vp, ctypes.c_uint32]),
         "g4a_embed_rows_q": (c_int, [ctxp, ctypes.POINTER(QWeightArgs), _u32p, ctypes.c_uint32, ctypes.c_float, vp]),
+        "g4a_capture_begin": (c_int, [ctxp]),
+        "g4a_capture_end": (c_int, [ctxp, ctypes.POINTER(ctypes.c_void_p)]),
+        "g4a_graph_launch": (c_int, [ctxp, ctypes.c_void_p]),
+        "g4a_graph_destroy": (c_int, [ctypes.c_void_p]),
         "g4a_timer_start": (c_int, [ctxp]),
         "g4a_timer_stop": (c_int, [ctxp, ctypes.POINTER(ctypes.c_float)]),
         "g4a_get_device_info": (c_int, [ctxp, ctypes.POINTER(DeviceInfo)]),
@@ -212,6 +216,21 @@ class DeviceQWeight:
     def free(self) -> None:
         self.qbytes.free()
         self.scales.free()
+
+
+class Graph:
+    """A captured sequence of a context's launches (g4a_capture_end); replay with launch()."""
+
+    def __init__(self, ctx: "Context", handle: int):
+        self.ctx, self.handle = ctx, handle
+
+    def launch(self) -> None:
+        self.ctx._check(self.ctx.lib.g4a_graph_launch(self.ctx.handle, self.handle))
+
+    def free(self) -> None:
+        if self.handle:
+            self.ctx.lib.g4a_graph_destroy(self.handle)
+            self.handle = None
 
 
 class Context:
@@ -379,6 +398,17 @@ class Context:
         arr, ptr = _u32_array(ids)
         n = 0 if arr is None else arr.size
         self._check(self.lib.g4a_embed_rows_q(self.handle, ctypes.byref(table.args), ptr, n, scale, out))
+
+    # ---- graph capture (launch-bound sequences) ----
+    def capture_begin(self) -> None:
+        """Record the launches of the following calls into a graph instead of running them."""
+        self._check(self.lib.g4a_capture_begin(self.handle))
+
+    def capture_end(self) -> "Graph":
+        """Close the capture; returns the replayable graph (raises if a captured call failed)."""
+        g = ctypes.c_void_p()
+        self._check(self.lib.g4a_capture_end(self.handle, ctypes.byref(g)))
+        return Graph(self, g.value)
 
     def timer_start(self) -> None:
         self._check(self.lib.g4a_timer_start(self.handle))

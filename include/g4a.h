@@ -308,6 +308,29 @@ int g4a_linear_q_gelu_mul_cols(g4a_ctx *ctx, const g4a_qweight *w, const float *
 int g4a_embed_rows_q(g4a_ctx *ctx, const g4a_qweight *table, const uint32_t *ids, uint32_t T, float scale,
                      float *out);
 
+/* ---- graph capture ------------------------------------------------------- */
+/* No counterpart in the reference (its wgpu backend records a command buffer
+ * per pass and submits it on flush, rust/src/backend_wgpu.rs:11-15, :357-366).
+ * For launch-bound callers
+ * (a decode step's 35 attention calls, each of a few microseconds): every
+ * launch the context enqueues between g4a_capture_begin and g4a_capture_end
+ * is recorded into a HIP graph instead of running; g4a_graph_launch replays
+ * it on the context's stream with the same pointers and arguments.
+ * Capturable: attention with contiguous positions (q_pos0 / k_pos0), the
+ * producer and norm/RoPE calls with contiguous positions, kv_write, every
+ * projection, elementwise and norm op. A call that needs host staging
+ * (explicit position arrays, embedding ids), a larger workspace or a new RoPE
+ * table, and g4a_h2d / g4a_d2h / g4a_zero / g4a_sync / the timers, fail with
+ * G4A_E_ARG while a capture is open: run such calls once before capturing.
+ * After any failure inside a capture, still call g4a_capture_end, which then
+ * reports the error and returns no graph. Rows without visible keys are
+ * cleared by a fill kernel, not a memset, so a replay clears them too. */
+typedef struct g4a_graph g4a_graph;
+int g4a_capture_begin(g4a_ctx *ctx);
+int g4a_capture_end(g4a_ctx *ctx, g4a_graph **graph);
+int g4a_graph_launch(g4a_ctx *ctx, g4a_graph *graph);
+int g4a_graph_destroy(g4a_graph *graph);
+
 /* ---- timing (HIP events on the context's stream) ----------------------- */
 int g4a_timer_start(g4a_ctx *ctx);
 /* Records the stop event, waits for it and returns the elapsed milliseconds. */

@@ -1,0 +1,121 @@
+"""Graph capture (g4a_capture_begin / g4a_capture_end / g4a_graph_launch): a
+captured sequence of attention calls replays bit-identically to the same calls
+run eagerly. Each replay runs after the output buffers are overwritten and
+after unrelated eager work and a synchronisation, and every replay is checked.
+Calls that need host staging are refused while a capture is open, and the
+context stays usable after such a refusal."""
+import numpy as np
+import pytest
+
+import g4a
+import g4a.synth as synth
+
+pytestmark = pytest.mark.gpu
+
+
+def step(msg):
+    print(f"[gpu] {msg}", flush=True)
+
+
+def _calls(ctx, keep):
+    """(attention() keyword sets, output buffers): sliding decode on a ring, a
+    multi-split global decode (partials + combine), multi-query decode, a
+    prefill, and a call whose keys all lie in the future (its rows are zero)."""
+    specs = [dict(T=1, S=5000, Dh=256, window=512, ring_cap=512, q_pos0=4999, seed=1),
+             dict(T=1, S=32768, Dh=512, seed=2, q_pos0=32767),
+             dict(T=5, S=777, Dh=256, window=512, seed=3, q_pos0=772),
+             dict(T=64, S=64, Dh=256, window=512, seed=4, q_pos0=0),
+             dict(T=2, S=100, Dh=512, seed=5, q_pos0=0, k_pos0=50)]
+    calls, outs = [], []
+    for sp in specs:
+        T, S, Dh = sp["T"], sp["S"], sp["Dh"]
+        rows = sp.get("ring_cap") or S
+        ins = synth.gemma_inputs(T=T, S=rows, Dh=Dh, seed=sp["seed"])
+        q, k, v = (keep(ctx.upload(x)) for x in (ins.q, ins.k, ins.v))
+        out = keep(ctx.empty((T, 8 * Dh)))
+        calls.append(dict(q=q.ptr, k=k.ptr, v=v.ptr, out=out.ptr, T=T, S=S, Hq=8, Hkv=1, Dh=Dh, Dv=Dh,
+                          q_pos0=sp["q_pos0"], k_pos0=sp.get("k_pos0", 0), window=sp.get("window", 0),
+                          ring_cap=sp.get("ring_cap", 0)))
+        outs.append(out)
+    return calls, outs
+
+
+def test_captured_sequence_replays_bit_exactly(ctx):
+    bufs = []
+    keep = lambda d: bufs.append(d) or d  # noqa: E731
+    try:
+        calls, outs = _calls(ctx, keep)
+        step("eager run")
+        ctx.attention_batch(calls)
+        want = [o.to_host() for o in outs]
+        assert not np.any(want[4]), "rows with only future keys are zero"
+        step("capture")
+        ctx.capture_begin()
+        try:
+            ctx.attention_batch(calls)
+            graph = ctx.capture_end()
+        except Exception:
+            _end_open_capture(ctx)
+            raise
+        # the capture ran nothing: the outputs still hold the eager results
+        for o, w in zip(outs, want):
+            assert np.array_equal(o.to_host(), w)
+        other = _calls(ctx, keep)[0][1]  # unrelated eager work between replays
+        rng = np.random.default_rng(0)
+        try:
+            for rep in range(4):
+                step(f"replay {rep}")
+                for o in outs:  # overwrite every output (the zero rows included)
+                    ctx.h2d(o.ptr, rng.standard_normal(o.shape).astype(np.float32))
+                ctx.attention(**other)
+                ctx.sync()
+                graph.launch()
+                ctx.sync()
+                for i, (o, w) in enumerate(zip(outs, want)):
+                    assert np.array_equal(o.to_host(), w), f"replay {rep}, call {i}"
+        finally:
+            graph.free()
+    finally:
+        for d in bufs:
+            d.free()
+
+
+def _end_open_capture(ctx):
+    """Close a capture a failed assertion left open (the context is shared by the session)."""
+    try:
+        ctx.capture_end().free()
+    except g4a.G4aError:
+        pass
+
+
+def test_capture_refuses_host_staging_and_recovers(ctx):
+    ins = synth.gemma_inputs(T=1, S=300, Dh=256, seed=9)
+    k_pos = np.arange(300, dtype=np.uint32)
+    k_pos[150:] += 7  # a gap: the positions must be staged to the device
+    q_pos = np.array([320], np.uint32)
+    q, k, v = (ctx.upload(x) for x in (ins.q, ins.k, ins.v))
+    out = ctx.empty((1, 8 * 256))
+    kw = dict(T=1, S=300, Hq=8, Hkv=1, Dh=256, Dv=256, q_pos=q_pos, k_pos=k_pos)
+    try:
+        ctx.capture_begin()
+        try:
+            with pytest.raises(g4a.G4aError, match="cannot hold"):
+                ctx.attention(q.ptr, k.ptr, v.ptr, out.ptr, **kw)
+            with pytest.raises(g4a.G4aError, match="cannot be captured"):
+                ctx.sync()
+            with pytest.raises(g4a.G4aError, match="already open"):
+                ctx.capture_begin()
+            ctx.capture_end().free()  # nothing was recorded
+        finally:
+            _end_open_capture(ctx)
+        with pytest.raises(g4a.G4aError, match="no capture is open"):
+            ctx.capture_end()
+        # the context works as before: the refused call runs eagerly, twice alike
+        ctx.attention(q.ptr, k.ptr, v.ptr, out.ptr, **kw)
+        a = out.to_host()
+        assert np.all(np.isfinite(a)) and np.any(a)
+        ctx.attention(q.ptr, k.ptr, v.ptr, out.ptr, **kw)
+        assert np.array_equal(out.to_host(), a)
+    finally:
+        for d in (q, k, v, out):
+            d.free()
