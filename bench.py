@@ -138,40 +138,19 @@ def schedule_35_layers(ctx, steps, warmup):
     """one token of the 35-layer Gemma-4-E2B attention schedule at 32768 context.
     Layers 4,9,...,34 are global (hd512, full context); the rest local (hd256, 512-slot ring).
     Layers 15..34 reuse the KV of layer 14 (global) or 13 (local) (rust/src/config.rs:152-159),
-    so 3 global caches and 12 local rings exist."""
+    so 3 global caches and 12 local rings exist (synth.schedule_token, which the parity test
+    tests/test_schedule_gpu.py checks against the oracle)."""
     S, seed = 32768, 4
-    layer_types = ["full" if (i % 5 == 4) else "sliding" for i in range(35)]
-    first_shared = 35 - 20
-    src = []
-    for i in range(35):
-        if i < first_shared:
-            src.append(i)
-        else:
-            src.append(max(j for j in range(first_shared) if layer_types[j] == layer_types[i]))
-    caches = {}
-    for li in sorted(set(src)):
-        if layer_types[li] == "full":
-            k = synth.rms_norm_rows(synth.normal_f32(seed * 100 + li, 1, S * 512).reshape(S, 1, 512))
-            v = synth.normal_f32(seed * 100 + li, 2, S * 512).reshape(S, 1, 512)
-        else:  # ring of 512 slots holding positions S-512..S-1 at slot p % 512
-            k = synth.rms_norm_rows(synth.normal_f32(seed * 100 + li, 1, 512 * 256).reshape(512, 1, 256))
-            v = synth.normal_f32(seed * 100 + li, 2, 512 * 256).reshape(512, 1, 256)
-        caches[li] = (ctx.upload(k), ctx.upload(v))
-    qs, outs = [], []
-    for i in range(35):
-        dh = 512 if layer_types[i] == "full" else 256
-        qs.append(ctx.upload(synth.rms_norm_rows(synth.normal_f32(seed * 100 + i, 0, HQ * dh).reshape(1, HQ, dh))))
-        outs.append(ctx.empty((1, HQ * dh)))
-
+    layers, host_caches = synth.schedule_token(S, seed)
+    caches = {li: (ctx.upload(c.k), ctx.upload(c.v)) for li, c in host_caches.items()}
+    qs = [ctx.upload(L.q) for L in layers]
+    outs = [ctx.empty((1, HQ * L.Dh)) for L in layers]
     token = []
-    for i in range(35):
-        k, v = caches[src[i]]
-        if layer_types[i] == "full":
-            token.append(dict(q=qs[i].ptr, k=k.ptr, v=v.ptr, out=outs[i].ptr, T=1, S=S, Hq=HQ, Hkv=1, Dh=512, Dv=512,
-                              q_pos0=S - 1, k_pos0=0))
-        else:
-            token.append(dict(q=qs[i].ptr, k=k.ptr, v=v.ptr, out=outs[i].ptr, T=1, S=S, Hq=HQ, Hkv=1, Dh=256, Dv=256,
-                              q_pos0=S - 1, k_pos0=0, window=512, ring_cap=512))
+    for L, q, out in zip(layers, qs, outs):
+        k, v = caches[L.src]
+        token.append(dict(q=q.ptr, k=k.ptr, v=v.ptr, out=out.ptr, T=1, S=S, Hq=HQ, Hkv=1, Dh=L.Dh, Dv=L.Dh,
+                          q_pos0=S - 1, k_pos0=0, window=0 if L.is_global else synth.E2B_WINDOW,
+                          ring_cap=host_caches[L.src].ring_cap))
 
     ms, _ = time_steps(ctx, [token], steps, warmup)
     algo = 7 * decode_bytes(S, 512) + 28 * decode_bytes(512, 256)
@@ -182,8 +161,13 @@ def schedule_35_layers(ctx, steps, warmup):
         ctx.capture_begin()
         try:
             ctx.attention_batch(token)
-        finally:
-            graph = ctx.capture_end()
+        except g4a.G4aError:
+            try:  # close the capture; it reports the same failure and makes no graph
+                ctx.capture_end().free()
+            except g4a.G4aError:
+                pass
+            raise
+        graph = ctx.capture_end()
         for _ in range(max(warmup, 1)):
             graph.launch()
         ctx.sync()

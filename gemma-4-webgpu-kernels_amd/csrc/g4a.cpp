@@ -15,6 +15,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -37,7 +39,30 @@ constexpr uint32_t BATCH_MAX_KEYS = SHORT_KEYS * MAX_SPLITS;
 
 std::string g_create_error;
 
+// Bytes of the static scratch array a call that allocates nothing may use.
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(64) << 20;
+
+// Tags each K/V pre-split's V range flag (G4aSplitParams::epoch). Process-wide,
+// so no two pre-splits of any context share a tag.
+std::atomic<uint32_t> g_split_epoch{0};
+
+uint32_t next_split_epoch() {
+    uint32_t e = g_split_epoch.fetch_add(1, std::memory_order_relaxed) + 1;
+    while (e == 0) e = g_split_epoch.fetch_add(1, std::memory_order_relaxed) + 1;
+    return e;
+}
+
 }  // namespace
+
+// The graphs captured on a context, shared by the context and each of its
+// graphs. A graph replays with the workspace it was captured with, so while
+// any graph is live a workspace the context outgrows is kept (retired), not
+// freed, until the last graph is destroyed.
+struct g4a_graph_book {
+    g4a_ctx* ctx = nullptr;      // null once the context is destroyed
+    uint32_t live = 0;           // graphs not yet destroyed
+    std::vector<void*> retired;  // workspaces replaced while graphs were live
+};
 
 struct g4a_ctx {
     int device = 0;
@@ -78,11 +103,11 @@ struct g4a_ctx {
         float* dev;
     };
     std::vector<FreqTable> freq_tables;
-    uint32_t split_epoch = 0;          // tags each pre-split's V range flag
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     hipEvent_t ev_staging = nullptr;  // last use of the pinned staging buffer
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
+    void* scratch = nullptr;  // this device's static scratch array (the allocation-free entry point)
     hipFunction_t prefill_merge = nullptr;  // merge of the split hd512 prefill blocks
     float* dummy = nullptr;  // 4 KiB of zeros: the load target of idle decode tiles
     uint32_t* pos_dev = nullptr;  // device copies of non-contiguous positions
@@ -93,6 +118,9 @@ struct g4a_ctx {
     // per-kernel event pairs (g4a_kernel_timing)
     bool timing = false;
     bool capturing = false;  // between g4a_capture_begin and g4a_capture_end
+    int capture_code = 0;    // the first failure inside the open capture (sticky until g4a_capture_end)
+    std::string capture_msg;
+    std::shared_ptr<g4a_graph_book> book;
     std::vector<hipEvent_t> kev;  // 2 * kMaxTimed
     uint32_t kev_used = 0;
     std::string err;
@@ -106,8 +134,17 @@ int fail(g4a_ctx* ctx, int code, const char* fmt, ...) {
     va_start(ap, fmt);
     vsnprintf(buf, sizeof buf, fmt, ap);
     va_end(ap);
-    if (ctx) ctx->err = buf;
-    else g_create_error = buf;
+    if (ctx) {
+        ctx->err = buf;
+        // a refused call inside a capture leaves a graph without it: remembered, so
+        // g4a_capture_end reports it instead of returning that graph
+        if (ctx->capturing && ctx->capture_code == 0) {
+            ctx->capture_code = code;
+            ctx->capture_msg = buf;
+        }
+    } else {
+        g_create_error = buf;
+    }
     return code;
 }
 
@@ -140,11 +177,21 @@ int ensure_workspace(g4a_ctx* ctx, size_t bytes) {
         return fail(ctx, G4A_E_ARG, "the workspace must grow to %zu bytes, which a graph capture cannot do: "
                     "run the calls once before capturing them", bytes);
     if (ctx->workspace) {
-        // the old buffer may still be read by queued kernels
-        HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-        HIP_TRY(ctx, hipFree(ctx->workspace));
+        if (ctx->book->live) {
+            // live graphs replay with this buffer: keep it until the last one is destroyed
+            ctx->book->retired.push_back(ctx->workspace);
+        } else {
+            // the old buffer may still be read by queued kernels
+            HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+            HIP_TRY(ctx, hipFree(ctx->workspace));
+        }
         ctx->workspace = nullptr;
         ctx->workspace_bytes = 0;
+    }
+    if (!ctx->book->live && !ctx->book->retired.empty()) {
+        HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        for (void* p : ctx->book->retired) HIP_TRY(ctx, hipFree(p));
+        ctx->book->retired.clear();
     }
     size_t want = std::max<size_t>(bytes, size_t(8) << 20);
     hipError_t e = hipMalloc(&ctx->workspace, want);
@@ -169,16 +216,15 @@ uint32_t prefill_split_blocks(const g4a_attn_args* a, uint32_t q_pos0, uint32_t 
         const int64_t lo = (int64_t)q_pos0 + i - (int64_t)k_pos0 - (int64_t)a->sliding_window + 1;
         return lo <= 0 ? 0 : std::min<int64_t>(lo, a->S);
     };
-    std::vector<int64_t> nt(NB);
-    int64_t total = 0;
-    for (uint32_t b = 0; b < NB; ++b) {
+    auto tiles = [&](uint32_t b) -> int64_t {  // 16-key tiles of query block b
         const int64_t lo = key_lo(8 * int64_t(b)), hi = key_hi(std::min<int64_t>(8 * int64_t(b) + 7, a->T - 1));
         const int64_t base = lo & ~int64_t(15);
-        nt[b] = hi > lo ? (hi - base + 15) / 16 : 0;
-        total += nt[b];
-    }
+        return hi > lo ? (hi - base + 15) / 16 : 0;
+    };
+    int64_t total = 0;
+    for (uint32_t b = 0; b < NB; ++b) total += tiles(b);
     uint32_t nbig = 0;
-    while (nbig < NB && nt[NB - 1 - nbig] * int64_t(NB) > total) ++nbig;
+    while (nbig < NB && tiles(NB - 1 - nbig) * int64_t(NB) > total) ++nbig;
     return nbig;
 }
 
@@ -387,6 +433,8 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (device < 0 || device >= n) return fail(nullptr, G4A_E_ARG, "device %d out of range [0, %d)", device, n);
     g4a_ctx* ctx = new g4a_ctx();
     ctx->device = device;
+    ctx->book = std::make_shared<g4a_graph_book>();
+    ctx->book->ctx = ctx;
     auto bail = [&](int code) {
         g_create_error = ctx->err;
         g4a_destroy(ctx);
@@ -499,6 +547,13 @@ void g4a_destroy(g4a_ctx* ctx) {
     if (ctx->stream) hipStreamSynchronize(ctx->stream);
     for (hipEvent_t ev : ctx->kev) hipEventDestroy(ev);
     if (ctx->workspace) hipFree(ctx->workspace);
+    if (ctx->book) {
+        // graphs that outlive the context can no longer be launched (g4a_graph_launch
+        // takes the context); they only need destroying
+        for (void* p : ctx->book->retired) hipFree(p);
+        ctx->book->retired.clear();
+        ctx->book->ctx = nullptr;
+    }
     if (ctx->dummy) hipFree(ctx->dummy);
     if (ctx->pos_dev) hipFree(ctx->pos_dev);
     for (auto& ft : ctx->freq_tables) hipFree(ft.dev);
@@ -581,9 +636,39 @@ int g4a_attention_plan(g4a_ctx* ctx, const g4a_attn_args* a, g4a_attn_plan* plan
 
 namespace {
 
+// Device memory for a call's split partials or pre-split K/V: the context's
+// workspace, grown on demand, or with `noalloc` the library's static scratch
+// array (g4a_attention_noalloc), which never grows.
+int call_workspace(g4a_ctx* ctx, size_t bytes, bool noalloc, void** ws) {
+    if (noalloc) {
+        if (bytes > NOALLOC_SCRATCH_BYTES || !ctx->scratch)
+            return fail(ctx, G4A_E_UNSUPPORTED, "the call needs %zu bytes of scratch; the static array holds %zu",
+                        bytes, ctx->scratch ? NOALLOC_SCRATCH_BYTES : size_t(0));
+        *ws = ctx->scratch;
+        return G4A_OK;
+    }
+    if (int rc = ensure_workspace(ctx, bytes)) return rc;
+    *ws = ctx->workspace;
+    return G4A_OK;
+}
+
+// Explicit positions that are not contiguous go to the device through buffers
+// the library allocates, which g4a_attention_noalloc never does.
+int stage_positions(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool noalloc, const uint32_t** qd,
+                    const uint32_t** kd) {
+    *qd = *kd = nullptr;
+    if (an.q_contig && an.k_contig) return G4A_OK;
+    if (noalloc)
+        return fail(ctx, G4A_E_UNSUPPORTED, "explicit non-contiguous positions are staged through buffers the "
+                    "library allocates; g4a_attention_noalloc takes contiguous positions only");
+    return upload_positions(ctx, an.q_contig ? nullptr : a->q_pos, an.q_contig ? 0 : a->T,
+                            an.k_contig ? nullptr : a->k_pos, an.k_contig ? 0 : a->S, qd, kd);
+}
+
 // Enqueues an analysed attention call. With combine == false a multi-split
-// decode leaves its partials in the workspace (the caller merges them).
-int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool combine) {
+// decode leaves its partials in the workspace (the caller merges them). With
+// noalloc the call allocates nothing: its scratch is the static array.
+int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool combine, bool noalloc = false) {
     const g4a_attn_plan& pl = an.plan;
     if (a->T == 0) return G4A_OK;
     const size_t out_bytes = size_t(a->T) * a->Hq * a->Dv * sizeof(float);
@@ -596,24 +681,15 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
         return launch(ctx, ctx->ew, dim3(blocks, 1, 1), dim3(256, 1, 1), p, "zero rows");
     }
     const uint32_t group = a->Hq / a->Hkv;
+    const uint32_t q_pos0 = a->q_pos ? a->q_pos[0] : a->q_pos0;
+    const uint32_t k_pos0 = a->k_pos ? (a->S ? a->k_pos[0] : 0) : a->k_pos0;
     if (pl.kernel == G4A_KERNEL_GENERIC) {
+        // contiguous positions travel as q_pos0 / k_pos0; only the others are staged
         const uint32_t *qd = nullptr, *kd = nullptr;
-        std::vector<uint32_t> qtmp, ktmp;
-        const uint32_t* qh = a->q_pos;
-        const uint32_t* kh = a->k_pos;
-        if (!qh) {
-            qtmp.resize(a->T);
-            for (uint32_t i = 0; i < a->T; ++i) qtmp[i] = a->q_pos0 + i;
-            qh = qtmp.data();
-        }
-        if (!kh) {
-            ktmp.resize(a->S);
-            for (uint32_t j = 0; j < a->S; ++j) ktmp[j] = a->k_pos0 + j;
-            kh = ktmp.data();
-        }
-        if (int rc = upload_positions(ctx, qh, a->T, kh, a->S, &qd, &kd)) return rc;
-        G4aGenericParams gp{a->q, a->k, a->v, a->out, qd, kd, a->T, a->S, a->Hq, a->Hkv, a->Dh, a->Dv,
-                            pl.k_start, pl.k_end, a->kv_ring_cap, a->sliding_window, a->scale, a->attn_softcap};
+        if (int rc = stage_positions(ctx, a, an, noalloc, &qd, &kd)) return rc;
+        G4aGenericParams gp{a->q, a->k, a->v, a->out, qd, kd, q_pos0, k_pos0, a->T, a->S, a->Hq, a->Hkv, a->Dh,
+                            a->Dv, pl.k_start, pl.k_end, a->kv_ring_cap, a->sliding_window, a->scale,
+                            a->attn_softcap};
         return launch(ctx, ctx->generic, dim3(a->Hq, a->T, 1), dim3(64, 1, 1), gp, "generic attention", true);
     }
     if (pl.kernel == G4A_KERNEL_PREFILL) {
@@ -626,11 +702,14 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
         pp.S = a->S;
         pp.Hq = a->Hq;
         pp.Hkv = a->Hkv;
-        pp.q_pos0 = a->q_pos ? a->q_pos[0] : a->q_pos0;
-        pp.k_pos0 = a->k_pos ? (a->S ? a->k_pos[0] : 0) : a->k_pos0;
+        pp.q_pos0 = q_pos0;
+        pp.k_pos0 = k_pos0;
         pp.ring_cap = a->kv_ring_cap;
         pp.window = a->sliding_window;
         pp.scale = a->scale;
+        // rescoring band: the keys left with their estimated score carry a weight share of at
+        // most N e^-tau / (1 + N e^-tau) for N keys per row, kept below e^-4.5
+        pp.tau = std::max(12.0f, logf(float(std::max(pl.k_end - pl.k_start, 1u))) + 4.5f);
         // 8-wave workgroups over 8 queries; scores estimated from bf16 hi/lo splits of K,
         // P.V from fp16 hi/lo splits of V, both made by a pre-pass into the workspace.
         // head_dim 256: two waves per 16-row block take the even / odd key tiles;
@@ -646,9 +725,9 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
             // a split block's partial: 8 waves x (O of 16 rows x 256 dims, then l and m of the rows)
             const size_t part_bytes = size_t(pp.nbig) * a->Hkv * 2 * 8 * (4 * 16 * 64 + 32) * sizeof(float);
             const size_t part_off = (256 + 2 * half + 255) & ~size_t(255);
-            if (int rc = ensure_workspace(ctx, part_off + part_bytes)) return rc;
-            char* const ws = static_cast<char*>(ctx->workspace);
-            if (++ctx->split_epoch == 0) ctx->split_epoch = 1;
+            void* wsp = nullptr;
+            if (int rc = call_workspace(ctx, part_off + part_bytes, noalloc, &wsp)) return rc;
+            char* const ws = static_cast<char*>(wsp);
             G4aSplitParams sp{};
             sp.k = a->k;
             sp.v = a->v;
@@ -661,7 +740,9 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
             sp.Hkv = a->Hkv;
             sp.Dh = a->Dh;
             sp.ring_cap = a->kv_ring_cap;
-            sp.epoch = ctx->split_epoch;
+            sp.epoch = next_split_epoch();
+            sp.vis_lo = pl.k_start;
+            sp.vis_hi = pl.k_end;
             const uint64_t threads = uint64_t(nkeys) * a->Hkv * (a->Dh / 8) + uint64_t(nkeys / 4) * a->Hkv * (a->Dh / 64) * 16;
             if (int rc = launch(ctx, ctx->split_kv, dim3(uint32_t((threads + 255) / 256), 1, 1), dim3(256, 1, 1), sp,
                                 "split K/V"))
@@ -682,24 +763,21 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
     }
     // split-K flash-decode (+ combine)
     const uint32_t *qd = nullptr, *kd = nullptr;
-    if (!an.q_contig || !an.k_contig) {
-        if (int rc = upload_positions(ctx, an.q_contig ? nullptr : a->q_pos, an.q_contig ? 0 : a->T,
-                                      an.k_contig ? nullptr : a->k_pos, an.k_contig ? 0 : a->S, &qd, &kd))
-            return rc;
-    }
+    if (int rc = stage_positions(ctx, a, an, noalloc, &qd, &kd)) return rc;
+    void* part = nullptr;
     if (pl.splits > 1)
-        if (int rc = ensure_workspace(ctx, pl.workspace_bytes)) return rc;
+        if (int rc = call_workspace(ctx, pl.workspace_bytes, noalloc, &part)) return rc;
     G4aDecodeParams dp{};
     dp.q = a->q;
     dp.k = a->k;
     dp.v = a->v;
     dp.out = a->out;
-    dp.part = static_cast<float*>(ctx->workspace);
+    dp.part = static_cast<float*>(part);
     dp.dummy = ctx->dummy;
     dp.q_pos = qd;
     dp.k_pos = kd;
-    dp.q_pos0 = a->q_pos ? a->q_pos[0] : a->q_pos0;
-    dp.k_pos0 = a->k_pos ? (a->S ? a->k_pos[0] : 0) : a->k_pos0;
+    dp.q_pos0 = q_pos0;
+    dp.k_pos0 = k_pos0;
     dp.T = a->T;
     dp.Hq = a->Hq;
     dp.Hkv = a->Hkv;
@@ -1324,6 +1402,7 @@ int g4a_attn_producer(g4a_ctx* ctx, const g4a_producer_args* a) {
 struct g4a_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    std::shared_ptr<g4a_graph_book> book;  // the context it was captured on
 };
 
 int g4a_capture_begin(g4a_ctx* ctx) {
@@ -1332,6 +1411,8 @@ int g4a_capture_begin(g4a_ctx* ctx) {
     if (ctx->timing) return fail(ctx, G4A_E_ARG, "per-kernel timing is on: turn it off before capturing");
     HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
     ctx->capturing = true;
+    ctx->capture_code = 0;
+    ctx->capture_msg.clear();
     return G4A_OK;
 }
 
@@ -1340,20 +1421,31 @@ int g4a_capture_end(g4a_ctx* ctx, g4a_graph** graph) {
     *graph = nullptr;
     if (!ctx->capturing) return fail(ctx, G4A_E_ARG, "no capture is open on this context");
     ctx->capturing = false;
+    const int code = ctx->capture_code;
+    ctx->capture_code = 0;
     hipGraph_t g = nullptr;
-    HIP_TRY(ctx, hipStreamEndCapture(ctx->stream, &g));
+    const hipError_t ee = hipStreamEndCapture(ctx->stream, &g);
+    if (code != 0) {
+        // a call refused inside the capture is missing from the recording: no graph
+        if (g) hipGraphDestroy(g);
+        return fail(ctx, code, "a call inside the capture failed, so no graph was made: %s", ctx->capture_msg.c_str());
+    }
+    if (ee != hipSuccess) return fail(ctx, G4A_E_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ee));
     hipGraphExec_t exec = nullptr;
     const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
     if (e != hipSuccess) {
         hipGraphDestroy(g);
         return fail(ctx, G4A_E_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
     }
-    *graph = new g4a_graph{g, exec};
+    *graph = new g4a_graph{g, exec, ctx->book};
+    ++ctx->book->live;
     return G4A_OK;
 }
 
 int g4a_graph_launch(g4a_ctx* ctx, g4a_graph* graph) {
     if (!ctx || !graph) return fail(ctx, G4A_E_ARG, "null ctx/graph");
+    if (graph->book != ctx->book)
+        return fail(ctx, G4A_E_ARG, "the graph was captured on another context: launch it on that one");
     if (int rc = refuse_in_capture(ctx, "g4a_graph_launch")) return rc;
     HIP_TRY(ctx, hipGraphLaunch(graph->exec, ctx->stream));
     return G4A_OK;
@@ -1361,8 +1453,22 @@ int g4a_graph_launch(g4a_ctx* ctx, g4a_graph* graph) {
 
 int g4a_graph_destroy(g4a_graph* graph) {
     if (!graph) return G4A_OK;
+    g4a_ctx* const ctx = graph->book ? graph->book->ctx : nullptr;
+    // a replay may still be running on the context's stream (a stream that is
+    // capturing cannot be waited on; its retired workspaces then wait for a later
+    // destroy or the context's end)
+    const bool can_wait = ctx && !ctx->capturing;
+    if (can_wait) hipStreamSynchronize(ctx->stream);
     if (graph->exec) hipGraphExecDestroy(graph->exec);
     if (graph->graph) hipGraphDestroy(graph->graph);
+    if (ctx) {
+        g4a_graph_book& b = *graph->book;
+        if (--b.live == 0 && can_wait) {
+            // no graph needs the workspaces the context has outgrown any more
+            for (void* p : b.retired) hipFree(p);
+            b.retired.clear();
+        }
+    }
     delete graph;
     return G4A_OK;
 }

@@ -184,7 +184,8 @@ struct DecodeCfg {
 // Completion is tracked by vmcnt like any vector load. Written as inline asm so
 // the compiler does not serialise every later LDS read behind all copies in
 // flight: the kernel waits for each chunk itself (wait_vm) before a barrier.
-// M0 is not otherwise live in these kernels.
+// M0 is declared clobbered, so the compiler never keeps a value of its own in
+// M0 across a copy.
 // NT marks the load non-temporal: for K/V that a long-context decode streams
 // once (measured 28.1 -> 27.0 us at 32K). Short contexts keep the default
 // policy: a token's small caches are reread by the next token.
@@ -192,10 +193,9 @@ template <bool NT = false>
 __device__ __forceinline__ void copy16_to_lds(const float* src, float* lds_dst) {
     const uint32_t m0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) float*)lds_dst);
     if constexpr (NT)
-        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(m0)
-                     : "memory");
+        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "{m0}"(m0) : "memory");
     else
-        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
+        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
 
 // Wait until at most N vector-memory operations of this wave are in flight
@@ -1266,7 +1266,7 @@ __device__ __forceinline__ void generic_attention(const G4aGenericParams& p) {
     const uint32_t h = blockIdx.x, qi = blockIdx.y;
     const uint32_t group = p.Hq / p.Hkv;
     const uint32_t kvh = h / group;
-    const uint32_t qpos = p.q_pos[qi];
+    const uint32_t qpos = p.q_pos ? p.q_pos[qi] : p.q_pos0 + qi;
     const float* __restrict__ qr = p.q + ((size_t)qi * p.Hq + h) * p.Dh;
     for (uint32_t d = lane; d < p.Dh; d += 64) qs[d] = qr[d];
     __syncthreads();
@@ -1281,7 +1281,7 @@ __device__ __forceinline__ void generic_attention(const G4aGenericParams& p) {
         const float* __restrict__ kr = p.k + ((size_t)phys_row(j, p.ring_cap) * p.Hkv + kvh) * p.Dh;
         float dot = 0.0f;
         for (uint32_t d = 0; d < p.Dh; ++d) dot = dot + qs[d] * kr[d];
-        const uint32_t kp = p.k_pos[j];
+        const uint32_t kp = p.k_pos ? p.k_pos[j] : p.k_pos0 + j;
         const bool vis = inr && kp <= qpos && (p.window == 0 || qpos - kp < p.window);
         const float sc = vis ? score_epilogue(dot, p.scale, p.softcap) : NEG_INF;
         const float mn = fmaxf(m, wave_max(sc));

@@ -22,16 +22,28 @@
 // maximum) get their score recomputed in the reference's exact order and their
 // contribution corrected:
 //   O[row] += (e^{s_exact - m} - e^{s_approx - m}) * v[key],  l[row] += same.
-// Keys farther than TAU below the maximum carry weight < e^-TAU relative to it,
-// and their score error moves the output by well under 1e-6. If the list fills
-// up (many near-ties), it is compacted against the current maxima and, if
-// still full, corrected on the spot.
+// Keys farther than TAU below the maximum keep their estimate, each with weight
+// < e^-TAU relative to the maximum's. Their errors (|delta| <= ~4e-4) move the
+// output by at most max|delta| * (W_out / l) * max|v - out|, W_out / l the
+// weight share of those keys, <= N e^-TAU / (1 + N e^-TAU) for N keys in a row.
+// So TAU (G4aPrefillParams::tau) grows with the key range: the host passes
+// max(12, ln N + 4.5), which keeps that share below e^-4.5 = 0.011 even when
+// every key sits just outside the band and every error pushes the same way.
+// If the list fills up (many near-ties), it is compacted against the current
+// maxima and, if still full, corrected on the spot.
 #include "g4a_params.h"
 
 namespace {
 
-constexpr float PF_TAU_BF = 7.0f;  // rescoring band of the split-bf16 scores
-constexpr float PF_RESCALE = 8.0f;  // e^8 ~ 3e3: probability headroom before O and l are rescaled
+// Probabilities are held as P = PSCALE * e^(s - m_ref), m_ref a lagging row
+// maximum that is raised (with O and l rescaled) once the running maximum
+// passes it by RESCALE. With fp16 P.V splits P <= PSCALE * e^RESCALE = 55.9e3
+// stays below the fp16 maximum, and the 2^10 scale keeps the P of keys down to
+// e^-16 below m_ref in fp16's normal range (relative error 2^-22 after the
+// hi/lo split) instead of its subnormals, whose absolute steps would add up
+// over many small weights. O and l carry the same scale, so O / l is unchanged.
+constexpr float PF_RESCALE = 4.0f;
+constexpr float PF_PSCALE = 1024.0f;
 
 __device__ __forceinline__ uint64_t ballot(bool b) { return __ballot(b); }
 __device__ __forceinline__ int lanes_below(uint64_t m) {
@@ -87,14 +99,20 @@ __device__ __forceinline__ void split_kv(const G4aSplitParams& p) {
         if (!p.ring_cap && j >= p.S) j = p.S - 1;
         return p.ring_cap ? j % p.ring_cap : j;
     };
+    auto seen = [&](size_t jj) -> bool {  // key k0 + jj lies in the call's key range
+        const uint32_t j = p.k0 + (uint32_t)jj;
+        return j >= p.vis_lo && j < p.vis_hi;
+    };
+    const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (i < nk_items) {
         const uint32_t b = (uint32_t)(i % nbk);
         const size_t rh = i / nbk;
         const uint32_t h = (uint32_t)(rh % p.Hkv);
         const size_t jj = rh / p.Hkv;
         const float* src = p.k + (row_of(jj) * p.Hkv + h) * p.Dh + 8 * b;
+        const bool in = seen(jj);
         bf8v hi, lo;
-        split8(ld4(src), ld4(src + 4), hi, lo);
+        split8(in ? ld4(src) : zero4, in ? ld4(src + 4) : zero4, hi, lo);
         float* dst = p.kout + (jj * p.Hkv + h) * p.Dh + 8 * b;
         *reinterpret_cast<bf8v*>(dst) = hi;
         *reinterpret_cast<bf8v*>(dst + 4) = lo;
@@ -110,7 +128,8 @@ __device__ __forceinline__ void split_kv(const G4aSplitParams& p) {
     const size_t qd = t / p.Hkv;
     float4 x[4];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) x[kk] = ld4(p.v + (row_of(4 * qd + kk) * p.Hkv + h) * p.Dh + 64 * c + 4 * n);
+    for (int kk = 0; kk < 4; ++kk)
+        x[kk] = seen(4 * qd + kk) ? ld4(p.v + (row_of(4 * qd + kk) * p.Hkv + h) * p.Dh + 64 * c + 4 * n) : zero4;
     float* const blk = p.vout + (qd * p.Hkv + h) * 4 * p.Dh;
     bool bad = false;
 #pragma unroll
@@ -193,6 +212,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
     const uint32_t nsteps = (nt + 1) / 2;
     // P.V from fp16 hi/lo splits of P and V unless some V value is outside their range
     const bool v16 = __builtin_amdgcn_readfirstlane(*p.vflag) != p.epoch;
+    const float psc = v16 ? PF_PSCALE : 1.0f;  // scale of P, O and l (the f32 P.V path needs none)
     const bool wave_valid = qw < p.T;
     const int32_t w_lo = wave_valid ? key_lo(qw) : 0;
     const int32_t w_hi = wave_valid ? key_hi(min(qw + 1, p.T - 1)) : 0;
@@ -223,7 +243,9 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
             const int row = idx / (DH / 256), piece = idx % (DH / 256);
             const int tsel = row / (2 * BK), isv = (row / BK) & 1, kf = row % BK;
             const uint32_t tile0 = (uint32_t)wg_base + (2 * st + tsel) * BK;
-            const uint32_t key = min(tile0 + kf, (uint32_t)wg_hi - 1u);
+            // keys outside the workgroup's visible range [wg_lo, wg_hi) read its nearest
+            // visible row (their P is 0; an unwritten slot could hold NaN)
+            const uint32_t key = min(max(tile0 + kf, (uint32_t)wg_lo), (uint32_t)wg_hi - 1u);
             // K rows come from the split copy (row key - split0); V from the split
             // quads (piece kf: quad kf/4, its 1 KiB piece kf%4) or the cache rows
             const uint32_t ks = min(key - min(key, p.split0), p.split_n - 1u);
@@ -255,7 +277,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
             const bool has = e < cnt;
             const uint32_t pk = has ? my_keys[e] : 0u;
             const float sa = has ? my_s[e] : 0.0f;
-            const bool keep = has && sa > my_m[pk >> 28] - PF_TAU_BF;
+            const bool keep = has && sa > my_m[pk >> 28] - p.tau;
             wave_sync();
             const uint64_t b = ballot(keep);
             if (keep) {
@@ -279,7 +301,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         float delta = 0.0f;
         if (has) {
             const float m = my_m[rho];
-            delta = expf(dot * p.scale - m) - expf(my_s[e] - m);
+            delta = psc * (expf(dot * p.scale - m) - expf(my_s[e] - m));
         }
         const int nb = min(64, cnt - base);
         for (int i = 0; i < nb; ++i) {
@@ -426,7 +448,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
             float delta = 0.0f;
             if (has) {
                 const float m = my_m[rho];
-                delta = expf(dot * p.scale - m) - expf(my_s[e] - m);
+                delta = psc * (expf(dot * p.scale - m) - expf(my_s[e] - m));
             }
             f4v lc = f4v{0.0f, 0.0f, 0.0f, 0.0f};
             correct_o4(base, delta, rho, kap, &lc);
@@ -487,7 +509,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         int nnew = 0;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            cand[r] = vis[r] && s[r] > mn - PF_TAU_BF;
+            cand[r] = vis[r] && s[r] > mn - p.tau;
             bal[r] = ballot(cand[r]);
             nnew += __builtin_popcountll(bal[r]);
         }
@@ -524,7 +546,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
 
         float pr[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? expf(s[r] - m_ref) : 0.0f;
+        for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? psc * expf(s[r] - m_ref) : 0.0f;
         l_part += (pr[0] + pr[1]) + (pr[2] + pr[3]);
         if (v16) {
             // O += P V on v_mfma_f32_16x16x16_f16: Phi Vhi + Phi Vlo + Plo Vhi (relative error
@@ -722,6 +744,7 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
     const uint32_t t_begin = split && half_id ? nt / 2 : 0u;
     const uint32_t t_end = split && !half_id ? nt / 2 : nt;
     const bool v16 = __builtin_amdgcn_readfirstlane(*p.vflag) != p.epoch;
+    const float psc = v16 ? PF_PSCALE : 1.0f;  // scale of P, O and l (the f32 P.V path needs none)
     const bool wave_valid = qw < p.T;
     const int32_t w_lo = wave_valid ? key_lo(qw) : 0;
     const int32_t w_hi = wave_valid ? key_hi(min(qw + 1, p.T - 1)) : 0;
@@ -765,7 +788,8 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int kf = 4 * (w - 4) + i;
-                const float* src = vbase + prow(min(tile0 + kf, last)) * row_stride + 4 * lane;
+                // keys before the workgroup's first visible key read its row (P is 0 there)
+                const float* src = vbase + prow(min(max(tile0 + kf, (uint32_t)wg_lo), last)) * row_stride + 4 * lane;
 #pragma unroll
                 for (int pc = 0; pc < NPR; ++pc) copy16_to_lds(src + 256 * pc, buf + BK * KRS + kf * DH + 256 * pc);
             }
@@ -792,7 +816,7 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
             const bool has = e < cnt;
             const uint32_t pk = has ? my_keys[e] : 0u;
             const float sa = has ? my_s[e] : 0.0f;
-            const bool keep = has && sa > my_m[pk >> 28] - PF_TAU_BF;
+            const bool keep = has && sa > my_m[pk >> 28] - p.tau;
             wave_sync();
             const uint64_t b = ballot(keep);
             if (keep) {
@@ -811,7 +835,7 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
         float delta = 0.0f;
         if (has) {
             const float m = my_m[rho];
-            delta = expf(dot * p.scale - m) - expf(my_s[e] - m);
+            delta = psc * (expf(dot * p.scale - m) - expf(my_s[e] - m));
         }
         const int nb = min(64, cnt - base);
         for (int i = 0; i < nb; ++i) {
@@ -1009,7 +1033,7 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
         int nnew = 0;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            cand[r] = vis[r] && s[r] > mn - PF_TAU_BF;
+            cand[r] = vis[r] && s[r] > mn - p.tau;
             bal[r] = ballot(cand[r]);
             nnew += __builtin_popcountll(bal[r]);
         }
@@ -1048,7 +1072,7 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
         // ---- probabilities against m_ref and P.V for this wave's columns ----
         float pr[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? expf(s[r] - m_ref) : 0.0f;
+        for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? psc * expf(s[r] - m_ref) : 0.0f;
         l_part += (pr[0] + pr[1]) + (pr[2] + pr[3]);
         if (v16) {
             // O += P V on v_mfma_f32_16x16x16_f16: Phi Vhi + Phi Vlo + Plo Vhi. Lane (g, rl)

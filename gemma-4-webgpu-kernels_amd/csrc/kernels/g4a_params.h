@@ -72,14 +72,16 @@ struct G4aCombineParams {
 };
 
 // Generic per-(query, head) attention for shapes outside the fast paths
-// (any Hq/Hkv/Dh/Dv). Positions are always device arrays here.
+// (any Hq/Hkv/Dh/Dv). Positions as in G4aDecodeParams: device arrays, or
+// q_pos0 + i / k_pos0 + j when the array is null.
 struct G4aGenericParams {
     const float* q;        // [T, Hq, Dh]
     const float* k;        // [rows, Hkv, Dh]
     const float* v;        // [rows, Hkv, Dv]
     float* out;            // [T, Hq*Dv]
-    const uint32_t* q_pos; // [T]
-    const uint32_t* k_pos; // [S]
+    const uint32_t* q_pos; // device [T] or null
+    const uint32_t* k_pos; // device [S] or null
+    uint32_t q_pos0, k_pos0;
     uint32_t T, S, Hq, Hkv, Dh, Dv;
     uint32_t k_start, k_end;
     uint32_t ring_cap;
@@ -104,6 +106,7 @@ struct G4aPrefillParams {
     uint32_t ring_cap, window;
     uint32_t split0, split_n, epoch;
     float scale;
+    float tau;             // rescoring band: keys whose estimated score is within tau of the row maximum are rescored exactly
     // head_dim 512 causal balance: the last `nbig` query blocks (8 queries each)
     // run as two workgroups over the two halves of their key tiles; each half
     // writes its partial (O, l, m) to `part` and g4a_prefill_merge_d512 merges
@@ -123,7 +126,12 @@ struct G4aPrefillParams {
 //         (i * Hkv + h) * 4 * Dh; dim 64c + 4n + e of it sits at slots
 //         4 * ((4c + e) * 16 + n) .. +3: the 4 keys' fp16 hi parts, then their
 //         fp16 lo parts (hi = fp16(x), lo = fp16(x - hi));
-//   vflag: set to epoch if some V value is not finite or beyond +-32768.
+//   vflag: set to epoch if some V value of a key in [vis_lo, vis_hi) is not
+//          finite or beyond +-32768.
+// Keys outside [vis_lo, vis_hi) (the call's trimmed key range; the tiles round
+// it out to multiples of 16) are seen by no query: their K and V splits are
+// written as zeros, so P = 0 times such a key's V is 0 whatever its slot holds
+// (an unwritten ring slot may hold NaN).
 struct G4aSplitParams {
     const float* k;        // [rows, Hkv, Dh]
     const float* v;        // [rows, Hkv, Dh]
@@ -132,6 +140,7 @@ struct G4aSplitParams {
     uint32_t* vflag;
     uint32_t k0, nkeys, S, Hkv, Dh;
     uint32_t ring_cap, epoch;
+    uint32_t vis_lo, vis_hi;
 };
 
 // Per-head RMSNorm + half-split partial RoPE over rows of Dh values (the

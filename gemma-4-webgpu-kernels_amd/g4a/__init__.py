@@ -405,7 +405,8 @@ class Context:
         self._check(self.lib.g4a_capture_begin(self.handle))
 
     def capture_end(self) -> "Graph":
-        """Close the capture; returns the replayable graph (raises if a captured call failed)."""
+        """Close the capture; returns the replayable graph. Raises, and makes no graph,
+        if any call inside the capture failed (the recording would lack it)."""
         g = ctypes.c_void_p()
         self._check(self.lib.g4a_capture_end(self.handle, ctypes.byref(g)))
         return Graph(self, g.value)

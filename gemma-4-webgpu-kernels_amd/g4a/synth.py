@@ -256,3 +256,78 @@ def quant_parity_inputs():
     sc = (r.next(v * (d // group)) * np.float32(0.04) + np.float32(0.02)).astype(np.float32)
     yield dict(name="embed_q4_grouped", qbytes=qb, scales=sc, N=v, K=d, bits=bits, signed_i8=False,
                group_size=group, ids=np.array([3, 7, 49, 0, 21], np.uint32), scale=float(np.sqrt(np.float32(d))))
+
+
+# ---- the Gemma-4-E2B per-token attention schedule ----------------
+# Layer facts of rust/assets/config.json: 35 layers, the last 20 share KV,
+# global (full-attention) layers 4, 9, ..., 34 with head_dim 512, the others
+# sliding-window-512 with head_dim 256.
+E2B_LAYERS = 35
+E2B_KV_SHARED = 20
+E2B_GLOBAL = frozenset(range(4, E2B_LAYERS, 5))
+E2B_WINDOW = 512
+
+
+def kv_source_layer(i: int, n_layers: int = E2B_LAYERS, n_shared: int = E2B_KV_SHARED,
+                    is_global=lambda j: j in E2B_GLOBAL) -> int:
+    """The layer whose KV cache layer i reads (rust/src/config.rs:152-159): itself
+    below the shared region, else the most recent earlier non-shared layer of the
+    same attention type."""
+    first_shared = max(n_layers - n_shared, 0)
+    if i < first_shared:
+        return i
+    for j in range(first_shared - 1, -1, -1):
+        if is_global(j) == is_global(i):
+            return j
+    return i
+
+
+@dataclass
+class ScheduleLayer:
+    index: int
+    is_global: bool
+    Dh: int
+    src: int           # kv_source_layer(index)
+    q: np.ndarray      # [1, 8, Dh], unit-RMS per head
+
+
+@dataclass
+class ScheduleCache:
+    k: np.ndarray      # global: [S, 1, 512] rows 0..S-1; local: a [ring, 1, 256] ring
+    v: np.ndarray
+    ring_cap: int      # 0 for a linear (global) cache
+    k_pos: np.ndarray  # absolute position of each logical key the layer can see
+
+
+def schedule_token(S: int = 32768, seed: int = 4, ring: int = E2B_WINDOW):
+    """One decode token of the 35-layer schedule at context S (the query at
+    position S-1): (layers, caches). Global caches hold keys 0..S-1; a local
+    layer's ring of `ring` slots holds positions S-ring..S-1, position p in slot
+    p % ring. Streams per layer li (seed*100 + li): q = 0, k = 1, v = 2, with q
+    and k RMS-normalised per head, v N(0,1). Only the 15 source layers own a
+    cache (3 global, 12 local)."""
+    layers, caches = [], {}
+    for i in range(E2B_LAYERS):
+        g = i in E2B_GLOBAL
+        dh = 512 if g else 256
+        q = rms_norm_rows(normal_f32(seed * 100 + i, 0, 8 * dh).reshape(1, 8, dh))
+        layers.append(ScheduleLayer(i, g, dh, kv_source_layer(i), q))
+    for li in sorted({l.src for l in layers}):
+        g = li in E2B_GLOBAL
+        rows, dh = (S, 512) if g else (ring, 256)
+        k = rms_norm_rows(normal_f32(seed * 100 + li, 1, rows * dh).reshape(rows, 1, dh))
+        v = normal_f32(seed * 100 + li, 2, rows * dh).reshape(rows, 1, dh)
+        if g:
+            caches[li] = ScheduleCache(k, v, 0, np.arange(S, dtype=np.uint32))
+        else:
+            # ring row r holds the position p in [S-ring, S) with p % ring == r
+            caches[li] = ScheduleCache(k, v, ring, np.arange(S - ring, S, dtype=np.uint32))
+    return layers, caches
+
+
+def unroll_ring(c: ScheduleCache):
+    """(k, v) of a schedule cache in logical key order (k_pos order), for the oracle."""
+    if not c.ring_cap:
+        return c.k, c.v
+    slots = c.k_pos % np.uint32(c.ring_cap)
+    return np.ascontiguousarray(c.k[slots]), np.ascontiguousarray(c.v[slots])

@@ -323,8 +323,13 @@ int g4a_embed_rows_q(g4a_ctx *ctx, const g4a_qweight *table, const uint32_t *ids
  * table, and g4a_h2d / g4a_d2h / g4a_zero / g4a_sync / the timers, fail with
  * G4A_E_ARG while a capture is open: run such calls once before capturing.
  * After any failure inside a capture, still call g4a_capture_end, which then
- * reports the error and returns no graph. Rows without visible keys are
- * cleared by a fill kernel, not a memset, so a replay clears them too. */
+ * returns that first failure's code and no graph (the recording would lack the
+ * refused call). Rows without visible keys are cleared by a fill kernel, not a
+ * memset, so a replay clears them too. A graph replays with the workspace it
+ * was captured with: a later eager call that needs a larger workspace gets a
+ * new one and the old one is kept until the context's last graph is
+ * destroyed. g4a_graph_launch refuses a graph captured on another context. A
+ * graph that outlives its context can only be destroyed. */
 typedef struct g4a_graph g4a_graph;
 int g4a_capture_begin(g4a_ctx *ctx);
 int g4a_capture_end(g4a_ctx *ctx, g4a_graph **graph);

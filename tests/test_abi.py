@@ -149,3 +149,12 @@ def test_short_decode_rule():
     assert g4a.KERNEL_NAMES[_plan(S=512, q_pos=[511], k_pos=np.arange(512) * 2).kernel] == "decode"
     assert g4a.KERNEL_NAMES[_plan(S=512, Hq=4, q_pos0=511).kernel] == "decode"
     assert g4a.KERNEL_NAMES[_plan(S=512, q_pos0=511, splits=8).kernel] == "decode"
+
+
+def test_kv_source_map_is_the_reference_one():
+    import g4a.synth as synth
+    # rust/src/config.rs:152-159 on the E2B layer types: 15 caches, shared layers read 13 / 14
+    src = [synth.kv_source_layer(i) for i in range(35)]
+    assert src[:15] == list(range(15))
+    assert all(src[i] == (14 if i in synth.E2B_GLOBAL else 13) for i in range(15, 35))
+    assert len(set(src)) == 15 and sum(1 for s in set(src) if s in synth.E2B_GLOBAL) == 3

@@ -105,7 +105,9 @@ def test_capture_refuses_host_staging_and_recovers(ctx):
                 ctx.sync()
             with pytest.raises(g4a.G4aError, match="already open"):
                 ctx.capture_begin()
-            ctx.capture_end().free()  # nothing was recorded
+            # the refused calls are missing from the recording: no graph, the first failure reported
+            with pytest.raises(g4a.G4aError, match="failed, so no graph was made.*cannot hold"):
+                ctx.capture_end()
         finally:
             _end_open_capture(ctx)
         with pytest.raises(g4a.G4aError, match="no capture is open"):
@@ -119,3 +121,66 @@ def test_capture_refuses_host_staging_and_recovers(ctx):
     finally:
         for d in (q, k, v, out):
             d.free()
+
+
+def test_replay_after_the_workspace_grows_and_graph_ownership(ctx):
+    # A graph keeps the workspace it was captured with: an eager call that needs a larger one
+    # afterwards (a 2048-token hd512 prefill) must not free it under the graph, whose replays stay
+    # bit-identical. A generic-path call (head_dim 64) with contiguous positions is capturable too.
+    # A graph replays only on the context it was captured on.
+    own = g4a.Context(0)  # a fresh context: its workspace starts small
+    bufs = []
+    keep = lambda d: bufs.append(d) or d  # noqa: E731
+    graph = None
+    try:
+        ins = synth.gemma_inputs(T=1, S=32768, Dh=512, seed=12)
+        q, k, v = (keep(own.upload(x)) for x in (ins.q, ins.k, ins.v))
+        out = keep(own.empty((1, 8 * 512)))
+        gen = synth.gemma_inputs(T=3, S=200, Dh=64, seed=13)
+        gq, gk, gv = (keep(own.upload(x)) for x in (gen.q, gen.k, gen.v))
+        gout = keep(own.empty((3, 8 * 64)))
+        calls = [dict(q=q.ptr, k=k.ptr, v=v.ptr, out=out.ptr, T=1, S=32768, Hq=8, Hkv=1, Dh=512, Dv=512,
+                      q_pos0=32767),
+                 dict(q=gq.ptr, k=gk.ptr, v=gv.ptr, out=gout.ptr, T=3, S=200, Hq=8, Hkv=1, Dh=64, Dv=64,
+                      q_pos0=197)]
+        assert g4a.KERNEL_NAMES[own.plan(**{k_: v_ for k_, v_ in calls[1].items() if k_ not in
+                                            ("q", "k", "v", "out")}).kernel] == "generic"
+        step("eager run (fresh context)")
+        own.attention_batch(calls)
+        want = [out.to_host(), gout.to_host()]
+        step("capture")
+        own.capture_begin()
+        try:
+            own.attention_batch(calls)
+        except Exception:
+            _end_open_capture(own)
+            raise
+        graph = own.capture_end()
+        step("eager 2048-token hd512 prefill (grows the workspace)")
+        pf = synth.gemma_inputs(T=2048, S=2048, Dh=512, seed=3, q_pos=np.arange(2048))
+        pq, pk, pv = (keep(own.upload(x)) for x in (pf.q, pf.k, pf.v))
+        pout = keep(own.empty((2048, 8 * 512)))
+        plan = own.plan(T=2048, S=2048, Hq=8, Hkv=1, Dh=512, Dv=512, q_pos0=0)
+        assert g4a.KERNEL_NAMES[plan.kernel] == "prefill"
+        own.attention(pq.ptr, pk.ptr, pv.ptr, pout.ptr, T=2048, S=2048, Hq=8, Hkv=1, Dh=512, Dv=512, q_pos0=0)
+        own.sync()
+        rng = np.random.default_rng(1)
+        for rep in range(3):
+            step(f"replay {rep} after the growth")
+            for o in (out, gout):
+                own.h2d(o.ptr, rng.standard_normal(o.shape).astype(np.float32))
+            graph.launch()
+            own.sync()
+            assert np.array_equal(out.to_host(), want[0]), f"replay {rep}: decode"
+            assert np.array_equal(gout.to_host(), want[1]), f"replay {rep}: generic"
+            # eager work in between, through the grown workspace
+            own.attention(pq.ptr, pk.ptr, pv.ptr, pout.ptr, T=2048, S=2048, Hq=8, Hkv=1, Dh=512, Dv=512, q_pos0=0)
+        step("a graph launched on another context is refused")
+        with pytest.raises(g4a.G4aError, match="another context"):
+            ctx._check(ctx.lib.g4a_graph_launch(ctx.handle, graph.handle))
+    finally:
+        if graph is not None:
+            graph.free()
+        for d in bufs:
+            d.free()
+        own.close()

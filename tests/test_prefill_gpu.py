@@ -134,3 +134,97 @@ def test_v_beyond_the_fp16_split_range(ctx, where):
     got = g4a.attention_host(ctx, big.q, big.k, big.v, q_pos=big.q_pos, k_pos=big.k_pos, window=512)
     unit = float(np.abs(v).max())
     assert_parity(got / unit, np.asarray(want) / unit, f"V beyond the fp16 range ({where}), in units of max|v|")
+
+
+@pytest.mark.parametrize("Dh,vscale", [(256, 1.0), (512, 1.0), (256, 1e5), (512, 1e5)])
+def test_ring_prefill_ignores_nan_in_dead_slots(ctx, Dh, vscale):
+    # A 37-token chunk at positions 600..636 (S = 637, not a multiple of 16) with window 512 reads
+    # keys 89..636 from a 560-slot ring. The slots of keys 77..88 are dead (outside every query's
+    # window) and hold NaN, as unwritten memory may: the tiles that round the key range out to
+    # multiples of 16 touch them (keys 80..88 before it, 637..639 past it wrap onto slots 77..79),
+    # with P = 0. The output must stay finite and equal the oracle's, on the fp16 P.V path and, with
+    # V scaled past the fp16 range, on the f32 one.
+    S, T, cap, W = 637, 37, 560, 512
+    ins = synth.gemma_inputs(T=T, S=S, Dh=Dh, seed=101 + Dh)
+    v = (ins.v * np.float32(vscale)).astype(np.float32)
+    ring_k = np.full((cap, 1, Dh), np.nan, np.float32)
+    ring_v = np.full((cap, 1, Dh), np.nan, np.float32)
+    lo = S - T - W + 1  # first key any query sees
+    for p_ in range(lo, S):
+        ring_k[p_ % cap] = ins.k[p_]
+        ring_v[p_ % cap] = v[p_]
+    assert np.isnan(ring_k[77:89]).all() and not np.isnan(ring_k[89:]).any() and not np.isnan(ring_k[:77]).any()
+    plan = ctx.plan(T=T, S=S, Hq=8, Hkv=1, Dh=Dh, Dv=Dh, q_pos0=S - T, k_pos0=0, window=W, ring_cap=cap)
+    assert g4a.KERNEL_NAMES[plan.kernel] == "prefill" and (plan.k_start, plan.k_end) == (lo, S)
+    want = oracle.attention(ins.q, ins.k, v, ins.q_pos, ins.k_pos, window=W)
+    dev = [ctx.upload(x) for x in (ins.q, ring_k, ring_v)]
+    out = ctx.empty((T, 8 * Dh))
+    try:
+        print(f"[gpu] ring prefill with NaN dead slots, Dh {Dh}, V x {vscale:g}", flush=True)
+        ctx.attention(dev[0].ptr, dev[1].ptr, dev[2].ptr, out.ptr, T=T, S=S, Hq=8, Hkv=1, Dh=Dh, Dv=Dh,
+                      q_pos0=S - T, k_pos0=0, window=W, ring_cap=cap)
+        got = out.to_host()
+    finally:
+        for d in dev:
+            d.free()
+        out.free()
+    assert np.isfinite(got).all(), "NaN from a dead ring slot reached the output"
+    unit = float(np.abs(v[lo:]).max()) if vscale != 1.0 else 1.0
+    assert_parity(got / unit, np.asarray(want) / unit, f"ring prefill, NaN dead slots, Dh {Dh}, V x {vscale:g}")
+
+
+def rescoring_band(n_keys):
+    """The band the host passes the prefill kernels (G4aPrefillParams::tau) for a
+    call over n_keys keys: keys whose estimated score is more than this below
+    their row's maximum keep the estimate."""
+    return max(12.0, float(np.log(np.float32(n_keys))) + 4.5)
+
+
+def _bf16(x):
+    """Round f32 to bf16 (nearest even), returned as f32."""
+    b = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return (((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+
+
+def _split_bf16_scores(q, k):
+    """The kernels' score estimate: Khi.Qhi + Klo.Qhi + Khi.Qlo of bf16 hi/lo splits (f64 sums)."""
+    qh = _bf16(q)
+    ql = _bf16(q - qh)
+    kh = _bf16(k)
+    kl = _bf16(k - kh)
+    f = np.float64
+    return kh.astype(f) @ qh.astype(f) + kl.astype(f) @ qh.astype(f) + kh.astype(f) @ ql.astype(f)
+
+
+@pytest.mark.parametrize("Dh", [256, 512])
+@pytest.mark.parametrize("below", [0.5, 2.0])
+def test_many_keys_just_outside_the_rescoring_band(ctx, Dh, below):
+    # Adversarial case for the approximate scores: one key scores 30, the other 2047 all score
+    # 30 - tau - `below` (just outside the exact-rescoring band, so each keeps its estimate,
+    # whose error delta is ~1e-4), and each such key's V row is sign(delta) in every dim, so all
+    # their errors push every output the same way. 16 queries x 8 heads share one q row.
+    # Aggregate bound: |d out| <= max|delta| * (W_out / l) * max|v - out|, W_out / l the weight
+    # share of the keys that keep their estimate.
+    S, T = 2048, 16
+    tau = rescoring_band(S)
+    q0 = synth.rms_norm_rows(synth.normal_f32(71, 0, Dh).reshape(1, Dh))[0].astype(np.float64)
+    r = synth.normal_f32(71, 1, S * Dh).reshape(S, Dh).astype(np.float64)
+    r -= np.outer(r @ q0, q0) / (q0 @ q0)  # orthogonal to q0
+    target = np.full(S, 30.0 - tau - below)
+    target[0] = 30.0
+    k = (np.outer(target / (q0 @ q0), q0) + r).astype(np.float32).reshape(S, 1, Dh)
+    q = np.broadcast_to(q0.astype(np.float32), (T, 8, Dh)).copy()
+    # the oracle's exact f32 scores, and the estimate's error per key
+    seq = np.zeros(S, np.float32)
+    for d in range(Dh):
+        seq = (seq + (np.float32(q0[d]) * k[:, 0, d]).astype(np.float32)).astype(np.float32)
+    delta = _split_bf16_scores(q0.astype(np.float32), k[:, 0, :]) - seq.astype(np.float64)
+    assert np.abs(seq[1:] - target[1:]).max() < 1e-3 and abs(seq[0] - 30.0) < 1e-3
+    v = np.repeat(np.sign(delta)[:, None], Dh, axis=1).astype(np.float32).reshape(S, 1, Dh)
+    v[0] = 0.0
+    ins = synth.AttnInputs(q, k, v, np.arange(S - T, S, dtype=np.uint32), np.arange(S, dtype=np.uint32))
+    w_out = (S - T) * np.exp(-(tau + below))
+    share = w_out / (1.0 + w_out)
+    print(f"  outside-band weight share {share:.3e}, |delta| mean {np.abs(delta[1:]).mean():.2e} "
+          f"max {np.abs(delta[1:]).max():.2e}; bound {np.abs(delta).max() * share * 2:.2e}", flush=True)
+    run(ctx, ins, 0, f"2047 keys at max - tau - {below}, V = sign(score error), Dh {Dh}")
