@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <atomic>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -40,7 +41,7 @@ constexpr uint32_t BATCH_MAX_KEYS = SHORT_KEYS * MAX_SPLITS;
 std::string g_create_error;
 
 // Bytes of the static scratch array a call that allocates nothing may use.
-constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(64) << 20;
+constexpr size_t NOALLOC_SCRATCH_BYTES = G4A_NOALLOC_SCRATCH_BYTES;
 
 // Tags each K/V pre-split's V range flag (G4aSplitParams::epoch). Process-wide,
 // so no two pre-splits of any context share a tag.
@@ -53,6 +54,13 @@ uint32_t next_split_epoch() {
 }
 
 }  // namespace
+
+// Scratch of g4a_attention_noalloc: split partials and pre-split K/V of calls
+// that may not allocate. Each GPU the library runs on holds its own copy of the
+// array, at its own address, from the first context on it until the process
+// ends. In host code `scratch` names a host-side stand-in, not device memory:
+// kernels get the device address from scratch_setup, never the name itself.
+static __device__ __align__(256) unsigned char scratch[G4A_NOALLOC_SCRATCH_BYTES];
 
 // The graphs captured on a context, shared by the context and each of its
 // graphs. A graph replays with the workspace it was captured with, so while
@@ -163,6 +171,25 @@ std::string default_hsaco_path() {
         return dir + "/g4a_kernels.hsaco";
     }
     return "g4a_kernels.hsaco";
+}
+
+// The device address of this device's scratch array, looked up once per device
+// (with that device current) and kept for every later context on it.
+int scratch_setup(g4a_ctx* ctx) {
+    static std::mutex mu;
+    static std::vector<void*> per_device;
+    std::lock_guard<std::mutex> lock(mu);
+    if (per_device.size() <= size_t(ctx->device)) per_device.resize(size_t(ctx->device) + 1, nullptr);
+    if (!per_device[ctx->device]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(ctx, G4A_E_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", ctx->device,
+                        hipGetErrorString(e));
+        per_device[ctx->device] = ptr;
+    }
+    ctx->scratch = per_device[ctx->device];
+    return G4A_OK;
 }
 
 int get_fn(g4a_ctx* ctx, hipFunction_t* f, const char* name) {
@@ -454,6 +481,7 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
         return bail(G4A_E_UNSUPPORTED);
     }
     ctx->cu_count = prop.multiProcessorCount;
+    if (int rc = scratch_setup(ctx)) return bail(rc);
     std::string path = hsaco_path ? std::string(hsaco_path) : default_hsaco_path();
     e = hipModuleLoad(&ctx->module, path.c_str());
     if (e != hipSuccess) {
@@ -821,6 +849,13 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
     Analysis an;
     if (int rc = analyse(ctx, a, &an, true)) return rc;
     return attention_run(ctx, a, an, true);
+}
+
+int g4a_attention_noalloc(g4a_ctx* ctx, const g4a_attn_args* a) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    Analysis an;
+    if (int rc = analyse(ctx, a, &an, true)) return rc;
+    return attention_run(ctx, a, an, true, /*noalloc=*/true);
 }
 
 int g4a_attention_batch(g4a_ctx* ctx, const g4a_attn_args* args, uint32_t n) {

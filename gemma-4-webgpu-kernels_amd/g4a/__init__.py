@@ -22,6 +22,8 @@ HSACO_PATH = BUILD_DIR / "g4a_kernels.hsaco"
 HEADER_PATH = PKG_DIR.parent / "include" / "g4a.h"
 
 G4A_OK = 0
+# G4A_NOALLOC_SCRATCH_BYTES of include/g4a.h: the static scratch of g4a_attention_noalloc
+NOALLOC_SCRATCH_BYTES = 64 << 20
 KERNEL_NAMES = {0: "none", 1: "decode", 2: "prefill", 3: "generic", 4: "decode_short"}
 
 _u32p = ctypes.POINTER(ctypes.c_uint32)
@@ -104,6 +106,7 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "g4a_zero": (c_int, [ctxp, vp, sz]),
         "g4a_sync": (c_int, [ctxp]),
         "g4a_attention": (c_int, [ctxp, ctypes.POINTER(AttnArgs)]),
+        "g4a_attention_noalloc": (c_int, [ctxp, ctypes.POINTER(AttnArgs)]),
         "g4a_attention_batch": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.c_uint32]),
         "g4a_attention_decode_batch": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.c_uint32, _u32p]),
         "g4a_attention_plan": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.POINTER(AttnPlan)]),
@@ -300,6 +303,12 @@ class Context:
     def attention(self, q: int, k: int, v: int, out: int, **kw) -> None:
         a, keep = make_args(q, k, v, out, **kw)
         self._check(self.lib.g4a_attention(self.handle, ctypes.byref(a)))
+
+    def attention_noalloc(self, q: int, k: int, v: int, out: int, **kw) -> None:
+        """g4a_attention_noalloc: attention() with its scratch in the library's static
+        array (no allocation)."""
+        a, keep = make_args(q, k, v, out, **kw)
+        self._check(self.lib.g4a_attention_noalloc(self.handle, ctypes.byref(a)))
 
     @staticmethod
     def prepare_batch(calls: list[dict]) -> tuple:

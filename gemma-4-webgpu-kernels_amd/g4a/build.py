@@ -60,8 +60,10 @@ def build_kernels(verbose: bool = False) -> Path:
 def build_host(verbose: bool = False) -> Path:
     OUT.mkdir(parents=True, exist_ok=True)
     tmp = LIBG4A.with_suffix(".so.tmp")
-    _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", f"-I{INCLUDE}", f"-I{CSRC}", CSRC / "g4a.cpp",
-          "-o", tmp, "-ldl"], verbose)
+    # compiled as HIP for gfx950: the library carries one device array of its own (the
+    # static scratch of g4a_attention_noalloc), registered with the HIP runtime at load
+    _run([HIPCC, "-x", "hip", *DEVICE_FLAGS[:1], "-O2", "-std=c++17", *DEVICE_FLAGS[4:], "-fPIC", "-shared",
+          f"-I{INCLUDE}", f"-I{CSRC}", CSRC / "g4a.cpp", "-o", tmp, "-ldl"], verbose)
     tmp.replace(LIBG4A)
     return LIBG4A
 

@@ -110,6 +110,26 @@ typedef struct g4a_attn_args {
 
 int g4a_attention(g4a_ctx *ctx, const g4a_attn_args *args);
 
+/* g4a_attention without any allocation. No counterpart in the reference: for
+ * callers that cannot allocate while they run (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Same arguments, same
+ * kernels and the same results (bit-identical) as g4a_attention, except that a
+ * call's split partials and pre-split K/V live in a static scratch array of
+ * G4A_NOALLOC_SCRATCH_BYTES compiled into libg4a.so instead of the context's
+ * workspace, and that it calls no allocator. Each GPU holds its own copy of the
+ * array, set up by g4a_create on that GPU and held until the process ends.
+ * Fails with G4A_E_UNSUPPORTED, enqueueing nothing, when the call needs more
+ * scratch than the array holds (decode: T*Hq*splits*(Dh+2)*4 bytes for more
+ * than one split; prefill: about 2*keys*Hkv*Dh*4 bytes plus the partials of
+ * split query blocks at head_dim 512; g4a_attention_plan gives the decode
+ * figure) or passes non-contiguous explicit positions (they are staged through
+ * allocated buffers). Every call on a GPU shares that GPU's array and leaves
+ * its contents behind (nothing in it needs clearing: each call writes what it
+ * reads first), so calls that overlap on one GPU race: keep them on one stream
+ * or order them with events. */
+#define G4A_NOALLOC_SCRATCH_BYTES (64u << 20)
+int g4a_attention_noalloc(g4a_ctx *ctx, const g4a_attn_args *args);
+
 /* n attention calls enqueued back-to-back on the context's stream, args[i]
  * exactly as for g4a_attention; stops at the first failing call and returns
  * its status (calls before it stay enqueued). No counterpart in the

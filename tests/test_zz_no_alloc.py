@@ -1,0 +1,112 @@
+"""g4a_attention_noalloc (the entry point that allocates nothing: its split
+partials and pre-split K/V live in the library's static scratch array) gives
+bit-identical results to g4a_attention on the same inputs, through the C-ABI:
+two calls in a row per kernel family, the second smaller than the first (so it
+runs over what the first left in the shared array), and it refuses, enqueueing
+nothing, what would need an allocation."""
+import numpy as np
+import pytest
+
+import g4a
+import g4a.synth as synth
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def step(msg):
+    print(f"[gpu] {msg}", flush=True)
+
+
+def _run_both(ctx, ins, label, **kw):
+    """Run one call through g4a_attention and g4a_attention_noalloc into separate outputs."""
+    T, Hq, Dh = ins.q.shape
+    S, Hkv, _ = ins.k.shape
+    Dv = ins.v.shape[2]
+    dev = [ctx.upload(x) for x in (ins.q, ins.k, ins.v)]
+    o1, o2 = ctx.empty((T, Hq * Dv)), ctx.empty((T, Hq * Dv))
+    args = dict(T=T, S=kw.pop("S", S), Hq=Hq, Hkv=Hkv, Dh=Dh, Dv=Dv, q_pos0=int(ins.q_pos[0]),
+                k_pos0=int(ins.k_pos[0]), **kw)
+    try:
+        plan = ctx.plan(**args)
+        step(f"{label}: kernel {g4a.KERNEL_NAMES[plan.kernel]}, {plan.splits} splits")
+        ctx.h2d(o2.ptr, np.full((T, Hq * Dv), np.nan, np.float32))
+        ctx.attention_noalloc(dev[0].ptr, dev[1].ptr, dev[2].ptr, o2.ptr, **args)
+        ctx.attention(dev[0].ptr, dev[1].ptr, dev[2].ptr, o1.ptr, **args)
+        return o1.to_host(), o2.to_host(), plan
+    finally:
+        for d in dev + [o1, o2]:
+            d.free()
+
+
+CASES = [
+    # label, (T, S, Dh, seed), extra kwargs; each pair: a larger call, then a smaller one
+    ("decode hd512 @32768 (256 splits)", (1, 32768, 512, 1), {}),
+    ("decode hd512 @9000 (streaming, fewer splits)", (1, 9000, 512, 2), {}),
+    ("sliding decode hd256 on a ring (short kernel)", (1, 5000, 256, 3), dict(window=512, ring=512)),
+    ("sliding decode hd256 @700 (short kernel)", (1, 700, 256, 4), dict(window=512)),
+    ("prefill hd512 T2048 causal (split blocks)", (2048, 2048, 512, 5), {}),
+    ("prefill hd256 T300 window 512", (300, 300, 256, 6), dict(window=512)),
+    ("generic head_dim 64, 3 queries", (3, 400, 64, 7), {}),
+    ("generic head_dim 64, 1 query", (1, 90, 64, 8), {}),
+]
+
+
+@pytest.mark.parametrize("first,second", [(0, 1), (2, 3), (4, 5), (6, 7)])
+def test_noalloc_matches_attention_twice(ctx, first, second):
+    for idx in (first, second):
+        label, (T, S, Dh, seed), kw = CASES[idx]
+        kw = dict(kw)
+        ring = kw.pop("ring", 0)
+        ins = synth.gemma_inputs(T=T, S=S, Dh=Dh, seed=seed, q_pos=np.arange(S - T, S) if T > 1 else None)
+        if ring:
+            # keep only a ring of the last `ring` positions (slot p % ring)
+            rk = np.zeros((ring, 1, Dh), np.float32)
+            rv = np.zeros((ring, 1, Dh), np.float32)
+            for p_ in range(S - ring, S):
+                rk[p_ % ring], rv[p_ % ring] = ins.k[p_], ins.v[p_]
+            full = ins
+            ins = synth.AttnInputs(full.q, rk, rv, full.q_pos, full.k_pos)
+            got, got_na, _ = _run_both(ctx, ins, label, S=S, ring_cap=ring, **kw)
+            want = oracle.attention(full.q, full.k, full.v, full.q_pos, full.k_pos, **kw)
+        else:
+            got, got_na, _ = _run_both(ctx, ins, label, **kw)
+            want = None if T * S * Dh > 2e8 else oracle.attention(ins.q, ins.k, ins.v, ins.q_pos, ins.k_pos, **kw)
+        assert np.array_equal(got_na, got), f"{label}: noalloc differs from g4a_attention"
+        if want is not None:
+            d = np.abs(got_na.astype(np.float64) - want)
+            print(f"  {label}: bit-identical; vs oracle max-abs {d.max():.3e} mean-abs {d.mean():.3e}", flush=True)
+            assert d.max() <= 1e-5 and d.mean() <= 1e-6, label
+        else:
+            print(f"  {label}: bit-identical", flush=True)
+
+
+def test_noalloc_refuses_what_needs_an_allocation(ctx):
+    ins = synth.gemma_inputs(T=1, S=300, Dh=256, seed=9)
+    k_pos = np.arange(300, dtype=np.uint32)
+    k_pos[150:] += 7  # a gap: explicit positions would have to be staged through allocated buffers
+    dev = [ctx.upload(x) for x in (ins.q, ins.k, ins.v)]
+    out = ctx.empty((1, 8 * 256))
+    try:
+        ctx.h2d(out.ptr, np.full((1, 8 * 256), 7.0, np.float32))
+        with pytest.raises(g4a.G4aError, match="contiguous positions only"):
+            ctx.attention_noalloc(dev[0].ptr, dev[1].ptr, dev[2].ptr, out.ptr, T=1, S=300, Hq=8, Hkv=1, Dh=256,
+                                  Dv=256, q_pos=np.array([310], np.uint32), k_pos=k_pos)
+        # 15 queries (decode path) over 65536 keys with 1024 forced splits: 15*8*1024*514*4 bytes
+        # of partials, beyond the array; refused before anything is enqueued
+        args = dict(T=15, S=65536, Hq=8, Hkv=1, Dh=512, Dv=512, q_pos0=65521, splits=1024)
+        plan = ctx.plan(**args)
+        assert plan.workspace_bytes > g4a.NOALLOC_SCRATCH_BYTES
+        big = ctx.malloc(65536 * 512 * 4)
+        qb, ob = ctx.malloc(15 * 8 * 512 * 4), ctx.malloc(15 * 8 * 512 * 4)
+        try:
+            with pytest.raises(g4a.G4aError, match="bytes of scratch"):
+                ctx.attention_noalloc(qb, big, big, ob, **args)
+        finally:
+            for x in (big, qb, ob):
+                ctx.free(x)
+        ctx.sync()
+        assert np.all(out.to_host() == 7.0), "a refused call wrote its output"
+    finally:
+        for d in dev + [out]:
+            d.free()
