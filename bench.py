@@ -4,8 +4,10 @@ Default workload (the BASELINE.json metric's configuration): one hd512 global
 decode step at 32K context — q [1,8,512], K/V [32768,1,512] f32, unit-RMS
 Gaussian q/k, N(0,1) v, seed 4, scale 1.0 — the global layer of configs[4].
 A step is one Backend::attention call (split-K decode + LSE combine) with
-inputs resident in HBM. K/V are rotated over 4 copies (537 MB > the 256 MB
-MALL) so every step streams from HBM.
+inputs resident in HBM. K/V copies are rotated so that a copy is re-read only
+after 512 MB of other reads (twice the 256 MB MALL): every step streams from
+HBM ("cold"); the same step on one copy read step after step is reported beside
+it ("warm").
 
 Also reported (extra keys of the same JSON line): configs[0..2] decode,
 configs[3] prefill TFLOP/s, the configs[4] 35-layer schedule in us/token, and
@@ -35,7 +37,15 @@ METRIC = "decode attn µs/step + HBM GB/s (hd512, 32K ctx); prefill attn TFLOP/s
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 FP32_MFMA_PEAK_TFLOPS = 157.3
 HQ = 8
-BUST_COPIES = 4
+# Cold measurements rotate K/V copies so that between two reads of one copy at
+# least this many other bytes are read (twice the 256 MB MALL): every step
+# streams from HBM. Warm figures use one copy, read step after step.
+COLD_REUSE_BYTES = 512 << 20
+
+
+def cold_copies(step_bytes: int) -> int:
+    """Copies to rotate so a copy is re-read only after >= COLD_REUSE_BYTES of other data."""
+    return max(2, -(-COLD_REUSE_BYTES // step_bytes) + 1)
 
 
 def decode_bytes(S_vis: int, Dh: int, Hq: int = HQ) -> int:
@@ -51,16 +61,28 @@ def prefill_flops(T: int, window: int, Dh: int, Hq: int = HQ) -> int:
 
 
 class Decode:
-    """A decode configuration resident on the GPU, with cache-busting copies of K/V."""
+    """A decode configuration resident on the GPU. `copies` K/V copies (device-to-device
+    replicas of the seeded cache) are rotated step by step; cold() sizes them so every
+    step streams from HBM, 1 gives the warm figure."""
 
-    def __init__(self, ctx, S, Dh, seed, window=0, copies=BUST_COPIES, ring_cap=0):
+    def __init__(self, ctx, S, Dh, seed, window=0, copies=1, ring_cap=0):
         self.ctx, self.S, self.Dh, self.window, self.ring_cap = ctx, S, Dh, window, ring_cap
         ins = synth.gemma_inputs(T=1, S=S, Dh=Dh, seed=seed)
         self.inputs = ins
         self.q = ctx.upload(ins.q)
-        self.kv = [(ctx.upload(ins.k), ctx.upload(ins.v)) for _ in range(copies)]
+        k0, v0 = ctx.upload(ins.k), ctx.upload(ins.v)
+        self.kv = [(k0, v0)]
+        for _ in range(copies - 1):
+            k, v = ctx.empty(k0.shape), ctx.empty(v0.shape)
+            ctx.d2d(k.ptr, k0.ptr, k0.nbytes)
+            ctx.d2d(v.ptr, v0.ptr, v0.nbytes)
+            self.kv.append((k, v))
+        ctx.sync()
         self.out = ctx.empty((1, HQ * Dh))
-        self.i = 0
+
+    @classmethod
+    def cold(cls, ctx, S, Dh, seed, window=0):
+        return cls(ctx, S, Dh, seed, window=window, copies=cold_copies(2 * S * Dh * 4))
 
     def kw(self, splits=0):
         return dict(T=1, S=self.S, Hq=HQ, Hkv=1, Dh=self.Dh, Dv=self.Dh, q_pos0=self.S - 1, k_pos0=0,
@@ -410,6 +432,39 @@ def linear_bench(ctx, op, N, K, bits, M, steps, cpu=True):
     return res
 
 
+DECODE_CONFIGS = [("configs[0] sliding hd256 S512", 512, 256, 512, 0),
+                  ("configs[1] global hd512 S8192", 8192, 512, 0, 0),
+                  ("configs[2] global hd512 S131072", 131072, 512, 0, 2)]
+
+
+def decode_configs(ctx, steps_arg, warmup_arg):
+    """configs[0..2] decode steps, cold (rotated K/V copies) with the warm figure
+    beside; configs[2] also under a forced split sweep (cold)."""
+    extras = {}
+    for name, S, Dh, W, seed in DECODE_CONFIGS:
+        b = decode_bytes(min(S, W) if W else S, Dh)
+        d = Decode.cold(ctx, S=S, Dh=Dh, seed=seed, window=W)
+        steps = max(10, steps_arg // (4 if S > 100000 else 1))
+        m, km = time_steps(ctx, d.calls(), steps, min(warmup_arg, 10))
+        pl = ctx.plan(**d.kw())
+        extras[name] = {"us_per_step": m * 1e3, "kernel_us": km * 1e3, "GB_s": b / (m * 1e-3) / 1e9,
+                        "kernel_GB_s": b / (km * 1e-3) / 1e9, "kernel": g4a.KERNEL_NAMES[pl.kernel],
+                        "splits": pl.splits, "kv_copies_rotated": len(d.kv)}
+        if S > 100000:
+            sweep = {}
+            for sp in (8, 16, 32, 64, 128, 256, 512):
+                m2, _ = time_steps(ctx, d.calls(sp), 10, 3)
+                sweep[sp] = round(m2 * 1e3, 2)
+            extras[name]["split_sweep_us"] = sweep
+        d.free()
+        w = Decode(ctx, S=S, Dh=Dh, seed=seed, window=W)
+        mw, kmw = time_steps(ctx, w.calls(), steps, min(warmup_arg, 10))
+        w.free()
+        extras[name]["warm"] = {"us_per_step": mw * 1e3, "kernel_us": kmw * 1e3, "GB_s": b / (mw * 1e-3) / 1e9}
+        print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
+    return extras
+
+
 def load_traffic():
     p = REPO / "profiles" / "decode_hd512_s32768_traffic.json"
     if p.exists():
@@ -427,7 +482,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="headline decode only (no extras, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "schedule", "producer", "batch", "linear"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "schedule", "producer", "batch", "linear"], default=None,
                     help="run only these extra workloads (for profiling) and print their JSON line")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="first run 3 device-to-device copies of MIB MiB (the reference dispatch for "
@@ -444,7 +499,9 @@ def main(argv=None):
 
     if args.only:
         out = {}
-        if args.only == "prefill":
+        if args.only == "decode":
+            out.update(decode_configs(ctx, args.steps, args.warmup))
+        elif args.only == "prefill":
             for name, T, Dh, W in PREFILL_CONFIGS:
                 out[name] = prefill(ctx, T, Dh, W, steps=args.steps, warmup=args.warmup)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
@@ -476,11 +533,15 @@ def main(argv=None):
         ctx.free(a)
         ctx.free(b)
 
-    # ---- headline: hd512 global decode at 32K context ----
-    head = Decode(ctx, S=32768, Dh=512, seed=4)
+    # ---- headline: hd512 global decode at 32K context (cold: rotated K/V copies) ----
+    head = Decode.cold(ctx, S=32768, Dh=512, seed=4)
     ms, kms = time_steps(ctx, head.calls(), args.steps, args.warmup)
     plan = ctx.plan(**head.kw())
+    head_copies = len(head.kv)
     head.free()
+    warm = Decode(ctx, S=32768, Dh=512, seed=4)
+    ms_warm, kms_warm = time_steps(ctx, warm.calls(), max(10, args.steps // 2), min(args.warmup, 20))
+    warm.free()
     algo = decode_bytes(32768, 512)
     gbs = algo / (ms * 1e-3) / 1e9
     kernel_gbs = algo / (kms * 1e-3) / 1e9
@@ -505,8 +566,11 @@ def main(argv=None):
             "workload": "hd512 global decode @ 32K context (global layer of configs[4])",
             "q": [1, 8, 512], "kv": [32768, 1, 512], "scale": 1.0, "window": 0,
             "splits": plan.splits, "keys_per_split": plan.keys_per_split,
-            "cache_busting": f"{BUST_COPIES} K/V copies rotated",
+            "cache_busting": f"{head_copies} K/V copies rotated (a copy is re-read after "
+                             f"{(head_copies - 1) * 2 * 32768 * 512 * 4 / 1e6:.0f} MB of other reads)",
         },
+        "warm": {"us_per_step": ms_warm * 1e3, "kernel_us": kms_warm * 1e3,
+                 "GB_s": algo / (ms_warm * 1e-3) / 1e9, "note": "one K/V copy read step after step"},
         "roofline": {
             "bound": "hbm",
             "kernel": "g4a_decode_d512_g8",
@@ -515,32 +579,18 @@ def main(argv=None):
             "unit": "GB/s",
             "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
             "traffic": load_traffic(),
+            "traffic_source": "stored: profiles/decode_hd512_s32768_traffic.json (rocprofv3 FETCH_SIZE and "
+                              "WRITE_SIZE runs of this workload, scaled by a device copy's counters); "
+                              "not measured in this run",
             "algorithmic_bytes_per_launch": algo,
             "kernel_us": kms * 1e3,
+            "kernel_us_source": "dispatch-attached HIP events on the launch stream, mean over the timed steps",
         },
     }
 
     if not args.quick:
         extras = {}
-        for name, S, Dh, W, seed in [("configs[0] sliding hd256 S512", 512, 256, 512, 0),
-                                     ("configs[1] global hd512 S8192", 8192, 512, 0, 0),
-                                     ("configs[2] global hd512 S131072", 131072, 512, 0, 2)]:
-            d = Decode(ctx, S=S, Dh=Dh, seed=seed, window=W, copies=1 if S > 100000 else BUST_COPIES)
-            steps = max(10, args.steps // (4 if S > 100000 else 1))
-            m, km = time_steps(ctx, d.calls(), steps, min(args.warmup, 10))
-            b = decode_bytes(d.visible(), Dh)
-            pl = ctx.plan(**d.kw())
-            extras[name] = {"us_per_step": m * 1e3, "kernel_us": km * 1e3, "GB_s": b / (m * 1e-3) / 1e9,
-                            "kernel_GB_s": b / (km * 1e-3) / 1e9, "kernel": g4a.KERNEL_NAMES[pl.kernel],
-                            "splits": pl.splits}
-            if S > 100000:
-                sweep = {}
-                for sp in (8, 16, 32, 64, 128, 256, 512):
-                    m2, _ = time_steps(ctx, d.calls(sp), 10, 3)
-                    sweep[sp] = round(m2 * 1e3, 2)
-                extras[name]["split_sweep_us"] = sweep
-            d.free()
-            print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
+        extras.update(decode_configs(ctx, args.steps, args.warmup))
         for name, T, Dh, W in PREFILL_CONFIGS:
             extras[name] = prefill(ctx, T, Dh, W, steps=5, warmup=2)
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)

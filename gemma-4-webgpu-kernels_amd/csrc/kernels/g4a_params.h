@@ -25,7 +25,7 @@ struct G4aDecodeParams {
     uint32_t q_pos0, k_pos0;
     uint32_t T, Hq, Hkv;
     uint32_t k_start, k_end;
-    uint32_t keys_per_split, nsplit;
+    uint32_t keys_per_split, nsplit;  // the 8-head streaming kernel deals tiles round-robin over nsplit instead
     uint32_t ring_cap;
     uint32_t window;
     float scale, softcap;
