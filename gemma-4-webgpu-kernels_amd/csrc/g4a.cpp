@@ -29,6 +29,13 @@ namespace {
 constexpr uint32_t TILE = 64;
 // Query tokens from which the query-tiled prefill kernel replaces decode.
 constexpr uint32_t PREFILL_MIN_T = 16;
+// The prefill's exact-rescoring band: tau = max(MIN, ln(N) + LOGN) for N keys per
+// row, so the keys left with their estimated scores hold at most a weight share
+// ~e^-LOGN of a row: their score errors (~5e-6 rms, 6e-5 max, from the scaled
+// fp16 splits and the matrix cores' summation order) then move the row's output
+// by ~1e-5 * e^-LOGN * max|v - out| even when all of them push the same way.
+constexpr float PREFILL_TAU_MIN = 7.0f;
+constexpr float PREFILL_TAU_LOGN = 2.0f;
 // Largest split-K count the LSE combine kernel takes (its LDS weight table).
 constexpr uint32_t MAX_SPLITS = 1024;
 // Split counts merged by the one-block-per-head combine kernel (combine_rows).
@@ -735,9 +742,13 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
         pp.ring_cap = a->kv_ring_cap;
         pp.window = a->sliding_window;
         pp.scale = a->scale;
-        // rescoring band: the keys left with their estimated score carry a weight share of at
-        // most N e^-tau / (1 + N e^-tau) for N keys per row, kept below e^-4.5
-        pp.tau = std::max(12.0f, logf(float(std::max(pl.k_end - pl.k_start, 1u))) + 4.5f);
+        // rescoring band: the keys left with their estimated score (N of them in a row at
+        // most) carry a weight share of at most N e^-tau / (1 + N e^-tau)
+        {
+            uint32_t n_row = pl.k_end - pl.k_start;
+            if (a->sliding_window) n_row = std::min(n_row, a->sliding_window);
+            pp.tau = std::max(PREFILL_TAU_MIN, logf(float(std::max(n_row, 1u))) + PREFILL_TAU_LOGN);
+        }
         // 8-wave workgroups over 8 queries; scores estimated from bf16 hi/lo splits of K,
         // P.V from fp16 hi/lo splits of V, both made by a pre-pass into the workspace.
         // head_dim 256: two waves per 16-row block take the even / odd key tiles;
@@ -746,13 +757,15 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
         {
             // keys [k_start, k_end) widened to multiples of 16 (the kernel's tile grid);
             // workspace: the V range flag (first 256 bytes), then the K and V splits,
-            // then (head_dim 512) the partials of the split query blocks
+            // the K rows' scale factors, then (head_dim 512) the partials of the split
+            // query blocks
             const uint32_t k0 = pl.k_start & ~15u, nkeys = ((pl.k_end + 15u) & ~15u) - k0;
             const size_t half = size_t(nkeys) * a->Hkv * a->Dh * sizeof(float);
+            const size_t kscale_bytes = size_t(a->Hkv) * (nkeys / 16) * sizeof(float);
             if (d512) pp.nbig = prefill_split_blocks(a, pp.q_pos0, pp.k_pos0);
             // a split block's partial: 8 waves x (O of 16 rows x 256 dims, then l and m of the rows)
             const size_t part_bytes = size_t(pp.nbig) * a->Hkv * 2 * 8 * (4 * 16 * 64 + 32) * sizeof(float);
-            const size_t part_off = (256 + 2 * half + 255) & ~size_t(255);
+            const size_t part_off = (256 + 2 * half + kscale_bytes + 255) & ~size_t(255);
             void* wsp = nullptr;
             if (int rc = call_workspace(ctx, part_off + part_bytes, noalloc, &wsp)) return rc;
             char* const ws = static_cast<char*>(wsp);
@@ -761,6 +774,7 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
             sp.v = a->v;
             sp.kout = reinterpret_cast<float*>(ws + 256);
             sp.vout = reinterpret_cast<float*>(ws + 256 + half);
+            sp.kscale = reinterpret_cast<float*>(ws + 256 + 2 * half);
             sp.vflag = reinterpret_cast<uint32_t*>(ws);
             sp.k0 = k0;
             sp.nkeys = nkeys;
@@ -771,11 +785,14 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
             sp.epoch = next_split_epoch();
             sp.vis_lo = pl.k_start;
             sp.vis_hi = pl.k_end;
-            const uint64_t threads = uint64_t(nkeys) * a->Hkv * (a->Dh / 8) + uint64_t(nkeys / 4) * a->Hkv * (a->Dh / 64) * 16;
-            if (int rc = launch(ctx, ctx->split_kv, dim3(uint32_t((threads + 255) / 256), 1, 1), dim3(256, 1, 1), sp,
+            // one block per (16-key tile, kv head) for K, then one thread per 4 dims of a V key quad
+            const uint64_t vthreads = uint64_t(nkeys / 4) * a->Hkv * (a->Dh / 64) * 16;
+            const uint64_t blocks = uint64_t(nkeys / 16) * a->Hkv + (vthreads + 255) / 256;
+            if (int rc = launch(ctx, ctx->split_kv, dim3(uint32_t(blocks), 1, 1), dim3(256, 1, 1), sp,
                                 "split K/V"))
                 return rc;
             pp.ksplit = sp.kout;
+            pp.kscale = sp.kscale;
             pp.vsplit = sp.vout;
             pp.vflag = sp.vflag;
             pp.split0 = k0;

@@ -64,19 +64,48 @@ __device__ __forceinline__ void wave_sync() {
 // tiles sit in LDS (global->LDS copies of the next pair in flight meanwhile). At
 // the end each wave compacts its candidates against the maximum over both
 // parities, corrects them exactly, and the parities merge through LDS.
-typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 
-// x = hi + lo + O(2^-16 |x|): hi = bf16(x), lo = bf16(x - hi), both rounded to nearest even.
-__device__ __forceinline__ void split8(const float4& x0, const float4& x1, bf8v& hi, bf8v& lo) {
+// The exponent a that puts values whose largest magnitude is mx into
+// [2^14, 2^15) once divided by 2^a (mx = 0 gives any a; the values stay 0).
+__device__ __forceinline__ int fp16_scale_exp(float mx) { return __builtin_amdgcn_frexp_expf(mx) - 15; }
+
+// x * 2^-a = hi + lo + O(2^-22 |x * 2^-a|): hi = fp16(x 2^-a), lo = fp16(x 2^-a - hi), both
+// rounded to nearest even; the scaling by a power of two is exact.
+__device__ __forceinline__ void split8h(const float4& x0, const float4& x1, int a, h8v& hi, h8v& lo) {
     const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        hi[i] = (__bf16)x[i];
-        lo[i] = (__bf16)(x[i] - (float)hi[i]);
+        const float y = ldexpf(x[i], -a);
+        hi[i] = (_Float16)y;
+        lo[i] = (_Float16)(y - (float)hi[i]);
     }
 }
 
-typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+// The largest of the wave's 64 non-negative values, as a scalar: read lane by
+// lane (once per kernel; a butterfly of shuffles here would share its lane-index
+// registers with the tile loop's shuffles and keep them live across it).
+__device__ __forceinline__ float wave_max_scalar(float x) {
+    uint32_t m = 0;
+    const int bits = __float_as_int(x);
+#pragma unroll
+    for (int l = 0; l < 64; ++l) m = max(m, (uint32_t)__builtin_amdgcn_readlane(bits, l));
+    return __int_as_float((int)m);
+}
+
+__device__ __forceinline__ float absmax8(const float4& x0, const float4& x1) {
+    return fmaxf(fmaxf(fmaxf(fabsf(x0.x), fabsf(x0.y)), fmaxf(fabsf(x0.z), fabsf(x0.w))),
+                 fmaxf(fmaxf(fabsf(x1.x), fabsf(x1.y)), fmaxf(fabsf(x1.z), fabsf(x1.w))));
+}
+
+// The factor 2^a the split K rows of the 16-key tile starting at key t0 were
+// divided by (a scalar load: the address is uniform).
+__device__ __forceinline__ float tile_kscale(const G4aPrefillParams& p, uint32_t kvh, int32_t t0) {
+    typedef const __attribute__((address_space(4))) float cfloat;
+    const uint32_t idx = kvh * (p.split_n / 16) + ((uint32_t)t0 - p.split0) / 16;
+    return ((cfloat*)p.kscale)[__builtin_amdgcn_readfirstlane(idx)];
+}
 
 // x = hi + lo + O(2^-22 |x|) (for |x| >= 2^-3; below, an absolute 2^-25):
 // hi = fp16(x), lo = fp16(x - hi), both rounded to nearest even.
@@ -86,14 +115,17 @@ __device__ __forceinline__ void split16(float x, h4v& hi, h4v& lo, int i) {
     lo[i] = (_Float16)(x - (float)h);
 }
 
-// The G4aSplitParams pre-pass: K rows -> bf16 hi/lo pairs (one thread per
-// 8-dim block), then V key quads -> fp16 hi/lo pairs (one thread per 4 dims
-// 64c + 4n .. +3 of a quad), flagging V values outside the fp16 range.
+// The G4aSplitParams pre-pass. Blocks [0, nkeys/16 * Hkv) split K: one
+// 256-thread block per (16-key tile, kv head) finds the tile's largest |k|,
+// scales the tile by the power of two that puts it in [2^14, 2^15) and writes
+// fp16 hi/lo pairs (items = 8-dim blocks of the tile's rows, strided over the
+// threads). The blocks after them split V key quads into fp16 hi/lo pairs (one
+// thread per 4 dims 64c + 4n .. +3 of a quad), flagging V values outside the
+// fp16 range.
 __device__ __forceinline__ void split_kv(const G4aSplitParams& p) {
     const uint32_t nbk = p.Dh / 8, nc = p.Dh / 64;
-    const size_t nk_items = (size_t)p.nkeys * p.Hkv * nbk;
+    const uint32_t kblocks = (p.nkeys / 16) * p.Hkv;
     const size_t nv_items = (size_t)(p.nkeys / 4) * p.Hkv * nc * 16;
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     auto row_of = [&](size_t jj) -> size_t {  // physical row of key k0 + jj
         uint32_t j = p.k0 + (uint32_t)jj;
         if (!p.ring_cap && j >= p.S) j = p.S - 1;
@@ -104,21 +136,48 @@ __device__ __forceinline__ void split_kv(const G4aSplitParams& p) {
         return j >= p.vis_lo && j < p.vis_hi;
     };
     const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (i < nk_items) {
-        const uint32_t b = (uint32_t)(i % nbk);
-        const size_t rh = i / nbk;
-        const uint32_t h = (uint32_t)(rh % p.Hkv);
-        const size_t jj = rh / p.Hkv;
-        const float* src = p.k + (row_of(jj) * p.Hkv + h) * p.Dh + 8 * b;
-        const bool in = seen(jj);
-        bf8v hi, lo;
-        split8(in ? ld4(src) : zero4, in ? ld4(src + 4) : zero4, hi, lo);
-        float* dst = p.kout + (jj * p.Hkv + h) * p.Dh + 8 * b;
-        *reinterpret_cast<bf8v*>(dst) = hi;
-        *reinterpret_cast<bf8v*>(dst + 4) = lo;
+    if (blockIdx.x < kblocks) {
+        constexpr int MAXI = 4;  // items per thread: 16 rows x Dh/8 blocks over 256 threads (Dh <= 512)
+        __shared__ float redmax[4];
+        const uint32_t tile = blockIdx.x / p.Hkv, h = blockIdx.x % p.Hkv;
+        const uint32_t nitems = 16 * nbk;
+        float4 x0[MAXI], x1[MAXI];
+        float mx = 0.0f;
+#pragma unroll
+        for (int u = 0; u < MAXI; ++u) {
+            const uint32_t it = threadIdx.x + 256 * u;
+            x0[u] = x1[u] = zero4;
+            if (it < nitems) {
+                const size_t jj = (size_t)tile * 16 + it / nbk;
+                if (seen(jj)) {
+                    const float* src = p.k + (row_of(jj) * p.Hkv + h) * p.Dh + 8 * (it % nbk);
+                    x0[u] = ld4(src);
+                    x1[u] = ld4(src + 4);
+                }
+                mx = fmaxf(mx, absmax8(x0[u], x1[u]));
+            }
+        }
+        mx = g4a_wave_max(mx);
+        if ((threadIdx.x & 63) == 0) redmax[threadIdx.x >> 6] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(redmax[0], redmax[1]), fmaxf(redmax[2], redmax[3]));
+        const int a = fp16_scale_exp(mx);
+#pragma unroll
+        for (int u = 0; u < MAXI; ++u) {
+            const uint32_t it = threadIdx.x + 256 * u;
+            if (it < nitems) {
+                const size_t jj = (size_t)tile * 16 + it / nbk;
+                h8v hi, lo;
+                split8h(x0[u], x1[u], a, hi, lo);
+                float* dst = p.kout + (jj * p.Hkv + h) * p.Dh + 8 * (it % nbk);
+                *reinterpret_cast<h8v*>(dst) = hi;
+                *reinterpret_cast<h8v*>(dst + 4) = lo;
+            }
+        }
+        if (threadIdx.x == 0) p.kscale[h * (p.nkeys / 16) + tile] = ldexpf(1.0f, a);
         return;
     }
-    i -= nk_items;
+    size_t i = (size_t)(blockIdx.x - kblocks) * blockDim.x + threadIdx.x;
     if (i >= nv_items) return;
     const uint32_t n = (uint32_t)(i % 16);
     size_t t = i / 16;
@@ -219,14 +278,26 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
     const uint32_t myq = qw + (rl >> 3);
     const bool qvalid = myq < p.T;
     const int32_t my_lo = key_lo(myq), my_hi = qvalid ? key_hi(myq) : 0;
-    // q rows in the B layout of v_mfma_f32_16x16x32_bf16, split into bf16 hi/lo:
-    // lane (g, rl) holds row rl's dims 32kb + 8g .. +7
+    // q rows in the B layout of v_mfma_f32_16x16x32_f16, split into fp16 hi/lo of
+    // q * 2^-aq (aq per wave: its largest |q 2^-aq| in [2^14, 2^15)): lane (g, rl)
+    // holds row rl's dims 32kb + 8g .. +7
     constexpr int QB = DH / 32;
-    bf8v qh[QB], ql[QB];
+    h8v qh[QB], ql[QB];
+    float qsc;  // 2^aq
     {
         const float* qrow = p.q + ((size_t)min(myq, p.T - 1) * p.Hq + h0 + (rl & 7)) * DH + 8 * g;
+        float4 qa[QB], qb4[QB];
+        float mx = 0.0f;
 #pragma unroll
-        for (int kb = 0; kb < QB; ++kb) split8(ld4(qrow + 32 * kb), ld4(qrow + 32 * kb + 4), qh[kb], ql[kb]);
+        for (int kb = 0; kb < QB; ++kb) {
+            qa[kb] = ld4(qrow + 32 * kb);
+            qb4[kb] = ld4(qrow + 32 * kb + 4);
+            mx = fmaxf(mx, absmax8(qa[kb], qb4[kb]));
+        }
+        const int aq = fp16_scale_exp(wave_max_scalar(mx));
+        qsc = ldexpf(1.0f, aq);
+#pragma unroll
+        for (int kb = 0; kb < QB; ++kb) split8h(qa[kb], qb4[kb], aq, qh[kb], ql[kb]);
     }
     const float* __restrict__ ksbase = p.ksplit + (size_t)kvh * DH;
     static_assert(DH == 256, "the V quads of a tile are 16 1 KiB pieces");
@@ -474,29 +545,31 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         const float* Kt = smem + (st & 1) * 2 * C::TILE + par * C::TILE;
         const float* Vt = Kt + BK * KRS;
 
-        // score estimate S^T = K Q^T from the bf16 splits: Khi Qhi + Klo Qhi + Khi Qlo
-        // (error ~2^-16 relative per term), three independent accumulators.
-        // Lane (g, rl) reads key rl's 8-dim block 4kb + g: hi then lo, 16 bytes each.
+        // score estimate S^T = K Q^T from the scaled fp16 splits: Khi Qhi + Klo Qhi + Khi Qlo
+        // (error ~2^-21 relative per term), three independent accumulators, then the
+        // wave's and the tile's powers of two. Lane (g, rl) reads key rl's 8-dim block
+        // 4kb + g: hi then lo, 16 bytes each.
         f4v SA[3];
 #pragma unroll
         for (int a = 0; a < 3; ++a) SA[a] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
         const float* kr = Kt + rl * KRS + 8 * g;
 #pragma unroll
         for (int kb = 0; kb < QB; ++kb) {
-            const bf8v khi = *reinterpret_cast<const bf8v*>(kr + 32 * kb);
-            const bf8v klo = *reinterpret_cast<const bf8v*>(kr + 32 * kb + 4);
-            SA[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qh[kb], SA[0], 0, 0, 0);
-            SA[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, qh[kb], SA[1], 0, 0, 0);
-            SA[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, ql[kb], SA[2], 0, 0, 0);
+            const h8v khi = *reinterpret_cast<const h8v*>(kr + 32 * kb);
+            const h8v klo = *reinterpret_cast<const h8v*>(kr + 32 * kb + 4);
+            SA[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi, qh[kb], SA[0], 0, 0, 0);
+            SA[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(klo, qh[kb], SA[1], 0, 0, 0);
+            SA[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi, ql[kb], SA[2], 0, 0, 0);
         }
         const f4v S = (SA[0] + SA[1]) + SA[2];
+        const float sc = qsc * tile_kscale(p, kvh, t0);  // a power of two: exact
         float s[4];
         bool vis[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int32_t j = t0 + 4 * g + r;
             vis[r] = j >= my_lo && j < my_hi;
-            s[r] = vis[r] ? S[r] * p.scale : NEG_INF;
+            s[r] = vis[r] ? (S[r] * sc) * p.scale : NEG_INF;
         }
         float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
         tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
@@ -751,13 +824,25 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
     const uint32_t myq = qw + (rl >> 3);
     const bool qvalid = myq < p.T;
     const int32_t my_lo = key_lo(myq), my_hi = qvalid ? key_hi(myq) : 0;
-    // this wave's half of the q rows in the B layout of v_mfma_f32_16x16x32_bf16,
-    // split into bf16 hi/lo: lane (g, rl) holds row rl's dims HD*dhf + 32kb + 8g .. +7
-    bf8v qh[QBH], ql[QBH];
+    // this wave's half of the q rows in the B layout of v_mfma_f32_16x16x32_f16, split
+    // into fp16 hi/lo of q * 2^-aq (aq per wave: its largest |q 2^-aq| in
+    // [2^14, 2^15)): lane (g, rl) holds row rl's dims HD*dhf + 32kb + 8g .. +7
+    h8v qh[QBH], ql[QBH];
+    float qsc;  // 2^aq
     {
         const float* qrow = p.q + ((size_t)min(myq, p.T - 1) * p.Hq + h0 + (rl & 7)) * DH + HD * dhf + 8 * g;
+        float4 qa[QBH], qb4[QBH];
+        float mx = 0.0f;
 #pragma unroll
-        for (int kb = 0; kb < QBH; ++kb) split8(ld4(qrow + 32 * kb), ld4(qrow + 32 * kb + 4), qh[kb], ql[kb]);
+        for (int kb = 0; kb < QBH; ++kb) {
+            qa[kb] = ld4(qrow + 32 * kb);
+            qb4[kb] = ld4(qrow + 32 * kb + 4);
+            mx = fmaxf(mx, absmax8(qa[kb], qb4[kb]));
+        }
+        const int aq = fp16_scale_exp(wave_max_scalar(mx));
+        qsc = ldexpf(1.0f, aq);
+#pragma unroll
+        for (int kb = 0; kb < QBH; ++kb) split8h(qa[kb], qb4[kb], aq, qh[kb], ql[kb]);
     }
     const float* __restrict__ ksbase = p.ksplit + (size_t)kvh * DH;
 
@@ -993,20 +1078,24 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
         const float* const Vt = Kt + BK * KRS;
         f4v Sp = f4v{0.0f, 0.0f, 0.0f, 0.0f};
         if (act) {
-            // this wave's half of S^T = K Q^T from the bf16 splits: Khi Qhi + Klo Qhi + Khi Qlo
+            // this wave's half of S^T = K Q^T from the scaled fp16 splits: Khi Qhi + Klo Qhi +
+            // Khi Qlo, then the wave's and the tile's powers of two
             f4v SA[3];
 #pragma unroll
             for (int a = 0; a < 3; ++a) SA[a] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
             const float* kr = Kt + rl * KRS + HD * dhf + 8 * g;
 #pragma unroll
             for (int kb = 0; kb < QBH; ++kb) {
-                const bf8v khi = *reinterpret_cast<const bf8v*>(kr + 32 * kb);
-                const bf8v klo = *reinterpret_cast<const bf8v*>(kr + 32 * kb + 4);
-                SA[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qh[kb], SA[0], 0, 0, 0);
-                SA[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, qh[kb], SA[1], 0, 0, 0);
-                SA[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, ql[kb], SA[2], 0, 0, 0);
+                const h8v khi = *reinterpret_cast<const h8v*>(kr + 32 * kb);
+                const h8v klo = *reinterpret_cast<const h8v*>(kr + 32 * kb + 4);
+                SA[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi, qh[kb], SA[0], 0, 0, 0);
+                SA[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(klo, qh[kb], SA[1], 0, 0, 0);
+                SA[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi, ql[kb], SA[2], 0, 0, 0);
             }
             Sp = (SA[0] + SA[1]) + SA[2];
+            const float sc = qsc * tile_kscale(p, kvh, t0);  // a power of two: exact
+#pragma unroll
+            for (int r = 0; r < 4; ++r) Sp[r] = Sp[r] * sc;
             xs[w * 64 + lane] = make_float4(Sp[0], Sp[1], Sp[2], Sp[3]);
         }
         barrier_lds();  // both halves of every active pair are in the exchange slots

@@ -97,8 +97,9 @@ struct G4aPrefillParams {
     const float* k;        // [rows, Hkv, Dh]
     const float* v;        // [rows, Hkv, Dh]
     float* out;            // [T, Hq*Dh]
-    // head_dim 256: keys [split0, split0 + split_n) pre-split by g4a_split_kv (G4aSplitParams)
-    const float* ksplit;   // K rows as bf16 hi/lo pairs
+    // keys [split0, split0 + split_n) pre-split by g4a_split_kv (G4aSplitParams)
+    const float* ksplit;   // K rows, scaled by their kscale^-1, as fp16 hi/lo pairs
+    const float* kscale;   // [Hkv][split_n / 16]: the power of two each split 16-key tile was divided by
     const float* vsplit;   // V key quads as fp16 hi/lo pairs
     const uint32_t* vflag; // == epoch: some V value is outside the fp16 split's range
     uint32_t T, S, Hq, Hkv;
@@ -120,8 +121,14 @@ struct G4aPrefillParams {
 // read through the ring; keys past the cache re-read its last row), k0 and
 // nkeys multiples of 16.
 //   kout: key j -> row j - k0 (Hkv * Dh 4-byte slots); each 8-dim block of a
-//         head is 8 slots: 8 bf16 hi parts, then 8 bf16 lo parts (hi = bf16(x),
-//         lo = bf16(x - hi), both rounded to nearest even);
+//         head is 8 slots: 8 fp16 hi parts, then 8 fp16 lo parts of x' = x * 2^-a
+//         (hi = fp16(x'), lo = fp16(x' - hi), both rounded to nearest even),
+//         with a per (16-key tile, head) chosen so the tile's largest |x'| lies in
+//         [2^14, 2^15): no fp16 overflow, and only values below 2^-17 of the
+//         tile's largest reach fp16's subnormals (an absolute error of 2^-39 of
+//         that largest);
+//   kscale: [Hkv][nkeys / 16] the factor 2^a of tile i (keys k0 + 16i ..) of
+//         head h at h * (nkeys / 16) + i;
 //   vout: keys 4i .. 4i+3 (relative to k0) of head h form a 4*Dh-slot block at
 //         (i * Hkv + h) * 4 * Dh; dim 64c + 4n + e of it sits at slots
 //         4 * ((4c + e) * 16 + n) .. +3: the 4 keys' fp16 hi parts, then their
@@ -136,6 +143,7 @@ struct G4aSplitParams {
     const float* k;        // [rows, Hkv, Dh]
     const float* v;        // [rows, Hkv, Dh]
     float* kout;
+    float* kscale;
     float* vout;
     uint32_t* vflag;
     uint32_t k0, nkeys, S, Hkv, Dh;
