@@ -1154,8 +1154,11 @@ __device__ __forceinline__ void combine(const G4aCombineParams& p, uint32_t qi) 
 // The same merge for up to COMBINE_ROW_SPLITS splits, one block per (head,
 // query): wave 0 computes the split weights into LDS, then thread t sums dims
 // t (+256) over the splits in split order, 8 loads in flight. A block per 16
-// dims would leave most of its threads idle at these split counts.
+// dims would leave most of its threads idle at these split counts. The first
+// COMBINE_ROW_EARLY splits' partials are loaded before the weights are known,
+// so a short decode's merge pays one memory round trip, not two.
 constexpr uint32_t COMBINE_ROW_SPLITS = 64;
+constexpr uint32_t COMBINE_ROW_EARLY = 16;
 
 template <int DH>
 __device__ __forceinline__ void combine_rows(const G4aCombineParams& p, uint32_t h, uint32_t qi) {
@@ -1164,14 +1167,24 @@ __device__ __forceinline__ void combine_rows(const G4aCombineParams& p, uint32_t
     const int tid = threadIdx.x;
     const size_t ih = (size_t)qi * p.Hq + h;
     const uint32_t ns = p.nsplit;
+    const uint32_t early = ns < COMBINE_ROW_EARLY ? ns : COMBINE_ROW_EARLY;
+    // wave 0's (m, l) loads go first: the wait for them then leaves the early partials in flight
+    const bool on = (uint32_t)tid < ns && tid < 64;
+    float2 mls = make_float2(NEG_INF, 0.0f);
+    if (on) mls = reinterpret_cast<const float2*>(p.part + (size_t)p.T * p.Hq * ns * DH + ih * ns * 2)[tid];
+    float x0[DH / 256][COMBINE_ROW_EARLY];
+#pragma unroll
+    for (int e = 0; e < DH / 256; ++e) {
+        const float* __restrict__ acc = p.part + part_index<DH>(ih, ns, 0, 256 * e + tid);
+#pragma unroll
+        for (uint32_t u = 0; u < COMBINE_ROW_EARLY; ++u)  // ns >= 1: the clamped loads stay in the split range
+            x0[e][u] = acc[(size_t)(u < early ? u : early - 1) * 16];
+    }
     if (tid < 64) {
-        const float* __restrict__ ml = p.part + (size_t)p.T * p.Hq * ns * DH + ih * ns * 2;
-        const bool on = (uint32_t)tid < ns;
-        const float ms = on ? ml[2 * tid] : NEG_INF;
-        const float M = wave_max(ms);
-        const float e = (ms == NEG_INF) ? 0.0f : expf(ms - M);
+        const float M = wave_max(mls.x);
+        const float e = (mls.x == NEG_INF) ? 0.0f : expf(mls.x - M);
         if (on) wgt[tid] = e;
-        const float L = wave_sum(on ? ml[2 * tid + 1] * e : 0.0f);
+        const float L = wave_sum(on ? mls.y * e : 0.0f);
         if (tid == 0) lsum = L;
     }
     __syncthreads();
@@ -1181,7 +1194,10 @@ __device__ __forceinline__ void combine_rows(const G4aCombineParams& p, uint32_t
         const uint32_t d = 256 * e + tid;
         const float* __restrict__ acc = p.part + part_index<DH>(ih, ns, 0, d);  // split s at acc[16 s]
         float A = 0.0f;
-        uint32_t s = 0;
+#pragma unroll
+        for (uint32_t u = 0; u < COMBINE_ROW_EARLY; ++u)
+            if (u < early) A += x0[e][u] * wgt[u];
+        uint32_t s = early;
         for (; s + 8 <= ns; s += 8) {
             float x[8];
 #pragma unroll
