@@ -75,74 +75,76 @@ __device__ __forceinline__ size_t part_index(size_t ih, uint32_t nsplit, uint32_
 // multiply is a single v_mul_f32_dpp; the leading s_nop covers the 2 wait
 // states a DPP read needs after a VALU write of its source.
 __device__ __forceinline__ void qk_dims16(float (&s)[2], float q0, float q1, const float4 (&k)[4]) {
-    float t0, t1;
+    // the multiplies of a dimension are issued before the adds of the one before
+    // it (two rotating temporary pairs), so no add waits for its own multiply
+    float t0a, t0b, t1a, t1b;
     asm volatile(
         "s_nop 1\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k0] row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k0] row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k1] row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k1] row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k2] row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k2] row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k3] row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k3] row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k4] row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k4] row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k5] row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k5] row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k6] row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k6] row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k7] row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k7] row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k8] row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k8] row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k9] row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k9] row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k10] row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k10] row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k11] row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k11] row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k12] row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k12] row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k13] row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k13] row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k14] row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k14] row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        "v_mul_f32_dpp %[t0], %[q0], %[k15] row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
-        "v_mul_f32_dpp %[t1], %[q1], %[k15] row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a0], %[a0], %[t0]\n\t"
-        "v_add_f32 %[a1], %[a1], %[t1]\n\t"
-        : [a0] "+v"(s[0]), [a1] "+v"(s[1]), [t0] "=&v"(t0), [t1] "=&v"(t1)
+        "v_mul_f32_dpp %[t0a], %[q0], %[k0] row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t0b], %[q1], %[k0] row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1a], %[q0], %[k1] row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1b], %[q1], %[k1] row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t0b]\n\t"
+        "v_mul_f32_dpp %[t0a], %[q0], %[k2] row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t0b], %[q1], %[k2] row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t1a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1b]\n\t"
+        "v_mul_f32_dpp %[t1a], %[q0], %[k3] row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1b], %[q1], %[k3] row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t0b]\n\t"
+        "v_mul_f32_dpp %[t0a], %[q0], %[k4] row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t0b], %[q1], %[k4] row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t1a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1b]\n\t"
+        "v_mul_f32_dpp %[t1a], %[q0], %[k5] row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1b], %[q1], %[k5] row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t0b]\n\t"
+        "v_mul_f32_dpp %[t0a], %[q0], %[k6] row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t0b], %[q1], %[k6] row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t1a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1b]\n\t"
+        "v_mul_f32_dpp %[t1a], %[q0], %[k7] row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1b], %[q1], %[k7] row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t0b]\n\t"
+        "v_mul_f32_dpp %[t0a], %[q0], %[k8] row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t0b], %[q1], %[k8] row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t1a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1b]\n\t"
+        "v_mul_f32_dpp %[t1a], %[q0], %[k9] row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1b], %[q1], %[k9] row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t0b]\n\t"
+        "v_mul_f32_dpp %[t0a], %[q0], %[k10] row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t0b], %[q1], %[k10] row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t1a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1b]\n\t"
+        "v_mul_f32_dpp %[t1a], %[q0], %[k11] row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1b], %[q1], %[k11] row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t0b]\n\t"
+        "v_mul_f32_dpp %[t0a], %[q0], %[k12] row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t0b], %[q1], %[k12] row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t1a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1b]\n\t"
+        "v_mul_f32_dpp %[t1a], %[q0], %[k13] row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1b], %[q1], %[k13] row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t0b]\n\t"
+        "v_mul_f32_dpp %[t0a], %[q0], %[k14] row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t0b], %[q1], %[k14] row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t1a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1b]\n\t"
+        "v_mul_f32_dpp %[t1a], %[q0], %[k15] row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1b], %[q1], %[k15] row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a0], %[a0], %[t0a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t0b]\n\t"
+        "v_add_f32 %[a0], %[a0], %[t1a]\n\t"
+        "v_add_f32 %[a1], %[a1], %[t1b]\n\t"
+        : [a0] "+v"(s[0]), [a1] "+v"(s[1]), [t0a] "=&v"(t0a), [t0b] "=&v"(t0b), [t1a] "=&v"(t1a), [t1b] "=&v"(t1b)
         : [q0] "v"(q0), [q1] "v"(q1), [k0] "v"(k[0].x), [k1] "v"(k[0].y), [k2] "v"(k[0].z), [k3] "v"(k[0].w), [k4] "v"(k[1].x), [k5] "v"(k[1].y), [k6] "v"(k[1].z), [k7] "v"(k[1].w), [k8] "v"(k[2].x), [k9] "v"(k[2].y), [k10] "v"(k[2].z), [k11] "v"(k[2].w), [k12] "v"(k[3].x), [k13] "v"(k[3].y), [k14] "v"(k[3].z), [k15] "v"(k[3].w));
 }
 
@@ -826,42 +828,44 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
 // each multiply takes it through a DPP row broadcast (row_newbcast:j), then
 // dot = dot + q*k, separately rounded, in the reference's order.
 __device__ __forceinline__ void qk1_dims16(float& s, float q, const float4 (&k)[4]) {
-    float t;
+    // the multiplies run 4 terms ahead of the adds (4 rotating temporaries), so an
+    // add waits only for the add before it, never for its own multiply
+    float t0, t1, t2, t3;
     asm volatile(
         "s_nop 1\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k0] row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k1] row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k2] row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k3] row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k4] row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k5] row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k6] row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k7] row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k8] row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k9] row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k10] row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k11] row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k12] row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k13] row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k14] row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        "v_mul_f32_dpp %[t], %[q], %[k15] row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32 %[a], %[a], %[t]\n\t"
-        : [a] "+v"(s), [t] "=&v"(t)
+        "v_mul_f32_dpp %[t0], %[q], %[k0] row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t1], %[q], %[k1] row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t2], %[q], %[k2] row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mul_f32_dpp %[t3], %[q], %[k3] row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t0]\n\t"
+        "v_mul_f32_dpp %[t0], %[q], %[k4] row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t1]\n\t"
+        "v_mul_f32_dpp %[t1], %[q], %[k5] row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t2]\n\t"
+        "v_mul_f32_dpp %[t2], %[q], %[k6] row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t3]\n\t"
+        "v_mul_f32_dpp %[t3], %[q], %[k7] row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t0]\n\t"
+        "v_mul_f32_dpp %[t0], %[q], %[k8] row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t1]\n\t"
+        "v_mul_f32_dpp %[t1], %[q], %[k9] row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t2]\n\t"
+        "v_mul_f32_dpp %[t2], %[q], %[k10] row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t3]\n\t"
+        "v_mul_f32_dpp %[t3], %[q], %[k11] row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t0]\n\t"
+        "v_mul_f32_dpp %[t0], %[q], %[k12] row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t1]\n\t"
+        "v_mul_f32_dpp %[t1], %[q], %[k13] row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t2]\n\t"
+        "v_mul_f32_dpp %[t2], %[q], %[k14] row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t3]\n\t"
+        "v_mul_f32_dpp %[t3], %[q], %[k15] row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32 %[a], %[a], %[t0]\n\t"
+        "v_add_f32 %[a], %[a], %[t1]\n\t"
+        "v_add_f32 %[a], %[a], %[t2]\n\t"
+        "v_add_f32 %[a], %[a], %[t3]\n\t"
+        : [a] "+v"(s), [t0] "=&v"(t0), [t1] "=&v"(t1), [t2] "=&v"(t2), [t3] "=&v"(t3)
         : [q] "v"(q), [k0] "v"(k[0].x), [k1] "v"(k[0].y), [k2] "v"(k[0].z), [k3] "v"(k[0].w), [k4] "v"(k[1].x),
           [k5] "v"(k[1].y), [k6] "v"(k[1].z), [k7] "v"(k[1].w), [k8] "v"(k[2].x), [k9] "v"(k[2].y), [k10] "v"(k[2].z),
           [k11] "v"(k[2].w), [k12] "v"(k[3].x), [k13] "v"(k[3].y), [k14] "v"(k[3].z), [k15] "v"(k[3].w));
