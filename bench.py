@@ -100,7 +100,7 @@ class Decode:
             a.free()
 
 
-def time_steps(ctx, calls, steps, warmup):
+def time_steps(ctx, calls, steps, warmup, repeats=1):
     """Times `steps` steps of the hot path after `warmup` untimed ones. `calls`
     lists the attention() keyword sets of consecutive steps (cycled); a step is
     len(calls[i]) attention calls. All steps of a region are enqueued through
@@ -111,7 +111,10 @@ def time_steps(ctx, calls, steps, warmup):
     first the steps alone (ms/step), then the same steps again with the main
     kernel of every call carrying dispatch-attached start/stop events (its
     average duration). The per-dispatch events add a few microseconds between
-    launches, so they stay out of the region that gives ms/step.
+    launches, so they stay out of the region that gives ms/step. With repeats > 1
+    both regions run that many times and the medians are returned (the extra
+    workloads use 3: single regions of these sizes vary by up to ~15 % between
+    runs on one box).
     Returns (ms/step, main-kernel ms/launch)."""
     def batch(n):
         return [kw for i in range(n) for kw in calls[i % len(calls)]]
@@ -119,15 +122,18 @@ def time_steps(ctx, calls, steps, warmup):
     if warmup:
         ctx.attention_batch(warm)
     ctx.sync()
-    ctx.timer_start()
-    ctx.attention_batch(timed)
-    total = ctx.timer_stop()
-    ctx.kernel_timing(True)
-    ctx.attention_batch(timed)
-    ctx.sync()
-    kms, n = ctx.kernel_timing_read()
-    ctx.kernel_timing(False)
-    return total / steps, (kms / n if n else float("nan"))
+    step_ms, kernel_ms = [], []
+    for _ in range(repeats):
+        ctx.timer_start()
+        ctx.attention_batch(timed)
+        step_ms.append(ctx.timer_stop() / steps)
+        ctx.kernel_timing(True)
+        ctx.attention_batch(timed)
+        ctx.sync()
+        kms, n = ctx.kernel_timing_read()
+        ctx.kernel_timing(False)
+        kernel_ms.append(kms / n if n else float("nan"))
+    return float(np.median(step_ms)), float(np.median(kernel_ms))
 
 
 def cpu_baseline(budget_s: float = 10.0):
@@ -174,7 +180,7 @@ def schedule_35_layers(ctx, steps, warmup):
                           q_pos0=S - 1, k_pos0=0, window=0 if L.is_global else synth.E2B_WINDOW,
                           ring_cap=host_caches[L.src].ring_cap))
 
-    ms, _ = time_steps(ctx, [token], steps, warmup)
+    ms, _ = time_steps(ctx, [token], steps, warmup, repeats=3)
     algo = 7 * decode_bytes(S, 512) + 28 * decode_bytes(512, 256)
     res = {"us_per_token": ms * 1e3, "algorithmic_bytes": algo, "GB_s": algo / (ms * 1e-3) / 1e9}
     # the same token's 35 calls captured once into a HIP graph and replayed
@@ -270,7 +276,7 @@ def prefill(ctx, T, Dh, window, steps, warmup):
 
     call = [dict(q=q.ptr, k=k.ptr, v=v.ptr, out=out.ptr, T=T, S=T, Hq=HQ, Hkv=1, Dh=Dh, Dv=Dh, q_pos0=0, k_pos0=0,
                  window=window)]
-    ms, kms = time_steps(ctx, [call], steps, warmup)
+    ms, kms = time_steps(ctx, [call], steps, warmup, repeats=3)
     for a in (q, k, v, out):
         a.free()
     fl = prefill_flops(T, window, Dh)
@@ -293,8 +299,9 @@ def batched_decode(ctx, n, L, Dh, window, ring_cap, steps, warmup):
     each a query at position L-1 over its own K/V cache: the batched entry point
     (g4a_attention_decode_batch, one call per step) against the same n calls
     issued as single g4a_attention calls (one g4a_attention_batch crossing per
-    step). Wall time per step from HIP events around the steps; kernel time per
-    step = the summed durations of the step's decode and combine launches."""
+    step). Time per step from HIP events around the back-to-back steps, and every
+    rate from it: per-launch event pairs would each add their dispatch (~1 us), so
+    their sum can exceed the step time once the launches overlap."""
     rows = ring_cap or L
     kv_bytes = 2 * rows * Dh * 4
     copies = int(min(16, max(2, -(-BATCH_BUST_BYTES // (n * kv_bytes)))))
@@ -322,13 +329,6 @@ def batched_decode(ctx, n, L, Dh, window, ring_cap, steps, warmup):
     for i in range(steps):
         ctx.attention_decode_batch(prepared[i % copies])
     ms = ctx.timer_stop() / steps
-    ctx.kernel_timing(True)
-    for i in range(steps):
-        ctx.attention_decode_batch(prepared[i % copies])
-    ctx.sync()
-    kms, _ = ctx.kernel_timing_read()
-    ctx.kernel_timing(False)
-    kms /= steps
     seq_ms, seq_kms = time_steps(ctx, steps_calls, max(10, steps // 4), min(warmup, 5))
     for a in (q, k0, v0, out):
         a.free()
@@ -336,9 +336,8 @@ def batched_decode(ctx, n, L, Dh, window, ring_cap, steps, warmup):
         ctx.free(k)
         ctx.free(v)
     b = n * decode_bytes(min(L, window) if window else L, Dh)
-    return {"us_per_step": ms * 1e3, "kernel_us_per_step": kms * 1e3, "GB_s": b / (ms * 1e-3) / 1e9,
-            "kernel_GB_s": b / (kms * 1e-3) / 1e9, "frac_hbm_peak": b / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "bytes_per_step": b, "kv_copies_rotated": copies,
+    return {"us_per_step": ms * 1e3, "GB_s": b / (ms * 1e-3) / 1e9,
+            "frac_hbm_peak": b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "bytes_per_step": b, "kv_copies_rotated": copies,
             "single_calls_us_per_step": seq_ms * 1e3, "speedup_vs_single_calls": seq_ms / ms}
 
 
@@ -439,28 +438,32 @@ DECODE_CONFIGS = [("configs[0] sliding hd256 S512", 512, 256, 512, 0),
 
 def decode_configs(ctx, steps_arg, warmup_arg):
     """configs[0..2] decode steps, cold (rotated K/V copies) with the warm figure
-    beside; configs[2] also under a forced split sweep (cold)."""
+    beside; configs[2] also under a forced split sweep (cold). us_per_step: the
+    call's launches back to back (the figure of merit); kernel_dispatch_us: one
+    event pair around each decode dispatch, i.e. the kernel plus its own launch
+    latency (~1-1.5 us), which back-to-back steps hide behind the previous
+    launch, so for the short calls it can exceed us_per_step."""
     extras = {}
     for name, S, Dh, W, seed in DECODE_CONFIGS:
         b = decode_bytes(min(S, W) if W else S, Dh)
         d = Decode.cold(ctx, S=S, Dh=Dh, seed=seed, window=W)
         steps = max(10, steps_arg // (4 if S > 100000 else 1))
-        m, km = time_steps(ctx, d.calls(), steps, min(warmup_arg, 10))
+        m, km = time_steps(ctx, d.calls(), steps, min(warmup_arg, 10), repeats=3)
         pl = ctx.plan(**d.kw())
-        extras[name] = {"us_per_step": m * 1e3, "kernel_us": km * 1e3, "GB_s": b / (m * 1e-3) / 1e9,
-                        "kernel_GB_s": b / (km * 1e-3) / 1e9, "kernel": g4a.KERNEL_NAMES[pl.kernel],
+        extras[name] = {"us_per_step": m * 1e3, "kernel_dispatch_us": km * 1e3, "GB_s": b / (m * 1e-3) / 1e9,
+                        "kernel_dispatch_GB_s": b / (km * 1e-3) / 1e9, "kernel": g4a.KERNEL_NAMES[pl.kernel],
                         "splits": pl.splits, "kv_copies_rotated": len(d.kv)}
         if S > 100000:
             sweep = {}
             for sp in (8, 16, 32, 64, 128, 256, 512):
-                m2, _ = time_steps(ctx, d.calls(sp), 10, 3)
-                sweep[sp] = round(m2 * 1e3, 2)
-            extras[name]["split_sweep_us"] = sweep
+                m2, k2 = time_steps(ctx, d.calls(sp), 20, 4, repeats=3)
+                sweep[sp] = {"us_per_step": round(m2 * 1e3, 2), "kernel_dispatch_us": round(k2 * 1e3, 2)}
+            extras[name]["split_sweep"] = sweep
         d.free()
         w = Decode(ctx, S=S, Dh=Dh, seed=seed, window=W)
-        mw, kmw = time_steps(ctx, w.calls(), steps, min(warmup_arg, 10))
+        mw, kmw = time_steps(ctx, w.calls(), steps, min(warmup_arg, 10), repeats=3)
         w.free()
-        extras[name]["warm"] = {"us_per_step": mw * 1e3, "kernel_us": kmw * 1e3, "GB_s": b / (mw * 1e-3) / 1e9}
+        extras[name]["warm"] = {"us_per_step": mw * 1e3, "kernel_dispatch_us": kmw * 1e3, "GB_s": b / (mw * 1e-3) / 1e9}
         print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
     return extras
 
@@ -540,7 +543,7 @@ def main(argv=None):
     head_copies = len(head.kv)
     head.free()
     warm = Decode(ctx, S=32768, Dh=512, seed=4)
-    ms_warm, kms_warm = time_steps(ctx, warm.calls(), max(10, args.steps // 2), min(args.warmup, 20))
+    ms_warm, kms_warm = time_steps(ctx, warm.calls(), max(10, args.steps // 2), min(args.warmup, 20), repeats=3)
     warm.free()
     algo = decode_bytes(32768, 512)
     gbs = algo / (ms * 1e-3) / 1e9
