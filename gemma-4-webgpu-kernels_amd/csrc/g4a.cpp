@@ -749,8 +749,9 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
             if (a->sliding_window) n_row = std::min(n_row, a->sliding_window);
             pp.tau = std::max(PREFILL_TAU_MIN, logf(float(std::max(n_row, 1u))) + PREFILL_TAU_LOGN);
         }
-        // 8-wave workgroups over 8 queries; scores estimated from bf16 hi/lo splits of K,
-        // P.V from fp16 hi/lo splits of V, both made by a pre-pass into the workspace.
+        // 8-wave workgroups over 8 queries; scores estimated from fp16 hi/lo splits of K
+        // (each 16-key tile scaled by a power of two), P.V from fp16 hi/lo splits of V,
+        // both made by a pre-pass into the workspace.
         // head_dim 256: two waves per 16-row block take the even / odd key tiles;
         // 512: two waves per 16-row block split the head dim
         const bool d512 = a->Dh == 512;

@@ -9,26 +9,29 @@
 // B = Q held in registers), so the scores land as lane = row, 4 keys per lane:
 // exactly the A-operand layout of the following P.V product (B = V from LDS),
 // with no transpose. Two 8-wave kernels, both on K and V pre-split by
-// split_kv, scores from bf16 hi/lo splits, P.V from fp16 hi/lo splits:
+// split_kv, scores from fp16 hi/lo splits of K and q each scaled by a power of
+// two (K per 16-key tile, q per wave) into fp16's top binade, P.V from fp16
+// hi/lo splits:
 //   prefill_pair<256>   two waves per row block take the even / odd key tiles;
 //   prefill_dsplit<512> two waves per row block split the head dim.
 //
 // Exactness. The matrix cores sum the 256/512-term dots in their own order
-// (and the split forms round their inputs), up to ~5e-4 away from the CPU
-// reference's sequential f32 sum on scores of ~90 - enough to move outputs by
-// up to ~1e-4 when keys nearly tie. So every key whose approximate score is
-// within TAU of its row's running maximum is recorded (per-wave list in LDS);
-// once the row block is done, the survivors (still within TAU of the final
-// maximum) get their score recomputed in the reference's exact order and their
-// contribution corrected:
+// (and the split forms round their inputs to ~22 bits), a few 1e-5 away from
+// the CPU reference's sequential f32 sum on scores of ~90 - enough to move
+// outputs by more than the 1e-5 bar when keys nearly tie. So every key whose
+// approximate score is within TAU of its row's running maximum is recorded
+// (per-wave list in LDS); once the row block is done, the survivors (still
+// within TAU of the final maximum) get their score recomputed in the
+// reference's exact order and their contribution corrected:
 //   O[row] += (e^{s_exact - m} - e^{s_approx - m}) * v[key],  l[row] += same.
 // Keys farther than TAU below the maximum keep their estimate, each with weight
-// < e^-TAU relative to the maximum's. Their errors (|delta| <= ~4e-4) move the
-// output by at most max|delta| * (W_out / l) * max|v - out|, W_out / l the
-// weight share of those keys, <= N e^-TAU / (1 + N e^-TAU) for N keys in a row.
-// So TAU (G4aPrefillParams::tau) grows with the key range: the host passes
-// max(12, ln N + 4.5), which keeps that share below e^-4.5 = 0.011 even when
-// every key sits just outside the band and every error pushes the same way.
+// < e^-TAU relative to the maximum's. Their errors delta move the output by at
+// most max|delta| * (W_out / l) * max|v - out|, W_out / l the weight share of
+// those keys, <= N e^-TAU / (1 + N e^-TAU) for N keys in a row. So TAU
+// (G4aPrefillParams::tau) grows with the key range: the host passes
+// max(7, ln N + 2), which keeps that share below e^-2 even when every key sits
+// just outside the band and every error pushes the same way (worst case with
+// the scaled fp16 estimate ~5e-7 on the outputs).
 // If the list fills up (many near-ties), it is compacted against the current
 // maxima and, if still full, corrected on the spot.
 #include "g4a_params.h"
@@ -740,7 +743,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
 // than two waves per SIMD can hold, so a row block is shared by two waves that
 // split the head dim: wave w owns rows 16*(w%4) .. +15 (2 queries x 8 heads)
 // and dims 256*(w/4) .. +255. Per 16-key tile each wave computes its half of
-// the score estimate (bf16 hi/lo splits), the pair adds the halves through LDS
+// the score estimate (scaled fp16 hi/lo splits), the pair adds the halves through LDS
 // in a fixed order (both waves then hold bit-identical scores, maxima,
 // candidate lists and l), and each wave runs P.V (fp16 hi/lo splits) and the
 // exact corrections for its own 256 output columns. Tiles stream into a 2-slot
