@@ -1098,9 +1098,12 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
 // step's partials are read by the whole GPU; the block's acc values are one
 // contiguous run (part_index). The split weights e^(m_s - M) are
 // computed once per block into LDS; thread (group g, dim i) then sums splits
-// s = g, g + 16, ... with several loads in flight, and the 16 groups reduce
-// through LDS.
+// s = g, g + 16, ... in split order, and the 16 groups reduce through LDS. The
+// first COMBINE_EARLY splits of each thread (all of them up to 256 splits) are
+// loaded together with the (m, l) pairs, before the weights are known, so a
+// step pays one memory round trip for them instead of two.
 constexpr int COMBINE_MAX_SPLITS = 1024;
+constexpr int COMBINE_EARLY = 16;
 
 template <int DH>
 __device__ __forceinline__ void combine(const G4aCombineParams& p, uint32_t qi) {
@@ -1117,26 +1120,49 @@ __device__ __forceinline__ void combine(const G4aCombineParams& p, uint32_t qi) 
     // this block's 16 dims: a contiguous [split][16] run
     const float* __restrict__ acc = p.part + part_index<DH>(ih, p.nsplit, 0, blockIdx.x * 16) + i;
     const uint32_t ns = p.nsplit;
+    // (m, l) of splits tid, tid + 256, ... first (their wait then leaves the partials in flight)
+    float2 mls[COMBINE_MAX_SPLITS / 256];
+#pragma unroll
+    for (int r = 0; r < COMBINE_MAX_SPLITS / 256; ++r) {
+        const uint32_t s = tid + 256 * r;
+        mls[r] = s < ns ? reinterpret_cast<const float2*>(ml)[s] : make_float2(NEG_INF, 0.0f);
+    }
+    // splits grp + 16 u, u < COMBINE_EARLY (clamped: loads past the last split repeat it and are not summed)
+    float x0[COMBINE_EARLY];
+#pragma unroll
+    for (int u = 0; u < COMBINE_EARLY; ++u) {
+        const uint32_t s = grp + 16 * u;
+        x0[u] = acc[(size_t)(s < ns ? s : ns - 1) * 16];
+    }
     float M = NEG_INF;
-    for (uint32_t s = tid; s < ns; s += 256) M = fmaxf(M, ml[2 * s]);
+#pragma unroll
+    for (int r = 0; r < COMBINE_MAX_SPLITS / 256; ++r) M = fmaxf(M, mls[r].x);
     M = wave_max(M);
     if (lane == 0) redm[w] = M;
     __syncthreads();
     M = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
     float L = 0.0f;
-    for (uint32_t s = tid; s < ns; s += 256) {
-        const float ms = ml[2 * s];
-        const float e = (ms == NEG_INF) ? 0.0f : expf(ms - M);
-        wgt[s] = e;
-        L += ml[2 * s + 1] * e;
+#pragma unroll
+    for (int r = 0; r < COMBINE_MAX_SPLITS / 256; ++r) {
+        const uint32_t s = tid + 256 * r;
+        if (s < ns) {
+            const float e = (mls[r].x == NEG_INF) ? 0.0f : expf(mls[r].x - M);
+            wgt[s] = e;
+            L += mls[r].y * e;
+        }
     }
     L = wave_sum(L);
     if (lane == 0) redl[w] = L;
     __syncthreads();
     L = redl[0] + redl[1] + redl[2] + redl[3];
-    constexpr int U = 8;
     float A = 0.0f;
-    uint32_t s = grp;
+#pragma unroll
+    for (int u = 0; u < COMBINE_EARLY; ++u) {
+        const uint32_t s = grp + 16 * u;
+        if (s < ns) A += x0[u] * wgt[s];
+    }
+    constexpr int U = 8;
+    uint32_t s = grp + 16 * COMBINE_EARLY;
     for (; s + 16 * (U - 1) < ns; s += 16 * U) {
         float x[U];
 #pragma unroll
