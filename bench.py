@@ -500,6 +500,16 @@ def main(argv=None):
     info = ctx.device_info()
     print(f"[bench] device {info.arch.decode()} with {info.compute_units} CUs", file=sys.stderr, flush=True)
 
+    if args.calibration_copy:
+        n = args.calibration_copy << 20
+        a, b = ctx.malloc(n), ctx.malloc(n)
+        ctx.zero(a, n)
+        for _ in range(3):
+            ctx.d2d(b, a, n)
+        ctx.sync()
+        ctx.free(a)
+        ctx.free(b)
+
     if args.only:
         out = {}
         if args.only == "decode":
@@ -525,16 +535,6 @@ def main(argv=None):
         ctx.close()
         print(json.dumps({"only": args.only, "results": out}))
         return 0
-
-    if args.calibration_copy:
-        n = args.calibration_copy << 20
-        a, b = ctx.malloc(n), ctx.malloc(n)
-        ctx.zero(a, n)
-        for _ in range(3):
-            ctx.d2d(b, a, n)
-        ctx.sync()
-        ctx.free(a)
-        ctx.free(b)
 
     # ---- headline: hd512 global decode at 32K context (cold: rotated K/V copies) ----
     head = Decode.cold(ctx, S=32768, Dh=512, seed=4)
