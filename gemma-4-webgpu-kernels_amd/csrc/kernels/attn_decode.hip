@@ -43,15 +43,6 @@ __device__ __forceinline__ float wave_max(float x) { return g4a_wave_max(x); }
 __device__ __forceinline__ float wave_sum(float x) { return g4a_wave_sum(x); }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
-// A store the next kernel reads back once (split partials): non-temporal, so it
-// does not linger in this kernel's L2 as a dirty line.
-__device__ __forceinline__ void st4_nt(float* p, const float4& v) {
-    __builtin_nontemporal_store(v.x, p);
-    __builtin_nontemporal_store(v.y, p + 1);
-    __builtin_nontemporal_store(v.z, p + 2);
-    __builtin_nontemporal_store(v.w, p + 3);
-}
-
 // Physical row of logical key j: a ring of ring_cap slots, or the identity.
 __device__ __forceinline__ uint32_t phys_row(uint32_t j, uint32_t ring_cap) {
     return ring_cap ? j % ring_cap : j;
@@ -822,7 +813,7 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
         o.w *= sc;
         const uint32_t d = 256 * e + 4 * lane;
         float* const dst = p.nsplit == 1 ? p.out + ih * DH + d : p.part + part_index<DH>(ih, p.nsplit, split, d);
-        st4_nt(dst, o);
+        g4a_store_nt(dst, o);
     }
     if (p.nsplit > 1 && lane == 0) {
         float* ml = p.part + (size_t)p.T * p.Hq * p.nsplit * DH + (ih * p.nsplit + split) * 2;
@@ -1090,7 +1081,7 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
             o.w = (a0[e].w * e0 + a1[e].w * e1) * sc;
             const uint32_t d = 256 * e + 4 * lane;
             float* const dst = p.nsplit == 1 ? p.out + ih * DH + d : p.part + part_index<DH>(ih, p.nsplit, split, d);
-            st4_nt(dst, o);
+            g4a_store_nt(dst, o);
         }
         if (p.nsplit > 1 && lane == 0) {
             float* const ml = mlp + (ih * p.nsplit + split) * 2;

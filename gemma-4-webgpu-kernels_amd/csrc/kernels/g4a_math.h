@@ -27,3 +27,13 @@ __device__ __forceinline__ float g4a_wave_sum(float x) {
     for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
     return x;
 }
+
+// A float4 store of data the next kernel reads once (split partials, output
+// rows): non-temporal, so it does not sit in this kernel's L2 as a dirty line
+// that the end-of-kernel write-back has to flush.
+__device__ __forceinline__ void g4a_store_nt(float* p, const float4& v) {
+    __builtin_nontemporal_store(v.x, p);
+    __builtin_nontemporal_store(v.y, p + 1);
+    __builtin_nontemporal_store(v.z, p + 2);
+    __builtin_nontemporal_store(v.w, p + 3);
+}
