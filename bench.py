@@ -285,18 +285,22 @@ def prefill(ctx, T, Dh, window, steps, warmup):
 
 
 BATCH_CONFIGS = [
-    # name, sequences, context length, head dim, window, ring capacity (0: linear cache)
-    ("batch 64 sliding hd256 ring512 @32768", 64, 32768, 256, 512, 512),
-    ("batch 16 sliding hd256 ring512 @32768", 16, 32768, 256, 512, 512),
-    ("batch 32 global hd512 @4096", 32, 4096, 512, 0, 0),
-    ("batch 8 global hd512 @8192", 8, 8192, 512, 0, 0),
+    # name, sequences, context length, head dim, window, ring capacity (0: linear cache),
+    # explicit key positions with a hole (an evicted slot) in every cache
+    ("batch 64 sliding hd256 ring512 @32768", 64, 32768, 256, 512, 512, False),
+    ("batch 16 sliding hd256 ring512 @32768", 16, 32768, 256, 512, 512, False),
+    ("batch 32 global hd512 @4096", 32, 4096, 512, 0, 0, False),
+    ("batch 8 global hd512 @8192", 8, 8192, 512, 0, 0, False),
+    ("batch 32 global hd512 @4096, explicit key positions", 32, 4096, 512, 0, 0, True),
 ]
 BATCH_BUST_BYTES = 512 << 20  # K/V copies rotated until a step's working set is this big (past the 256 MB MALL)
 
 
-def batched_decode(ctx, n, L, Dh, window, ring_cap, steps, warmup):
+def batched_decode(ctx, n, L, Dh, window, ring_cap, steps, warmup, holes=False):
     """One decode step of n independent sequences (a serving batch at one layer),
-    each a query at position L-1 over its own K/V cache: the batched entry point
+    each a query at position L-1 over its own K/V cache (with `holes`, key j at
+    explicit position j + (j >= L/2): one evicted slot mid-cache, the query at
+    position L, the same bytes read): the batched entry point
     (g4a_attention_decode_batch, one call per step) against the same n calls
     issued as single g4a_attention calls (one g4a_attention_batch crossing per
     step). Time per step from HIP events around the back-to-back steps, and every
@@ -316,11 +320,17 @@ def batched_decode(ctx, n, L, Dh, window, ring_cap, steps, warmup):
         kv.append((k, v))
     out = ctx.empty((n, HQ * Dh))
     qb, ob = HQ * Dh * 4, HQ * Dh * 4
+    if holes:
+        kp = np.arange(L, dtype=np.uint32)
+        kp[L // 2:] += 1
+        pos = dict(q_pos=np.array([L], np.uint32), k_pos=kp)
+    else:
+        pos = dict(q_pos0=L - 1, k_pos0=0)
     steps_calls = []
     for c in range(copies):
         steps_calls.append([dict(q=q.ptr + i * qb, k=kv[c * n + i][0], v=kv[c * n + i][1], out=out.ptr + i * ob, T=1,
-                                 S=L, Hq=HQ, Hkv=1, Dh=Dh, Dv=Dh, q_pos0=L - 1, k_pos0=0, window=window,
-                                 ring_cap=ring_cap) for i in range(n)])
+                                 S=L, Hq=HQ, Hkv=1, Dh=Dh, Dv=Dh, window=window, ring_cap=ring_cap, **pos)
+                            for i in range(n)])
     prepared = [ctx.prepare_batch(c) for c in steps_calls]
     for i in range(warmup):
         assert ctx.attention_decode_batch(prepared[i % copies]) == n
@@ -523,8 +533,8 @@ def main(argv=None):
                 out[name] = linear_bench(ctx, op, N, K, bits, M, steps=args.steps)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         elif args.only == "batch":
-            for name, n, L, Dh, W, cap in BATCH_CONFIGS:
-                out[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=args.steps, warmup=args.warmup)
+            for name, n, L, Dh, W, cap, holes in BATCH_CONFIGS:
+                out[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=args.steps, warmup=args.warmup, holes=holes)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         elif args.only == "producer":
             for name, T, Dh, theta, rot, pos0, cap in PRODUCER_CONFIGS:
@@ -603,8 +613,8 @@ def main(argv=None):
         for name, op, N, K, bits, M in LINEAR_CONFIGS:
             extras[name] = linear_bench(ctx, op, N, K, bits, M, steps=100)
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
-        for name, n, L, Dh, W, cap in BATCH_CONFIGS:
-            extras[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=50, warmup=10)
+        for name, n, L, Dh, W, cap, holes in BATCH_CONFIGS:
+            extras[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=50, warmup=10, holes=holes)
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
         extras["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=20, warmup=3)
         print(f"[bench] schedule: {extras['configs[4] 35-layer schedule @32768']}", file=sys.stderr, flush=True)

@@ -88,6 +88,7 @@ struct g4a_ctx {
     hipFunction_t decode_short[2] = {nullptr, nullptr};  // [dh512]
     hipFunction_t decode_batch[2] = {nullptr, nullptr};   // [dh512] short decode over many sequences
     hipFunction_t decode_wave_batch[2] = {nullptr, nullptr};  // [dh512] streaming decode over many sequences
+    hipFunction_t decode_wave_batch_kpos[2] = {nullptr, nullptr};  // [dh512] the same, explicit key positions
     hipFunction_t combine_batch[2] = {nullptr, nullptr};  // [dh512]
     hipFunction_t combine_rows[2] = {nullptr, nullptr};        // [dh512] combine of <= 64 splits
     hipFunction_t combine_rows_batch[2] = {nullptr, nullptr};  // [dh512]
@@ -509,6 +510,8 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->decode_batch[1], "g4a_decode_short_batch_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_wave_batch[0], "g4a_decode_wave_batch_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_wave_batch[1], "g4a_decode_wave_batch_d512")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->decode_wave_batch_kpos[0], "g4a_decode_wave_batch_kpos_d256")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->decode_wave_batch_kpos[1], "g4a_decode_wave_batch_kpos_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->combine_batch[0], "g4a_combine_batch_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->combine_batch[1], "g4a_combine_batch_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->combine_rows[0], "g4a_combine_rows_d256")) return bail(rc);
@@ -893,13 +896,16 @@ int g4a_attention_decode_batch(g4a_ctx* ctx, const g4a_attn_args* args, uint32_t
     std::vector<Analysis> an(n);
     for (uint32_t i = 0; i < n; ++i)
         if (int rc = analyse(ctx, &args[i], &an[i], true)) return fail(ctx, rc, "call %u: %s", i, ctx->err.c_str());
-    // the batched calls: single-query decode steps of the first such call's shape
+    // the batched calls: single-query decode steps of the first such call's
+    // shape; those with explicit, non-contiguous key positions (staged from host
+    // memory, so not while a graph is captured) go to launches of their own
     const g4a_attn_args* ref = nullptr;
-    std::vector<uint32_t> batch;
+    std::vector<uint32_t> batch, batch_kpos;
     for (uint32_t i = 0; i < n; ++i) {
         const g4a_attn_args& a = args[i];
         const Analysis& r = an[i];
-        if (a.T != 1 || !r.fast_shape || !r.k_contig || a.splits != 0 || a.Hq != 8 * a.Hkv) continue;
+        if (a.T != 1 || !r.fast_shape || a.splits != 0 || a.Hq != 8 * a.Hkv) continue;
+        if (!r.k_contig && ctx->capturing) continue;
         if (r.plan.kernel != G4A_KERNEL_DECODE && r.plan.kernel != G4A_KERNEL_DECODE_SHORT) continue;
         if (r.plan.k_end - r.plan.k_start > BATCH_MAX_KEYS) continue;
         if (!ref) ref = &a;
@@ -907,23 +913,44 @@ int g4a_attention_decode_batch(g4a_ctx* ctx, const g4a_attn_args* args, uint32_t
             a.kv_ring_cap != ref->kv_ring_cap || memcmp(&a.scale, &ref->scale, sizeof(float)) != 0 ||
             memcmp(&a.attn_softcap, &ref->attn_softcap, sizeof(float)) != 0)
             continue;
-        batch.push_back(i);
+        (r.k_contig ? batch : batch_kpos).push_back(i);
     }
+    // the visible keys' positions of the explicit-position calls, staged in one upload
+    std::vector<uint32_t> kpos_host, kpos_off(batch_kpos.size());
+    for (size_t j = 0; j < batch_kpos.size(); ++j) {
+        const g4a_attn_args& a = args[batch_kpos[j]];
+        const g4a_attn_plan& pl = an[batch_kpos[j]].plan;
+        if (kpos_host.size() + (pl.k_end - pl.k_start) >= G4A_NO_KPOS)
+            return fail(ctx, G4A_E_SHAPE, "batched decode key positions exceed 2^32 entries");
+        kpos_off[j] = uint32_t(kpos_host.size());
+        kpos_host.insert(kpos_host.end(), a.k_pos + pl.k_start, a.k_pos + pl.k_end);
+    }
+    const uint32_t* kpos_dev = nullptr;
+    if (!kpos_host.empty())
+        if (int rc = upload_positions(ctx, kpos_host.data(), kpos_host.size(), nullptr, 0, &kpos_dev, nullptr))
+            return rc;
+    const uint32_t n_contig = uint32_t(batch.size());
+    batch.insert(batch.end(), batch_kpos.begin(), batch_kpos.end());
     const uint64_t cus = uint64_t(std::max(ctx->cu_count, 1));
-    // Launches of up to G4A_BATCH_SEQ sequences. A launch whose 32-key splits fit
-    // one short-kernel workgroup per CU runs the short kernel; otherwise the
-    // streaming kernel with 64-key-multiple splits sized for one 8-wave
-    // workgroup per CU over the launch's keys.
+    // Launches of up to G4A_BATCH_SEQ sequences, the contiguous-position calls
+    // (batch[0 .. n_contig)) apart from the explicit-position ones. A launch
+    // whose 32-key splits fit one short-kernel workgroup per CU runs the short
+    // kernel; otherwise (and always for explicit positions) the streaming kernel
+    // with 64-key-multiple splits sized for one 8-wave workgroup per CU over the
+    // launch's keys.
     struct Launch {
         uint32_t first, count, kps, max_split;
         bool wave, rows, wide;  // streaming kernel; combines of <= 64 / more splits
+        bool kpos;              // explicit key positions
         size_t part;  // floats
     };
     std::vector<Launch> launches;
     size_t part_floats = 0;
-    for (uint32_t c0 = 0; c0 < batch.size(); c0 += G4A_BATCH_SEQ) {
-        Launch L{c0, std::min<uint32_t>(G4A_BATCH_SEQ, uint32_t(batch.size()) - c0), SHORT_KEYS, 0, false, false,
-                 false, part_floats};
+    for (uint32_t c0 = 0; c0 < batch.size();) {
+        const uint32_t c1 = c0 < n_contig ? n_contig : uint32_t(batch.size());
+        Launch L{c0, std::min<uint32_t>(G4A_BATCH_SEQ, c1 - c0), SHORT_KEYS, 0, false, false, false, c0 >= n_contig,
+                 part_floats};
+        c0 += L.count;
         uint64_t short_wgs = 0, keys = 0;
         uint32_t max_keys = 0;
         for (uint32_t j = L.first; j < L.first + L.count; ++j) {
@@ -932,7 +959,7 @@ int g4a_attention_decode_batch(g4a_ctx* ctx, const g4a_attn_args* args, uint32_t
             keys += nk;
             max_keys = std::max(max_keys, nk);
         }
-        if (ctx->batch_kernel == 2 || (ctx->batch_kernel == 0 && short_wgs * ref->Hkv > cus)) {
+        if (L.kpos || ctx->batch_kernel == 2 || (ctx->batch_kernel == 0 && short_wgs * ref->Hkv > cus)) {
             L.wave = true;
             uint64_t kps = ctx->batch_kps ? ctx->batch_kps : (keys * ref->Hkv + cus - 1) / cus;
             kps = std::max<uint64_t>(kps, (max_keys + MAX_SPLITS - 1) / MAX_SPLITS);
@@ -964,6 +991,7 @@ int g4a_attention_decode_batch(g4a_ctx* ctx, const g4a_attn_args* args, uint32_t
         bp.window = ref->sliding_window;
         bp.scale = ref->scale;
         bp.softcap = ref->attn_softcap;
+        bp.kpos = kpos_dev;
         size_t off = L.part;
         for (uint32_t j = 0; j < L.count; ++j) {
             const g4a_attn_args& a = args[batch[L.first + j]];
@@ -975,14 +1003,22 @@ int g4a_attention_decode_batch(g4a_ctx* ctx, const g4a_attn_args* args, uint32_t
             d.out = a.out;
             d.k_start = pl.k_start;
             d.k_end = pl.k_end;
-            // key j sits at position k_pos0 + j; the kernel takes positions relative to k_pos0
-            // (the visible keys end at or before the query, so q_pos >= k_pos0)
-            d.q_pos = (a.q_pos ? a.q_pos[0] : a.q_pos0) - (a.k_pos ? a.k_pos[0] : a.k_pos0);
+            if (L.kpos) {
+                // explicit positions: absolute, key j's at kpos[kpos_off - k_start + j]
+                d.q_pos = a.q_pos ? a.q_pos[0] : a.q_pos0;
+                d.kpos = kpos_off[L.first + j - n_contig];
+            } else {
+                // key j sits at position k_pos0 + j; the kernel takes positions relative to k_pos0
+                // (the visible keys end at or before the query, so q_pos >= k_pos0)
+                d.q_pos = (a.q_pos ? a.q_pos[0] : a.q_pos0) - (a.k_pos ? a.k_pos[0] : a.k_pos0);
+                d.kpos = G4A_NO_KPOS;
+            }
             const uint32_t ns = (pl.k_end - pl.k_start + L.kps - 1) / L.kps;
             d.part = uint32_t(ns > 1 ? off : 0);
             if (ns > 1) off += (size_t(ref->Hq) * ns * (ref->Dh + 2) + 63) & ~size_t(63);
         }
-        hipFunction_t f = L.wave ? ctx->decode_wave_batch[d512] : ctx->decode_batch[d512];
+        hipFunction_t f = L.kpos ? ctx->decode_wave_batch_kpos[d512]
+                          : L.wave ? ctx->decode_wave_batch[d512] : ctx->decode_batch[d512];
         if (int rc = launch(ctx, f, dim3(L.max_split, L.count, bp.Hkv), dim3(L.wave ? 512 : 256, 1, 1), bp,
                             "batched decode", true))
             return rc;

@@ -1241,9 +1241,9 @@ __device__ __forceinline__ void combine_rows(const G4aCombineParams& p, uint32_t
 
 // Batched decode: one launch over the independent single-query steps of
 // b.seq[]; grid (largest split count, sequences, Hkv). The decode parameters of
-// sequence blockIdx.y are rebuilt from its descriptor (T = 1, key positions
-// relative to its first cache key); a workgroup past the sequence's split count
-// exits at once.
+// sequence blockIdx.y are rebuilt from its descriptor (T = 1; key positions
+// relative to its first cache key, or explicit ones from b.kpos); a workgroup
+// past the sequence's split count exits at once.
 __device__ __forceinline__ bool batch_params(const G4aBatchParams& b, uint32_t si, G4aDecodeParams& p) {
     const G4aSeqDesc& sd = b.seq[si];
     p = G4aDecodeParams{};
@@ -1256,6 +1256,8 @@ __device__ __forceinline__ bool batch_params(const G4aBatchParams& b, uint32_t s
     p.dummy = b.dummy;
     p.q_pos0 = sd.q_pos;
     p.k_pos0 = 0;
+    // explicit positions (the KPOS kernel): sd.kpos locates the position of key k_start
+    if (sd.kpos != G4A_NO_KPOS) p.k_pos = b.kpos + sd.kpos - sd.k_start;
     p.T = 1;
     p.Hq = b.Hq;
     p.Hkv = b.Hkv;
@@ -1276,11 +1278,11 @@ __device__ __forceinline__ void decode_short_batch(const G4aBatchParams& b) {
     decode_short<DH>(p, blockIdx.x, 0u);
 }
 
-template <int DH>
+template <int DH, bool KPOS>
 __device__ __forceinline__ void decode_wave_batch(const G4aBatchParams& b) {
     G4aDecodeParams p;
     if (!batch_params(b, blockIdx.y, p) || blockIdx.x >= p.nsplit) return;
-    decode_wave<DH, false>(p, blockIdx.x, 0u);
+    decode_wave<DH, KPOS>(p, blockIdx.x, 0u);
 }
 
 // The LSE combines of a batched decode, each sequence merged by the kernel a
@@ -1390,8 +1392,15 @@ __global__ __launch_bounds__(256) void g4a_decode_short_d512(G4aDecodeParams p) 
 }
 __global__ __launch_bounds__(256) void g4a_decode_short_batch_d256(G4aBatchParams b) { decode_short_batch<256>(b); }
 __global__ __launch_bounds__(256) void g4a_decode_short_batch_d512(G4aBatchParams b) { decode_short_batch<512>(b); }
-__global__ __launch_bounds__(512) void g4a_decode_wave_batch_d256(G4aBatchParams b) { decode_wave_batch<256>(b); }
-__global__ __launch_bounds__(512) void g4a_decode_wave_batch_d512(G4aBatchParams b) { decode_wave_batch<512>(b); }
+__global__ __launch_bounds__(512) void g4a_decode_wave_batch_d256(G4aBatchParams b) { decode_wave_batch<256, false>(b); }
+__global__ __launch_bounds__(512) void g4a_decode_wave_batch_d512(G4aBatchParams b) { decode_wave_batch<512, false>(b); }
+// sequences with explicit key positions (every descriptor of the launch has kpos set)
+__global__ __launch_bounds__(512) void g4a_decode_wave_batch_kpos_d256(G4aBatchParams b) {
+    decode_wave_batch<256, true>(b);
+}
+__global__ __launch_bounds__(512) void g4a_decode_wave_batch_kpos_d512(G4aBatchParams b) {
+    decode_wave_batch<512, true>(b);
+}
 __global__ __launch_bounds__(256) void g4a_combine_batch_d256(G4aBatchParams b) { combine_batch<256>(b); }
 __global__ __launch_bounds__(256) void g4a_combine_batch_d512(G4aBatchParams b) { combine_batch<512>(b); }
 __global__ __launch_bounds__(256) void g4a_combine_rows_batch_d256(G4aBatchParams b) { combine_rows_batch<256>(b); }

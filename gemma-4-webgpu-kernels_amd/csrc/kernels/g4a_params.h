@@ -35,7 +35,10 @@ struct G4aDecodeParams {
 // g4a_combine_batch_*): a single query over the cache rows k / v, keys
 // [k_start, k_end) in splits of G4aBatchParams::keys_per_split. Positions are
 // relative to the sequence's first cache key: key j sits at position j
-// (physical row j % ring_cap for a ring), the query at q_pos.
+// (physical row j % ring_cap for a ring), the query at q_pos; or, with kpos set,
+// key j at G4aBatchParams::kpos[kpos + j - k_start] and the query at q_pos, both
+// absolute (only the positions of the visible keys k_start .. k_end are staged).
+constexpr uint32_t G4A_NO_KPOS = 0xFFFFFFFFu;
 struct G4aSeqDesc {
     const float* q;        // [1, Hq, Dh]
     const float* k;        // [rows, Hkv, Dh]
@@ -44,10 +47,11 @@ struct G4aSeqDesc {
     uint32_t k_start, k_end;
     uint32_t q_pos;
     uint32_t part;         // offset of its partials in G4aBatchParams::part, in floats
+    uint32_t kpos;         // offset of its key positions in G4aBatchParams::kpos, or G4A_NO_KPOS
 };
 
 // Sequences per batched decode launch: their descriptors travel in the kernel
-// arguments (48 bytes each), so a launch needs no upload of its own.
+// arguments (56 bytes each), so a launch needs no upload of its own.
 constexpr uint32_t G4A_BATCH_SEQ = 64;
 
 // Arguments of a batched decode launch: sequences seq[0 .. gridDim.y) (decode)
@@ -57,12 +61,15 @@ struct G4aBatchParams {
     G4aSeqDesc seq[G4A_BATCH_SEQ];
     float* part;
     const float* dummy;
+    const uint32_t* kpos;  // the explicit key positions of the launch's sequences (device)
     uint32_t Hq, Hkv;
     uint32_t keys_per_split;
     uint32_t ring_cap;
     uint32_t window;
     float scale, softcap;
 };
+
+static_assert(sizeof(G4aBatchParams) <= 4096, "batched decode arguments fit the kernel argument segment");
 
 // Log-sum-exp merge of the split partials written by the decode kernel.
 struct G4aCombineParams {

@@ -147,10 +147,13 @@ int g4a_attention_batch(g4a_ctx *ctx, const g4a_attn_args *args, uint32_t n);
  * keys. args[i] is exactly as for g4a_attention and gives its result within
  * the same tolerance (bit-identical where g4a_attention would run the short
  * kernel with the same splits). A call runs in the batched launches when
- * T = 1, Hq = 8 * Hkv, Dh = Dv in {256, 512}, its key positions are
- * contiguous, `splits` is 0, it sees at most 32768 keys and its Hq, Hkv, Dh,
- * sliding_window, kv_ring_cap, scale and attn_softcap equal those of the first
- * such call; every other call runs afterwards as g4a_attention. Every call is
+ * T = 1, Hq = 8 * Hkv, Dh = Dv in {256, 512}, `splits` is 0, it sees at most
+ * 32768 keys and its Hq, Hkv, Dh, sliding_window, kv_ring_cap, scale and
+ * attn_softcap equal those of the first such call; every other call runs
+ * afterwards as g4a_attention. Calls with explicit, ascending, non-contiguous
+ * key positions run in streaming-kernel launches of their own, their visible
+ * keys' positions staged from host memory in one upload (while a graph is
+ * being captured they run as g4a_attention, which then reports the capture). Every call is
  * validated before any work is enqueued. The calls must be independent: no
  * call's out may overlap another call's q, k, v or out. *n_batched (may be
  * NULL) receives the number of calls that ran batched. No counterpart in the

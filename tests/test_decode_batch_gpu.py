@@ -6,8 +6,8 @@ arguments) through the C-ABI. Each batched step must equal the CPU oracle
 <= 1e-5, mean-abs <= 1e-6 (f32), and where the batch runs the short kernel,
 the single g4a_attention call bit for bit. Covers both kernels, batches across
 the 64-sequence launch boundary, ragged lengths, windows, wrapping rings, the
-32768-key limit, calls that must not batch, scale and soft-cap, two kv heads
-and argument errors."""
+32768-key limit, explicit non-contiguous key positions, calls that must not
+batch, scale and soft-cap, two kv heads and argument errors."""
 import numpy as np
 import pytest
 
@@ -164,8 +164,9 @@ def test_streaming_kernel_batches(ctx):
 
 def test_calls_that_do_not_batch_run_as_single_calls(ctx):
     """Multi-query steps, another head dim than the first batched call, a fixed
-    split count, group 4 and explicit non-contiguous key positions are run by
-    g4a_attention; the batched ones keep their results."""
+    split count and group 4 are run by g4a_attention; the batched ones keep
+    their results, among them a step with explicit non-contiguous key positions
+    (a launch of its own beside the contiguous ones)."""
     c = ctx
     a = Seq(c, 700, 256, seed=400, window=512)
     b = Seq(c, 900, 512, seed=401)          # other Dh than the first batched call
@@ -190,13 +191,13 @@ def test_calls_that_do_not_batch_run_as_single_calls(ctx):
             dict(q=dev_g4[0].ptr, k=dev_g4[1].ptr, v=dev_g4[2].ptr, out=dev_g4[3].ptr, T=1, S=300, Hq=4, Hkv=1,
                  Dh=256, Dv=256, q_pos0=299, k_pos0=0),
             dict(q=dev_kp[0].ptr, k=dev_kp[1].ptr, v=dev_kp[2].ptr, out=dev_kp[3].ptr, T=1, S=500, Hq=8, Hkv=1,
-                 Dh=256, Dv=256, q_pos=qp, k_pos=kp),
+                 Dh=256, Dv=256, q_pos=qp, k_pos=kp, window=512),
             dict(q=dev_fs[0].ptr, k=dev_fs[1].ptr, v=dev_fs[2].ptr, out=dev_fs[3].ptr, T=1, S=700, Hq=8, Hkv=1,
                  Dh=256, Dv=256, q_pos0=699, k_pos0=0, window=512, splits=3),
             d.kw(),
         ]
         step("mixed batch")
-        assert c.attention_decode_batch(calls) == 2  # a and d
+        assert c.attention_decode_batch(calls) == 3  # a, the explicit positions and d
         assert_parity(a.out.to_host(), a.want(), "batched a")
         assert_parity(d.out.to_host(), d.want(), "batched d")
         assert_parity(b.out.to_host(), b.want(), "other head dim")
@@ -204,7 +205,7 @@ def test_calls_that_do_not_batch_run_as_single_calls(ctx):
                                                            window=512), "three queries")
         assert_parity(dev_g4[3].to_host(), oracle.attention(ins_g4.q, ins_g4.k, ins_g4.v, ins_g4.q_pos,
                                                             ins_g4.k_pos), "group 4")
-        assert_parity(dev_kp[3].to_host(), oracle.attention(ins_kp.q, ins_kp.k, ins_kp.v, qp, kp),
+        assert_parity(dev_kp[3].to_host(), oracle.attention(ins_kp.q, ins_kp.k, ins_kp.v, qp, kp, window=512),
                       "explicit key positions")
         assert_parity(dev_fs[3].to_host(), a.want(), "fixed splits")
     finally:
@@ -269,3 +270,70 @@ def test_positions_offset_from_the_cache_start(ctx):
                 assert_parity(s.out.to_host(), s.want(), f"offset {label} L={s.L}")
         finally:
             _free(seqs)
+
+
+class KposSeq:
+    """A decode step over a linear cache whose S keys sit at explicit ascending
+    positions with holes (gaps of 1-3: evicted or padded slots); the query sits
+    at `q_at` (an index into the positions, plus 0-2), so the keys after it are
+    cut off, and a window cuts the cache's start."""
+
+    def __init__(self, c, S, Dh, seed, window, q_at, rng):
+        self.c, self.window = c, window
+        ins = synth.gemma_inputs(T=1, S=S, Dh=Dh, seed=seed)
+        self.q, self.k, self.v = ins.q, ins.k, ins.v
+        self.k_pos = np.cumsum(rng.integers(1, 4, S)).astype(np.uint32)
+        self.q_pos = np.array([int(self.k_pos[q_at]) + int(rng.integers(0, 3))], np.uint32)
+        self.S, self.Dh = S, Dh
+        self.dev = [c.upload(x) for x in (self.q, self.k, self.v)]
+        self.out = c.empty((1, 8 * Dh))
+        c.zero(self.out.ptr, self.out.nbytes)
+
+    def kw(self):
+        return dict(q=self.dev[0].ptr, k=self.dev[1].ptr, v=self.dev[2].ptr, out=self.out.ptr, T=1, S=self.S,
+                    Hq=8, Hkv=1, Dh=self.Dh, Dv=self.Dh, q_pos=self.q_pos, k_pos=self.k_pos, window=self.window)
+
+    def want(self):
+        return oracle.attention(self.q, self.k, self.v, self.q_pos, self.k_pos, window=self.window)
+
+    def free(self):
+        for d in self.dev:
+            d.free()
+        self.out.free()
+
+
+def test_explicit_key_positions_batch(ctx):
+    """Steps whose keys sit at explicit, ascending, non-contiguous positions
+    batch in streaming-kernel launches of their own, beside contiguous steps of
+    the same shape in the same call: 70 hd256 sliding-window steps (two
+    launches, 64 + 6) whose windows start far into their caches and whose
+    queries sit before their last keys, then hd512 full attention up to the
+    32768-key limit, where a step over 32769 visible keys runs as a single
+    call."""
+    c = ctx
+    rng = np.random.default_rng(12)
+    sizes = [1, 2, 17, 300, 1000, 5000] + [int(x) for x in rng.integers(1, 6000, 64)]
+    seqs = [KposSeq(c, S, 256, 900 + i, 512, int(rng.integers(S // 2, S)), rng) for i, S in enumerate(sizes)]
+    contig = [Seq(c, L, 256, seed=980 + i, window=512) for i, L in enumerate((40, 700, 3000))]
+    try:
+        step("explicit positions, hd256 window 512: 70 + 3 contiguous calls")
+        assert c.attention_decode_batch([contig[0].kw()] + [s.kw() for s in seqs] +
+                                        [x.kw() for x in contig[1:]]) == len(seqs) + len(contig)
+        worst = 0.0
+        for i, s in enumerate(seqs):
+            worst = max(worst, assert_parity(s.out.to_host(), s.want(), f"explicit call {i} S={s.S}"))
+        for s in contig:
+            assert_parity(s.out.to_host(), s.want(), f"contiguous L={s.L}")
+        print(f"  explicit positions hd256: max-abs {worst:.3e}", flush=True)
+    finally:
+        _free(seqs)
+        _free(contig)
+    seqs = [KposSeq(c, S, 512, 990 + i, 0, qa, rng)
+            for i, (S, qa) in enumerate([(64, 63), (4099, 4000), (20000, 12345), (32768, 32767), (32769, 32768)])]
+    try:
+        step("explicit positions, hd512 global")
+        assert c.attention_decode_batch([s.kw() for s in seqs]) == 4
+        for s in seqs:
+            assert_parity(s.out.to_host(), s.want(), f"explicit hd512 S={s.S}")
+    finally:
+        _free(seqs)
