@@ -511,9 +511,9 @@ __device__ __forceinline__ void decode_split(const G4aDecodeParams& p) {
 // decode_split, but its waves never synchronise inside the streaming loop:
 // wave w owns the split's 16-key wave tiles u = 8*it + w (the split's tiles
 // are every nsplit-th tile of the key range, see below) and streams their K
-// and V rows into a private LDS ring of NB 4 KiB chunks, AHEAD chunks ahead, so
-// each wave waits only for its own copies (vmcnt) and a slow wave delays
-// nobody. Per wave tile, DH/64 K chunks (16 keys x 64 dims, 16-byte columns
+// and V rows into a private LDS ring of NB 4 KiB chunks, one chunk ahead of
+// the one it computes on, so each wave waits only for its own copies (vmcnt)
+// and a slow wave delays nobody. Per wave tile, DH/64 K chunks (16 keys x 64 dims, 16-byte columns
 // XOR-swizzled by key) then 16/KPC V chunks (KPC keys x DH dims):
 //   scores: lane l = (key l%16, head pair l/16): heads 2(l/16), 2(l/16)+1 of
 //           key l%16, the exact sequential dot of qk_dims16 (each 16-lane row
@@ -528,8 +528,12 @@ struct WaveCfg {
     static constexpr int GROUP = 8;
     static constexpr int KEYS = 16;                   // keys per wave tile
     static constexpr int BUF = 1024;                  // floats per chunk buffer (4 KiB)
-    static constexpr int NB = 4;                      // chunk buffers per wave (16 KiB)
-    static constexpr int AHEAD = NB - 1;
+    static constexpr int NB = 4;                      // chunk buffers per wave (16 KiB: the merge's partial)
+    // Chunks in flight beyond the one in use. One beats three (8 MB instead of
+    // 24 MB outstanding over the GPU): hd512 decode at 32K keys 25.05 -> 24.69 us,
+    // at 131072 keys 83.8 -> 81.4 us; only calls forced to a few splits (8 or 32
+    // workgroups at 131072 keys) lose, ~1.5 %. Zero is 15 % slower.
+    static constexpr int AHEAD = 1;
     static constexpr int LPT = BUF / 256;             // 16-byte copies per lane per chunk
     static constexpr int NKS = DH / 64;               // K chunks per wave tile
     static constexpr int KPC = BUF / DH;              // keys per V chunk
@@ -670,8 +674,9 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
         for (int c = 0; c < NCH; ++c) {
             const int bi = c % NB;
             const float* const buf = my_ring + bi * BUF;
-            // this wave's reads of chunk c-1 are complete, so its buffer can be refilled
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            // chunk c + AHEAD refills the buffer of chunk c + AHEAD - NB; with AHEAD + 1 == NB
+            // that is chunk c - 1, whose LDS reads must have completed
+            if constexpr (AHEAD + 1 >= NB) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             if (c + AHEAD < NCH) issue_chunk(cur, c + AHEAD, (c + AHEAD) % NB);
             else if (!last) issue_chunk(nxt, c + AHEAD - NCH, (c + AHEAD) % NB);
             // chunk c has landed: the copies issued after it are the next AHEAD chunks
@@ -711,10 +716,7 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
                         const float sc = vis ? score_epilogue(s[h], p.scale, p.softcap) : NEG_INF;
-                        float rm = sc;
-#pragma unroll
-                        for (int o = 8; o > 0; o >>= 1) rm = fmaxf(rm, __shfl_xor(rm, o, 64));
-                        const float mn = fmaxf(m[h], rm);
+                        const float mn = fmaxf(m[h], g4a_row_max16(sc));
                         const float corr = (m[h] == NEG_INF) ? 0.0f : expf(m[h] - mn);
                         const float pr = (sc == NEG_INF) ? 0.0f : expf(sc - mn);
                         lpart[h] = lpart[h] * corr + pr;
@@ -766,9 +768,7 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
     __builtin_amdgcn_s_setprio(0);
     wait_vm<0>();
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) lpart[h] += __shfl_xor(lpart[h], o, 64);
+    for (int h = 0; h < 2; ++h) lpart[h] = g4a_row_sum16(lpart[h]);
     if (key == 0) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -782,17 +782,24 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
         for (int e = 0; e < ND; ++e)
             *reinterpret_cast<float4*>(my_ring + h * DH + 256 * e + 4 * lane) = acc[h][e];
     __syncthreads();
-    // wave w merges head w: M = max over waves, L = sum of l * e^(m - M)
+    // Wave w merges head w: M = max over waves, L = sum of l * e^(m - M). The 8
+    // wave partials are read first; lane x of each 8-lane group computes wave x's
+    // weight e^(m_x - M) and l_x e^(m_x - M), which every lane takes in wave order.
     const int h = w;
-    float M = NEG_INF;
+    float4 a[8][ND];
 #pragma unroll
-    for (int x = 0; x < 8; ++x) M = fmaxf(M, mlbuf[x * 2 * GROUP + h]);
+    for (int x = 0; x < 8; ++x)
+#pragma unroll
+        for (int e = 0; e < ND; ++e) a[x][e] = ld4(ring + x * NB * BUF + h * DH + 256 * e + 4 * lane);
+    const float mx = mlbuf[(lane & 7) * 2 * GROUP + h];
+    const float M = g4a_max8(mx);
+    const float ex = (mx == NEG_INF) ? 0.0f : expf(mx - M);
+    const float lx = mlbuf[(lane & 7) * 2 * GROUP + GROUP + h] * ex;
     float L = 0.0f, es[8];
 #pragma unroll
     for (int x = 0; x < 8; ++x) {
-        const float mx = mlbuf[x * 2 * GROUP + h];
-        es[x] = (mx == NEG_INF) ? 0.0f : expf(mx - M);
-        L += mlbuf[x * 2 * GROUP + GROUP + h] * es[x];
+        es[x] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), x));
+        L += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lx), x));
     }
     const size_t ih = (size_t)qi * p.Hq + h0 + h;
     const float sc = p.nsplit == 1 ? (L > 0.0f ? 1.0f / L : 0.0f) : 1.0f;
@@ -801,11 +808,10 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
         float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
-            const float4 a = ld4(ring + x * NB * BUF + h * DH + 256 * e + 4 * lane);
-            o.x += a.x * es[x];
-            o.y += a.y * es[x];
-            o.z += a.z * es[x];
-            o.w += a.w * es[x];
+            o.x = __builtin_fmaf(a[x][e].x, es[x], o.x);
+            o.y = __builtin_fmaf(a[x][e].y, es[x], o.y);
+            o.z = __builtin_fmaf(a[x][e].z, es[x], o.z);
+            o.w = __builtin_fmaf(a[x][e].w, es[x], o.w);
         }
         o.x *= sc;
         o.y *= sc;
@@ -999,13 +1005,11 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
         const bool vis = (uint32_t)key < nk && kp <= qpos && (p.window == 0 || qpos - kp < p.window);
         if (vis) s = score_epilogue(dot, p.scale, p.softcap);
     }
-    float m = s;
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    // row max and sum over the tile's 16 keys by DPP (the additions of an xor
+    // 1, 2, 4, 8 butterfly, without LDS round trips)
+    const float m = g4a_row_max16(s);
     const float pr = (s == NEG_INF) ? 0.0f : expf(s - m);
-    float l = pr;
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o, 64);
+    const float l = g4a_row_sum16(pr);
     my_p[key * 4 + r] = pr;
     if (key == 0) {
         my_ml[r] = m;

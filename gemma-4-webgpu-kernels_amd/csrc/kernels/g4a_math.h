@@ -28,6 +28,43 @@ __device__ __forceinline__ float g4a_wave_sum(float x) {
     return x;
 }
 
+// x of another lane of the same 16-lane row, by a DPP pattern (no LDS round trip).
+constexpr int G4A_DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int G4A_DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int G4A_DPP_HALF_MIRROR = 0x141;  // lane i of each 8-lane half reads lane 7 - i
+constexpr int G4A_DPP_ROW_MIRROR = 0x140;   // lane i of each 16-lane row reads lane 15 - i
+template <int CTRL>
+__device__ __forceinline__ float g4a_dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum / max over each 16-lane row: pairs, quads, half rows, rows. Every lane of
+// a row computes the same additions with the operands swapped, so all 16 hold
+// the same bits.
+__device__ __forceinline__ float g4a_row_sum16(float x) {
+    x += g4a_dpp<G4A_DPP_XOR1>(x);
+    x += g4a_dpp<G4A_DPP_XOR2>(x);
+    x += g4a_dpp<G4A_DPP_HALF_MIRROR>(x);
+    x += g4a_dpp<G4A_DPP_ROW_MIRROR>(x);
+    return x;
+}
+
+__device__ __forceinline__ float g4a_row_max16(float x) {
+    x = fmaxf(x, g4a_dpp<G4A_DPP_XOR1>(x));
+    x = fmaxf(x, g4a_dpp<G4A_DPP_XOR2>(x));
+    x = fmaxf(x, g4a_dpp<G4A_DPP_HALF_MIRROR>(x));
+    x = fmaxf(x, g4a_dpp<G4A_DPP_ROW_MIRROR>(x));
+    return x;
+}
+
+// Max over each 8-lane group (lanes 8g .. 8g+7), in every lane of the group.
+__device__ __forceinline__ float g4a_max8(float x) {
+    x = fmaxf(x, g4a_dpp<G4A_DPP_XOR1>(x));
+    x = fmaxf(x, g4a_dpp<G4A_DPP_XOR2>(x));
+    x = fmaxf(x, g4a_dpp<G4A_DPP_HALF_MIRROR>(x));
+    return x;
+}
+
 // A float4 store of data the next kernel reads once (split partials, output
 // rows): non-temporal, so it does not sit in this kernel's L2 as a dirty line
 // that the end-of-kernel write-back has to flush.
