@@ -15,18 +15,6 @@ __device__ __forceinline__ float g4a_gelu_tanh(float v) {
 
 constexpr float G4A_NEG_INF = -__builtin_huge_valf();
 
-// Butterfly max / sum over the 64 lanes of a wave (every lane gets the result).
-__device__ __forceinline__ float g4a_wave_max(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
-    return x;
-}
-
-__device__ __forceinline__ float g4a_wave_sum(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-    return x;
-}
 
 // x of another lane of the same 16-lane row, by a DPP pattern (no LDS round trip).
 constexpr int G4A_DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
@@ -55,6 +43,24 @@ __device__ __forceinline__ float g4a_row_max16(float x) {
     x = fmaxf(x, g4a_dpp<G4A_DPP_HALF_MIRROR>(x));
     x = fmaxf(x, g4a_dpp<G4A_DPP_ROW_MIRROR>(x));
     return x;
+}
+
+// Max / sum over the 64 lanes of a wave (every lane gets the same bits): the
+// 16-lane rows by DPP, then the four row results through readlane, with no LDS
+// round trip. The whole wave must be active (readlane reads lanes 0, 16, 32
+// and 48 whatever EXEC holds).
+__device__ __forceinline__ float g4a_lane(float x, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+
+__device__ __forceinline__ float g4a_wave_max(float x) {
+    x = g4a_row_max16(x);
+    return fmaxf(fmaxf(g4a_lane(x, 0), g4a_lane(x, 16)), fmaxf(g4a_lane(x, 32), g4a_lane(x, 48)));
+}
+
+__device__ __forceinline__ float g4a_wave_sum(float x) {
+    x = g4a_row_sum16(x);
+    return (g4a_lane(x, 0) + g4a_lane(x, 16)) + (g4a_lane(x, 32) + g4a_lane(x, 48));
 }
 
 // Max over each 8-lane group (lanes 8g .. 8g+7), in every lane of the group.
