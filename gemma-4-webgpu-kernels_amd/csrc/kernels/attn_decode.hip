@@ -655,6 +655,15 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
 
     const float* const q0row = qs + (2 * hp) * DH + key;      // head 2hp, dims d + key
     const float* const q1row = qs + (2 * hp + 1) * DH + key;  // head 2hp + 1
+    // the lane's query values for every tile, read from LDS once: dims 16 i + key
+    // of heads 2hp, 2hp+1 (64 VGPRs at Dh 512; 25.9 against 26.35 us at 32K keys
+    // with the reads inside the dot loop)
+    float qreg[2][DH / 16];
+#pragma unroll
+    for (int i = 0; i < DH / 16; ++i) {
+        qreg[0][i] = q0row[16 * i];
+        qreg[1][i] = q1row[16 * i];
+    }
     const float* kcol[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) kcol[j] = my_ring + key * 64 + 4 * (j ^ key);
@@ -700,8 +709,8 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
             if (c < NKS) {
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
-                    const float q0 = q0row[64 * c + 16 * b];
-                    const float q1 = q1row[64 * c + 16 * b];
+                    const float q0 = qreg[0][4 * c + b];
+                    const float q1 = qreg[1][4 * c + b];
                     float4 k4[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) k4[i] = ld4(kcol[4 * b + i] + bi * BUF);
@@ -727,8 +736,9 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
                 }
             } else {
                 const int vc = c - NKS;
-                if (vc == 0) {
+                if (vc == 0 && it > 0) {
                     // rescale the running output of every head by its correction factor
+                    // (none before the first tile: the output is still zero)
                     const float4 c0 = ld4(my_corr), c1 = ld4(my_corr + 4);
                     const float cr[GROUP] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
