@@ -575,8 +575,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
             s[r] = vis[r] ? (S[r] * sc) * p.scale : NEG_INF;
         }
         float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-        tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
-        tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+        tm = g4a_col_max4(tm);
         const float mn = fmaxf(m_run, tm);
 
         // candidates: count first, make room if needed, then record
@@ -686,8 +685,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
     __syncthreads();  // the q rows are visible
     if (wave_valid) flush_rows(qlds);
     float l = l_part;
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    l = g4a_col_sum4(l);
     __syncthreads();  // staging done: the merge area overlays it
     float* const mo_ = smem + rb * (NC * 16 * 64 + 2 * 64);  // odd parity -> even parity, per row block
     if (par == 1) {
@@ -1115,8 +1113,7 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
             s[r] = vis[r] ? S[r] * p.scale : NEG_INF;
         }
         float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-        tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
-        tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+        tm = g4a_col_max4(tm);
         const float mn = fmaxf(m_run, tm);
 
         // ---- record the keys within TAU of the running maximum ----
@@ -1213,8 +1210,7 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
         flush_staged(smem + w * C::STAGE);
     }
     float l = l_part;
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    l = g4a_col_sum4(l);
     // O row 4g + r' is query qw + row/8, head h0 + row%8; this wave's columns HD*dhf + 64c + 4rl + e
     if (!split) {
         if (!wave_valid) return;

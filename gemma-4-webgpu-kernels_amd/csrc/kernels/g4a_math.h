@@ -63,6 +63,35 @@ __device__ __forceinline__ float g4a_wave_sum(float x) {
     return (g4a_lane(x, 0) + g4a_lane(x, 16)) + (g4a_lane(x, 32) + g4a_lane(x, 48));
 }
 
+// Lane l's x and lane (l ^ 16)'s (or (l ^ 32)'s) by a gfx950 permlane swap with
+// both operands x: .x holds the lower row's value, .y the upper row's, in both
+// lanes of the pair, so a sum of the two has the same bits in both.
+__device__ __forceinline__ float2 g4a_pair16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float2 g4a_pair32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four rows' lanes of one
+// column), in every one of them: the order and bits of an xor 16, 32 butterfly.
+__device__ __forceinline__ float g4a_col_max4(float x) {
+    float2 t = g4a_pair16(x);
+    x = fmaxf(t.x, t.y);
+    t = g4a_pair32(x);
+    return fmaxf(t.x, t.y);
+}
+
+__device__ __forceinline__ float g4a_col_sum4(float x) {
+    float2 t = g4a_pair16(x);
+    x = t.x + t.y;
+    t = g4a_pair32(x);
+    return t.x + t.y;
+}
+
 // Max over each 8-lane group (lanes 8g .. 8g+7), in every lane of the group.
 __device__ __forceinline__ float g4a_max8(float x) {
     x = fmaxf(x, g4a_dpp<G4A_DPP_XOR1>(x));
