@@ -899,7 +899,7 @@ __device__ __forceinline__ void qk1_dims16(float& s, float q, const float4 (&k)[
 //           registers and broadcast along each row with DPP, K read from LDS
 //           (rows padded to DH + 4 floats: the 16 keys of a read sit on
 //           distinct banks), one 16-dim block ahead of its use;
-//   softmax: per head over the tile's 16 keys (4 xor-shuffles in the row);
+//   softmax: per head over the tile's 16 keys (row max and sum by DPP);
 //   P.V:    lane l owns dims 4l..4l+3 (+256 for DH 512) of its 4 heads, fused
 //           multiply-adds over the tile's V rows in LDS;
 //   end:    the two tiles merge through LDS (wave w merges heads 2w, 2w+1)
