@@ -48,6 +48,13 @@ namespace {
 constexpr float PF_RESCALE = 4.0f;
 constexpr float PF_PSCALE = 1024.0f;
 
+// e^x for the in-loop probabilities: the hardware 2^x of x log2(e). The rounded
+// product moves a weight by ~|x| 1e-7 relatively, ~4e-8 at most once weighted
+// by e^x itself; the exact rescoring cancels this same form, so only the
+// estimate's contribution changes.
+constexpr float PF_LOG2E = 1.44269504088896341f;
+__device__ __forceinline__ float pf_exp(float x) { return __builtin_amdgcn_exp2f(x * PF_LOG2E); }
+
 __device__ __forceinline__ uint64_t ballot(bool b) { return __ballot(b); }
 __device__ __forceinline__ int lanes_below(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
@@ -375,7 +382,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
         float delta = 0.0f;
         if (has) {
             const float m = my_m[rho];
-            delta = psc * (expf(dot * p.scale - m) - expf(my_s[e] - m));
+            delta = psc * (expf(dot * p.scale - m) - pf_exp(my_s[e] - m));
         }
         const int nb = min(64, cnt - base);
         for (int i = 0; i < nb; ++i) {
@@ -522,7 +529,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
             float delta = 0.0f;
             if (has) {
                 const float m = my_m[rho];
-                delta = psc * (expf(dot * p.scale - m) - expf(my_s[e] - m));
+                delta = psc * (expf(dot * p.scale - m) - pf_exp(my_s[e] - m));
             }
             f4v lc = f4v{0.0f, 0.0f, 0.0f, 0.0f};
             correct_o4(base, delta, rho, kap, &lc);
@@ -621,7 +628,7 @@ __device__ __forceinline__ void prefill_pair(const G4aPrefillParams& p) {
 
         float pr[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? psc * expf(s[r] - m_ref) : 0.0f;
+        for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? psc * pf_exp(s[r] - m_ref) : 0.0f;
         l_part += (pr[0] + pr[1]) + (pr[2] + pr[3]);
         if (v16) {
             // O += P V on v_mfma_f32_16x16x16_f16: Phi Vhi + Phi Vlo + Plo Vhi (relative error
@@ -921,7 +928,7 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
         float delta = 0.0f;
         if (has) {
             const float m = my_m[rho];
-            delta = psc * (expf(dot * p.scale - m) - expf(my_s[e] - m));
+            delta = psc * (expf(dot * p.scale - m) - pf_exp(my_s[e] - m));
         }
         const int nb = min(64, cnt - base);
         for (int i = 0; i < nb; ++i) {
@@ -1161,7 +1168,7 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
         // ---- probabilities against m_ref and P.V for this wave's columns ----
         float pr[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? psc * expf(s[r] - m_ref) : 0.0f;
+        for (int r = 0; r < 4; ++r) pr[r] = vis[r] ? psc * pf_exp(s[r] - m_ref) : 0.0f;
         l_part += (pr[0] + pr[1]) + (pr[2] + pr[3]);
         if (v16) {
             // O += P V on v_mfma_f32_16x16x16_f16: Phi Vhi + Phi Vlo + Plo Vhi. Lane (g, rl)
