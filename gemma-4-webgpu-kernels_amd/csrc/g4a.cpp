@@ -103,6 +103,10 @@ struct g4a_ctx {
     hipFunction_t linear_words[3][3][3] = {};  // [bits 2/4/8][(MT, RU) = (1, 2), (1, 8), (4, 4)][mode]
     hipFunction_t linear_elem[3] = {};         // [mode]
     hipFunction_t linear_mfma[3][2][3] = {};   // [bits 2/4/8][64 / 128 weight rows per tile][mode]: M >= 16
+    hipFunction_t linear_i8[3][2] = {};        // [bits 2/4/8][M = 1, 2]: int8 matrix cores, mode 0
+    // G4A_LINEAR_I8=0 keeps M <= 2 projections off the int8 matrix-core kernel,
+    // =1 sends every eligible one there (for comparisons); unset: by weight size
+    int linear_i8_use = -1;
     hipFunction_t embed_q = nullptr;
     hipFunction_t linear_half[2][3] = {};       // 2-bit, M = 1, 32 lanes per row: [RU = 1, 4][mode]
     hipFunction_t linear_f32_words[3] = {};  // f32 weights: (MT, RU) = (1, 2), (1, 8), (4, 4)
@@ -553,6 +557,13 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
                     if (int rc = get_fn(ctx, &ctx->linear_mfma[b][t][m], name)) return bail(rc);
                 }
         }
+        for (int b = 0; b < 3; ++b)
+            for (int m = 0; m < 2; ++m) {
+                char name[64];
+                snprintf(name, sizeof name, "g4a_linear_q_i8_b%d_m%d", bits[b], m + 1);
+                if (int rc = get_fn(ctx, &ctx->linear_i8[b][m], name)) return bail(rc);
+            }
+        if (const char* env = getenv("G4A_LINEAR_I8")) ctx->linear_i8_use = atoi(env) != 0 ? 1 : 0;
         if (int rc = get_fn(ctx, &ctx->embed_q, "g4a_embed_rows_q")) return bail(rc);
         static const char* f32_words[3] = {"g4a_linear_q_b32_m1_r2_mode0", "g4a_linear_q_b32_m1_r8_mode0",
                                            "g4a_linear_q_b32_m4_r4_mode0"};
@@ -1138,6 +1149,10 @@ int norm_rope_launch(g4a_ctx* ctx, G4aNormRopeSeg* segs, uint32_t nseg, uint32_t
 constexpr size_t LINEAR_LDS_BYTES = 64 << 10;
 // Activation rows from which a projection runs on the matrix cores.
 constexpr uint32_t LINEAR_MFMA_MIN_M = 16;
+// Packed weight bytes from which an M <= 2 projection runs on the int8 matrix
+// cores (below it the word kernel's shorter start wins; both are at the
+// dispatch floor there).
+constexpr uint64_t LINEAR_I8_MIN_BYTES = 16ull << 20;
 
 // Grid of a grid-stride elementwise launch over n items.
 dim3 ew_grid(g4a_ctx* ctx, size_t n) {
@@ -1238,6 +1253,21 @@ int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qwei
                 return rc;
         }
         return G4A_OK;
+    }
+    // M <= 2, large weights: int8 matrix cores with x cut into exact digits (mode 0)
+    const uint64_t weight_bytes = uint64_t(w->N) * p.row_bytes;
+    const bool i8_ok = mode == 0 && M <= 2 && p.scale_stride == 1 && p.row_bytes % G4A_LI8_UNIT_BYTES == 0 &&
+                       w->K % 64 == 0 && uint64_t(w->K / 64) * 1024 <= LINEAR_LDS_BYTES &&
+                       (reinterpret_cast<uintptr_t>(w->qbytes) & 15) == 0;
+    if (i8_ok && (ctx->linear_i8_use == 1 || (ctx->linear_i8_use < 0 && weight_bytes >= LINEAR_I8_MIN_BYTES))) {
+        p.wb = static_cast<const uint8_t*>(w->qbytes);
+        // chunks of 32 weight rows, one per wave at a time; 16 waves per CU (four
+        // workgroups, whose x digit staging then overlaps the others' streams)
+        const uint64_t waves = G4A_LI8_THREADS / 64, chunks = (uint64_t(w->N) + 31) / 32;
+        const uint64_t cap = uint64_t(std::max(ctx->cu_count, 1)) * (16 / waves);
+        const uint32_t gx = uint32_t(std::max<uint64_t>(1, std::min(cap, (chunks + waves - 1) / waves)));
+        return launch(ctx, ctx->linear_i8[bi][M - 1], dim3(gx, 1, 1), dim3(G4A_LI8_THREADS, 1, 1), p,
+                      "quantised linear (int8 matrix cores)", true, unsigned(w->K / 64 * 1024));
     }
     // the word kernel's activation rows, zero-padded to whole wave strides of words
     const uint64_t vpw = 32 / w->bits, words_per_row = uint64_t(w->K) * w->bits / 32;

@@ -183,6 +183,11 @@ struct G4aNormRopeParams {
     float eps;
 };
 
+// The int8 matrix-core projection (M <= 2): threads per workgroup, and the row
+// bytes each 16-row block streams per unit (K * bits / 8 must be a multiple).
+constexpr uint32_t G4A_LI8_THREADS = 256;
+constexpr uint32_t G4A_LI8_UNIT_BYTES = 128;
+
 // Quantised projection y[M, N] = epilogue(x[M, K] . W^T) (g4a_linear_q_*).
 // W rows are packed fields of `bits` bits, LSB-first (offset binary, or native
 // I8 when bits = 8 and xm = 0), each row starting on a 32-bit word for the

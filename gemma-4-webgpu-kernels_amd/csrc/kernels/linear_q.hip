@@ -500,6 +500,317 @@ __device__ __forceinline__ void linear_q_elem(const G4aLinearParams& p) {
     p.y[(size_t)m * p.N + n] = o;
 }
 
+// ---------------------------------------------------------------------------
+// Decode projections (M <= 2) over large weights on the int8 matrix cores
+// (v_mfma_i32_16x16x64_i8), with exact integer products and sums.
+//
+// x is cut into LI8_NSL signed digits per element against one power of two per
+// activation row: with max|x| < 2^E, u = x * 2^(6-E) has |u| < 64, and
+// b_0 = rint(u), b_j = rint(128 r_(j-1)), r_j = 128 r_(j-1) - b_j (r_0 = u - b_0)
+// are integers in [-64, 64] (int8), each step exact in f32. So
+// x = 2^(E-6) * sum_j b_j 2^(-7j) exactly for every element within 2^-32 of the
+// row's maximum (smaller ones keep all bits down to 2^(E-56)). The weight
+// fields times F (the sign-extended bytes of the word kernel) are int8 too, so
+// each digit column's dot product is exact in int32, and the only roundings are
+// the f32 sum of the LI8_NSL column totals (largest weight 2^0, each next one
+// 2^-7 of it) and the final scaling. The result is within a few f32 ulps of the
+// exact sum of x_k * deq(n, k): closer to it than any f32 summation order,
+// including the CPU's. A row holding an inf or NaN is computed in the CPU's
+// exact order instead (the element kernel's loop), since the digits cannot hold
+// it.
+//
+// Layout. A = 16 weight rows x 64 k, B = 64 k x 16 columns (column 8m + j: digit
+// j of activation row m), D = 16 rows x 16 columns in int32. Lane l holds row /
+// column l % 16 and k-group l / 16 of A / B, and rows 4 (l / 16) + v of column
+// l % 16 of D. Which k sits in which byte of a lane's 16 A bytes is a choice
+// here, made so that the fields come out of the loaded words with one shift and
+// one mask per 4 bytes; the digits are staged in LDS in the same order, and the
+// sum over k does not depend on it. Lane (row r, group g) loads 16 bytes at
+// byte 64 j + 16 g of its row for 64-byte row segment j ("unit"), i.e. 8 / BITS
+// MFMA steps of 64 k.
+//
+// Work split: chunks of 16 RB rows (RB A blocks share each B fragment read from
+// LDS); every wave streams a contiguous range of chunks, unit by unit, through a
+// ring of D register sets, so the loads of the next D - 1 units are in flight
+// while a unit computes (the word kernel's ring).
+typedef int i4v __attribute__((ext_vector_type(4)));
+constexpr int LI8_NSL = 8;      // digits per activation element
+constexpr int LI8_KMAX = 4096;  // K limit: the digits of one row fill at most 64 KiB of LDS
+constexpr bool LI8_STRIDED = true;
+
+template <int BITS>
+struct I8Fmt {
+    static constexpr int MPS = 8 / BITS;                                  // MFMA steps per unit
+    static constexpr int LOG2F = BITS == 2 ? 6 : BITS == 4 ? 4 : 0;     // fields are value * 2^LOG2F
+};
+
+// The k of byte 4 i + p of the A / B operand of lane group g at MFMA step s. A
+// unit of LPU 64-byte pieces: lane group g loads 16-byte piece h < LPU of it at
+// byte 16 (LPU g + h), i.e. words 4 (LPU g + h) .. + 3; piece v = LPU J + h of
+// the row (J the unit) holds MFMA steps MPS v .. MPS v + MPS - 1.
+template <int BITS, int LPU>
+__device__ __forceinline__ uint32_t i8_k(uint32_t s, uint32_t g, uint32_t i, uint32_t p) {
+    constexpr uint32_t MPS = 8 / BITS;
+    const uint32_t v = s / MPS, t = s % MPS, h = v % LPU;
+    const uint32_t wb = 16 * (v - h) + 4 * (LPU * g + h);  // the piece's first word
+    if constexpr (BITS == 2) {
+        return 16 * (wb + t) + 4 * p + i;  // byte p of (word << (6 - 2 i)) & 0xC0C0C0C0, word t of the piece
+    } else if constexpr (BITS == 4) {
+        return 8 * (wb + 2 * t + (i >> 1)) + 2 * p + (i & 1);  // i even: (word << 4) & 0xF0F0F0F0, odd: word & ..
+    } else {
+        return 4 * (wb + i) + p;  // register i is word i of the piece
+    }
+}
+
+// The A operand of MFMA step t of a unit from the lane's 16 loaded bytes.
+template <int BITS, int T>
+__device__ __forceinline__ i4v i8_operand(const uint4& w, uint32_t xm) {
+    if constexpr (BITS == 2) {
+        const uint32_t v = (T == 0 ? w.x : T == 1 ? w.y : T == 2 ? w.z : w.w) ^ xm;
+        return i4v{(int)((v << 6) & 0xC0C0C0C0u), (int)((v << 4) & 0xC0C0C0C0u), (int)((v << 2) & 0xC0C0C0C0u),
+                   (int)(v & 0xC0C0C0C0u)};
+    } else if constexpr (BITS == 4) {
+        const uint32_t v0 = (T == 0 ? w.x : w.z) ^ xm, v1 = (T == 0 ? w.y : w.w) ^ xm;
+        return i4v{(int)((v0 << 4) & 0xF0F0F0F0u), (int)(v0 & 0xF0F0F0F0u), (int)((v1 << 4) & 0xF0F0F0F0u),
+                   (int)(v1 & 0xF0F0F0F0u)};
+    } else {
+        return i4v{(int)(w.x ^ xm), (int)(w.y ^ xm), (int)(w.z ^ xm), (int)(w.w ^ xm)};
+    }
+}
+
+template <int BITS, int MT, int RB, int D, int LPU, int NW>
+__device__ __forceinline__ void linear_q_i8(const G4aLinearParams& p) {
+    using F = I8Fmt<BITS>;
+    constexpr int MPS = F::MPS;
+    constexpr int TPT = LI8_KMAX / (256 * NW);  // digit tasks per thread at most (K / 4 tasks, 64 NW threads)
+    extern __shared__ __attribute__((aligned(16))) uint32_t bsh[];  // [K / 64 steps][64 lanes][4 words] digits
+    __shared__ float redmax[NW][MT];
+    __shared__ int redbad[NW][MT];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t K = p.K, N = p.N;
+    const uint32_t NU = K * BITS / (512 * LPU);  // units per row
+    const uint32_t NS = K / 64;                  // MFMA steps per row
+    const uint32_t row_bytes = K * BITS / 8;
+    const uint32_t nchunk = (N + 16 * RB - 1) / (16 * RB);
+    const uint32_t GW = gridDim.x * NW, gw = blockIdx.x * NW + wv;
+    // the wave's chunks: ordinals 0 .. nc - 1
+    uint32_t nc, c0 = 0;
+    if constexpr (LI8_STRIDED) {
+        nc = nchunk > gw ? (nchunk - gw + GW - 1) / GW : 0;
+    } else {
+        const uint32_t per = (nchunk + GW - 1) / GW;
+        c0 = min(gw * per, nchunk);
+        nc = min(c0 + per, nchunk) - c0;
+    }
+    auto chunk = [&](uint32_t i) { return LI8_STRIDED ? gw + i * GW : c0 + i; };
+    const uint32_t T = nc * NU;  // the wave's units
+    const int r = lane & 15, g = lane >> 4;
+    // the output this lane stores at a chunk's end: digit column cc = 8 m + jj,
+    // rows 4 g + v of D; lanes jj < 4 store row 4 g + jj of activation row m
+    const int cc = lane & 15, om = cc >> 3, jj = cc & 7;
+
+    // Unit loads: the chunk's row bases are set when a chunk starts (rows past N
+    // clamped to the last row), then each unit adds 64 LPU bytes: one wave-uniform
+    // base and a 32-bit lane offset per load. Each ring slot holds the RB 16-byte
+    // loads, and at a chunk's first unit the scale of the row this lane stores.
+    uint32_t li = 0, lj = 0;  // the next unit to load: chunk ordinal, unit
+    uint32_t roff[RB];
+    auto load = [&](uint4 (&a)[RB][LPU], float (&sc)[RB]) {
+        // past the wave's last unit: that unit again (its lines are in cache), never
+        // the next wave's rows
+        const bool past = li >= nc;
+        const uint32_t c = chunk(past ? nc - 1 : li), jl = past ? NU - 1 : lj;
+        if (lj == 0 && !past) {
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                roff[rb] = (min(16 * (RB * c + rb) + r, N - 1) - 16 * RB * c) * row_bytes + 16 * LPU * g;
+                sc[rb] = p.s[min(16 * (RB * c + rb) + 4 * g + (jj & 3), N - 1)];
+            }
+        }
+        const uint8_t* __restrict__ base = p.wb + (size_t)(16 * RB * c) * row_bytes + 64 * LPU * jl;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int h = 0; h < LPU; ++h) a[rb][h] = *reinterpret_cast<const uint4*>(base + roff[rb] + 16 * h);
+        if (++lj == NU) {
+            lj = 0;
+            ++li;
+        }
+    };
+    // --- digits of x. Thread task (s, g, i) covers the 4 k's of bytes 4 i .. 4 i + 3
+    // of lane group g at step s; the tasks partition k, so the values loaded for
+    // them also give the row maxima (and a non-finite flag). The x loads go out
+    // first, then the first units' weight loads (which they would otherwise queue
+    // behind), then the digits are staged.
+    float xv[MT][TPT][4];
+    float mx[MT];
+    int bad[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        mx[m] = 0.0f;
+        bad[m] = 0;
+    }
+#pragma unroll
+    for (int tt = 0; tt < TPT; ++tt) {
+        const uint32_t task = tid + 64 * NW * tt;
+        const bool on = task < NS * 16;
+        const uint32_t s = task >> 4, tg = (task >> 2) & 3, ti = task & 3;
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int pp = 0; pp < 4; ++pp) {
+                const float v = (on && m < (int)p.M) ? p.x[(size_t)m * K + i8_k<BITS, LPU>(s, tg, ti, pp)] : 0.0f;
+                xv[m][tt][pp] = v;
+                mx[m] = fmaxf(mx[m], fabsf(v));
+                bad[m] |= !(fabsf(v) <= 3.40282347e38f);  // inf or NaN
+            }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 wa[D][RB][LPU];
+    float ws[D][RB];
+#pragma unroll
+    for (int d = 0; d + 1 < D; ++d)
+        if (T) load(wa[d], ws[d]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        mx[m] = g4a_wave_max(mx[m]);
+        bad[m] = __any(bad[m]) ? 1 : 0;
+        if (lane == 0) {
+            redmax[wv][m] = mx[m];
+            redbad[wv][m] = bad[m];
+        }
+    }
+    __syncthreads();
+    int xe[MT], xb[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        float M4 = redmax[0][m];
+        xb[m] = redbad[0][m];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            M4 = fmaxf(M4, redmax[w][m]);
+            xb[m] |= redbad[w][m];
+        }
+        xe[m] = 0;
+        if (M4 > 0.0f) frexpf(M4, &xe[m]);  // M4 < 2^e
+    }
+#pragma unroll
+    for (int tt = 0; tt < TPT; ++tt) {
+        const uint32_t task = tid + 64 * NW * tt;
+        if (task >= NS * 16) break;
+        const uint32_t s = task >> 4, tg = (task >> 2) & 3, ti = task & 3;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            uint32_t dg[LI8_NSL];
+#pragma unroll
+            for (int j = 0; j < LI8_NSL; ++j) dg[j] = 0;
+            if (!xb[m]) {
+#pragma unroll
+                for (int pp = 0; pp < 4; ++pp) {
+                    float u = ldexpf(xv[m][tt][pp], 6 - xe[m]);
+#pragma unroll
+                    for (int j = 0; j < LI8_NSL; ++j) {
+                        const float b = rintf(u);
+                        dg[j] |= ((uint32_t)(int)b & 0xFFu) << (8 * pp);
+                        u = (u - b) * 128.0f;
+                    }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < LI8_NSL; ++j) bsh[(s * 64 + 16 * tg + 8 * m + j) * 4 + ti] = dg[j];
+        }
+        if constexpr (MT == 1) {
+#pragma unroll
+            for (int j = 8; j < 16; ++j) bsh[(s * 64 + 16 * tg + j) * 4 + ti] = 0u;
+        }
+    }
+    __syncthreads();
+    const int my_e = xe[0] + (MT > 1 && om == 1 ? xe[MT - 1] - xe[0] : 0);
+    const int my_bad = MT > 1 && om == 1 ? xb[MT - 1] : xb[0];
+
+    i4v acc[RB];
+    float cur_s[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        acc[rb] = i4v{0, 0, 0, 0};
+        cur_s[rb] = 0.0f;
+    }
+    uint32_t si = 0, sj = 0;  // the unit to compute
+    auto step = [&](const uint4 (&a)[RB][LPU], const float (&sc)[RB], bool live) {
+        const uint32_t c = chunk(si), j = sj;
+        if (++sj == NU) {
+            sj = 0;
+            ++si;
+        }
+        if (j == 0) {
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) cur_s[rb] = sc[rb];
+        }
+#pragma unroll
+        for (int h = 0; h < LPU; ++h)
+#pragma unroll
+            for (int tt = 0; tt < MPS; ++tt) {
+                const uint32_t st = (LPU * j + h) * MPS + tt;
+                const uint4 bw = *reinterpret_cast<const uint4*>(bsh + (st * 64 + lane) * 4);
+                const i4v bv = i4v{(int)bw.x, (int)bw.y, (int)bw.z, (int)bw.w};
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) {
+                    i4v av;
+                    if (tt == 0) av = i8_operand<BITS, 0>(a[rb][h], p.xm);
+                    if (tt == 1) av = i8_operand<BITS, (MPS > 1 ? 1 : 0)>(a[rb][h], p.xm);
+                    if (tt == 2) av = i8_operand<BITS, (MPS > 2 ? 2 : 0)>(a[rb][h], p.xm);
+                    if (tt == 3) av = i8_operand<BITS, (MPS > 3 ? 3 : 0)>(a[rb][h], p.xm);
+                    acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc[rb], 0, 0, 0);
+                }
+            }
+        if (j + 1 == NU) {
+            // the chunk's digit-column sums are complete: weight column j by 2^(-7 j),
+            // sum the LI8_NSL columns of each activation row (8 lanes), scale, store
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                float tot[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float x = ldexpf((float)acc[rb][v], -7 * jj);
+                    x += g4a_dpp<G4A_DPP_XOR1>(x);
+                    x += g4a_dpp<G4A_DPP_XOR2>(x);
+                    x += g4a_dpp<G4A_DPP_HALF_MIRROR>(x);
+                    tot[v] = x;
+                }
+                acc[rb] = i4v{0, 0, 0, 0};
+                const uint32_t n = 16 * (RB * c + rb) + 4 * g + jj;
+                if (live && jj < 4 && om < (int)p.M && n < N) {
+                    const float tv = jj == 0 ? tot[0] : jj == 1 ? tot[1] : jj == 2 ? tot[2] : tot[3];
+                    float o;
+                    if (!my_bad) {
+                        o = (float)((double)tv * (double)cur_s[rb] * ldexp(1.0, my_e - 6 - F::LOG2F));
+                    } else {
+                        o = 0.0f;  // the CPU's order (an inf or NaN in the row)
+                        const float* __restrict__ xr = p.x + (size_t)om * K;
+                        for (uint32_t k = 0; k < K; ++k)
+                            o += xr[k] * deq(p.wb, p.s, p.bits, p.row_bytes, p.group_size, p.scale_stride,
+                                             p.signed_i8, n, k);
+                    }
+                    p.y[(size_t)om * N + n] = o;
+                }
+            }
+        }
+    };
+
+    // Whole groups of D units, no branch between them; units past T (at most
+    // D - 1) re-read the wave's last unit and store nothing.
+    for (uint32_t t = 0; t < T; t += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            load(wa[(d + D - 1) % D], ws[(d + D - 1) % D]);
+            __builtin_amdgcn_sched_barrier(0);
+            step(wa[d], ws[d], t + d < T);
+        }
+    }
+}
+
 // embed_rows on a quantised table (rust/src/backend_cpu.rs:127-137): one thread
 // per output element.
 __device__ __forceinline__ void embed_rows_q(const G4aEmbedParams& p) {
@@ -558,6 +869,20 @@ G4A_LINEAR_MFMA(4, 2)
 G4A_LINEAR_MFMA(8, 0)
 G4A_LINEAR_MFMA(8, 1)
 G4A_LINEAR_MFMA(8, 2)
+
+// int8 matrix cores, M <= MT, MODE 0: (bits, MT); 2 A blocks per chunk, units of
+// 128 row bytes, one unit in flight ahead of the one computing
+#define G4A_LINEAR_I8(B, MT)                                                                              \
+    extern "C" __global__ __launch_bounds__(G4A_LI8_THREADS) void g4a_linear_q_i8_b##B##_m##MT(             \
+        G4aLinearParams p) {                                                                              \
+        linear_q_i8<B, MT, 2, 2, G4A_LI8_UNIT_BYTES / 64, G4A_LI8_THREADS / 64>(p);                        \
+    }
+G4A_LINEAR_I8(2, 1)
+G4A_LINEAR_I8(2, 2)
+G4A_LINEAR_I8(4, 1)
+G4A_LINEAR_I8(4, 2)
+G4A_LINEAR_I8(8, 1)
+G4A_LINEAR_I8(8, 2)
 
 G4A_LINEAR_WORDS(32, 1, 2, 4, 0)
 G4A_LINEAR_WORDS(32, 1, 8, 2, 0)

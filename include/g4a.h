@@ -300,8 +300,13 @@ int g4a_linear(g4a_ctx *ctx, const float *w, uint32_t N, uint32_t K, const float
  * 64 run the word-parallel kernel (HBM-bound, f32 sums in another order than the
  * reference's, within f32 reordering error); with M >= 16, K % 64 == 0 and an
  * 8-byte aligned qbytes they run on the matrix cores instead (exact products,
- * f32 accumulation, the same error bound); every other weight runs one thread
- * per output in the reference CPU's order (bit-identical for g4a_linear_q). */
+ * f32 accumulation, the same error bound). g4a_linear_q with M <= 2, one scale
+ * per row, rows of a multiple of 128 bytes, K <= 4096 (K % 64 == 0), a 16-byte
+ * aligned qbytes and at least 16 MB of packed weights (the lm_head) runs on the
+ * int8 matrix cores with x cut into exact digits: within a few f32 ulps of the
+ * exact sum (an activation row holding an inf or NaN: the reference CPU's
+ * order). Every other weight runs one thread per output in the reference CPU's
+ * order (bit-identical for g4a_linear_q). */
 typedef struct {
     const void *qbytes;
     const float *scales;
