@@ -199,6 +199,13 @@ __device__ __forceinline__ void copy16_to_lds(const float* src, float* lds_dst) 
         asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
 
+// The same copy with 4 bytes per lane (global_load_lds_dword): lane l's 4 bytes
+// at `src` land at lds_dst + 4*l (lanes switched off by the exec mask write nothing).
+__device__ __forceinline__ void copy4_to_lds(const void* src, void* lds_dst) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)lds_dst);
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+
 // Wait until at most N vector-memory operations of this wave are in flight
 // (they retire in issue order, so every copy issued before the last N has landed).
 template <int N>
@@ -545,6 +552,7 @@ struct WaveCfg {
     static constexpr int QS = GROUP * DH;
     static constexpr int PB = 8 * KEYS * GROUP;       // [wave][key][head]
     static constexpr int SMEM = RING + QS + PB + 8 * GROUP + 8 * 2 * GROUP + 8;
+    static constexpr int KPB = 8 * 2 * KEYS;          // explicit positions: [wave][tile parity][key]
     static_assert(MERGE <= NB * BUF, "a wave's partial fits its ring");
     static_assert(KPC * DH == BUF && KEYS % KPC == 0, "V chunks hold whole keys of the tile");
     static_assert(QS % 2048 == 0, "the query rows are copied in 8 waves x 1 KiB copies");
@@ -558,7 +566,7 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
     constexpr int GROUP = C::GROUP, KEYS = C::KEYS, BUF = C::BUF, NB = C::NB, AHEAD = C::AHEAD, LPT = C::LPT,
                   NKS = C::NKS, KPC = C::KPC, NCH = C::NCH, ND = C::ND;
 
-    __shared__ __attribute__((aligned(16))) float smem[C::SMEM];
+    __shared__ __attribute__((aligned(16))) float smem[C::SMEM + (KPOS ? C::KPB : 0)];
     float* const ring = smem;                   // [8 waves][NB][BUF]; after the loop wave w's
                                                 // [GROUP][DH] partial in its ring
     float* const qs = smem + C::RING;           // [GROUP][DH]
@@ -580,6 +588,7 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
     float* const my_ring = ring + w * NB * BUF;
     float* const my_pbuf = pbuf + w * KEYS * GROUP;
     float* const my_corr = corrbuf + w * GROUP;
+    uint32_t* const my_kp = reinterpret_cast<uint32_t*>(smem + C::SMEM) + w * 2 * KEYS;  // KPOS: [parity][key]
 
     // query rows: wave w copies 1 KiB pieces w, w + 8, ... (issued before any chunk)
     {
@@ -610,10 +619,11 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
         const uint32_t u = it * 8 + w;
         T.t0 = p.k_start + (split + u * p.nsplit) * KEYS;
         T.active = it < niter && u < ntiles;
-        if (T.active) {
-            const uint32_t kpos_first = KPOS ? p.k_pos[T.t0] : p.k_pos0 + T.t0;
-            T.active = kpos_first <= qpos;  // ascending positions: a future first key means a future tile
-        }
+        // contiguous positions: a tile whose first key is past this query is skipped
+        // (ascending positions). Explicit positions are not read here: the host trims
+        // [k_start, k_end) to keys at or before the last query, the per-key mask covers
+        // earlier queries, and a load here would hold up the tile's copies.
+        if (!KPOS && T.active) T.active = p.k_pos0 + T.t0 <= qpos;
         T.nk = T.active ? min((uint32_t)KEYS, p.k_end - T.t0) : 1u;
         T.row0 = T.active ? phys_row(T.t0, p.ring_cap) : 0u;
         T.kb = T.active ? kbase : p.dummy;
@@ -628,7 +638,18 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
     // chunk c of a wave tile into ring buffer bi: K chunks c < NKS hold dims
     // 64c..64c+63 of the 16 keys (key r's 16-byte column j at slot j ^ r), V chunks
     // hold keys KPC*(c-NKS) .. +KPC-1, all DH dims. Lane l fills 16-byte slot 64i + l.
-    auto issue_chunk = [&](const Tile& T, int c, int bi) {
+    // With explicit positions chunk 0 is preceded by one more copy, the tile's 16
+    // key positions into my_kp[parity] (clamped to the tile's last key; an idle tile
+    // copies dummy words): waiting for chunk 0 then also covers them, and every
+    // other wait below counts one copy short at most, i.e. waits a little longer.
+    auto issue_chunk = [&](const Tile& T, int c, int bi, uint32_t parity) {
+        if constexpr (KPOS) {
+            if (c == 0 && lane < KEYS) {
+                const void* src = T.active ? (const void*)(p.k_pos + T.t0 + min((uint32_t)lane, T.nk - 1))
+                                           : (const void*)(p.dummy + lane);
+                copy4_to_lds(src, my_kp + parity * KEYS);
+            }
+        }
         float* const dst = my_ring + bi * BUF;
 #pragma unroll
         for (int i = 0; i < LPT; ++i) {
@@ -648,7 +669,7 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
 
     Tile cur = tile_info(0);
 #pragma unroll
-    for (int c = 0; c < AHEAD; ++c) issue_chunk(cur, c, c);
+    for (int c = 0; c < AHEAD; ++c) issue_chunk(cur, c, c, 0u);
     if (lane == 0) progress[w] = -1;
     wait_vm<LPT * AHEAD>();  // this wave's query pieces have landed
     barrier_lds();           // ... and every wave's
@@ -686,8 +707,8 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
             // chunk c + AHEAD refills the buffer of chunk c + AHEAD - NB; with AHEAD + 1 == NB
             // that is chunk c - 1, whose LDS reads must have completed
             if constexpr (AHEAD + 1 >= NB) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (c + AHEAD < NCH) issue_chunk(cur, c + AHEAD, (c + AHEAD) % NB);
-            else if (!last) issue_chunk(nxt, c + AHEAD - NCH, (c + AHEAD) % NB);
+            if (c + AHEAD < NCH) issue_chunk(cur, c + AHEAD, (c + AHEAD) % NB, it & 1u);
+            else if (!last) issue_chunk(nxt, c + AHEAD - NCH, (c + AHEAD) % NB, (it + 1) & 1u);
             // chunk c has landed: the copies issued after it are the next AHEAD chunks
             // (fewer at the end of the last wave tile)
             if (last && c + AHEAD >= NCH) wait_vm_upto16(LPT * (NCH - 1 - c));
@@ -719,7 +740,7 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
                 if (c == NKS - 1) {
                     // online softmax of heads 2hp, 2hp+1 over the row's 16 keys
                     const uint32_t j = cur.t0 + min((uint32_t)key, cur.nk - 1);
-                    const uint32_t kp = KPOS ? p.k_pos[j] : p.k_pos0 + j;
+                    const uint32_t kp = KPOS ? my_kp[(it & 1u) * KEYS + key] : p.k_pos0 + j;
                     const bool vis =
                         (uint32_t)key < cur.nk && kp <= qpos && (p.window == 0 || qpos - kp < p.window);
 #pragma unroll
