@@ -525,22 +525,23 @@ __device__ __forceinline__ void linear_q_elem(const G4aLinearParams& p) {
 // l % 16 of D. Which k sits in which byte of a lane's 16 A bytes is a choice
 // here, made so that the fields come out of the loaded words with one shift and
 // one mask per 4 bytes; the digits are staged in LDS in the same order, and the
-// sum over k does not depend on it. Lane (row r, group g) loads 16 bytes at
-// byte 64 j + 16 g of its row for 64-byte row segment j ("unit"), i.e. 8 / BITS
-// MFMA steps of 64 k.
+// sum over k does not depend on it. A row is read in units of LPU 64-byte
+// pieces (LPU = 2: whole 128-byte lines); lane (row r, group g) loads the LPU
+// adjacent 16-byte pieces at byte 16 LPU g of each unit, each piece holding
+// 8 / BITS MFMA steps of 64 k.
 //
 // Work split: chunks of 16 RB rows (RB A blocks share each B fragment read from
-// LDS); every wave streams a contiguous range of chunks, unit by unit, through a
-// ring of D register sets, so the loads of the next D - 1 units are in flight
-// while a unit computes (the word kernel's ring).
+// LDS), dealt round-robin over the waves of the grid (wave gw takes chunks gw,
+// gw + GW, ...: at any time the whole GPU reads nearby rows). Each wave streams
+// its chunks unit by unit through a ring of D register sets, so the loads of the
+// next D - 1 units are in flight while a unit computes (the word kernel's ring).
 typedef int i4v __attribute__((ext_vector_type(4)));
 constexpr int LI8_NSL = 8;      // digits per activation element
 constexpr int LI8_KMAX = 4096;  // K limit: the digits of one row fill at most 64 KiB of LDS
-constexpr bool LI8_STRIDED = true;
 
 template <int BITS>
 struct I8Fmt {
-    static constexpr int MPS = 8 / BITS;                                  // MFMA steps per unit
+    static constexpr int MPS = 8 / BITS;                                  // MFMA steps per 64-byte piece
     static constexpr int LOG2F = BITS == 2 ? 6 : BITS == 4 ? 4 : 0;     // fields are value * 2^LOG2F
 };
 
@@ -594,16 +595,9 @@ __device__ __forceinline__ void linear_q_i8(const G4aLinearParams& p) {
     const uint32_t row_bytes = K * BITS / 8;
     const uint32_t nchunk = (N + 16 * RB - 1) / (16 * RB);
     const uint32_t GW = gridDim.x * NW, gw = blockIdx.x * NW + wv;
-    // the wave's chunks: ordinals 0 .. nc - 1
-    uint32_t nc, c0 = 0;
-    if constexpr (LI8_STRIDED) {
-        nc = nchunk > gw ? (nchunk - gw + GW - 1) / GW : 0;
-    } else {
-        const uint32_t per = (nchunk + GW - 1) / GW;
-        c0 = min(gw * per, nchunk);
-        nc = min(c0 + per, nchunk) - c0;
-    }
-    auto chunk = [&](uint32_t i) { return LI8_STRIDED ? gw + i * GW : c0 + i; };
+    // the wave's chunks: ordinals 0 .. nc - 1, chunk gw + i GW
+    const uint32_t nc = nchunk > gw ? (nchunk - gw + GW - 1) / GW : 0;
+    auto chunk = [&](uint32_t i) { return gw + i * GW; };
     const uint32_t T = nc * NU;  // the wave's units
     const int r = lane & 15, g = lane >> 4;
     // the output this lane stores at a chunk's end: digit column cc = 8 m + jj,
