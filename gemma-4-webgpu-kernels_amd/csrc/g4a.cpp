@@ -39,7 +39,7 @@ constexpr float PREFILL_TAU_LOGN = 2.0f;
 // Largest split-K count the LSE combine kernel takes (its LDS weight table).
 constexpr uint32_t MAX_SPLITS = 1024;
 // Split counts merged by the one-block-per-head combine kernel (combine_rows).
-constexpr uint32_t COMBINE_ROW_SPLITS = 64;
+constexpr uint32_t COMBINE_ROW_SPLITS = 16;
 // Keys per 4-wave workgroup of the short-context decode kernel (two 16-key tiles).
 constexpr uint32_t SHORT_KEYS = 32;
 // Most visible keys of a batched decode step (1024 splits of the short kernel).
@@ -90,7 +90,7 @@ struct g4a_ctx {
     hipFunction_t decode_wave_batch[2] = {nullptr, nullptr};  // [dh512] streaming decode over many sequences
     hipFunction_t decode_wave_batch_kpos[2] = {nullptr, nullptr};  // [dh512] the same, explicit key positions
     hipFunction_t combine_batch[2] = {nullptr, nullptr};  // [dh512]
-    hipFunction_t combine_rows[2] = {nullptr, nullptr};        // [dh512] combine of <= 64 splits
+    hipFunction_t combine_rows[2] = {nullptr, nullptr};        // [dh512] combine of <= 16 splits
     hipFunction_t combine_rows_batch[2] = {nullptr, nullptr};  // [dh512]
     // batched decode tuning (G4A_BATCH_KERNEL=short|wave, G4A_BATCH_KEYS_PER_SPLIT=n): for comparisons
     int batch_kernel = 0;  // 0 auto, 1 short, 2 streaming
@@ -951,7 +951,7 @@ int g4a_attention_decode_batch(g4a_ctx* ctx, const g4a_attn_args* args, uint32_t
     // launch's keys.
     struct Launch {
         uint32_t first, count, kps, max_split;
-        bool wave, rows, wide;  // streaming kernel; combines of <= 64 / more splits
+        bool wave, rows, wide;  // streaming kernel; combines of <= COMBINE_ROW_SPLITS / more splits
         bool kpos;              // explicit key positions
         size_t part;  // floats
     };

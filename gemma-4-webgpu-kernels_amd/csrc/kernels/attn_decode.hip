@@ -1221,7 +1221,7 @@ __device__ __forceinline__ void combine(const G4aCombineParams& p, uint32_t qi) 
 // dims would leave most of its threads idle at these split counts. The first
 // COMBINE_ROW_EARLY splits' partials are loaded before the weights are known,
 // so a short decode's merge pays one memory round trip, not two.
-constexpr uint32_t COMBINE_ROW_SPLITS = 64;
+constexpr uint32_t COMBINE_ROW_SPLITS = 16;
 constexpr uint32_t COMBINE_ROW_EARLY = 16;
 
 template <int DH>
