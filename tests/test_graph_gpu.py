@@ -1,6 +1,6 @@
 """Graph capture (g4a_capture_begin / g4a_capture_end / g4a_graph_launch): a
-captured sequence of attention calls replays bit-identically to the same calls
-run eagerly. Each replay runs after the output buffers are overwritten and
+captured sequence of attention calls (and one of projections) replays
+bit-identically to the same calls run eagerly. Each replay runs after the output buffers are overwritten and
 after unrelated eager work and a synchronisation, and every replay is checked.
 Calls that need host staging are refused while a capture is open, and the
 context stays usable after such a refusal."""
@@ -184,3 +184,55 @@ def test_replay_after_the_workspace_grows_and_graph_ownership(ctx):
         for d in bufs:
             d.free()
         own.close()
+
+
+def test_captured_projections_replay_bit_exactly(ctx):
+    """The projection kernels under capture: a 2-bit [49152, 1536] weight at M = 1
+    (the int8 matrix-core kernel, with its dynamic LDS), a 4-bit [2048, 1536] at
+    M = 1 (the word kernel) and a 2-bit [12288, 1536] at M = 64 (the bf16 matrix
+    cores), captured as one graph and replayed three times, each replay checked
+    bit-exactly against the eager run."""
+    cases = [(49152, 1536, 2, 1), (2048, 1536, 4, 1), (12288, 1536, 2, 64)]
+    bufs = []
+    try:
+        calls = []
+        for i, (N, K, bits, M) in enumerate(cases):
+            qb, sc, _ = synth.quant_weight(60 + i, N, K, bits)
+            w = ctx.upload_qweight(qb, sc, N, K, bits)
+            x = ctx.upload(synth.normal_f32(70 + i, 0, M * K).reshape(M, K))
+            y = ctx.empty((M, N))
+            bufs += [w, x, y]
+            calls.append((w, x, y, M))
+        step("eager projections")
+        for w, x, y, M in calls:
+            ctx.linear_q(w, x.ptr, y.ptr, M)
+        want = [y.to_host() for _, _, y, _ in calls]
+        step("capture")
+        ctx.capture_begin()
+        try:
+            for w, x, y, M in calls:
+                ctx.linear_q(w, x.ptr, y.ptr, M)
+            graph = ctx.capture_end()
+        except Exception:
+            _end_open_capture(ctx)
+            raise
+        rng = np.random.default_rng(1)
+        try:
+            for rep in range(3):
+                step(f"replay {rep}")
+                for _, _, y, _ in calls:
+                    ctx.h2d(y.ptr, rng.standard_normal(y.shape).astype(np.float32))
+                w0, x0, _, _ = calls[1]
+                scratch = ctx.empty((1, 2048))
+                ctx.linear_q(w0, x0.ptr, scratch.ptr, 1)  # unrelated eager work
+                ctx.sync()
+                scratch.free()
+                graph.launch()
+                ctx.sync()
+                for i, ((_, _, y, _), wv) in enumerate(zip(calls, want)):
+                    assert np.array_equal(y.to_host(), wv), f"replay {rep}, projection {i}"
+        finally:
+            graph.free()
+    finally:
+        for d in bufs:
+            d.free()
