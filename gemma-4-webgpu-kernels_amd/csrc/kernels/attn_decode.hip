@@ -926,38 +926,48 @@ __device__ __forceinline__ void qk1_dims16(float& s, float q, const float4 (&k)[
 //   end:    the two tiles merge through LDS (wave w merges heads 2w, 2w+1)
 //           into the split's partial (m, l, acc), or the output for one split;
 //           the combine kernel merges the split partials.
-template <int DH>
+// With DS = 2 two workgroups share a split: both compute the same scores, and
+// each copies, accumulates, merges and stores one half of the output dims
+// (workgroup dh: dims dh * DH / 2 ..), which shortens the P.V and the merge
+// when the GPU has CUs to spare (a sliding call's 16 splits). Every output
+// dim sees the same sequence of operations either way, so the results are
+// bit-identical to DS = 1.
+template <int DH, int DS = 1>
 struct ShortCfg {
     static constexpr int GROUP = 8;
+    static constexpr int HD = DH / DS;           // output dims of a workgroup (V, P.V, merge, stores)
+    static constexpr int DPL = HD / 64;          // output dims per lane: 2, 4 or 8
+    static constexpr int VC = HD >= 256 ? HD / 256 : 1;  // copies per V row (a 512-byte row: 32 lanes)
     static constexpr int KEYS = 16;              // keys per tile
     static constexpr int TILES = 2;              // tiles per workgroup (4 waves)
     static constexpr int RS = DH + 4;            // K row stride in LDS (floats)
     static constexpr int QRS = DH + 16;          // query row stride in LDS: 4 rows x 16 floats on distinct banks
     static constexpr int NRC = DH / 256;         // 1 KiB copies per row
-    static constexpr int ND = DH / 256;          // float4 dim groups per lane in P.V
     static constexpr int NB = DH / 16;           // 16-dim blocks of a dot
     static constexpr int QS = GROUP * QRS;
     static constexpr int KS = TILES * KEYS * RS;
-    static constexpr int VS = TILES * KEYS * DH;
+    static constexpr int VS = TILES * KEYS * HD;
     static constexpr int PB = 4 * KEYS * 4;      // [wave][key][4 heads]
     static constexpr int ML = 4 * 2 * 4;         // [wave][m, l][4 heads]
-    static constexpr int MERGE = 4 * 4 * DH;     // [wave][4 heads][DH], over the K rows after the scores
+    static constexpr int MERGE = 4 * 4 * HD;     // [wave][4 heads][HD], over the K rows after the scores
     static constexpr int SMEM = QS + KS + VS + PB + ML;
-    static constexpr int COPIES = 2 * NRC + 2 * (KEYS / 2) * NRC;  // per wave: query, K and V rows
+    static constexpr int COPIES = 2 * NRC + (KEYS / 2) * (NRC + VC);  // per wave: query, K and V rows
     static_assert(MERGE <= KS, "the wave partials fit over the K rows");
     static_assert(SMEM * 4 <= 160 * 1024, "LDS budget of a CU");
     static_assert(COPIES < 64, "vmcnt range");
+    static_assert(DPL == 2 || DPL % 4 == 0, "P.V lanes hold a float2 or whole float4 groups");
 };
 
-template <int DH>
-__device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t split, uint32_t qi) {
-    using C = ShortCfg<DH>;
-    constexpr int GROUP = C::GROUP, KEYS = C::KEYS, RS = C::RS, QRS = C::QRS, NRC = C::NRC, ND = C::ND, NB = C::NB;
+template <int DH, int DS = 1>
+__device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t split, uint32_t qi, uint32_t dh = 0) {
+    using C = ShortCfg<DH, DS>;
+    constexpr int GROUP = C::GROUP, KEYS = C::KEYS, RS = C::RS, QRS = C::QRS, NRC = C::NRC, NB = C::NB;
+    constexpr int HD = C::HD, DPL = C::DPL, VC = C::VC;
 
     __shared__ __attribute__((aligned(16))) float smem[C::SMEM];
     float* const qs = smem;              // [GROUP][QRS]
     float* const kbuf = qs + C::QS;      // [TILES][KEYS][RS]; after the scores: [4 waves][4 heads][DH]
-    float* const vbuf = kbuf + C::KS;    // [TILES][KEYS][DH]
+    float* const vbuf = kbuf + C::KS;    // [TILES][KEYS][HD]
     float* const pbuf = vbuf + C::VS;    // [4 waves][KEYS][4]
     float* const mlbuf = pbuf + C::PB;   // [4 waves][2][4]
 
@@ -975,7 +985,7 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
     const uint32_t h0 = kvh * GROUP;
     const size_t row_stride = (size_t)p.Hkv * DH;
     float* const tk = kbuf + tile * KEYS * RS;
-    float* const tv = vbuf + tile * KEYS * DH;
+    float* const tv = vbuf + tile * KEYS * HD;
     float* const my_p = pbuf + w * KEYS * 4;
     float* const my_ml = mlbuf + w * 8;
 
@@ -1001,12 +1011,16 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
 #pragma unroll
             for (int c = 0; c < NRC; ++c)
                 copy16_to_lds(kb + rows[i] * row_stride + 256 * c + 4 * lane, tk + (8 * half + i) * RS + 256 * c);
+        // V: this workgroup's dims dh * HD .. + HD - 1 of each row
+        if (HD >= 256 || lane < HD / 4) {
 #pragma unroll
-        for (int i = 0; i < KEYS / 2; ++i)
+            for (int i = 0; i < KEYS / 2; ++i)
 #pragma unroll
-            for (int c = 0; c < NRC; ++c)
-                copy16_to_lds(vb + rows[i] * row_stride + 256 * c + 4 * lane, tv + (8 * half + i) * DH + 256 * c);
-        wait_vm<(KEYS / 2) * NRC>();  // this wave's query pieces and K rows have landed
+                for (int c = 0; c < VC; ++c)
+                    copy16_to_lds(vb + rows[i] * row_stride + dh * HD + 256 * c + 4 * lane,
+                                  tv + (8 * half + i) * HD + 256 * c);
+        }
+        wait_vm<(KEYS / 2) * VC>();  // this wave's query pieces and K rows have landed
     } else {
         wait_vm<0>();
     }
@@ -1049,33 +1063,56 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
 
     wait_vm<0>();   // this wave's V rows have landed
     barrier_lds();  // ... and its partner's; every wave is done with the K rows
-    float4 acc[4][ND];
+    // lane l's output dims within the workgroup's HD: 4l + 256 g + j (g < DPL / 4), or 2l + j (DPL = 2)
+    auto dim_of = [&](int d) -> int { return DPL == 2 ? 2 * lane + d : 256 * (d >> 2) + 4 * lane + (d & 3); };
+    auto ld_dims = [&](const float* row, float (&x)[DPL]) {
+        if constexpr (DPL == 2) {
+            const float2 v = *reinterpret_cast<const float2*>(row + 2 * lane);
+            x[0] = v.x;
+            x[1] = v.y;
+        } else {
+#pragma unroll
+            for (int g = 0; g < DPL / 4; ++g) {
+                const float4 v = ld4(row + 256 * g + 4 * lane);
+                x[4 * g] = v.x;
+                x[4 * g + 1] = v.y;
+                x[4 * g + 2] = v.z;
+                x[4 * g + 3] = v.w;
+            }
+        }
+    };
+    auto st_dims = [&](float* row, const float (&x)[DPL]) {
+        if constexpr (DPL == 2) {
+            *reinterpret_cast<float2*>(row + 2 * lane) = make_float2(x[0], x[1]);
+        } else {
+#pragma unroll
+            for (int g = 0; g < DPL / 4; ++g)
+                *reinterpret_cast<float4*>(row + 256 * g + 4 * lane) =
+                    make_float4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3]);
+        }
+    };
+    float acc[4][DPL];
 #pragma unroll
     for (int h = 0; h < 4; ++h)
 #pragma unroll
-        for (int e = 0; e < ND; ++e) acc[h][e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int d = 0; d < DPL; ++d) acc[h][d] = 0.0f;
     if (active) {
 #pragma unroll
         for (int k0 = 0; k0 < KEYS; k0 += 8) {
-            float4 pk[8], vk[8][ND];
+            float4 pk[8];
+            float vk[8][DPL];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 pk[j] = ld4(my_p + (k0 + j) * 4);
-#pragma unroll
-                for (int e = 0; e < ND; ++e) vk[j][e] = ld4(tv + (k0 + j) * DH + 256 * e + 4 * lane);
+                ld_dims(tv + (k0 + j) * HD, vk[j]);
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float pw[4] = {pk[j].x, pk[j].y, pk[j].z, pk[j].w};
 #pragma unroll
-                for (int e = 0; e < ND; ++e)
+                for (int d = 0; d < DPL; ++d)
 #pragma unroll
-                    for (int h = 0; h < 4; ++h) {
-                        acc[h][e].x = __builtin_fmaf(pw[h], vk[j][e].x, acc[h][e].x);
-                        acc[h][e].y = __builtin_fmaf(pw[h], vk[j][e].y, acc[h][e].y);
-                        acc[h][e].z = __builtin_fmaf(pw[h], vk[j][e].z, acc[h][e].z);
-                        acc[h][e].w = __builtin_fmaf(pw[h], vk[j][e].w, acc[h][e].w);
-                    }
+                    for (int h = 0; h < 4; ++h) acc[h][d] = __builtin_fmaf(pw[h], vk[j][d], acc[h][d]);
             }
         }
     }
@@ -1083,10 +1120,7 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
     // merge the two tiles: wave w merges heads 2w, 2w + 1 (waves half and 2 + half hold them)
     float* const merge = kbuf;
 #pragma unroll
-    for (int h = 0; h < 4; ++h)
-#pragma unroll
-        for (int e = 0; e < ND; ++e)
-            *reinterpret_cast<float4*>(merge + (w * 4 + h) * DH + 256 * e + 4 * lane) = acc[h][e];
+    for (int h = 0; h < 4; ++h) st_dims(merge + (w * 4 + h) * HD, acc[h]);
     barrier_lds();
     float* const mlp = p.part + (size_t)p.T * p.Hq * p.nsplit * DH;  // (m, l) pairs of the partials
 #pragma unroll
@@ -1095,12 +1129,9 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
         const int x0 = h >> 2, x1 = 2 + (h >> 2), hr = h & 3;
         const float m0 = mlbuf[x0 * 8 + hr], m1 = mlbuf[x1 * 8 + hr];
         const float l0 = mlbuf[x0 * 8 + 4 + hr], l1 = mlbuf[x1 * 8 + 4 + hr];
-        float4 a0[ND], a1[ND];
-#pragma unroll
-        for (int e = 0; e < ND; ++e) {
-            a0[e] = ld4(merge + (x0 * 4 + hr) * DH + 256 * e + 4 * lane);
-            a1[e] = ld4(merge + (x1 * 4 + hr) * DH + 256 * e + 4 * lane);
-        }
+        float a0[DPL], a1[DPL];
+        ld_dims(merge + (x0 * 4 + hr) * HD, a0);
+        ld_dims(merge + (x1 * 4 + hr) * HD, a1);
         const float M = fmaxf(m0, m1);
         const float e0 = (m0 == NEG_INF) ? 0.0f : expf(m0 - M);
         const float e1 = (m1 == NEG_INF) ? 0.0f : expf(m1 - M);
@@ -1108,17 +1139,16 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
         const size_t ih = (size_t)qi * p.Hq + h0 + h;
         const float sc = p.nsplit == 1 ? (L > 0.0f ? 1.0f / L : 0.0f) : 1.0f;
 #pragma unroll
-        for (int e = 0; e < ND; ++e) {
-            float4 o;
-            o.x = (a0[e].x * e0 + a1[e].x * e1) * sc;
-            o.y = (a0[e].y * e0 + a1[e].y * e1) * sc;
-            o.z = (a0[e].z * e0 + a1[e].z * e1) * sc;
-            o.w = (a0[e].w * e0 + a1[e].w * e1) * sc;
-            const uint32_t d = 256 * e + 4 * lane;
-            float* const dst = p.nsplit == 1 ? p.out + ih * DH + d : p.part + part_index<DH>(ih, p.nsplit, split, d);
-            g4a_store_nt(dst, o);
+        for (int d = 0; d < DPL; d += 2) {
+            // two dims at a time (a float4's halves, or the lane's float2)
+            const float o0 = (a0[d] * e0 + a1[d] * e1) * sc;
+            const float o1 = (a0[d + 1] * e0 + a1[d + 1] * e1) * sc;
+            const uint32_t dd = dh * HD + dim_of(d);
+            float* const dst = p.nsplit == 1 ? p.out + ih * DH + dd : p.part + part_index<DH>(ih, p.nsplit, split, dd);
+            __builtin_nontemporal_store(o0, dst);
+            __builtin_nontemporal_store(o1, dst + 1);
         }
-        if (p.nsplit > 1 && lane == 0) {
+        if (p.nsplit > 1 && lane == 0 && dh == 0) {
             float* const ml = mlp + (ih * p.nsplit + split) * 2;
             ml[0] = M;
             ml[1] = L;
@@ -1424,6 +1454,13 @@ __global__ __launch_bounds__(256) void g4a_decode_short_d256(G4aDecodeParams p) 
 }
 __global__ __launch_bounds__(256) void g4a_decode_short_d512(G4aDecodeParams p) {
     decode_short<512>(p, blockIdx.x, blockIdx.y);
+}
+// two workgroups per split (grid x = 2 * splits): workgroup 2s + dh owns output dims half dh
+__global__ __launch_bounds__(256) void g4a_decode_short2_d256(G4aDecodeParams p) {
+    decode_short<256, 2>(p, blockIdx.x >> 1, blockIdx.y, blockIdx.x & 1u);
+}
+__global__ __launch_bounds__(256) void g4a_decode_short2_d512(G4aDecodeParams p) {
+    decode_short<512, 2>(p, blockIdx.x >> 1, blockIdx.y, blockIdx.x & 1u);
 }
 __global__ __launch_bounds__(256) void g4a_decode_short_batch_d256(G4aBatchParams b) { decode_short_batch<256>(b); }
 __global__ __launch_bounds__(256) void g4a_decode_short_batch_d512(G4aBatchParams b) { decode_short_batch<512>(b); }
