@@ -87,6 +87,7 @@ struct g4a_ctx {
     hipFunction_t combine[2] = {nullptr, nullptr};                          // [dh512]
     hipFunction_t decode_short[2] = {nullptr, nullptr};  // [dh512]
     hipFunction_t decode_short2[2] = {nullptr, nullptr};  // [dh512] two workgroups per split (output dim halves)
+    hipFunction_t decode_short4[2] = {nullptr, nullptr};  // [dh512] four workgroups per split (quarters)
     hipFunction_t decode_batch[2] = {nullptr, nullptr};   // [dh512] short decode over many sequences
     hipFunction_t decode_wave_batch[2] = {nullptr, nullptr};  // [dh512] streaming decode over many sequences
     hipFunction_t decode_wave_batch_kpos[2] = {nullptr, nullptr};  // [dh512] the same, explicit key positions
@@ -97,7 +98,7 @@ struct g4a_ctx {
     int batch_kernel = 0;  // 0 auto, 1 short, 2 streaming
     uint32_t batch_kps = 0;  // streaming split size; 0 auto
     bool short_decode = true;  // G4A_DECODE_SHORT=0 turns the short-context kernel off (for comparisons)
-    bool short_two = true;     // G4A_DECODE_SHORT2=0: one workgroup per split only (for comparisons)
+    uint32_t short_ds = 4;     // G4A_DECODE_SHORT_DS=1|2|4: most workgroups per short split (for comparisons)
     hipFunction_t generic = nullptr;
     hipFunction_t prefill[2] = {nullptr, nullptr};                          // [dh512]
     hipFunction_t split_kv = nullptr;  // K/V pre-split for the head_dim 256 prefill
@@ -513,8 +514,13 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->decode_short[1], "g4a_decode_short_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_short2[0], "g4a_decode_short2_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_short2[1], "g4a_decode_short2_d512")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->decode_short4[0], "g4a_decode_short4_d256")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->decode_short4[1], "g4a_decode_short4_d512")) return bail(rc);
     if (const char* env = getenv("G4A_DECODE_SHORT")) ctx->short_decode = atoi(env) != 0;
-    if (const char* env = getenv("G4A_DECODE_SHORT2")) ctx->short_two = atoi(env) != 0;
+    if (const char* env = getenv("G4A_DECODE_SHORT_DS")) {
+        const int ds = atoi(env);
+        ctx->short_ds = ds >= 4 ? 4u : ds >= 2 ? 2u : 1u;
+    }
     if (int rc = get_fn(ctx, &ctx->decode_batch[0], "g4a_decode_short_batch_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_batch[1], "g4a_decode_short_batch_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_wave_batch[0], "g4a_decode_wave_batch_d256")) return bail(rc);
@@ -857,13 +863,12 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
     const int d512 = a->Dh == 512 ? 1 : 0;
     const int g8 = group == 8 ? 1 : 0;
     if (pl.kernel == G4A_KERNEL_DECODE_SHORT) {
-        // two workgroups per split (each one half of the output dims) when they still
+        // up to four workgroups per split (each a part of the output dims) while they
         // fit the CUs: a shorter P.V and merge per workgroup, bit-identical results
-        const bool two =
-            ctx->short_two && uint64_t(2) * pl.splits * a->T * a->Hkv <= uint64_t(std::max(ctx->cu_count, 1));
-        hipFunction_t fn = two ? ctx->decode_short2[d512] : ctx->decode_short[d512];
-        if (int rc = launch(ctx, fn, dim3(pl.splits * (two ? 2 : 1), a->T, a->Hkv), dim3(256, 1, 1), dp,
-                            "short decode", true))
+        const uint64_t wg = uint64_t(pl.splits) * a->T * a->Hkv, cus = uint64_t(std::max(ctx->cu_count, 1));
+        const uint32_t ds = ctx->short_ds >= 4 && 4 * wg <= cus ? 4u : ctx->short_ds >= 2 && 2 * wg <= cus ? 2u : 1u;
+        hipFunction_t fn = ds == 4 ? ctx->decode_short4[d512] : ds == 2 ? ctx->decode_short2[d512] : ctx->decode_short[d512];
+        if (int rc = launch(ctx, fn, dim3(pl.splits * ds, a->T, a->Hkv), dim3(256, 1, 1), dp, "short decode", true))
             return rc;
     } else if (int rc = launch(ctx, ctx->decode[d512][g8][kd ? 1 : 0], dim3(pl.splits, a->T, a->Hkv),
                                dim3(512, 1, 1), dp, "decode", true)) {

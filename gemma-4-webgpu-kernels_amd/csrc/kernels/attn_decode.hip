@@ -926,9 +926,9 @@ __device__ __forceinline__ void qk1_dims16(float& s, float q, const float4 (&k)[
 //   end:    the two tiles merge through LDS (wave w merges heads 2w, 2w+1)
 //           into the split's partial (m, l, acc), or the output for one split;
 //           the combine kernel merges the split partials.
-// With DS = 2 two workgroups share a split: both compute the same scores, and
-// each copies, accumulates, merges and stores one half of the output dims
-// (workgroup dh: dims dh * DH / 2 ..), which shortens the P.V and the merge
+// With DS = 2 or 4, DS workgroups share a split: all compute the same scores,
+// and each copies, accumulates, merges and stores 1 / DS of the output dims
+// (workgroup dh: dims dh * DH / DS ..), which shortens the P.V and the merge
 // when the GPU has CUs to spare (a sliding call's 16 splits). Every output
 // dim sees the same sequence of operations either way, so the results are
 // bit-identical to DS = 1.
@@ -936,7 +936,7 @@ template <int DH, int DS = 1>
 struct ShortCfg {
     static constexpr int GROUP = 8;
     static constexpr int HD = DH / DS;           // output dims of a workgroup (V, P.V, merge, stores)
-    static constexpr int DPL = HD / 64;          // output dims per lane: 2, 4 or 8
+    static constexpr int DPL = HD / 64;          // output dims per lane: 1, 2, 4 or 8
     static constexpr int VC = HD >= 256 ? HD / 256 : 1;  // copies per V row (a 512-byte row: 32 lanes)
     static constexpr int KEYS = 16;              // keys per tile
     static constexpr int TILES = 2;              // tiles per workgroup (4 waves)
@@ -955,7 +955,7 @@ struct ShortCfg {
     static_assert(MERGE <= KS, "the wave partials fit over the K rows");
     static_assert(SMEM * 4 <= 160 * 1024, "LDS budget of a CU");
     static_assert(COPIES < 64, "vmcnt range");
-    static_assert(DPL == 2 || DPL % 4 == 0, "P.V lanes hold a float2 or whole float4 groups");
+    static_assert(DPL <= 2 || DPL % 4 == 0, "P.V lanes hold a float, a float2 or whole float4 groups");
 };
 
 template <int DH, int DS = 1>
@@ -1063,10 +1063,14 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
 
     wait_vm<0>();   // this wave's V rows have landed
     barrier_lds();  // ... and its partner's; every wave is done with the K rows
-    // lane l's output dims within the workgroup's HD: 4l + 256 g + j (g < DPL / 4), or 2l + j (DPL = 2)
-    auto dim_of = [&](int d) -> int { return DPL == 2 ? 2 * lane + d : 256 * (d >> 2) + 4 * lane + (d & 3); };
+    // lane l's output dims within the workgroup's HD: 4l + 256 g + j (g < DPL / 4), 2l + j (DPL = 2), l (DPL = 1)
+    auto dim_of = [&](int d) -> int {
+        return DPL == 1 ? lane : DPL == 2 ? 2 * lane + d : 256 * (d >> 2) + 4 * lane + (d & 3);
+    };
     auto ld_dims = [&](const float* row, float (&x)[DPL]) {
-        if constexpr (DPL == 2) {
+        if constexpr (DPL == 1) {
+            x[0] = row[lane];
+        } else if constexpr (DPL == 2) {
             const float2 v = *reinterpret_cast<const float2*>(row + 2 * lane);
             x[0] = v.x;
             x[1] = v.y;
@@ -1082,7 +1086,9 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
         }
     };
     auto st_dims = [&](float* row, const float (&x)[DPL]) {
-        if constexpr (DPL == 2) {
+        if constexpr (DPL == 1) {
+            row[lane] = x[0];
+        } else if constexpr (DPL == 2) {
             *reinterpret_cast<float2*>(row + 2 * lane) = make_float2(x[0], x[1]);
         } else {
 #pragma unroll
@@ -1139,14 +1145,11 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
         const size_t ih = (size_t)qi * p.Hq + h0 + h;
         const float sc = p.nsplit == 1 ? (L > 0.0f ? 1.0f / L : 0.0f) : 1.0f;
 #pragma unroll
-        for (int d = 0; d < DPL; d += 2) {
-            // two dims at a time (a float4's halves, or the lane's float2)
-            const float o0 = (a0[d] * e0 + a1[d] * e1) * sc;
-            const float o1 = (a0[d + 1] * e0 + a1[d + 1] * e1) * sc;
+        for (int d = 0; d < DPL; ++d) {
+            const float o = (a0[d] * e0 + a1[d] * e1) * sc;
             const uint32_t dd = dh * HD + dim_of(d);
             float* const dst = p.nsplit == 1 ? p.out + ih * DH + dd : p.part + part_index<DH>(ih, p.nsplit, split, dd);
-            __builtin_nontemporal_store(o0, dst);
-            __builtin_nontemporal_store(o1, dst + 1);
+            __builtin_nontemporal_store(o, dst);
         }
         if (p.nsplit > 1 && lane == 0 && dh == 0) {
             float* const ml = mlp + (ih * p.nsplit + split) * 2;
@@ -1455,12 +1458,18 @@ __global__ __launch_bounds__(256) void g4a_decode_short_d256(G4aDecodeParams p) 
 __global__ __launch_bounds__(256) void g4a_decode_short_d512(G4aDecodeParams p) {
     decode_short<512>(p, blockIdx.x, blockIdx.y);
 }
-// two workgroups per split (grid x = 2 * splits): workgroup 2s + dh owns output dims half dh
+// DS workgroups per split (grid x = DS * splits): workgroup DS s + dh owns output dims part dh
 __global__ __launch_bounds__(256) void g4a_decode_short2_d256(G4aDecodeParams p) {
     decode_short<256, 2>(p, blockIdx.x >> 1, blockIdx.y, blockIdx.x & 1u);
 }
 __global__ __launch_bounds__(256) void g4a_decode_short2_d512(G4aDecodeParams p) {
     decode_short<512, 2>(p, blockIdx.x >> 1, blockIdx.y, blockIdx.x & 1u);
+}
+__global__ __launch_bounds__(256) void g4a_decode_short4_d256(G4aDecodeParams p) {
+    decode_short<256, 4>(p, blockIdx.x >> 2, blockIdx.y, blockIdx.x & 3u);
+}
+__global__ __launch_bounds__(256) void g4a_decode_short4_d512(G4aDecodeParams p) {
+    decode_short<512, 4>(p, blockIdx.x >> 2, blockIdx.y, blockIdx.x & 3u);
 }
 __global__ __launch_bounds__(256) void g4a_decode_short_batch_d256(G4aBatchParams b) { decode_short_batch<256>(b); }
 __global__ __launch_bounds__(256) void g4a_decode_short_batch_d512(G4aBatchParams b) { decode_short_batch<512>(b); }
