@@ -1063,98 +1063,152 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
 
     wait_vm<0>();   // this wave's V rows have landed
     barrier_lds();  // ... and its partner's; every wave is done with the K rows
-    // lane l's output dims within the workgroup's HD: 4l + 256 g + j (g < DPL / 4), 2l + j (DPL = 2), l (DPL = 1)
-    auto dim_of = [&](int d) -> int {
-        return DPL == 1 ? lane : DPL == 2 ? 2 * lane + d : 256 * (d >> 2) + 4 * lane + (d & 3);
-    };
-    auto ld_dims = [&](const float* row, float (&x)[DPL]) {
-        if constexpr (DPL == 1) {
-            x[0] = row[lane];
-        } else if constexpr (DPL == 2) {
-            const float2 v = *reinterpret_cast<const float2*>(row + 2 * lane);
-            x[0] = v.x;
-            x[1] = v.y;
-        } else {
-#pragma unroll
-            for (int g = 0; g < DPL / 4; ++g) {
-                const float4 v = ld4(row + 256 * g + 4 * lane);
-                x[4 * g] = v.x;
-                x[4 * g + 1] = v.y;
-                x[4 * g + 2] = v.z;
-                x[4 * g + 3] = v.w;
-            }
-        }
-    };
-    auto st_dims = [&](float* row, const float (&x)[DPL]) {
-        if constexpr (DPL == 1) {
-            row[lane] = x[0];
-        } else if constexpr (DPL == 2) {
-            *reinterpret_cast<float2*>(row + 2 * lane) = make_float2(x[0], x[1]);
-        } else {
-#pragma unroll
-            for (int g = 0; g < DPL / 4; ++g)
-                *reinterpret_cast<float4*>(row + 256 * g + 4 * lane) =
-                    make_float4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3]);
-        }
-    };
-    float acc[4][DPL];
-#pragma unroll
-    for (int h = 0; h < 4; ++h)
-#pragma unroll
-        for (int d = 0; d < DPL; ++d) acc[h][d] = 0.0f;
-    if (active) {
-#pragma unroll
-        for (int k0 = 0; k0 < KEYS; k0 += 8) {
-            float4 pk[8];
-            float vk[8][DPL];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                pk[j] = ld4(my_p + (k0 + j) * 4);
-                ld_dims(tv + (k0 + j) * HD, vk[j]);
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float pw[4] = {pk[j].x, pk[j].y, pk[j].z, pk[j].w};
-#pragma unroll
-                for (int d = 0; d < DPL; ++d)
-#pragma unroll
-                    for (int h = 0; h < 4; ++h) acc[h][d] = __builtin_fmaf(pw[h], vk[j][d], acc[h][d]);
-            }
-        }
-    }
-
-    // merge the two tiles: wave w merges heads 2w, 2w + 1 (waves half and 2 + half hold them)
-    float* const merge = kbuf;
-#pragma unroll
-    for (int h = 0; h < 4; ++h) st_dims(merge + (w * 4 + h) * HD, acc[h]);
-    barrier_lds();
+    float* const merge = kbuf;  // the two tiles' partials, over the K rows
     float* const mlp = p.part + (size_t)p.T * p.Hq * p.nsplit * DH;  // (m, l) pairs of the partials
+    if constexpr (DPL % 4 == 0) {
+        // lanes hold whole float4 groups (dims 4l + 256 e)
+        constexpr int NG = DPL / 4;
+        float4 acc[4][NG];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int h = 2 * w + i;               // head of the group
-        const int x0 = h >> 2, x1 = 2 + (h >> 2), hr = h & 3;
-        const float m0 = mlbuf[x0 * 8 + hr], m1 = mlbuf[x1 * 8 + hr];
-        const float l0 = mlbuf[x0 * 8 + 4 + hr], l1 = mlbuf[x1 * 8 + 4 + hr];
-        float a0[DPL], a1[DPL];
-        ld_dims(merge + (x0 * 4 + hr) * HD, a0);
-        ld_dims(merge + (x1 * 4 + hr) * HD, a1);
-        const float M = fmaxf(m0, m1);
-        const float e0 = (m0 == NEG_INF) ? 0.0f : expf(m0 - M);
-        const float e1 = (m1 == NEG_INF) ? 0.0f : expf(m1 - M);
-        const float L = l0 * e0 + l1 * e1;
-        const size_t ih = (size_t)qi * p.Hq + h0 + h;
-        const float sc = p.nsplit == 1 ? (L > 0.0f ? 1.0f / L : 0.0f) : 1.0f;
+        for (int h = 0; h < 4; ++h)
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) {
-            const float o = (a0[d] * e0 + a1[d] * e1) * sc;
-            const uint32_t dd = dh * HD + dim_of(d);
-            float* const dst = p.nsplit == 1 ? p.out + ih * DH + dd : p.part + part_index<DH>(ih, p.nsplit, split, dd);
-            __builtin_nontemporal_store(o, dst);
+            for (int e = 0; e < NG; ++e) acc[h][e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (active) {
+#pragma unroll
+            for (int k0 = 0; k0 < KEYS; k0 += 8) {
+                float4 pk[8], vk[8][NG];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    pk[j] = ld4(my_p + (k0 + j) * 4);
+#pragma unroll
+                    for (int e = 0; e < NG; ++e) vk[j][e] = ld4(tv + (k0 + j) * HD + 256 * e + 4 * lane);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float pw[4] = {pk[j].x, pk[j].y, pk[j].z, pk[j].w};
+#pragma unroll
+                    for (int e = 0; e < NG; ++e)
+#pragma unroll
+                        for (int h = 0; h < 4; ++h) {
+                            acc[h][e].x = __builtin_fmaf(pw[h], vk[j][e].x, acc[h][e].x);
+                            acc[h][e].y = __builtin_fmaf(pw[h], vk[j][e].y, acc[h][e].y);
+                            acc[h][e].z = __builtin_fmaf(pw[h], vk[j][e].z, acc[h][e].z);
+                            acc[h][e].w = __builtin_fmaf(pw[h], vk[j][e].w, acc[h][e].w);
+                        }
+                }
+            }
         }
-        if (p.nsplit > 1 && lane == 0 && dh == 0) {
-            float* const ml = mlp + (ih * p.nsplit + split) * 2;
-            ml[0] = M;
-            ml[1] = L;
+        // merge the two tiles: wave w merges heads 2w, 2w + 1 (waves half and 2 + half hold them)
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+#pragma unroll
+            for (int e = 0; e < NG; ++e)
+                *reinterpret_cast<float4*>(merge + (w * 4 + h) * HD + 256 * e + 4 * lane) = acc[h][e];
+        barrier_lds();
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int h = 2 * w + i;  // head of the group
+            const int x0 = h >> 2, x1 = 2 + (h >> 2), hr = h & 3;
+            const float m0 = mlbuf[x0 * 8 + hr], m1 = mlbuf[x1 * 8 + hr];
+            const float l0 = mlbuf[x0 * 8 + 4 + hr], l1 = mlbuf[x1 * 8 + 4 + hr];
+            float4 a0[NG], a1[NG];
+#pragma unroll
+            for (int e = 0; e < NG; ++e) {
+                a0[e] = ld4(merge + (x0 * 4 + hr) * HD + 256 * e + 4 * lane);
+                a1[e] = ld4(merge + (x1 * 4 + hr) * HD + 256 * e + 4 * lane);
+            }
+            const float M = fmaxf(m0, m1);
+            const float e0 = (m0 == NEG_INF) ? 0.0f : expf(m0 - M);
+            const float e1 = (m1 == NEG_INF) ? 0.0f : expf(m1 - M);
+            const float L = l0 * e0 + l1 * e1;
+            const size_t ih = (size_t)qi * p.Hq + h0 + h;
+            const float sc = p.nsplit == 1 ? (L > 0.0f ? 1.0f / L : 0.0f) : 1.0f;
+#pragma unroll
+            for (int e = 0; e < NG; ++e) {
+                float4 o;
+                o.x = (a0[e].x * e0 + a1[e].x * e1) * sc;
+                o.y = (a0[e].y * e0 + a1[e].y * e1) * sc;
+                o.z = (a0[e].z * e0 + a1[e].z * e1) * sc;
+                o.w = (a0[e].w * e0 + a1[e].w * e1) * sc;
+                const uint32_t d = dh * HD + 256 * e + 4 * lane;
+                float* const dst = p.nsplit == 1 ? p.out + ih * DH + d : p.part + part_index<DH>(ih, p.nsplit, split, d);
+                g4a_store_nt(dst, o);
+            }
+            if (p.nsplit > 1 && lane == 0 && dh == 0) {
+                float* const ml = mlp + (ih * p.nsplit + split) * 2;
+                ml[0] = M;
+                ml[1] = L;
+            }
+        }
+    } else {
+        // 1 or 2 dims per lane (dims l, or 2l and 2l + 1): the split parts of head_dim 256
+        float acc[4][DPL];
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) acc[h][d] = 0.0f;
+        auto ld_dims = [&](const float* row, float (&x)[DPL]) {
+            if constexpr (DPL == 1) {
+                x[0] = row[lane];
+            } else {
+                const float2 v = *reinterpret_cast<const float2*>(row + 2 * lane);
+                x[0] = v.x;
+                x[1] = v.y;
+            }
+        };
+        if (active) {
+#pragma unroll
+            for (int k0 = 0; k0 < KEYS; k0 += 8) {
+                float4 pk[8];
+                float vk[8][DPL];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    pk[j] = ld4(my_p + (k0 + j) * 4);
+                    ld_dims(tv + (k0 + j) * HD, vk[j]);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float pw[4] = {pk[j].x, pk[j].y, pk[j].z, pk[j].w};
+#pragma unroll
+                    for (int d = 0; d < DPL; ++d)
+#pragma unroll
+                        for (int h = 0; h < 4; ++h) acc[h][d] = __builtin_fmaf(pw[h], vk[j][d], acc[h][d]);
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) merge[(w * 4 + h) * HD + DPL * lane + d] = acc[h][d];
+        barrier_lds();
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int h = 2 * w + i;
+            const int x0 = h >> 2, x1 = 2 + (h >> 2), hr = h & 3;
+            const float m0 = mlbuf[x0 * 8 + hr], m1 = mlbuf[x1 * 8 + hr];
+            const float l0 = mlbuf[x0 * 8 + 4 + hr], l1 = mlbuf[x1 * 8 + 4 + hr];
+            float a0[DPL], a1[DPL];
+            ld_dims(merge + (x0 * 4 + hr) * HD, a0);
+            ld_dims(merge + (x1 * 4 + hr) * HD, a1);
+            const float M = fmaxf(m0, m1);
+            const float e0 = (m0 == NEG_INF) ? 0.0f : expf(m0 - M);
+            const float e1 = (m1 == NEG_INF) ? 0.0f : expf(m1 - M);
+            const float L = l0 * e0 + l1 * e1;
+            const size_t ih = (size_t)qi * p.Hq + h0 + h;
+            const float sc = p.nsplit == 1 ? (L > 0.0f ? 1.0f / L : 0.0f) : 1.0f;
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) {
+                const float o = (a0[d] * e0 + a1[d] * e1) * sc;
+                const uint32_t dd = dh * HD + DPL * lane + d;
+                float* const dst =
+                    p.nsplit == 1 ? p.out + ih * DH + dd : p.part + part_index<DH>(ih, p.nsplit, split, dd);
+                __builtin_nontemporal_store(o, dst);
+            }
+            if (p.nsplit > 1 && lane == 0 && dh == 0) {
+                float* const ml = mlp + (ih * p.nsplit + split) * 2;
+                ml[0] = M;
+                ml[1] = L;
+            }
         }
     }
 }
