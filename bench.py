@@ -10,7 +10,8 @@ HBM ("cold"); the same step on one copy read step after step is reported beside
 it ("warm").
 
 Also reported (extra keys of the same JSON line): configs[0..2] decode,
-configs[3] prefill TFLOP/s, the configs[4] 35-layer schedule in us/token, and
+configs[3] prefill TFLOP/s, the configs[4] 35-layer schedule in us/token (and
+the same token with each layer's output projection, separate and fused), and
 the CPU oracle (oracle/attn_oracle.c, the restatement of
 rust/src/backend_cpu.rs:270-336) timed on the host cores on a bounded sample.
 
@@ -209,6 +210,95 @@ def schedule_35_layers(ctx, steps, warmup):
         res["graph_error"] = str(e)
     for a in list(qs) + list(outs) + [x for kv in caches.values() for x in kv]:
         a.free()
+    return res
+
+
+def schedule_with_projection(ctx, steps, warmup):
+    """configs[4]'s token with each attention call followed by its output
+    projection, as Gemma4Model::attention ends (rust/src/model.rs:287-303):
+    o_proj 4-bit [1536, 8 Dh], one scale per row, seeded random. Two forms of
+    the same 35 layers: g4a_attention + g4a_linear_q (attention, LSE combine,
+    projection: three launches per layer; what g4a_attention_linear_q runs on
+    a default context), and g4a_attention_linear_q on a context created with
+    G4A_FUSE_PROJECTION=1 (a sliding layer's 16-split step merges its partials
+    inside the projection: two launches). Each form is captured once as a HIP
+    graph and replayed, so both figures are free of host dispatch time; the
+    two forms' projections are checked bit-identical."""
+    S, seed, N = 32768, 4, 1536
+    layers, host_caches = synth.schedule_token(S, seed)
+    caches = {li: (ctx.upload(c.k), ctx.upload(c.v)) for li, c in host_caches.items()}
+    qs = [ctx.upload(L.q) for L in layers]
+    outs = [ctx.empty((1, HQ * L.Dh)) for L in layers]
+    ys = {form: [ctx.empty((1, N)) for _ in layers] for form in ("separate", "fused")}
+    weights = {}
+    for Dh in (256, 512):
+        qb, sc, _ = synth.quant_weight(seed + Dh, N, HQ * Dh, 4)
+        weights[Dh] = ctx.upload_qweight(qb, sc, N, HQ * Dh, 4)
+    token = []
+    for L, q, out in zip(layers, qs, outs):
+        k, v = caches[L.src]
+        token.append((dict(q=q.ptr, k=k.ptr, v=v.ptr, out=out.ptr),
+                      dict(T=1, S=S, Hq=HQ, Hkv=1, Dh=L.Dh, Dv=L.Dh, q_pos0=S - 1, k_pos0=0,
+                           window=0 if L.is_global else synth.E2B_WINDOW, ring_cap=host_caches[L.src].ring_cap)))
+
+    old = os.environ.get("G4A_FUSE_PROJECTION")
+    os.environ["G4A_FUSE_PROJECTION"] = "1"
+    try:
+        fctx = g4a.Context(0)
+    finally:
+        if old is None:
+            del os.environ["G4A_FUSE_PROJECTION"]
+        else:
+            os.environ["G4A_FUSE_PROJECTION"] = old
+    ctxs = {"separate": ctx, "fused": fctx}
+
+    def enqueue(form):
+        for (bufs, kw), y in zip(token, ys[form]):
+            w = weights[kw["Dh"]]
+            if form == "fused":
+                fctx.attention_linear_q(bufs["q"], bufs["k"], bufs["v"], bufs["out"], w, y.ptr, **kw)
+            else:
+                ctx.attention(**bufs, **kw)
+                ctx.linear_q(w, bufs["out"], y.ptr, 1)
+
+    algo = 7 * (decode_bytes(S, 512) + N * HQ * 512 // 2) + 28 * (decode_bytes(512, 256) + N * HQ * 256 // 2)
+    res = {"algorithmic_bytes": algo, "launches_per_token": {"separate": 35 * 3, "fused": 7 * 3 + 28 * 2}}
+    try:
+        for form in ("separate", "fused"):
+            c = ctxs[form]
+            enqueue(form)  # eagerly first: the workspace reaches its size outside the capture
+            c.sync()
+            c.capture_begin()
+            try:
+                enqueue(form)
+            except g4a.G4aError:
+                try:
+                    c.capture_end().free()
+                except g4a.G4aError:
+                    pass
+                raise
+            graph = c.capture_end()
+            for _ in range(max(warmup, 1)):
+                graph.launch()
+            c.sync()
+            times = []
+            for _ in range(3):
+                c.timer_start()
+                for _ in range(steps):
+                    graph.launch()
+                times.append(c.timer_stop() / steps)
+            graph.free()
+            ms = float(np.median(times))
+            res[f"us_per_token_{form}"] = ms * 1e3
+        res["identical"] = all(np.array_equal(a.to_host(), b.to_host())
+                               for a, b in zip(ys["separate"], ys["fused"]))
+    except g4a.G4aError as e:
+        res["error"] = str(e)
+    for a in list(qs) + list(outs) + [y for f in ys.values() for y in f] + [x for kv in caches.values() for x in kv]:
+        a.free()
+    for w in weights.values():
+        w.free()
+    fctx.close()
     return res
 
 
@@ -495,7 +585,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="headline decode only (no extras, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "schedule", "producer", "batch", "linear"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "schedule", "producer", "batch", "linear", "oproj"],
+                    default=None,
                     help="run only these extra workloads (for profiling) and print their JSON line")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="first run 3 device-to-device copies of MIB MiB (the reference dispatch for "
@@ -536,6 +627,9 @@ def main(argv=None):
             for name, n, L, Dh, W, cap, holes in BATCH_CONFIGS:
                 out[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=args.steps, warmup=args.warmup, holes=holes)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
+        elif args.only == "oproj":
+            out["configs[4] token + o_proj @32768"] = schedule_with_projection(ctx, steps=args.steps,
+                                                                               warmup=args.warmup)
         elif args.only == "producer":
             for name, T, Dh, theta, rot, pos0, cap in PRODUCER_CONFIGS:
                 out[name] = producer(ctx, T, Dh, theta, rot, pos0, cap, steps=args.steps)
@@ -618,6 +712,8 @@ def main(argv=None):
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
         extras["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=20, warmup=3)
         print(f"[bench] schedule: {extras['configs[4] 35-layer schedule @32768']}", file=sys.stderr, flush=True)
+        extras["configs[4] token + o_proj @32768"] = schedule_with_projection(ctx, steps=20, warmup=3)
+        print(f"[bench] token + o_proj: {extras['configs[4] token + o_proj @32768']}", file=sys.stderr, flush=True)
         result["extra"] = extras
         result["prefill_TFLOP_s"] = {k: round(v["TFLOP_s"], 2) for k, v in extras.items() if "TFLOP_s" in v}
     if not (args.quick or args.no_cpu):

@@ -110,6 +110,11 @@ struct g4a_ctx {
     // G4A_LINEAR_I8=0 keeps M <= 2 projections off the int8 matrix-core kernel,
     // =1 sends every eligible one there (for comparisons); unset: by weight size
     int linear_i8_use = -1;
+    hipFunction_t linear_fused[3] = {};  // [bits 2/4/8]: a decode step's split partials merged into x
+    // G4A_FUSE_PROJECTION=1: g4a_attention_linear_q merges eligible decode steps'
+    // partials in the projection (measured slower than the separate combine on
+    // MI355X, so off by default)
+    bool fuse_projection = false;
     hipFunction_t embed_q = nullptr;
     hipFunction_t linear_half[2][3] = {};       // 2-bit, M = 1, 32 lanes per row: [RU = 1, 4][mode]
     hipFunction_t linear_f32_words[3] = {};  // f32 weights: (MT, RU) = (1, 2), (1, 8), (4, 4)
@@ -575,6 +580,12 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
                 if (int rc = get_fn(ctx, &ctx->linear_i8[b][m], name)) return bail(rc);
             }
         if (const char* env = getenv("G4A_LINEAR_I8")) ctx->linear_i8_use = atoi(env) != 0 ? 1 : 0;
+        for (int b = 0; b < 3; ++b) {
+            char name[64];
+            snprintf(name, sizeof name, "g4a_linear_q_b%d_m1_r2_mode3", bits[b]);
+            if (int rc = get_fn(ctx, &ctx->linear_fused[b], name)) return bail(rc);
+        }
+        if (const char* env = getenv("G4A_FUSE_PROJECTION")) ctx->fuse_projection = atoi(env) != 0;
         if (int rc = get_fn(ctx, &ctx->embed_q, "g4a_embed_rows_q")) return bail(rc);
         static const char* f32_words[3] = {"g4a_linear_q_b32_m1_r2_mode0", "g4a_linear_q_b32_m1_r8_mode0",
                                            "g4a_linear_q_b32_m4_r4_mode0"};
@@ -1358,6 +1369,82 @@ int g4a_linear_q_geglu(g4a_ctx* ctx, const g4a_qweight* w_gate, const g4a_qweigh
 int g4a_linear_q_gelu_mul_cols(g4a_ctx* ctx, const g4a_qweight* w, const float* x, const float* b, uint32_t b_stride,
                                uint32_t b_off, float* y, uint32_t M) {
     return linear_q_launch(ctx, 2, w, nullptr, x, b, b_stride, b_off, y, M);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Whether linear_q_launch takes (w, M = 1, mode 0) to the word kernel's
+// (MT, RU) = (1, 2) form with 64 lanes per row: the form whose mode 3 merges a
+// decode step's split partials while staging x, with the same sums.
+bool projection_on_short_words(const g4a_ctx* ctx, const g4a_qweight* w) {
+    const uint32_t row_bytes = w->signed_i8 ? w->K : w->K / (8 / w->bits);
+    const uint32_t scale_stride = (w->K + w->group_size - 1) / w->group_size;
+    const uintptr_t qa = reinterpret_cast<uintptr_t>(w->qbytes);
+    const bool i8_ok = scale_stride == 1 && row_bytes % G4A_LI8_UNIT_BYTES == 0 && w->K % 64 == 0 &&
+                       uint64_t(w->K / 64) * 1024 <= LINEAR_LDS_BYTES && (qa & 15) == 0;
+    const uint64_t weight_bytes = uint64_t(w->N) * row_bytes;
+    if (i8_ok && (ctx->linear_i8_use == 1 || (ctx->linear_i8_use < 0 && weight_bytes >= LINEAR_I8_MIN_BYTES)))
+        return false;
+    const uint64_t vpw = 32 / w->bits, words_per_row = uint64_t(w->K) * w->bits / 32;
+    const uint64_t kpad = (words_per_row + 63) / 64 * 64 * vpw;
+    if ((uint64_t(w->K) * w->bits) % 32 != 0 || scale_stride != 1 || (qa & 3) != 0 || kpad * 4 > LINEAR_LDS_BYTES)
+        return false;
+    if (uint64_t(w->N) >= uint64_t(std::max(ctx->cu_count, 1)) * 64) return false;  // the (1, 8) form
+    return !(w->bits == 2 && words_per_row % 64 == 32);                            // 32 lanes per row
+}
+
+}  // namespace
+
+extern "C" {
+
+int g4a_attention_linear_q(g4a_ctx* ctx, const g4a_attn_args* a, const g4a_qweight* w, float* y) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (!a) return fail(ctx, G4A_E_ARG, "null args");
+    if (int rc = check_qweight(ctx, w, "projection")) return rc;
+    if (uint64_t(a->Hq) * a->Dv != w->K)
+        return fail(ctx, G4A_E_SHAPE, "projection K = %u, attention rows are %u x %u", w->K, a->Hq, a->Dv);
+    Analysis an;
+    if (int rc = analyse(ctx, a, &an, true)) return rc;
+    if (a->T == 0) return G4A_OK;
+    if (!y) return fail(ctx, G4A_E_ARG, "null y");
+    const g4a_attn_plan& pl = an.plan;
+    // one decode step with a few splits and a projection on the short word
+    // kernel, on a context that asks for it: the projection merges the
+    // partials while it stages its x row
+    const bool fuse = ctx->fuse_projection && a->T == 1 && (pl.kernel == G4A_KERNEL_DECODE || pl.kernel == G4A_KERNEL_DECODE_SHORT) &&
+                      pl.splits >= 2 && pl.splits <= G4A_FUSE_MAX_SPLITS && pl.splits <= COMBINE_ROW_SPLITS &&
+                      a->Hq <= G4A_FUSE_MAX_HEADS && (a->Dh == 256 || a->Dh == 512) && a->Dv == a->Dh &&
+                      (reinterpret_cast<uintptr_t>(a->out) & 15) == 0 && projection_on_short_words(ctx, w);
+    if (int rc = attention_run(ctx, a, an, !fuse)) return rc;
+    if (!fuse) return linear_q_launch(ctx, 0, w, nullptr, a->out, nullptr, 0, 0, y, a->T);
+    G4aLinearParams p{};
+    p.w = static_cast<const uint32_t*>(w->qbytes);
+    p.s = w->scales;
+    p.y = y;
+    p.M = 1;
+    p.N = w->N;
+    p.K = w->K;
+    p.W = uint32_t(uint64_t(w->K) * w->bits / 32);
+    p.bits = w->bits;
+    p.signed_i8 = w->signed_i8 ? 1 : 0;
+    p.xm = w->signed_i8 ? 0u : w->bits == 4 ? 0x88888888u : w->bits == 2 ? 0xAAAAAAAAu : 0x80808080u;
+    p.part = static_cast<const float*>(ctx->workspace);  // where attention_run left the partials
+    p.xout = a->out;
+    p.nsplit = pl.splits;
+    p.dh = a->Dh;
+    p.hq = a->Hq;
+    // the plain projection's grid (about 16 waves per CU over the rows): fewer,
+    // taller workgroups, each merging the whole row, measured slower
+    const uint64_t target = uint64_t(std::max(ctx->cu_count, 1)) * 16;
+    uint64_t rpw = (uint64_t(w->N) + target - 1) / target;
+    rpw = std::max<uint64_t>(2, (rpw + 1) / 2 * 2);
+    p.rows_per_wave = uint32_t(rpw);
+    const uint64_t vpw = 32 / w->bits, kpad = (uint64_t(p.W) + 63) / 64 * 64 * vpw;
+    const int bi = w->bits == 2 ? 0 : w->bits == 4 ? 1 : 2;
+    return launch(ctx, ctx->linear_fused[bi], dim3(uint32_t((w->N + 4 * rpw - 1) / (4 * rpw)), 1, 1),
+                  dim3(256, 1, 1), p, "attention row + projection", true, unsigned(kpad * 4));
 }
 
 int g4a_embed_rows_q(g4a_ctx* ctx, const g4a_qweight* table, const uint32_t* ids, uint32_t T, float scale,

@@ -1361,6 +1361,82 @@ __device__ __forceinline__ void combine_rows(const G4aCombineParams& p, uint32_t
     }
 }
 
+// combine_rows' merge of every head of one query (T = 1, 1 .. G4A_FUSE_MAX_SPLITS
+// splits) done by one 256-thread workgroup into LDS: xs[h * DH + d] is the
+// merged attention row (the activation row of the output projection that
+// follows), zeros from Hq * DH up to KP; xout, if set, receives the row too.
+// Each wave computes the split weights of heads wave, wave + 4, ... exactly as
+// combine_rows' wave 0 does; each dim then sums its splits in order from 0,
+// multiplies and adds rounded separately, so every value has combine_rows'
+// bits. Thread t merges four adjacent dims (one float4 of a split's 16-dim
+// row) in each 1024-dim group; the loads of two groups (every split) are in
+// flight at once, the first two groups' issued before the split weights are
+// known. `after_issue` runs right after those first loads are issued (the
+// projection requests its first weight words there).
+template <int DH, typename F>
+__device__ __forceinline__ void combine_row_stage(const float* __restrict__ part, uint32_t Hq, uint32_t ns, float* xs,
+                                                  uint32_t KP, float* xout, F&& after_issue) {
+    constexpr int FS = G4A_FUSE_MAX_SPLITS;
+    __shared__ float cw[G4A_FUSE_MAX_HEADS][FS];
+    __shared__ float cl[G4A_FUSE_MAX_HEADS];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t K = Hq * DH;
+    float4 x[2][FS];
+    auto issue = [&](int g, uint32_t k) {
+        const uint32_t kk = k < K ? k : K - 4;
+        const uint32_t h = kk / DH, d = kk - h * DH;
+        const float* __restrict__ acc = part + part_index<DH>(h, ns, 0, d);  // split s at acc[16 s]
+#pragma unroll
+        for (int s = 0; s < FS; ++s)  // ns >= 1: the clamped loads stay in the split range
+            x[g][s] = *reinterpret_cast<const float4*>(acc + (size_t)((uint32_t)s < ns ? s : ns - 1) * 16);
+    };
+    issue(0, 4 * tid);
+    issue(1, 1024 + 4 * tid);
+    after_issue();
+    const float2* __restrict__ ml = reinterpret_cast<const float2*>(part + (size_t)Hq * ns * DH);
+    for (uint32_t h = wv; h < Hq; h += 4) {
+        const bool on = (uint32_t)lane < ns;
+        const float2 m = on ? ml[h * ns + lane] : make_float2(NEG_INF, 0.0f);
+        const float M = wave_max(m.x);
+        const float e = (m.x == NEG_INF) ? 0.0f : expf(m.x - M);
+        if (on) cw[h][lane] = e;
+        const float L = wave_sum(on ? m.y * e : 0.0f);
+        if (lane == 0) cl[h] = L;
+    }
+    __syncthreads();
+    for (uint32_t k0 = 0; k0 < KP; k0 += 2048) {
+        if (k0 && k0 < K) {
+            issue(0, k0 + 4 * tid);
+            issue(1, k0 + 1024 + 4 * tid);
+        }
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const uint32_t k = k0 + 1024 * g + 4 * tid;
+            if (k < K) {
+                const uint32_t h = k / DH;
+                float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+                for (int s = 0; s < FS; ++s)
+                    if ((uint32_t)s < ns) {
+                        const float w = cw[h][s];
+                        a0 += x[g][s].x * w;
+                        a1 += x[g][s].y * w;
+                        a2 += x[g][s].z * w;
+                        a3 += x[g][s].w * w;
+                    }
+                const float L = cl[h];
+                const float4 o =
+                    L > 0.0f ? make_float4(a0 / L, a1 / L, a2 / L, a3 / L) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                *reinterpret_cast<float4*>(xs + k) = o;
+                if (xout) *reinterpret_cast<float4*>(xout + k) = o;
+            } else if (k < KP) {
+                *reinterpret_cast<float4*>(xs + k) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        }
+    }
+}
+
 // Batched decode: one launch over the independent single-query steps of
 // b.seq[]; grid (largest split count, sequences, Hkv). The decode parameters of
 // sequence blockIdx.y are rebuilt from its descriptor (T = 1; key positions

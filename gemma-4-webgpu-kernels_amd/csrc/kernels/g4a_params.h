@@ -209,7 +209,18 @@ struct G4aLinearParams {
     uint32_t b_stride, b_off;
     uint32_t xm;            // word mask turning each field into two's complement
     uint32_t bits, row_bytes, group_size, scale_stride, signed_i8;
+    // mode 3 (x is one attention row merged from a decode step's split partials
+    // while it is staged): the partials (T = 1: acc, then (m, l)), their split
+    // count, head dim and query heads; xout, if set, receives the merged row
+    const float* part;
+    float* xout;
+    uint32_t nsplit, dh, hq;
 };
+
+// Split counts up to which a decode step's output projection merges the split
+// partials itself (mode 3), and the query heads it takes.
+constexpr uint32_t G4A_FUSE_MAX_SPLITS = 16;
+constexpr uint32_t G4A_FUSE_MAX_HEADS = 64;
 
 // Quantised embedding rows: out[i, d] = deq(ids[i], d) * scale.
 struct G4aEmbedParams {

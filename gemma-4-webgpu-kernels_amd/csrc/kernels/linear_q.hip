@@ -166,15 +166,26 @@ __device__ __forceinline__ void linear_q_words(const G4aLinearParams& p) {
     uint32_t wd[D][RU], wd2[D][RU];
     float ep[D][2];
     // the first steps' words are requested before the activations are staged
+    // (mode 3: right after the loads of the partials the staging merges)
+    auto prefetch = [&]() {
 #pragma unroll
-    for (int d = 0; d + 1 < D; ++d)
-        if (T) load(wd[d], wd2[d], ep[d], min((uint32_t)d, T - 1));
-
-    for (uint32_t i = threadIdx.x; i < MT * KP / 4; i += blockDim.x) {
-        const uint32_t e = 4 * i, mt = e / KP, k = e - mt * KP;
-        float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (m0 + mt < p.M && k < K) xv = *reinterpret_cast<const float4*>(p.x + (size_t)(m0 + mt) * K + k);
-        *reinterpret_cast<float4*>(xs + e) = xv;
+        for (int d = 0; d + 1 < D; ++d)
+            if (T) load(wd[d], wd2[d], ep[d], min((uint32_t)d, T - 1));
+    };
+    if constexpr (MODE == 3) {
+        // x: one attention row merged from its decode step's split partials
+        // (MT = 1; workgroup 0 also stores the row)
+        float* const xout = blockIdx.x == 0 ? p.xout : nullptr;
+        if (p.dh == 512) combine_row_stage<512>(p.part, p.hq, p.nsplit, xs, KP, xout, prefetch);
+        else combine_row_stage<256>(p.part, p.hq, p.nsplit, xs, KP, xout, prefetch);
+    } else {
+        prefetch();
+        for (uint32_t i = threadIdx.x; i < MT * KP / 4; i += blockDim.x) {
+            const uint32_t e = 4 * i, mt = e / KP, k = e - mt * KP;
+            float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (m0 + mt < p.M && k < K) xv = *reinterpret_cast<const float4*>(p.x + (size_t)(m0 + mt) * K + k);
+            *reinterpret_cast<float4*>(xs + e) = xv;
+        }
     }
     __syncthreads();
 
@@ -846,6 +857,10 @@ G4A_LINEAR_SET(4, 2)
 G4A_LINEAR_SET(8, 0)
 G4A_LINEAR_SET(8, 1)
 G4A_LINEAR_SET(8, 2)
+// mode 3: a decode step's output projection, merging the split partials while staging x
+G4A_LINEAR_WORDS(2, 1, 2, 4, 3)
+G4A_LINEAR_WORDS(4, 1, 2, 4, 3)
+G4A_LINEAR_WORDS(8, 1, 2, 4, 3)
 
 #define G4A_LINEAR_MFMA(B, MODE)                                                                     \
     extern "C" __global__ __launch_bounds__(256) void g4a_linear_q_mfma_b##B##_n64_mode##MODE(G4aLinearParams p) {  \

@@ -129,6 +129,7 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
                                    vp]),
         "g4a_linear": (c_int, [ctxp, vp, ctypes.c_uint32, ctypes.c_uint32, vp, vp, ctypes.c_uint32]),
         "g4a_linear_q": (c_int, [ctxp, ctypes.POINTER(QWeightArgs), vp, vp, ctypes.c_uint32]),
+        "g4a_attention_linear_q": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.POINTER(QWeightArgs), vp]),
         "g4a_linear_q_geglu": (c_int, [ctxp, ctypes.POINTER(QWeightArgs), ctypes.POINTER(QWeightArgs), vp, vp,
                                        ctypes.c_uint32]),
         "g4a_linear_q_gelu_mul_cols": (c_int, [ctxp, ctypes.POINTER(QWeightArgs), vp, vp, ctypes.c_uint32,
@@ -390,6 +391,13 @@ class Context:
         sc = self.upload(np.ascontiguousarray(scales, np.float32))
         args = QWeightArgs(qb.ptr, sc.ptr, N, K, bits, 1 if signed_i8 else 0, group_size or K)
         return DeviceQWeight(args, qb, sc)
+
+    def attention_linear_q(self, q: int, k: int, v: int, out: int, w: "DeviceQWeight", y: int, **kw) -> None:
+        """g4a_attention_linear_q: attention() (same keywords) into out, then its
+        output projection w into y; a decode step of 2..16 splits merges its split
+        partials inside the projection instead of a combine launch."""
+        a, keep = make_args(q, k, v, out, **kw)
+        self._check(self.lib.g4a_attention_linear_q(self.handle, ctypes.byref(a), ctypes.byref(w.args), y))
 
     def linear_q(self, w: "DeviceQWeight", x: int, y: int, M: int) -> None:
         self._check(self.lib.g4a_linear_q(self.handle, ctypes.byref(w.args), x, y, M))

@@ -330,6 +330,23 @@ int g4a_linear_q_geglu(g4a_ctx *ctx, const g4a_qweight *w_gate, const g4a_qweigh
  * b[m * b_stride + b_off + n], b_off + N <= b_stride. */
 int g4a_linear_q_gelu_mul_cols(g4a_ctx *ctx, const g4a_qweight *w, const float *x, const float *b, uint32_t b_stride,
                                uint32_t b_off, float *y, uint32_t M);
+/* The attention block's output projection after its attention call
+ * (Gemma4Model::attention, rust/src/model.rs:287-303: o_proj(attention(q, k, v))):
+ * the results of g4a_attention(args) then g4a_linear_q(w, args->out, y, T),
+ * with w->K = Hq * Dv; args->out receives the attention rows as usual. On a
+ * context created with G4A_FUSE_PROJECTION=1 in the environment, a decode
+ * step (T = 1) that runs 2 .. 16 splits, with a projection the short-weight
+ * word kernel takes (N below 64 per CU, one scale per row, a weight under the
+ * int8 kernel's size threshold) and a 16-byte aligned args->out, launches no
+ * LSE combine: the projection merges the split partials while it stages its
+ * activation row, in the combine kernel's order, so y and args->out are
+ * bit-identical to the two separate calls (sliding-window decode steps, 512
+ * keys in 16 splits, qualify). Every other call, and every call on a default
+ * context, runs the two separately: on MI355X the merged form measured
+ * slower (each projection workgroup reads all 16 partials of the row). Replaces a decode step's ATTN_COMBINE dispatch
+ * (rust/src/backend_wgpu.rs:958-968) and the o_proj linear after it
+ * (rust/src/backend_wgpu.rs:768-806, called at rust/src/model.rs:303). */
+int g4a_attention_linear_q(g4a_ctx *ctx, const g4a_attn_args *args, const g4a_qweight *w, float *y);
 /* Backend::embed_rows on a quantised table [V, D] = [N, K] (rust/src/backend.rs:101-102;
  * rust/src/backend_cpu.rs:127-137; EMBED_Q, rust/src/backend_wgpu.rs:734-760):
  * out[i, d] = deq(ids[i], d) * scale, ids a host array of T values < N. */
