@@ -199,6 +199,19 @@ __device__ __forceinline__ void copy16_to_lds(const float* src, float* lds_dst) 
         asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
 
+// The same copy addressed as a wave-uniform 64-bit base (SGPRs) plus a 32-bit
+// per-lane byte offset: a stream whose lanes keep fixed offsets from a moving
+// base needs no per-copy vector address arithmetic (the decode loop issued ~11
+// VALU instructions per copy, two of them 64-bit multiplies, before this form).
+template <bool NT = false>
+__device__ __forceinline__ void copy16s_to_lds(const void* sbase, uint32_t voff, float* lds_dst) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) float*)lds_dst);
+    if constexpr (NT)
+        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+    else
+        asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
+
 // The same copy with 4 bytes per lane (global_load_lds_dword): lane l's 4 bytes
 // at `src` land at lds_dst + 4*l (lanes switched off by the exec mask write nothing).
 __device__ __forceinline__ void copy4_to_lds(const void* src, void* lds_dst) {
@@ -534,15 +547,19 @@ template <int DH>
 struct WaveCfg {
     static constexpr int GROUP = 8;
     static constexpr int KEYS = 16;                   // keys per wave tile
+    // 4 KiB chunks in a 4-deep ring; 8 KiB chunks in a 2-deep ring (the same LDS, twice
+    // the bytes in flight, half the chunk steps) measured 25.7 against 24.9 us at 32K keys
     static constexpr int BUF = 1024;                  // floats per chunk buffer (4 KiB)
     static constexpr int NB = 4;                      // chunk buffers per wave (16 KiB: the merge's partial)
+    static constexpr int KCD = BUF / KEYS;            // dims per K chunk (16 keys x KCD dims)
+    static constexpr int NCOL = KCD / 4;              // 16-byte columns of a K chunk row
     // Chunks in flight beyond the one in use. One beats three (8 MB instead of
     // 24 MB outstanding over the GPU): hd512 decode at 32K keys 25.05 -> 24.69 us,
     // at 131072 keys 83.8 -> 81.4 us; only calls forced to a few splits (8 or 32
     // workgroups at 131072 keys) lose, ~1.5 %. Zero is 15 % slower.
     static constexpr int AHEAD = 1;
     static constexpr int LPT = BUF / 256;             // 16-byte copies per lane per chunk
-    static constexpr int NKS = DH / 64;               // K chunks per wave tile
+    static constexpr int NKS = DH / KCD;              // K chunks per wave tile
     static constexpr int KPC = BUF / DH;              // keys per V chunk
     static constexpr int NVC = KEYS / KPC;            // V chunks per wave tile
     static constexpr int NCH = NKS + NVC;
@@ -554,6 +571,7 @@ struct WaveCfg {
     static constexpr int SMEM = RING + QS + PB + 8 * GROUP + 8 * 2 * GROUP + 8;
     static constexpr int KPB = 8 * 2 * KEYS;          // explicit positions: [wave][tile parity][key]
     static_assert(MERGE <= NB * BUF, "a wave's partial fits its ring");
+    static_assert(NCOL >= KEYS && NCOL % 4 == 0, "the K column swizzle (column ^ key) stays inside a row");
     static_assert(KPC * DH == BUF && KEYS % KPC == 0, "V chunks hold whole keys of the tile");
     static_assert(QS % 2048 == 0, "the query rows are copied in 8 waves x 1 KiB copies");
     static_assert(LPT * AHEAD + QS / 2048 < 64, "vmcnt immediate range");
@@ -564,7 +582,7 @@ template <int DH, bool KPOS>
 __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t split, uint32_t qi) {
     using C = WaveCfg<DH>;
     constexpr int GROUP = C::GROUP, KEYS = C::KEYS, BUF = C::BUF, NB = C::NB, AHEAD = C::AHEAD, LPT = C::LPT,
-                  NKS = C::NKS, KPC = C::KPC, NCH = C::NCH, ND = C::ND;
+                  NKS = C::NKS, KPC = C::KPC, NCH = C::NCH, ND = C::ND, KCD = C::KCD, NCOL = C::NCOL;
 
     __shared__ __attribute__((aligned(16))) float smem[C::SMEM + (KPOS ? C::KPB : 0)];
     float* const ring = smem;                   // [8 waves][NB][BUF]; after the loop wave w's
@@ -611,6 +629,7 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
     struct Tile {
         uint32_t t0, row0, nk;
         bool active;
+        bool whole;  // all KEYS keys in consecutive physical rows: the copies take the fixed lane offsets
         const float* kb;
         const float* vb;
     };
@@ -626,17 +645,28 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
         if (!KPOS && T.active) T.active = p.k_pos0 + T.t0 <= qpos;
         T.nk = T.active ? min((uint32_t)KEYS, p.k_end - T.t0) : 1u;
         T.row0 = T.active ? phys_row(T.t0, p.ring_cap) : 0u;
+        T.whole = T.active && T.nk == (uint32_t)KEYS && (p.ring_cap == 0u || T.row0 + KEYS <= p.ring_cap);
         T.kb = T.active ? kbase : p.dummy;
         T.vb = T.active ? vbase : p.dummy;
         return T;
     };
+    // Byte offsets of lane slot 64i + lane from the first row of a whole tile (see
+    // issue_chunk): K chunks add KCD c floats, V chunks KPC (c - NKS) rows, to the base.
+    uint32_t koff[LPT], voff[LPT];
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+        const int sl = 64 * i + lane;
+        const int r = sl / NCOL;
+        koff[i] = (uint32_t)((r * row_stride + 4 * ((sl % NCOL) ^ r)) * sizeof(float));
+        voff[i] = (uint32_t)(((sl / (DH / 4)) * row_stride + 4 * (sl % (DH / 4))) * sizeof(float));
+    }
     auto prow = [&](const Tile& T, uint32_t r) -> uint32_t {  // physical row of tile key r, clamped to the tile
         uint32_t x = T.row0 + min(r, T.nk - 1);
         if (p.ring_cap && x >= p.ring_cap) x -= p.ring_cap;
         return x;
     };
     // chunk c of a wave tile into ring buffer bi: K chunks c < NKS hold dims
-    // 64c..64c+63 of the 16 keys (key r's 16-byte column j at slot j ^ r), V chunks
+    // KCD c .. KCD c + KCD-1 of the 16 keys (key r's 16-byte column j at slot j ^ r), V chunks
     // hold keys KPC*(c-NKS) .. +KPC-1, all DH dims. Lane l fills 16-byte slot 64i + l.
     // With explicit positions chunk 0 is preceded by one more copy, the tile's 16
     // key positions into my_kp[parity] (clamped to the tile's last key; an idle tile
@@ -651,14 +681,22 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
             }
         }
         float* const dst = my_ring + bi * BUF;
+        if (T.whole) {
+            // the tile's rows are consecutive: a wave-uniform base plus each lane's fixed offset
+            const float* const base = c < NKS ? kbase + (size_t)T.row0 * row_stride + KCD * c
+                                              : vbase + ((size_t)T.row0 + (c - NKS) * KPC) * row_stride;
+#pragma unroll
+            for (int i = 0; i < LPT; ++i) copy16s_to_lds<true>(base, c < NKS ? koff[i] : voff[i], dst + 256 * i);
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < LPT; ++i) {
             const int sl = 64 * i + lane;
             const float* src;
             if (c < NKS) {
-                const int r = sl >> 4;
-                const int j = (sl & 15) ^ r;
-                src = T.kb + (size_t)prow(T, r) * row_stride + 64 * c + 4 * j;
+                const int r = sl / NCOL;
+                const int j = (sl % NCOL) ^ r;
+                src = T.kb + (size_t)prow(T, r) * row_stride + KCD * c + 4 * j;
             } else {
                 const int kr = (c - NKS) * KPC + sl / (DH / 4);
                 src = T.vb + (size_t)prow(T, kr) * row_stride + 4 * (sl % (DH / 4));
@@ -685,9 +723,9 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
         qreg[0][i] = q0row[16 * i];
         qreg[1][i] = q1row[16 * i];
     }
-    const float* kcol[16];
+    const float* kcol[NCOL];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) kcol[j] = my_ring + key * 64 + 4 * (j ^ key);
+    for (int j = 0; j < NCOL; ++j) kcol[j] = my_ring + key * KCD + 4 * (j ^ key);
 
     float m[2] = {NEG_INF, NEG_INF}, lpart[2] = {0.0f, 0.0f};
     float4 acc[GROUP][ND];
@@ -696,6 +734,7 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
 #pragma unroll
         for (int e = 0; e < ND; ++e) acc[h][e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
+    int other_seen = -1;  // the partner wave's chunk count, one chunk step old
     for (uint32_t it = 0; it < niter; ++it) {
         const bool last = it + 1 == niter;  // no copies beyond the last wave tile
         const Tile nxt = tile_info(it + 1);
@@ -716,10 +755,12 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
             {
                 // The two waves sharing a SIMD (w and w ^ 4) would otherwise issue oldest
                 // first, starving the younger one: a wave behind its partner raises its
-                // issue priority until it catches up.
+                // issue priority until it catches up. The partner's count is the one read
+                // a chunk step earlier, so the read never holds this wave up.
                 const int done = (int)(it * NCH) + c;
                 progress[w] = done;
-                const int other = __builtin_amdgcn_readfirstlane(progress[w ^ 4]);
+                const int other = __builtin_amdgcn_readfirstlane(other_seen);
+                other_seen = progress[w ^ 4];
                 if (other > done) __builtin_amdgcn_s_setprio(1);
                 else __builtin_amdgcn_s_setprio(0);
                 // left alone, the scheduler gathers the priority changes of all
@@ -729,9 +770,9 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
             if (!cur.active) continue;
             if (c < NKS) {
 #pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const float q0 = qreg[0][4 * c + b];
-                    const float q1 = qreg[1][4 * c + b];
+                for (int b = 0; b < KCD / 16; ++b) {
+                    const float q0 = qreg[0][(KCD / 16) * c + b];
+                    const float q1 = qreg[1][(KCD / 16) * c + b];
                     float4 k4[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) k4[i] = ld4(kcol[4 * b + i] + bi * BUF);
@@ -807,21 +848,33 @@ __device__ __forceinline__ void decode_wave(const G4aDecodeParams& p, uint32_t s
             mlbuf[w * 2 * GROUP + GROUP + 2 * hp + h] = lpart[h];
         }
     }
+    // head w stays in this wave's registers: wave w merges it (w is wave-uniform, so
+    // these are scalar branches)
+    float4 a[8][ND];
 #pragma unroll
-    for (int h = 0; h < GROUP; ++h)
+    for (int h = 0; h < GROUP; ++h) {
+        if (h == w) {
 #pragma unroll
-        for (int e = 0; e < ND; ++e)
-            *reinterpret_cast<float4*>(my_ring + h * DH + 256 * e + 4 * lane) = acc[h][e];
+            for (int e = 0; e < ND; ++e) a[h][e] = acc[h][e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < ND; ++e) *reinterpret_cast<float4*>(my_ring + h * DH + 256 * e + 4 * lane) = acc[h][e];
+        }
+    }
     __syncthreads();
     // Wave w merges head w: M = max over waves, L = sum of l * e^(m - M). The 8
     // wave partials are read first; lane x of each 8-lane group computes wave x's
     // weight e^(m_x - M) and l_x e^(m_x - M), which every lane takes in wave order.
     const int h = w;
-    float4 a[8][ND];
 #pragma unroll
-    for (int x = 0; x < 8; ++x)
+    for (int x = 0; x < 8; ++x) {
+        if (x == w) {
+            // a[x] holds this wave's own head w, from the copy above (h == x == w)
+        } else {
 #pragma unroll
-        for (int e = 0; e < ND; ++e) a[x][e] = ld4(ring + x * NB * BUF + h * DH + 256 * e + 4 * lane);
+            for (int e = 0; e < ND; ++e) a[x][e] = ld4(ring + x * NB * BUF + h * DH + 256 * e + 4 * lane);
+        }
+    }
     const float mx = mlbuf[(lane & 7) * 2 * GROUP + h];
     const float M = g4a_max8(mx);
     const float ex = (mx == NEG_INF) ? 0.0f : expf(mx - M);
