@@ -42,6 +42,12 @@ HQ = 8
 # least this many other bytes are read (twice the 256 MB MALL): every step
 # streams from HBM. Warm figures use one copy, read step after step.
 COLD_REUSE_BYTES = 512 << 20
+# Timing protocol of every figure: the --warmup steps, then the same workload
+# run back to back for at least WARM_MS of wall time, then REGIONS timed
+# regions of exactly --steps steps each; the median region is reported.
+WARM_MS = 50.0
+REGIONS = 3
+EXTRA_REGION_MS = 2.0  # the extra workloads' regions hold at least this much GPU time
 
 
 def cold_copies(step_bytes: int) -> int:
@@ -101,30 +107,59 @@ class Decode:
             a.free()
 
 
-def time_steps(ctx, calls, steps, warmup, repeats=1):
-    """Times `steps` steps of the hot path after `warmup` untimed ones. `calls`
-    lists the attention() keyword sets of consecutive steps (cycled); a step is
+def warm_up(run, min_ms: float = WARM_MS) -> None:
+    """Calls `run()` (one batch of the workload, run to completion) until at
+    least `min_ms` of wall time has passed: the GPU reaches its steady clocks
+    on the same work before anything is timed, whatever --warmup asks for."""
+    t_end = time.perf_counter() + min_ms * 1e-3
+    while True:
+        run()
+        if time.perf_counter() >= t_end:
+            break
+
+
+def time_steps(ctx, calls, steps, warmup, regions=REGIONS, min_region_ms=0.0):
+    """Times `steps` steps of the hot path after `warmup` untimed ones and a
+    time-based warm-up of the same steps (>= WARM_MS). `calls` lists the
+    attention() keyword sets of consecutive steps (cycled); a step is
     len(calls[i]) attention calls. All steps of a region are enqueued through
     one g4a_attention_batch call, so the region measures the library (host
     dispatch + kernels), not Python's per-call overhead.
 
-    Two timed regions, both bracketed by HIP events on the library's stream:
-    first the steps alone (ms/step), then the same steps again with the main
-    kernel of every call carrying dispatch-attached start/stop events (its
-    average duration). The per-dispatch events add a few microseconds between
-    launches, so they stay out of the region that gives ms/step. With repeats > 1
-    both regions run that many times and the medians are returned (the extra
-    workloads use 3: single regions of these sizes vary by up to ~15 % between
-    runs on one box).
-    Returns (ms/step, main-kernel ms/launch)."""
+    Each of `regions` rounds has two timed regions, both bracketed by HIP
+    events on the library's stream: first exactly `steps` steps alone
+    (ms/step), then the same steps again with the main kernel of every call
+    carrying dispatch-attached start/stop events (its average duration). The
+    per-dispatch events add a few microseconds between launches, so they stay
+    out of the region that gives ms/step. The medians over the rounds are
+    returned (single regions vary by several per cent between runs). With
+    min_region_ms > 0 (the extra workloads; the headline times exactly
+    --steps), a region grows past `steps` steps until it holds about that much
+    GPU time, estimated from the warm-up: 20 steps of a 7 µs call are too
+    short a region to repeat within 2 %.
+    Returns (ms/step, main-kernel ms/launch, per-round ms/step list)."""
     def batch(n):
         return [kw for i in range(n) for kw in calls[i % len(calls)]]
     warm, timed = ctx.prepare_batch(batch(warmup)), ctx.prepare_batch(batch(steps))
     if warmup:
         ctx.attention_batch(warm)
     ctx.sync()
+
+    def one_batch():
+        ctx.attention_batch(timed)
+        ctx.sync()
+    warm_up(one_batch)
+    if min_region_ms > 0:
+        t0 = time.perf_counter()
+        one_batch()
+        est = (time.perf_counter() - t0) * 1e3 / steps  # host-side bound on ms/step
+        grown = int(np.ceil(min_region_ms / max(est, 1e-6)))
+        if grown > steps:
+            steps = grown
+            timed = ctx.prepare_batch(batch(steps))
+            one_batch()
     step_ms, kernel_ms = [], []
-    for _ in range(repeats):
+    for _ in range(regions):
         ctx.timer_start()
         ctx.attention_batch(timed)
         step_ms.append(ctx.timer_stop() / steps)
@@ -134,7 +169,20 @@ def time_steps(ctx, calls, steps, warmup, repeats=1):
         kms, n = ctx.kernel_timing_read()
         ctx.kernel_timing(False)
         kernel_ms.append(kms / n if n else float("nan"))
-    return float(np.median(step_ms)), float(np.median(kernel_ms))
+    return float(np.median(step_ms)), float(np.median(kernel_ms)), step_ms
+
+
+def kernel_regions(ctx, run, regions=REGIONS):
+    """Median over `regions` runs of run() (a Python loop of calls, run to completion)
+    of the mean dispatch-attached kernel time, ms per launch."""
+    per = []
+    for _ in range(regions):
+        ctx.kernel_timing(True)
+        run()
+        kms, n = ctx.kernel_timing_read()
+        ctx.kernel_timing(False)
+        per.append(kms / n if n else float("nan"))
+    return float(np.median(per))
 
 
 def cpu_baseline(budget_s: float = 10.0):
@@ -163,7 +211,25 @@ def cpu_baseline(budget_s: float = 10.0):
     }
 
 
-def schedule_35_layers(ctx, steps, warmup):
+def cpu_time(fn, budget_s: float, max_reps: int = 50):
+    """Median wall time (µs) of fn() on the host, repeated for about budget_s
+    (at least once): the CPU oracle timed beside a GPU figure."""
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while not times or (time.perf_counter() < t_end and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)) * 1e6, len(times)
+
+
+def oracle_module():
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle
+    return oracle
+
+
+def schedule_35_layers(ctx, steps, warmup, cpu=True):
     """one token of the 35-layer Gemma-4-E2B attention schedule at 32768 context.
     Layers 4,9,...,34 are global (hd512, full context); the rest local (hd256, 512-slot ring).
     Layers 15..34 reuse the KV of layer 14 (global) or 13 (local) (rust/src/config.rs:152-159),
@@ -181,9 +247,22 @@ def schedule_35_layers(ctx, steps, warmup):
                           q_pos0=S - 1, k_pos0=0, window=0 if L.is_global else synth.E2B_WINDOW,
                           ring_cap=host_caches[L.src].ring_cap))
 
-    ms, _ = time_steps(ctx, [token], steps, warmup, repeats=3)
+    ms, _, regions = time_steps(ctx, [token], steps, warmup, min_region_ms=EXTRA_REGION_MS)
     algo = 7 * decode_bytes(S, 512) + 28 * decode_bytes(512, 256)
-    res = {"us_per_token": ms * 1e3, "algorithmic_bytes": algo, "GB_s": algo / (ms * 1e-3) / 1e9}
+    res = {"us_per_token": ms * 1e3, "regions_us": [round(x * 1e3, 2) for x in regions], "algorithmic_bytes": algo,
+           "GB_s": algo / (ms * 1e-3) / 1e9}
+    if cpu:
+        # the CPU oracle on the same 35 calls (a ring's rows unrolled into key order)
+        oracle = oracle_module()
+        host = {li: synth.unroll_ring(c) + (c.k_pos,) for li, c in host_caches.items()}
+
+        def token_cpu():
+            for L in layers:
+                k, v, kp = host[L.src]
+                oracle.attention(L.q, k, v, np.array([S - 1], np.uint32), kp,
+                                 window=0 if L.is_global else synth.E2B_WINDOW)
+        us, n = cpu_time(token_cpu, 1.0, 5)
+        res.update(cpu_us=us, cpu_threads=oracle.thread_count(HQ), cpu_sample=f"{n} whole tokens (35 calls), median")
     # the same token's 35 calls captured once into a HIP graph and replayed
     # (reported beside the eager figure; a capture error is reported, not fatal)
     try:
@@ -200,10 +279,19 @@ def schedule_35_layers(ctx, steps, warmup):
         for _ in range(max(warmup, 1)):
             graph.launch()
         ctx.sync()
-        ctx.timer_start()
-        for _ in range(steps):
-            graph.launch()
-        ms_graph = ctx.timer_stop() / steps
+
+        def replay():
+            for _ in range(steps):
+                graph.launch()
+            ctx.sync()
+        warm_up(replay)
+        times = []
+        for _ in range(REGIONS):
+            ctx.timer_start()
+            for _ in range(steps):
+                graph.launch()
+            times.append(ctx.timer_stop() / steps)
+        ms_graph = float(np.median(times))
         graph.free()
         res.update(us_per_token_graph=ms_graph * 1e3, GB_s_graph=algo / (ms_graph * 1e-3) / 1e9)
     except g4a.G4aError as e:
@@ -281,8 +369,14 @@ def schedule_with_projection(ctx, steps, warmup):
             for _ in range(max(warmup, 1)):
                 graph.launch()
             c.sync()
+
+            def replay():
+                for _ in range(steps):
+                    graph.launch()
+                c.sync()
+            warm_up(replay)
             times = []
-            for _ in range(3):
+            for _ in range(REGIONS):
                 c.timer_start()
                 for _ in range(steps):
                     graph.launch()
@@ -332,15 +426,12 @@ def producer(ctx, T, Dh, theta, rot, pos0, ring_cap, steps, cpu_reps=3):
     kw = dict(q=q.ptr, k=k.ptr, v=v.ptr, q_norm=w.ptr, k_norm=w.ptr, q_out=qo.ptr, k_cache=kc.ptr, v_cache=vc.ptr,
               T=T, Hq=HQ, Hkv=1, Dh=Dh, rotary_dim=rot, pos0=pos0, cache_row=pos0, ring_cap=ring_cap, theta=theta,
               eps=1e-6)
-    for _ in range(5):
-        ctx.attn_producer(**kw)
-    ctx.sync()
-    ctx.kernel_timing(True)
-    for _ in range(steps):
-        ctx.attn_producer(**kw)
-    ctx.sync()
-    kms, n = ctx.kernel_timing_read()
-    ctx.kernel_timing(False)
+    def run():
+        for _ in range(steps):
+            ctx.attn_producer(**kw)
+        ctx.sync()
+    warm_up(run)
+    kms = kernel_regions(ctx, run)
     for a in (q, k, v, w, qo, kc, vc):
         a.free()
     pos = np.arange(pos0, pos0 + T, dtype=np.uint32)
@@ -349,7 +440,7 @@ def producer(ctx, T, Dh, theta, rot, pos0, ring_cap, steps, cpu_reps=3):
         t0 = time.perf_counter()
         oracle.producer(q_h, k_h, v_h, w_h, w_h, pos, theta, rot, 1e-6)
         times.append(time.perf_counter() - t0)
-    us = kms / n * 1e3
+    us = kms * 1e3
     b = producer_bytes(T, Dh)
     return {"kernel_us": us, "GB_s": b / (us * 1e-6) / 1e9, "frac_hbm_peak": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "bytes": b, "cpu_oracle_us": float(np.median(times)) * 1e6, "cpu_threads": 1}
@@ -359,19 +450,37 @@ PREFILL_CONFIGS = [("configs[3a] prefill hd256 T2048 window512", 2048, 256, 512)
                    ("configs[3b] prefill hd512 T2048 causal", 2048, 512, 0)]
 
 
-def prefill(ctx, T, Dh, window, steps, warmup):
+# configs[3b] takes ~20 s on 8 cores through the CPU oracle: it is timed on every
+# CPU_PREFILL_STRIDE-th query (the full K/V, the same per-row work as the whole call)
+# and scaled by the row count; configs[3a] (~0.6 s) is timed whole.
+CPU_PREFILL_STRIDE = {256: 1, 512: 8}
+
+
+def prefill(ctx, T, Dh, window, steps, warmup, cpu=True):
     ins = synth.gemma_inputs(T=T, S=T, Dh=Dh, seed=3, q_pos=np.arange(T))
     q, k, v = ctx.upload(ins.q), ctx.upload(ins.k), ctx.upload(ins.v)
     out = ctx.empty((T, HQ * Dh))
 
     call = [dict(q=q.ptr, k=k.ptr, v=v.ptr, out=out.ptr, T=T, S=T, Hq=HQ, Hkv=1, Dh=Dh, Dv=Dh, q_pos0=0, k_pos0=0,
                  window=window)]
-    ms, kms = time_steps(ctx, [call], steps, warmup, repeats=3)
+    ms, kms, regions = time_steps(ctx, [call], steps, warmup, min_region_ms=EXTRA_REGION_MS)
     for a in (q, k, v, out):
         a.free()
     fl = prefill_flops(T, window, Dh)
-    return {"us": ms * 1e3, "kernel_us": kms * 1e3, "TFLOP_s": fl / (ms * 1e-3) / 1e12, "flops": fl,
-            "frac_fp32_mfma_peak": fl / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+    res = {"us": ms * 1e3, "kernel_us": kms * 1e3, "regions_us": [round(x * 1e3, 2) for x in regions],
+           "TFLOP_s": fl / (ms * 1e-3) / 1e12, "flops": fl,
+           "frac_fp32_mfma_peak": fl / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS}
+    if cpu:
+        oracle = oracle_module()
+        stride = CPU_PREFILL_STRIDE.get(Dh, 1)
+        rows = np.arange(stride // 2, T, stride) if stride > 1 else np.arange(T)
+        qs, qp = np.ascontiguousarray(ins.q[rows]), np.ascontiguousarray(ins.q_pos[rows])
+        us, n = cpu_time(lambda: oracle.attention(qs, ins.k, ins.v, qp, ins.k_pos, window=window), 0.5, 3)
+        res.update(cpu_us=us * T / len(rows), cpu_threads=oracle.thread_count(len(rows) * HQ),
+                   cpu_sample=(f"all {T} queries, {n} run(s), median" if stride == 1 else
+                               f"every {stride}th query ({len(rows)} of {T}, full K/V), {n} run(s), median, "
+                               f"scaled by {T}/{len(rows)}"))
+    return res
 
 
 BATCH_CONFIGS = [
@@ -425,11 +534,20 @@ def batched_decode(ctx, n, L, Dh, window, ring_cap, steps, warmup, holes=False):
     for i in range(warmup):
         assert ctx.attention_decode_batch(prepared[i % copies]) == n
     ctx.sync()
-    ctx.timer_start()
-    for i in range(steps):
-        ctx.attention_decode_batch(prepared[i % copies])
-    ms = ctx.timer_stop() / steps
-    seq_ms, seq_kms = time_steps(ctx, steps_calls, max(10, steps // 4), min(warmup, 5))
+
+    def run_steps():
+        for i in range(steps):
+            ctx.attention_decode_batch(prepared[i % copies])
+        ctx.sync()
+    warm_up(run_steps)
+    times = []
+    for _ in range(REGIONS):
+        ctx.timer_start()
+        for i in range(steps):
+            ctx.attention_decode_batch(prepared[i % copies])
+        times.append(ctx.timer_stop() / steps)
+    ms = float(np.median(times))
+    seq_ms, _, _ = time_steps(ctx, steps_calls, max(10, steps // 4), min(warmup, 5))
     for a in (q, k0, v0, out):
         a.free()
     for k, v in kv:
@@ -493,15 +611,12 @@ def linear_bench(ctx, op, N, K, bits, M, steps, cpu=True):
             ctx.linear_q_geglu(pair[0], pair[1], x.ptr, y.ptr, M)
         else:
             ctx.linear_q(pair[0], x.ptr, y.ptr, M)
-    for i in range(min(copies, 20)):
-        call(i)
-    ctx.sync()
-    ctx.kernel_timing(True)
-    for i in range(steps):
-        call(i)
-    ctx.sync()
-    kms, n = ctx.kernel_timing_read()
-    ctx.kernel_timing(False)
+    def run():
+        for i in range(steps):
+            call(i)
+        ctx.sync()
+    warm_up(run)
+    kms = kernel_regions(ctx, run)
     for pair in ws:
         for w in pair:
             ctx.free(w.args.qbytes)
@@ -509,7 +624,7 @@ def linear_bench(ctx, op, N, K, bits, M, steps, cpu=True):
         w.free()
     x.free()
     y.free()
-    us = kms / n * 1e3
+    us = kms * 1e3
     b = linear_bytes(op, N, K, bits, M)
     res = {"kernel_us": us, "GB_s": b / (us * 1e-6) / 1e9, "frac_hbm_peak": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
            "bytes": b, "weight_copies_rotated": copies}
@@ -536,36 +651,85 @@ DECODE_CONFIGS = [("configs[0] sliding hd256 S512", 512, 256, 512, 0),
                   ("configs[2] global hd512 S131072", 131072, 512, 0, 2)]
 
 
-def decode_configs(ctx, steps_arg, warmup_arg):
+def decode_configs(ctx, steps_arg, warmup_arg, cpu=True):
     """configs[0..2] decode steps, cold (rotated K/V copies) with the warm figure
-    beside; configs[2] also under a forced split sweep (cold). us_per_step: the
-    call's launches back to back (the figure of merit); kernel_dispatch_us: one
-    event pair around each decode dispatch, i.e. the kernel plus its own launch
-    latency (~1-1.5 us), which back-to-back steps hide behind the previous
-    launch, so for the short calls it can exceed us_per_step."""
+    beside; configs[2] also under a forced split sweep (cold, the same protocol
+    as its main figure, so the automatic choice's entry repeats it). us_per_step:
+    the call's launches back to back (the figure of merit); kernel_dispatch_us:
+    one event pair around each decode dispatch, i.e. the kernel plus its own
+    launch latency (~1-1.5 us), which back-to-back steps hide behind the previous
+    launch, so for the short calls it can exceed us_per_step. cpu_us: the CPU
+    oracle on the same inputs, on this host's cores."""
     extras = {}
     for name, S, Dh, W, seed in DECODE_CONFIGS:
         b = decode_bytes(min(S, W) if W else S, Dh)
         d = Decode.cold(ctx, S=S, Dh=Dh, seed=seed, window=W)
-        steps = max(10, steps_arg // (4 if S > 100000 else 1))
-        m, km = time_steps(ctx, d.calls(), steps, min(warmup_arg, 10), repeats=3)
+        m, km, regions = time_steps(ctx, d.calls(), steps_arg, warmup_arg, min_region_ms=EXTRA_REGION_MS)
         pl = ctx.plan(**d.kw())
-        extras[name] = {"us_per_step": m * 1e3, "kernel_dispatch_us": km * 1e3, "GB_s": b / (m * 1e-3) / 1e9,
+        extras[name] = {"us_per_step": m * 1e3, "kernel_dispatch_us": km * 1e3,
+                        "regions_us": [round(x * 1e3, 2) for x in regions], "GB_s": b / (m * 1e-3) / 1e9,
                         "kernel_dispatch_GB_s": b / (km * 1e-3) / 1e9, "kernel": g4a.KERNEL_NAMES[pl.kernel],
                         "splits": pl.splits, "kv_copies_rotated": len(d.kv)}
         if S > 100000:
             sweep = {}
             for sp in (8, 16, 32, 64, 128, 256, 512):
-                m2, k2 = time_steps(ctx, d.calls(sp), 20, 4, repeats=3)
+                m2, k2, _ = time_steps(ctx, d.calls(sp), steps_arg, warmup_arg, min_region_ms=EXTRA_REGION_MS)
                 sweep[sp] = {"us_per_step": round(m2 * 1e3, 2), "kernel_dispatch_us": round(k2 * 1e3, 2)}
             extras[name]["split_sweep"] = sweep
+        if cpu:
+            oracle = oracle_module()
+            ins = d.inputs
+            us, n = cpu_time(lambda: oracle.attention(ins.q, ins.k, ins.v, ins.q_pos, ins.k_pos, window=W),
+                             1.0 if S < 100000 else 2.0, 20)
+            extras[name].update(cpu_us=us, cpu_threads=oracle.thread_count(HQ), cpu_sample=f"{n} call(s), median")
         d.free()
         w = Decode(ctx, S=S, Dh=Dh, seed=seed, window=W)
-        mw, kmw = time_steps(ctx, w.calls(), steps, min(warmup_arg, 10), repeats=3)
+        mw, kmw, _ = time_steps(ctx, w.calls(), steps_arg, warmup_arg, min_region_ms=EXTRA_REGION_MS)
         w.free()
         extras[name]["warm"] = {"us_per_step": mw * 1e3, "kernel_dispatch_us": kmw * 1e3, "GB_s": b / (mw * 1e-3) / 1e9}
         print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
     return extras
+
+
+# The reference's own attention timings (Apple M4, wgpu/Metal, ms per op, wall
+# clock around 60 back-to-back ops: rust/README.md:136-140, rust/src/main.rs:574-587)
+# for the cases of its `bench --kernels` (rust/src/main.rs:544-560) it publishes.
+REFERENCE_M4_MS = {(256, 512, 512): 0.060, (256, 8192, 512): 0.070, (512, 8192, 0): 0.60}
+
+
+def reference_bench(ctx, steps, warmup, cpu=True):
+    """The five attention cases of the reference's `bench --kernels`
+    (rust/src/main.rs:544-560) on their own inputs: Xorshift(987654321) after
+    the earlier cases' draws, U(-0.1, 0.1), scale 1/16, q at position S-1
+    (synth.reference_bench_inputs). The reference re-runs one set of buffers,
+    so these are warm figures (one K/V copy), beside its published M4 time
+    where it has one, and the CPU oracle on the same inputs."""
+    res = {}
+    for (dh, S, window), q_h, k_h, v_h in synth.reference_bench_inputs():
+        q, k, v = ctx.upload(q_h), ctx.upload(k_h), ctx.upload(v_h)
+        out = ctx.empty((1, HQ * dh))
+        call = dict(q=q.ptr, k=k.ptr, v=v.ptr, out=out.ptr, T=1, S=S, Hq=HQ, Hkv=1, Dh=dh, Dv=dh, q_pos0=S - 1,
+                    k_pos0=0, window=window, scale=1.0 / 16.0)
+        ms, kms, regions = time_steps(ctx, [[call]], steps, warmup, min_region_ms=EXTRA_REGION_MS)
+        for a in (q, k, v, out):
+            a.free()
+        vis = min(S, window) if window else S
+        name = f"attention Dh{dh} S{S}" + (f" window{window}" if (dh, S) != (256, 512) else "")
+        r = {"us_per_step": ms * 1e3, "kernel_dispatch_us": kms * 1e3,
+             "regions_us": [round(x * 1e3, 2) for x in regions],
+             "GB_s": decode_bytes(vis, dh) / (ms * 1e-3) / 1e9}
+        m4 = REFERENCE_M4_MS.get((dh, S, window))
+        if m4 is not None:
+            r["reference_m4_us"] = m4 * 1e3
+            r["speedup_vs_reference_m4"] = m4 / ms
+        if cpu:
+            oracle = oracle_module()
+            qp, kp = np.array([S - 1], np.uint32), np.arange(S, dtype=np.uint32)
+            us, n = cpu_time(lambda: oracle.attention(q_h, k_h, v_h, qp, kp, scale=1.0 / 16.0, window=window), 0.5, 20)
+            r.update(cpu_us=us, cpu_threads=oracle.thread_count(HQ), cpu_sample=f"{n} call(s), median")
+        res[name] = r
+        print(f"[bench] reference case {name}: {r}", file=sys.stderr, flush=True)
+    return res
 
 
 def load_traffic():
@@ -585,7 +749,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="headline decode only (no extras, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "schedule", "producer", "batch", "linear", "oproj"],
+    ap.add_argument("--only", choices=["decode", "prefill", "schedule", "producer", "batch", "linear", "oproj",
+                                       "reference"],
                     default=None,
                     help="run only these extra workloads (for profiling) and print their JSON line")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
@@ -627,6 +792,8 @@ def main(argv=None):
             for name, n, L, Dh, W, cap, holes in BATCH_CONFIGS:
                 out[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=args.steps, warmup=args.warmup, holes=holes)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
+        elif args.only == "reference":
+            out["reference bench --kernels cases"] = reference_bench(ctx, args.steps, args.warmup)
         elif args.only == "oproj":
             out["configs[4] token + o_proj @32768"] = schedule_with_projection(ctx, steps=args.steps,
                                                                                warmup=args.warmup)
@@ -642,12 +809,12 @@ def main(argv=None):
 
     # ---- headline: hd512 global decode at 32K context (cold: rotated K/V copies) ----
     head = Decode.cold(ctx, S=32768, Dh=512, seed=4)
-    ms, kms = time_steps(ctx, head.calls(), args.steps, args.warmup)
+    ms, kms, head_regions = time_steps(ctx, head.calls(), args.steps, args.warmup)
     plan = ctx.plan(**head.kw())
     head_copies = len(head.kv)
     head.free()
     warm = Decode(ctx, S=32768, Dh=512, seed=4)
-    ms_warm, kms_warm = time_steps(ctx, warm.calls(), max(10, args.steps // 2), min(args.warmup, 20), repeats=3)
+    ms_warm, kms_warm, _ = time_steps(ctx, warm.calls(), args.steps, args.warmup)
     warm.free()
     algo = decode_bytes(32768, 512)
     gbs = algo / (ms * 1e-3) / 1e9
@@ -662,6 +829,9 @@ def main(argv=None):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "timing": f"--warmup steps, then >= {WARM_MS:.0f} ms of the same steps back to back, then {REGIONS} timed "
+                  f"regions of exactly --steps steps; ms_per_step is the median region",
+        "regions_us_per_step": [round(x * 1e3, 3) for x in head_regions],
         "ms_per_step": ms,
         "us_per_step": ms * 1e3,
         "higher_is_better": True,
@@ -691,15 +861,18 @@ def main(argv=None):
                               "not measured in this run",
             "algorithmic_bytes_per_launch": algo,
             "kernel_us": kms * 1e3,
-            "kernel_us_source": "dispatch-attached HIP events on the launch stream, mean over the timed steps",
+            "kernel_us_source": "dispatch-attached HIP events on the launch stream: mean over the timed steps of "
+                                "a region, median of the regions",
         },
     }
 
     if not args.quick:
         extras = {}
-        extras.update(decode_configs(ctx, args.steps, args.warmup))
+        cpu = not args.no_cpu
+        extras.update(decode_configs(ctx, args.steps, args.warmup, cpu=cpu))
+        extras["reference bench --kernels cases"] = reference_bench(ctx, args.steps, args.warmup, cpu=cpu)
         for name, T, Dh, W in PREFILL_CONFIGS:
-            extras[name] = prefill(ctx, T, Dh, W, steps=5, warmup=2)
+            extras[name] = prefill(ctx, T, Dh, W, steps=5, warmup=2, cpu=cpu)
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
         for name, T, Dh, theta, rot, pos0, cap in PRODUCER_CONFIGS:
             extras[name] = producer(ctx, T, Dh, theta, rot, pos0, cap, steps=50)
@@ -710,7 +883,7 @@ def main(argv=None):
         for name, n, L, Dh, W, cap, holes in BATCH_CONFIGS:
             extras[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=50, warmup=10, holes=holes)
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
-        extras["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=20, warmup=3)
+        extras["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=20, warmup=3, cpu=cpu)
         print(f"[bench] schedule: {extras['configs[4] 35-layer schedule @32768']}", file=sys.stderr, flush=True)
         extras["configs[4] token + o_proj @32768"] = schedule_with_projection(ctx, steps=20, warmup=3)
         print(f"[bench] token + o_proj: {extras['configs[4] token + o_proj @32768']}", file=sys.stderr, flush=True)

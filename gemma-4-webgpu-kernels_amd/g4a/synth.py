@@ -331,3 +331,130 @@ def unroll_ring(c: ScheduleCache):
         return c.k, c.v
     slots = c.k_pos % np.uint32(c.ring_cap)
     return np.ascontiguousarray(c.k[slots]), np.ascontiguousarray(c.v[slots])
+
+
+# ---- the reference's kernel benchmark inputs ----------------------------------
+
+def _xs_step(s: int) -> int:
+    """One step of rust/src/main.rs:306-316: s ^= s << 13; s ^= s >> 17; s ^= s << 5 (u32)."""
+    s ^= (s << 13) & 0xFFFFFFFF
+    s ^= s >> 17
+    s ^= (s << 5) & 0xFFFFFFFF
+    return s
+
+
+def _gf2_matrix_of(step) -> np.ndarray:
+    """The 32x32 GF(2) matrix of a linear map on u32 states, as 32 column images."""
+    return np.array([step(1 << b) for b in range(32)], dtype=np.uint64)
+
+
+def _gf2_apply(cols: np.ndarray, states: np.ndarray) -> np.ndarray:
+    """Applies the linear map given by its column images to every state
+    (vectorised: one 256-entry table per state byte, four lookups a state)."""
+    bits = np.arange(8, dtype=np.uint64)
+    idx = np.arange(256, dtype=np.uint64)
+    st = states.astype(np.uint64)
+    out = np.zeros(st.shape, dtype=np.uint64)
+    for byte in range(4):
+        col = cols[8 * byte:8 * byte + 8]
+        on = ((idx[:, None] >> bits[None, :]) & np.uint64(1)).astype(bool)
+        table = np.bitwise_xor.reduce(np.where(on, col[None, :], np.uint64(0)), axis=1)
+        out ^= table[((st >> np.uint64(8 * byte)) & np.uint64(255)).astype(np.intp)]
+    return out
+
+
+def _gf2_compose(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Column images of a(b(x))."""
+    return _gf2_apply(a, b)
+
+
+def _gf2_power(cols: np.ndarray, n: int) -> np.ndarray:
+    result = np.array([1 << b for b in range(32)], dtype=np.uint64)  # identity
+    base = cols.copy()
+    while n:
+        if n & 1:
+            result = _gf2_compose(base, result)
+        base = _gf2_compose(base, base)
+        n >>= 1
+    return result
+
+
+class Xorshift:
+    """The xorshift32 of the reference's benchmark (rust/src/main.rs:306-333):
+    next() is the state after one step; f() = next() as f32 / u32::MAX as f32;
+    f32s(n, sc, base) = base + (f()*2 - 1)*sc, every op in f32. The map is linear
+    over GF(2), so skip(n) jumps ahead by a matrix power, and n draws come out
+    in log2(n) vectorised doublings: states 1..m advanced by m steps are states
+    m+1..2m."""
+
+    _POW2: list = []  # column images of the step map raised to 2^k
+
+    def __init__(self, seed: int):
+        self.s = seed & 0xFFFFFFFF
+        if not Xorshift._POW2:
+            Xorshift._POW2.append(_gf2_matrix_of(_xs_step))
+            for _ in range(40):
+                m = Xorshift._POW2[-1]
+                Xorshift._POW2.append(_gf2_compose(m, m))
+
+    def skip(self, n: int) -> None:
+        st = np.array([self.s], np.uint64)
+        k = 0
+        while n:
+            if n & 1:
+                st = _gf2_apply(self._POW2[k], st)
+            n >>= 1
+            k += 1
+        self.s = int(st[0])
+
+    def next(self, n: int) -> np.ndarray:
+        """The next n outputs (u32), advancing the state."""
+        if n == 0:
+            return np.empty(0, dtype=np.uint32)
+        states = np.array([_xs_step(self.s)], dtype=np.uint64)
+        k = 0
+        while states.size < n:
+            states = np.concatenate([states, _gf2_apply(self._POW2[k], states)])
+            k += 1
+        out = states[:n].astype(np.uint32)
+        self.s = int(out[-1])
+        return out
+
+    def f32s(self, n: int, sc: float, base: float = 0.0) -> np.ndarray:
+        f = (self.next(n).astype(np.float32) / np.float32(4294967295.0)).astype(np.float32)
+        return (np.float32(base) + (f * np.float32(2.0) - np.float32(1.0)) * np.float32(sc)).astype(np.float32)
+
+
+# The attention cases of the reference's `bench --kernels` (rust/src/main.rs:544-560):
+# (Dh, S, window), batch 1, 8 query heads over 1 kv head, scale 1/16, q_pos = S-1.
+REFERENCE_BENCH_CASES = [(256, 512, 512), (256, 2048, 512), (512, 2048, 0), (256, 8192, 512), (512, 8192, 0)]
+
+
+def reference_bench_draws_before_attention() -> int:
+    """Xorshift(987654321) draws the reference's kernel benchmark makes before its
+    first attention case (rust/src/main.rs:493-543): each quantised weight draws
+    its packed bytes (one draw per 4 bytes; 8/bits fields a byte) then one scale
+    per row, each activation one draw per element, the f32 GEMV weight one per
+    element, in the order the cases are built."""
+    def qt(n, k, bits):
+        return (n * k // (8 // bits) + 3) // 4 + n
+    return (qt(262144, 1536, 2) + 1536            # lm_head 2b + x
+            + qt(6144, 1536, 4) + 1536            # mlp gate 4b + x
+            + 2 * qt(6144, 1536, 4) + 1536        # gate + up GeGLU + x
+            + qt(12288, 1536, 2) + 64 * 1536      # prefill gate 2b + x (M = 64)
+            + qt(1536, 6144, 2) + 6144            # mlp down 2b + x
+            + qt(2048, 1536, 4) + 1536            # q_proj 4b + x
+            + 8960 * 1536 + 1536)                 # gemv f32 weight + x
+
+
+def reference_bench_inputs():
+    """Yield ((Dh, S, window), q [1,8,Dh], k [S,1,Dh], v [S,1,Dh]) for the five
+    attention cases of rust/src/main.rs:544-560, drawn from Xorshift(987654321)
+    after the earlier cases' draws: U(-0.1, 0.1) in f32 (rust/src/main.rs:328-330)."""
+    r = Xorshift(987654321)
+    r.skip(reference_bench_draws_before_attention())
+    for dh, s, window in REFERENCE_BENCH_CASES:
+        q = r.f32s(8 * dh, 0.1).reshape(1, 8, dh)
+        k = r.f32s(s * dh, 0.1).reshape(s, 1, dh)
+        v = r.f32s(s * dh, 0.1).reshape(s, 1, dh)
+        yield (dh, s, window), q, k, v

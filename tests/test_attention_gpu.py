@@ -193,3 +193,16 @@ def test_zero_queries_is_a_no_op(ctx):
     k = np.zeros((10, 1, 256), np.float32)
     ctx.attention(0, 0, 0, 0, T=0, S=10, Hq=8, Hkv=1, Dh=256, Dv=256)
     ctx.sync()
+
+
+def test_reference_kernel_bench_cases(ctx):
+    """The five attention cases of the reference's `bench --kernels` (rust/src/main.rs:544-560)
+    on their own inputs (Xorshift(987654321) after the earlier cases' draws, U(-0.1, 0.1),
+    scale 1/16, q at position S-1): the inputs bench.py times them on."""
+    for (dh, S, window), q, k, v in synth.reference_bench_inputs():
+        label = f"reference bench Dh{dh} S{S} window{window}"
+        step(label)
+        qp, kp = np.array([S - 1], np.uint32), np.arange(S, dtype=np.uint32)
+        want = oracle.attention(q, k, v, qp, kp, scale=1.0 / 16.0, window=window)
+        got = g4a.attention_host(ctx, q, k, v, q_pos=qp, k_pos=kp, scale=1.0 / 16.0, window=window)
+        assert_parity(got, want, label)
