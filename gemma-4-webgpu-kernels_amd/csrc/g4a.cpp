@@ -131,6 +131,17 @@ struct g4a_ctx {
         float* dev;
     };
     std::vector<FreqTable> freq_tables;
+    // RoPE (sinf, cosf) tables of pos * freq[j], one per (theta, rotary_dim) seen,
+    // covering positions [0, rows); grown on demand. A grown table's old buffer is
+    // kept until the context ends: a captured graph may still read it.
+    struct SinCosTable {
+        float theta;
+        uint32_t rot;
+        uint32_t rows;
+        float2* dev;
+    };
+    std::vector<SinCosTable> sc_tables;
+    std::vector<void*> sc_retired;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     hipEvent_t ev_staging = nullptr;  // last use of the pinned staging buffer
     void* workspace = nullptr;
@@ -628,6 +639,8 @@ void g4a_destroy(g4a_ctx* ctx) {
     if (ctx->dummy) hipFree(ctx->dummy);
     if (ctx->pos_dev) hipFree(ctx->pos_dev);
     for (auto& ft : ctx->freq_tables) hipFree(ft.dev);
+    for (auto& st : ctx->sc_tables) hipFree(st.dev);
+    for (void* p : ctx->sc_retired) hipFree(p);
     if (ctx->pos_host) hipHostFree(ctx->pos_host);
     if (ctx->ev_start) hipEventDestroy(ctx->ev_start);
     if (ctx->ev_stop) hipEventDestroy(ctx->ev_stop);
@@ -1129,6 +1142,58 @@ int freq_table(g4a_ctx* ctx, float theta, uint32_t rot, const float** out) {
     return G4A_OK;
 }
 
+// Positions the (sinf, cosf) tables cover at most: 2^20 (1 GiB at rotary_dim 256).
+// Later positions take the device's sincosf (within a few ulps of libm).
+constexpr uint32_t SC_TABLE_MAX_ROWS = 1u << 20;
+
+// Device table of (sinf(ang), cosf(ang)), ang = (float)pos * freq[j] in f32, for
+// j < rot/2 and every position below `rows`: the reference's rope takes
+// ang.sin_cos() (rust/src/backend_cpu.rs:255-259), i.e. libm's sinf and cosf,
+// and the device's sincosf is an ulp away in places. Grown (at least doubled)
+// when a call's largest position is past it; the host computes the new rows.
+int sincos_table(g4a_ctx* ctx, float theta, uint32_t rot, const float* freq_host, uint32_t max_pos,
+                 const float2** out, uint32_t* rows_out) {
+    const uint32_t half = rot / 2;
+    g4a_ctx::SinCosTable* tab = nullptr;
+    for (auto& st : ctx->sc_tables)
+        if (st.rot == rot && memcmp(&st.theta, &theta, sizeof theta) == 0) tab = &st;
+    if (!tab) {
+        ctx->sc_tables.push_back({theta, rot, 0u, nullptr});
+        tab = &ctx->sc_tables.back();
+    }
+    const uint32_t want = std::min<uint64_t>(uint64_t(max_pos) + 1, SC_TABLE_MAX_ROWS);
+    if (want > tab->rows) {
+        if (ctx->capturing)
+            return fail(ctx, G4A_E_ARG, "the RoPE sin/cos table (theta %g, rotary_dim %u) grows to position %u on "
+                        "this call, which a graph capture cannot do: run the call once before capturing it",
+                        theta, rot, max_pos);
+        uint64_t rows = std::max<uint64_t>({uint64_t(want), 2 * uint64_t(tab->rows), 4096});
+        rows = std::min<uint64_t>((rows + 4095) / 4096 * 4096, SC_TABLE_MAX_ROWS);
+        float2* dev = nullptr;
+        if (hipMalloc(reinterpret_cast<void**>(&dev), rows * half * sizeof(float2)) != hipSuccess)
+            return fail(ctx, G4A_E_NOMEM, "RoPE sin/cos table of %llu positions", (unsigned long long)rows);
+        std::vector<float2> host((rows - tab->rows) * half);
+        for (uint64_t pos = tab->rows; pos < rows; ++pos)
+            for (uint32_t j = 0; j < half; ++j) {
+                const float ang = (float)pos * freq_host[j];
+                host[(pos - tab->rows) * half + j] = make_float2(sinf(ang), cosf(ang));
+            }
+        if (tab->rows)
+            HIP_TRY(ctx, hipMemcpyAsync(dev, tab->dev, size_t(tab->rows) * half * sizeof(float2),
+                                        hipMemcpyDeviceToDevice, ctx->stream));
+        HIP_TRY(ctx, hipMemcpyAsync(dev + size_t(tab->rows) * half, host.data(), host.size() * sizeof(float2),
+                                    hipMemcpyHostToDevice, ctx->stream));
+        // the copy from pageable memory must finish before `host` goes away
+        HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        if (tab->dev) ctx->sc_retired.push_back(tab->dev);
+        tab->dev = dev;
+        tab->rows = uint32_t(rows);
+    }
+    *out = tab->dev;
+    *rows_out = tab->rows;
+    return G4A_OK;
+}
+
 // One g4a_norm_rope launch over up to three row segments.
 int norm_rope_launch(g4a_ctx* ctx, G4aNormRopeSeg* segs, uint32_t nseg, uint32_t T, uint32_t Dh, uint32_t rot,
                      const uint32_t* positions, uint32_t pos0, float theta, float eps, uint32_t cache_row,
@@ -1155,15 +1220,29 @@ int norm_rope_launch(g4a_ctx* ctx, G4aNormRopeSeg* segs, uint32_t nseg, uint32_t
     p.ring_cap = ring_cap;
     p.pos0 = pos0;
     bool needs_rope = false;
-    for (uint32_t i = 0; i < nseg; ++i) needs_rope |= segs[i].rope != 0;
+    for (uint32_t i = 0; i < nseg; ++i) {
+        needs_rope |= segs[i].rope != 0;
+        p.any_norm |= segs[i].norm;
+    }
     if (needs_rope && rot) {
         if (int rc = freq_table(ctx, theta, rot, &p.freq)) return rc;
+        uint32_t max_pos = pos0 + (T ? T - 1 : 0);
         if (positions) {
             bool contig = true;
-            for (uint32_t i = 0; i < T; ++i) contig &= positions[i] == positions[0] + i;
+            max_pos = 0;
+            for (uint32_t i = 0; i < T; ++i) {
+                contig &= positions[i] == positions[0] + i;
+                max_pos = std::max(max_pos, positions[i]);
+            }
             if (contig) p.pos0 = positions[0];
             else if (int rc = upload_positions(ctx, positions, T, nullptr, 0, &p.pos, nullptr)) return rc;
+        } else if (uint64_t(pos0) + T > (uint64_t(1) << 32)) {
+            return fail(ctx, G4A_E_ARG, "positions pos0 %u + %u tokens pass 2^32", pos0, T);
         }
+        const float* freq_host = nullptr;
+        for (auto& ft : ctx->freq_tables)
+            if (ft.rot == rot && memcmp(&ft.theta, &theta, sizeof theta) == 0) freq_host = ft.host.data();
+        if (int rc = sincos_table(ctx, theta, rot, freq_host, max_pos, &p.sc, &p.sc_rows)) return rc;
     }
     const uint32_t blocks = uint32_t((rows + 3) / 4);
     return launch(ctx, ctx->norm_rope, dim3(blocks, 1, 1), dim3(256, 1, 1), p, "norm/rope rows", true);

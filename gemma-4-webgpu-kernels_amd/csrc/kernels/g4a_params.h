@@ -175,6 +175,9 @@ struct G4aNormRopeSeg {
 struct G4aNormRopeParams {
     G4aNormRopeSeg seg[3];
     const float* freq;      // [rotary_dim / 2]: theta^(-2j/rotary_dim), computed on the host
+    const float2* sc;       // [sc_rows][rotary_dim / 2]: (sinf, cosf) of pos * freq[j], computed on the host
+    uint32_t sc_rows;       // positions the table covers; later positions use sincosf on the device
+    uint32_t any_norm;      // some segment is normalised: the workgroup runs the sequential sums
     const uint32_t* pos;    // device [T], or null: position pos0 + t
     uint32_t pos0;
     uint32_t T, Dh, rotary_dim;

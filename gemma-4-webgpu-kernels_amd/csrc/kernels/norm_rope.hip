@@ -17,12 +17,23 @@
 // as the model applies them to one attention block (rust/src/model.rs:256-281).
 //
 // One wave per row (token, head) of Dh values; lane l owns dims 4l..4l+3
-// (+256, +512, +768). The sum of squares reduces across the wave (a different
-// order from the reference's sequential sum: a few ulps in inv). Every other
-// operation is the reference's, separately rounded (this file is built with
-// -ffp-contract=off). The frequencies come from the host (libm powf, as Rust's
-// f32::powf on the same platform): a one-ulp difference in freq would move the
-// angle by pos * ulp, i.e. by ~2e-3 rad at position 32768.
+// (+256, +512, +768). Every operation is the reference's, separately rounded
+// (this file is built with -ffp-contract=off), so the rows come out
+// bit-identical to the CPU backend's:
+//   - the sum of squares runs d = 0..Dh-1 in order, as the reference's
+//     iterator sum does: the rows' squares go to LDS and lane r of wave 0 adds
+//     row r's in sequence (one dependent chain of Dh adds per row, the rows of
+//     a workgroup side by side). A tree reduction over the wave moves inv by
+//     an ulp now and then, which scores of ~90 turn into ~5e-5 of attention
+//     output;
+//   - sin and cos of the angle come from a table the host fills with libm's
+//     sinf / cosf of pos * freq (Rust's f32::sin_cos on the same platform)
+//     for positions below the table's size; the device's sincosf differs from
+//     libm by an ulp in places. Past the table (positions the host did not
+//     tabulate) the kernel falls back to sincosf of pos * freq;
+//   - the frequencies come from the host too (libm powf, as Rust's f32::powf):
+//     a one-ulp difference in freq would move the angle by pos * ulp, i.e. by
+//     ~2e-3 rad at position 32768.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -34,41 +45,76 @@ namespace {
 constexpr int NR_WAVES = 4;    // rows per workgroup
 constexpr int NR_MAXE = 4;     // float4 groups per lane: Dh <= 1024
 
-__device__ __forceinline__ float nr_wave_sum(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
-    return x;
-}
+// Row stride of the LDS stage: 4 floats of padding put the rows of the
+// sequential sums (lane r reads row r) on different banks.
+constexpr int NR_STRIDE = NR_MAXE * 256 + 4;
 
 __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
-    __shared__ __attribute__((aligned(16))) float stage[NR_WAVES][NR_MAXE * 256];
+    __shared__ __attribute__((aligned(16))) float stage[NR_WAVES][NR_STRIDE];
+    __shared__ float row_ss[NR_WAVES];
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
     const uint32_t row = blockIdx.x * NR_WAVES + w;
-    if (row >= p.total_rows) return;
+    // no early return: every wave reaches the workgroup barriers of the norm
+    bool live = row < p.total_rows;
     // segment of this row (rows are segment-major: seg s covers T * heads_s rows)
     int si = 0;
-    uint32_t r = row;
+    uint32_t r = live ? row : 0u;
     while (si + 1 < (int)p.nseg && r >= p.T * p.seg[si].heads) {
         r -= p.T * p.seg[si].heads;
         ++si;
     }
     const G4aNormRopeSeg& S = p.seg[si];
     const uint32_t t = r / S.heads, h = r % S.heads;
-    if (t < S.first_t) return;  // its ring slot is taken by a later token of this call
+    live = live && t >= S.first_t;  // else its ring slot is taken by a later token of this call
     const uint32_t Dh = p.Dh;
     const float* __restrict__ xr = S.x + ((size_t)t * S.heads + h) * Dh;
     float4 v[NR_MAXE];
 #pragma unroll
     for (int e = 0; e < NR_MAXE; ++e) {
         const uint32_t d = 4 * lane + 256 * e;
-        v[e] = d < Dh ? *reinterpret_cast<const float4*>(xr + d) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[e] = live && d < Dh ? *reinterpret_cast<const float4*>(xr + d) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    if (S.norm) {
-        float ss = 0.0f;
+    const bool norm_row = live && S.norm;
+    if (p.any_norm) {
+        // squares (each rounded, as v * v) into the stage, then lane r of wave 0 sums row r
+        // in order: ss = ((x0^2 + x1^2) + x2^2) + ...
+        if (norm_row) {
 #pragma unroll
-        for (int e = 0; e < NR_MAXE; ++e) ss += v[e].x * v[e].x + v[e].y * v[e].y + v[e].z * v[e].z + v[e].w * v[e].w;
-        ss = nr_wave_sum(ss);
+            for (int e = 0; e < NR_MAXE; ++e) {
+                const uint32_t d = 4 * lane + 256 * e;
+                if (d < Dh) {
+                    const float4 sq = make_float4(v[e].x * v[e].x, v[e].y * v[e].y, v[e].z * v[e].z, v[e].w * v[e].w);
+                    *reinterpret_cast<float4*>(&stage[w][d]) = sq;
+                }
+            }
+        }
+        __syncthreads();
+        if (w == 0 && lane < NR_WAVES) {
+            const float* const sr = stage[lane];
+            float ss = 0.0f;
+            uint32_t d = 0;
+            for (; d + 16 <= Dh; d += 16) {
+                const float4 a = *reinterpret_cast<const float4*>(sr + d);
+                const float4 b = *reinterpret_cast<const float4*>(sr + d + 4);
+                const float4 c = *reinterpret_cast<const float4*>(sr + d + 8);
+                const float4 e = *reinterpret_cast<const float4*>(sr + d + 12);
+                ss = ss + a.x; ss = ss + a.y; ss = ss + a.z; ss = ss + a.w;
+                ss = ss + b.x; ss = ss + b.y; ss = ss + b.z; ss = ss + b.w;
+                ss = ss + c.x; ss = ss + c.y; ss = ss + c.z; ss = ss + c.w;
+                ss = ss + e.x; ss = ss + e.y; ss = ss + e.z; ss = ss + e.w;
+            }
+            for (; d < Dh; d += 4) {  // head_dim % 16 != 0
+                const float4 a = *reinterpret_cast<const float4*>(sr + d);
+                ss = ss + a.x; ss = ss + a.y; ss = ss + a.z; ss = ss + a.w;
+            }
+            row_ss[lane] = ss;
+        }
+        __syncthreads();
+    }
+    if (!live) return;
+    if (S.norm) {
+        const float ss = row_ss[w];
         const float inv = 1.0f / sqrtf(ss / (float)Dh + p.eps);
 #pragma unroll
         for (int e = 0; e < NR_MAXE; ++e) {
@@ -97,7 +143,10 @@ __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
         __builtin_amdgcn_wave_barrier();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const uint32_t rot = p.rotary_dim, half = rot / 2;
-        const float pos = (float)(p.pos ? p.pos[t] : p.pos0 + t);
+        const uint32_t ipos = p.pos ? p.pos[t] : p.pos0 + t;
+        const float pos = (float)ipos;
+        const bool tab = ipos < p.sc_rows;
+        const float2* const sc_row = p.sc + (size_t)(tab ? ipos : 0u) * half;
 #pragma unroll
         for (int e = 0; e < NR_MAXE; ++e) {
             const uint32_t d0 = 4 * lane + 256 * e;
@@ -109,9 +158,14 @@ __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
                 if (d >= rot) continue;  // pass-through tail
                 const uint32_t j = d < half ? d : d - half;
                 const float a = ys[j], b = ys[j + half];
-                const float ang = pos * p.freq[j];
                 float sn, cs;
-                sincosf(ang, &sn, &cs);
+                if (tab) {
+                    const float2 v2 = sc_row[j];
+                    sn = v2.x;
+                    cs = v2.y;
+                } else {
+                    sincosf(pos * p.freq[j], &sn, &cs);
+                }
                 o[i] = d < half ? a * cs - b * sn : b * cs + a * sn;
             }
             v[e] = make_float4(o[0], o[1], o[2], o[3]);

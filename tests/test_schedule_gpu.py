@@ -107,12 +107,11 @@ def test_35_layer_token_batch_and_graph_replay(ctx, schedule):
 def test_shared_layer_producer_then_attention(ctx, schedule, layer):
     # a layer of the shared region (19: global, reads 14; 15: sliding, reads 13): the producer
     # normalises and rotates q only (k = v = NULL, rust/src/model.rs:256-261 then :282-285), and
-    # attention reads the source layer's cache, which the producer leaves untouched. Each op is
-    # held to the bar on its own inputs: q against the oracle's head_norm_rope (the device's
-    # sincosf and the reordered sum of squares leave q a few ulps from libm's), attention on that
-    # q against the oracle's attention on the same q (scores of ~90 amplify a q difference of an
-    # ulp to ~1e-5, so comparing with attention over the oracle's q would measure the producer's
-    # ulps, not the attention)
+    # attention reads the source layer's cache, which the producer leaves untouched. The chain is
+    # held to the bar against the CPU chain: attention over the device's q against the oracle's
+    # attention over the oracle's head_norm_rope q. Scores of ~90 turn an ulp of q into ~1e-5 of
+    # output, so this needs q bit-identical: the sum of squares in the reference's order and
+    # libm's sin/cos (the device's tree sum alone moved layer 19 by 5e-5).
     layers, caches, _ = schedule
     L = layers[layer]
     assert L.src != layer
@@ -137,8 +136,10 @@ def test_shared_layer_producer_then_attention(ctx, schedule, layer):
     finally:
         for d in (dq, dw, dk, dv, qo, out):
             d.free()
-    assert_parity(got_q, q_ref, f"layer {layer} q")
-    want = oracle.attention(got_q, k_lin, v_lin, pos, c.k_pos,
+    nq = int((got_q != q_ref).sum())
+    print(f"  layer {layer} q: {nq} of {q_ref.size} values differ from the oracle's head_norm_rope", flush=True)
+    assert nq == 0, f"layer {layer}: q differs from the oracle's in {nq} values"
+    want = oracle.attention(q_ref, k_lin, v_lin, pos, c.k_pos,
                             window=0 if L.is_global else synth.E2B_WINDOW).reshape(1, -1)
-    mx, mean = assert_parity(got, want, f"layer {layer} attention")
+    mx, mean = assert_parity(got, want, f"layer {layer} attention vs the oracle chain")
     print(f"  layer {layer}: max-abs {mx:.3e} mean-abs {mean:.3e}", flush=True)
