@@ -38,6 +38,7 @@ HSACO = OUT / "g4a_kernels.hsaco"
 LIBG4A = OUT / "libg4a.so"
 LIBBACKEND = OUT / "libg4a_backend.so"
 TEST_BACKEND = REPO / "tests" / "cpp" / "_build" / "test_backend"
+TEST_MODEL = REPO / "tests" / "cpp" / "_build" / "test_model"
 LIBORACLE = ORACLE_OUT / "liboracle.so"
 
 
@@ -87,6 +88,12 @@ def build_backend(verbose: bool = False) -> Path:
           oracle_obj, linear_obj, "-o", tmp, f"-L{OUT}", "-lg4a_backend", "-lg4a", "-Wl,-rpath,$ORIGIN/../../../gemma-4-webgpu-kernels_amd/_build", "-lpthread", "-lm"],
          verbose)
     tmp.replace(TEST_BACKEND)
+    # the whole-model driver: Gemma4Model's composition over HipBackend and over the oracle
+    tmp = TEST_MODEL.with_suffix(".tmp")
+    _run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", f"-I{INCLUDE}", f"-I{CSRC}",
+          REPO / "tests" / "cpp" / "test_model.cpp", oracle_obj, linear_obj, "-o", tmp, f"-L{OUT}", "-lg4a_backend",
+          "-lg4a", "-Wl,-rpath,$ORIGIN/../../../gemma-4-webgpu-kernels_amd/_build", "-lpthread", "-lm"], verbose)
+    tmp.replace(TEST_MODEL)
     return LIBBACKEND
 
 
