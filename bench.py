@@ -308,7 +308,7 @@ def schedule_with_projection(ctx, steps, warmup):
     the same 35 layers: g4a_attention + g4a_linear_q (attention, LSE combine,
     projection: three launches per layer; what g4a_attention_linear_q runs on
     a default context), and g4a_attention_linear_q on a context created with
-    G4A_FUSE_PROJECTION=1 (a sliding layer's 16-split step merges its partials
+    the fuse_projection option (a sliding layer's 16-split step merges its partials
     inside the projection: two launches). Each form is captured once as a HIP
     graph and replayed, so both figures are free of host dispatch time; the
     two forms' projections are checked bit-identical."""
@@ -329,15 +329,7 @@ def schedule_with_projection(ctx, steps, warmup):
                       dict(T=1, S=S, Hq=HQ, Hkv=1, Dh=L.Dh, Dv=L.Dh, q_pos0=S - 1, k_pos0=0,
                            window=0 if L.is_global else synth.E2B_WINDOW, ring_cap=host_caches[L.src].ring_cap)))
 
-    old = os.environ.get("G4A_FUSE_PROJECTION")
-    os.environ["G4A_FUSE_PROJECTION"] = "1"
-    try:
-        fctx = g4a.Context(0)
-    finally:
-        if old is None:
-            del os.environ["G4A_FUSE_PROJECTION"]
-        else:
-            os.environ["G4A_FUSE_PROJECTION"] = old
+    fctx = g4a.Context(0, options={"fuse_projection": 1})
     ctxs = {"separate": ctx, "fused": fctx}
 
     def enqueue(form):

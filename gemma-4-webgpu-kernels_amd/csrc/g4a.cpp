@@ -97,8 +97,8 @@ struct g4a_ctx {
     // batched decode tuning (G4A_BATCH_KERNEL=short|wave, G4A_BATCH_KEYS_PER_SPLIT=n): for comparisons
     int batch_kernel = 0;  // 0 auto, 1 short, 2 streaming
     uint32_t batch_kps = 0;  // streaming split size; 0 auto
-    bool short_decode = true;  // G4A_DECODE_SHORT=0 turns the short-context kernel off (for comparisons)
-    uint32_t short_ds = 4;     // G4A_DECODE_SHORT_DS=1|2|4: most workgroups per short split (for comparisons)
+    bool short_decode = true;  // g4a_options::short_decode
+    uint32_t short_ds = 4;     // g4a_options::short_max_wgs: most workgroups per short split
     hipFunction_t generic = nullptr;
     hipFunction_t prefill[2] = {nullptr, nullptr};                          // [dh512]
     hipFunction_t split_kv = nullptr;  // K/V pre-split for the head_dim 256 prefill
@@ -146,6 +146,8 @@ struct g4a_ctx {
     hipEvent_t ev_staging = nullptr;  // last use of the pinned staging buffer
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
+    size_t prev_workspace_bytes = 0;  // the size of the buffer the last growth replaced
+    int query_depth = 0;              // > 0 inside a query entry point (g4a_attention_plan)
     void* scratch = nullptr;  // this device's static scratch array (the allocation-free entry point)
     hipFunction_t prefill_merge = nullptr;  // merge of the split hd512 prefill blocks
     float* dummy = nullptr;  // 4 KiB of zeros: the load target of idle decode tiles
@@ -176,8 +178,9 @@ int fail(g4a_ctx* ctx, int code, const char* fmt, ...) {
     if (ctx) {
         ctx->err = buf;
         // a refused call inside a capture leaves a graph without it: remembered, so
-        // g4a_capture_end reports it instead of returning that graph
-        if (ctx->capturing && ctx->capture_code == 0) {
+        // g4a_capture_end reports it instead of returning that graph (a failing
+        // query, which enqueues nothing, leaves the capture alone)
+        if (ctx->capturing && ctx->capture_code == 0 && ctx->query_depth == 0) {
             ctx->capture_code = code;
             ctx->capture_msg = buf;
         }
@@ -243,6 +246,7 @@ int ensure_workspace(g4a_ctx* ctx, size_t bytes) {
             HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
             HIP_TRY(ctx, hipFree(ctx->workspace));
         }
+        ctx->prev_workspace_bytes = ctx->workspace_bytes;
         ctx->workspace = nullptr;
         ctx->workspace_bytes = 0;
     }
@@ -251,7 +255,8 @@ int ensure_workspace(g4a_ctx* ctx, size_t bytes) {
         for (void* p : ctx->book->retired) HIP_TRY(ctx, hipFree(p));
         ctx->book->retired.clear();
     }
-    size_t want = std::max<size_t>(bytes, size_t(8) << 20);
+    // geometric growth: a run of slightly larger calls retires a bounded number of buffers
+    size_t want = std::max<size_t>({bytes, 2 * ctx->prev_workspace_bytes, size_t(8) << 20});
     hipError_t e = hipMalloc(&ctx->workspace, want);
     if (e != hipSuccess) return fail(ctx, G4A_E_NOMEM, "workspace of %zu bytes: %s", want, hipGetErrorString(e));
     ctx->workspace_bytes = want;
@@ -482,9 +487,38 @@ int analyse(g4a_ctx* ctx, const g4a_attn_args* a, Analysis* an, bool check_point
 
 extern "C" {
 
+void g4a_default_options(g4a_options* o) {
+    if (!o) return;
+    *o = g4a_options{};
+    o->size = sizeof(g4a_options);
+    o->short_decode = 1;
+    o->short_max_wgs = 4;
+    o->batch_kernel = 0;
+    o->batch_keys_per_split = 0;
+    o->linear_i8 = -1;
+    o->fuse_projection = 0;
+}
+
 int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
+    return g4a_create_with(device, hsaco_path, nullptr, out);
+}
+
+int g4a_create_with(int device, const char* hsaco_path, const g4a_options* opts, g4a_ctx** out) {
     if (!out) return fail(nullptr, G4A_E_ARG, "null out");
     *out = nullptr;
+    g4a_options o;
+    g4a_default_options(&o);
+    if (opts) {
+        if (opts->size != sizeof(g4a_options))
+            return fail(nullptr, G4A_E_ARG, "g4a_options of %u bytes; this library's has %zu", opts->size,
+                        sizeof(g4a_options));
+        o = *opts;
+        if ((o.short_decode != 0 && o.short_decode != 1) ||
+            (o.short_max_wgs != 1 && o.short_max_wgs != 2 && o.short_max_wgs != 4) || o.batch_kernel < 0 ||
+            o.batch_kernel > 2 || o.linear_i8 < -1 || o.linear_i8 > 1 ||
+            (o.fuse_projection != 0 && o.fuse_projection != 1))
+            return fail(nullptr, G4A_E_ARG, "g4a_options: an option is out of range");
+    }
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
     if (e != hipSuccess || n == 0) return fail(nullptr, G4A_E_HIP, "no HIP device (%s)", hipGetErrorString(e));
@@ -512,7 +546,12 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
         return bail(G4A_E_UNSUPPORTED);
     }
     ctx->cu_count = prop.multiProcessorCount;
-    if (int rc = scratch_setup(ctx)) return bail(rc);
+    ctx->short_decode = o.short_decode != 0;
+    ctx->short_ds = o.short_max_wgs;
+    ctx->batch_kernel = o.batch_kernel;
+    ctx->batch_kps = o.batch_keys_per_split;
+    ctx->linear_i8_use = o.linear_i8;
+    ctx->fuse_projection = o.fuse_projection != 0;
     std::string path = hsaco_path ? std::string(hsaco_path) : default_hsaco_path();
     e = hipModuleLoad(&ctx->module, path.c_str());
     if (e != hipSuccess) {
@@ -532,11 +571,6 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->decode_short2[1], "g4a_decode_short2_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_short4[0], "g4a_decode_short4_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_short4[1], "g4a_decode_short4_d512")) return bail(rc);
-    if (const char* env = getenv("G4A_DECODE_SHORT")) ctx->short_decode = atoi(env) != 0;
-    if (const char* env = getenv("G4A_DECODE_SHORT_DS")) {
-        const int ds = atoi(env);
-        ctx->short_ds = ds >= 4 ? 4u : ds >= 2 ? 2u : 1u;
-    }
     if (int rc = get_fn(ctx, &ctx->decode_batch[0], "g4a_decode_short_batch_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_batch[1], "g4a_decode_short_batch_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_wave_batch[0], "g4a_decode_wave_batch_d256")) return bail(rc);
@@ -549,9 +583,6 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
     if (int rc = get_fn(ctx, &ctx->combine_rows[1], "g4a_combine_rows_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->combine_rows_batch[0], "g4a_combine_rows_batch_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->combine_rows_batch[1], "g4a_combine_rows_batch_d512")) return bail(rc);
-    if (const char* env = getenv("G4A_BATCH_KERNEL"))
-        ctx->batch_kernel = !strcmp(env, "short") ? 1 : !strcmp(env, "wave") ? 2 : 0;
-    if (const char* env = getenv("G4A_BATCH_KEYS_PER_SPLIT")) ctx->batch_kps = uint32_t(strtoul(env, nullptr, 10));
     if (int rc = get_fn(ctx, &ctx->combine[0], "g4a_combine_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->combine[1], "g4a_combine_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->generic, "g4a_generic_attention")) return bail(rc);
@@ -590,13 +621,11 @@ int g4a_create(int device, const char* hsaco_path, g4a_ctx** out) {
                 snprintf(name, sizeof name, "g4a_linear_q_i8_b%d_m%d", bits[b], m + 1);
                 if (int rc = get_fn(ctx, &ctx->linear_i8[b][m], name)) return bail(rc);
             }
-        if (const char* env = getenv("G4A_LINEAR_I8")) ctx->linear_i8_use = atoi(env) != 0 ? 1 : 0;
         for (int b = 0; b < 3; ++b) {
             char name[64];
             snprintf(name, sizeof name, "g4a_linear_q_b%d_m1_r2_mode3", bits[b]);
             if (int rc = get_fn(ctx, &ctx->linear_fused[b], name)) return bail(rc);
         }
-        if (const char* env = getenv("G4A_FUSE_PROJECTION")) ctx->fuse_projection = atoi(env) != 0;
         if (int rc = get_fn(ctx, &ctx->embed_q, "g4a_embed_rows_q")) return bail(rc);
         static const char* f32_words[3] = {"g4a_linear_q_b32_m1_r2_mode0", "g4a_linear_q_b32_m1_r8_mode0",
                                            "g4a_linear_q_b32_m4_r4_mode0"};
@@ -709,6 +738,12 @@ int g4a_sync(g4a_ctx* ctx) {
 }
 
 int g4a_attention_plan(g4a_ctx* ctx, const g4a_attn_args* a, g4a_attn_plan* plan) {
+    // a query: its failures do not discard an open graph capture
+    struct Query {
+        g4a_ctx* c;
+        explicit Query(g4a_ctx* x) : c(x) { if (c) ++c->query_depth; }
+        ~Query() { if (c) --c->query_depth; }
+    } q(ctx);
     if (!plan) return fail(ctx, G4A_E_ARG, "null plan");
     Analysis an;
     if (int rc = analyse(ctx, a, &an, false)) return rc;
@@ -924,6 +959,13 @@ int g4a_attention(g4a_ctx* ctx, const g4a_attn_args* a) {
 
 int g4a_attention_noalloc(g4a_ctx* ctx, const g4a_attn_args* a) {
     if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    // the static scratch array is looked up (and so loaded onto the GPU) by the first
+    // no-alloc call on a device, not by g4a_create: a process that never calls this
+    // entry point does not hold it
+    if (!ctx->scratch) {
+        HIP_TRY(ctx, hipSetDevice(ctx->device));
+        if (int rc = scratch_setup(ctx)) return rc;
+    }
     Analysis an;
     if (int rc = analyse(ctx, a, &an, true)) return rc;
     return attention_run(ctx, a, an, true, /*noalloc=*/true);
@@ -1298,6 +1340,65 @@ int check_qweight(g4a_ctx* ctx, const g4a_qweight* w, const char* what) {
 }
 
 // y[M, N] = epilogue(x . W^T); mode 0 plain, 1 GeGLU with w2, 2 gelu times b's columns.
+// Which projection kernel linear_q_launch runs for a call: the one place that
+// decides it (g4a_attention_linear_q asks it too, so the projection it merges a
+// decode step's partials into is the one the plain call would run).
+struct LinearChoice {
+    enum Kind { MFMA, I8, ELEM, WORDS } kind = ELEM;
+    int wide = 0;       // MFMA: 128-row tiles
+    int variant = 0;    // WORDS: (MT, RU) = (1, 2), (1, 8), (4, 4)
+    int MT = 1, RU = 2;
+    bool half = false;  // WORDS: 2-bit rows of an odd multiple of 32 words, two rows per wave
+    uint64_t kpad = 0;  // WORDS: activation floats per row in LDS
+};
+
+LinearChoice choose_linear(const g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qweight* w2, const float* x,
+                           uint32_t M) {
+    LinearChoice c;
+    const uint32_t row_bytes = w->signed_i8 ? w->K : w->K / (8 / w->bits);
+    const uint32_t scale_stride = (w->K + w->group_size - 1) / w->group_size;
+    const uintptr_t qa = reinterpret_cast<uintptr_t>(w->qbytes);
+    const uintptr_t qa2 = mode == 1 ? reinterpret_cast<uintptr_t>(w2->qbytes) : 0;
+    const bool aligned = (qa & 3) == 0 && (qa2 & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    const bool aligned8 = aligned && (qa & 7) == 0 && (qa2 & 7) == 0;
+    const uint64_t cus = uint64_t(std::max(ctx->cu_count, 1));
+    if (M >= LINEAR_MFMA_MIN_M && w->K % 64 == 0 && scale_stride == 1 && aligned8) {
+        c.kind = LinearChoice::MFMA;
+        const uint64_t tiles128 = uint64_t((w->N + 127) / 128) * ((M + 63) / 64);
+        c.wide = tiles128 >= 2 * cus ? 1 : 0;
+        return c;
+    }
+    const uint64_t weight_bytes = uint64_t(w->N) * row_bytes;
+    const bool i8_ok = mode == 0 && M <= 2 && scale_stride == 1 && row_bytes % G4A_LI8_UNIT_BYTES == 0 &&
+                       w->K % 64 == 0 && uint64_t(w->K / 64) * 1024 <= LINEAR_LDS_BYTES && (qa & 15) == 0;
+    if (i8_ok && (ctx->linear_i8_use == 1 || (ctx->linear_i8_use < 0 && weight_bytes >= LINEAR_I8_MIN_BYTES))) {
+        c.kind = LinearChoice::I8;
+        return c;
+    }
+    const uint64_t vpw = 32 / w->bits, words_per_row = uint64_t(w->K) * w->bits / 32;
+    c.kpad = (words_per_row + 63) / 64 * 64 * vpw;
+    const bool words = (uint64_t(w->K) * w->bits) % 32 == 0 && scale_stride == 1 && aligned &&
+                       c.kpad * 4 <= LINEAR_LDS_BYTES;
+    if (!words) {
+        c.kind = LinearChoice::ELEM;
+        return c;
+    }
+    c.kind = LinearChoice::WORDS;
+    // 4 activation rows per workgroup when they fit its LDS share, else 1; 8 weight
+    // rows in flight per wave for tall weights, 2 for short ones (more waves)
+    if (M >= 2 && 4 * c.kpad * 4 <= LINEAR_LDS_BYTES) {
+        c.variant = 2, c.MT = 4, c.RU = 4;
+    } else if (w->N >= cus * 64) {
+        c.variant = 1, c.MT = 1, c.RU = 8;
+    } else {
+        c.variant = 0, c.MT = 1, c.RU = 2;
+    }
+    // 2-bit rows of an odd multiple of 32 words (K = 1536 is 96 words): half-waves
+    // walk two rows at once, so no lane idles on the row's last word step
+    c.half = c.MT == 1 && w->bits == 2 && words_per_row % 64 == 32;
+    return c;
+}
+
 int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qweight* w2, const float* x,
                     const float* b, uint32_t b_stride, uint32_t b_off, float* y, uint32_t M) {
     if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
@@ -1331,21 +1432,16 @@ int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qwei
     p.row_bytes = w->signed_i8 ? w->K : w->K / (8 / w->bits);
     p.group_size = w->group_size;
     p.scale_stride = (w->K + w->group_size - 1) / w->group_size;
-    const bool aligned = (reinterpret_cast<uintptr_t>(w->qbytes) & 3) == 0 &&
-                         (mode != 1 || (reinterpret_cast<uintptr_t>(w2->qbytes) & 3) == 0) &&
-                         (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-    const bool aligned8 = aligned && (reinterpret_cast<uintptr_t>(w->qbytes) & 7) == 0 &&
-                          (mode != 1 || (reinterpret_cast<uintptr_t>(w2->qbytes) & 7) == 0);
+    const LinearChoice ch = choose_linear(ctx, mode, w, w2, x, M);
     // sub-byte fields are offset binary: flipping each field's top bit makes it two's complement
     p.xm = w->signed_i8 ? 0u : w->bits == 4 ? 0x88888888u : w->bits == 2 ? 0xAAAAAAAAu : 0x80808080u;
     const int bi = w->bits == 2 ? 0 : w->bits == 4 ? 1 : 2;
-    if (M >= LINEAR_MFMA_MIN_M && w->K % 64 == 0 && p.scale_stride == 1 && aligned8) {
+    if (ch.kind == LinearChoice::MFMA) {
         // 64 activation rows x 128 weight rows per workgroup on the matrix cores,
         // or x 64 rows when the larger tile would leave fewer than 2 workgroups per CU
         p.wb = static_cast<const uint8_t*>(w->qbytes);
         p.wb2 = mode == 1 ? static_cast<const uint8_t*>(w2->qbytes) : nullptr;
-        const uint64_t tiles128 = uint64_t((w->N + 127) / 128) * ((M + 63) / 64);
-        const int wide = tiles128 >= 2 * uint64_t(std::max(ctx->cu_count, 1)) ? 1 : 0;
+        const int wide = ch.wide;
         const uint32_t gx = wide ? (w->N + 127) / 128 : (w->N + 63) / 64;
         for (uint32_t m0 = 0; m0 < M; m0 += 65535u * 64) {
             G4aLinearParams q = p;
@@ -1360,11 +1456,7 @@ int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qwei
         return G4A_OK;
     }
     // M <= 2, large weights: int8 matrix cores with x cut into exact digits (mode 0)
-    const uint64_t weight_bytes = uint64_t(w->N) * p.row_bytes;
-    const bool i8_ok = mode == 0 && M <= 2 && p.scale_stride == 1 && p.row_bytes % G4A_LI8_UNIT_BYTES == 0 &&
-                       w->K % 64 == 0 && uint64_t(w->K / 64) * 1024 <= LINEAR_LDS_BYTES &&
-                       (reinterpret_cast<uintptr_t>(w->qbytes) & 15) == 0;
-    if (i8_ok && (ctx->linear_i8_use == 1 || (ctx->linear_i8_use < 0 && weight_bytes >= LINEAR_I8_MIN_BYTES))) {
+    if (ch.kind == LinearChoice::I8) {
         p.wb = static_cast<const uint8_t*>(w->qbytes);
         // chunks of 32 weight rows, one per wave at a time; 16 waves per CU (four
         // workgroups, whose x digit staging then overlaps the others' streams)
@@ -1376,10 +1468,8 @@ int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qwei
     }
     // the word kernel's activation rows, zero-padded to whole wave strides of words
     const uint64_t vpw = 32 / w->bits, words_per_row = uint64_t(w->K) * w->bits / 32;
-    const uint64_t kpad = (words_per_row + 63) / 64 * 64 * vpw;
-    const bool words = (uint64_t(w->K) * w->bits) % 32 == 0 && p.scale_stride == 1 && aligned &&
-                       kpad * 4 <= LINEAR_LDS_BYTES;
-    if (!words) {
+    const uint64_t kpad = ch.kpad;
+    if (ch.kind == LinearChoice::ELEM) {
         // one thread per output in the CPU's order: any K, grouped scales
         p.wb = static_cast<const uint8_t*>(w->qbytes);
         p.wb2 = mode == 1 ? static_cast<const uint8_t*>(w2->qbytes) : nullptr;
@@ -1399,16 +1489,7 @@ int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qwei
     p.w2 = mode == 1 ? static_cast<const uint32_t*>(w2->qbytes) : nullptr;
     p.W = uint32_t(words_per_row);
     const uint64_t cus = uint64_t(std::max(ctx->cu_count, 1));
-    // 4 activation rows per workgroup when they fit its LDS share, else 1; 8 weight
-    // rows in flight per wave for tall weights, 2 for short ones (more waves)
-    int variant, MT, RU;
-    if (M >= 2 && 4 * kpad * 4 <= LINEAR_LDS_BYTES) {
-        variant = 2, MT = 4, RU = 4;
-    } else if (w->N >= cus * 64) {
-        variant = 1, MT = 1, RU = 8;
-    } else {
-        variant = 0, MT = 1, RU = 2;
-    }
+    const int variant = ch.variant, MT = ch.MT, RU = ch.RU;
     // about 16 waves per CU over the rows (four 4-wave workgroups): weight
     // streaming needs many loads in flight
     const uint64_t target = cus * 16;
@@ -1416,9 +1497,7 @@ int linear_q_launch(g4a_ctx* ctx, int mode, const g4a_qweight* w, const g4a_qwei
     rpw = std::max<uint64_t>(RU, (rpw + RU - 1) / RU * RU);
     p.rows_per_wave = uint32_t(rpw);
     const uint32_t gx = uint32_t((w->N + 4 * rpw - 1) / (4 * rpw));
-    // 2-bit rows of an odd multiple of 32 words (K = 1536 is 96 words): half-waves
-    // walk two rows at once, so no lane idles on the row's last word step
-    const bool half = MT == 1 && w->bits == 2 && words_per_row % 64 == 32;
+    const bool half = ch.half;
     hipFunction_t fn = half ? ctx->linear_half[variant][mode] : ctx->linear_words[bi][variant][mode];
     const unsigned lds = unsigned(MT * (half ? (words_per_row + 31) / 32 * 32 * vpw : kpad) * 4);
     for (uint32_t m0 = 0; m0 < M; m0 += 65535u * MT) {
@@ -1457,21 +1536,9 @@ namespace {
 // Whether linear_q_launch takes (w, M = 1, mode 0) to the word kernel's
 // (MT, RU) = (1, 2) form with 64 lanes per row: the form whose mode 3 merges a
 // decode step's split partials while staging x, with the same sums.
-bool projection_on_short_words(const g4a_ctx* ctx, const g4a_qweight* w) {
-    const uint32_t row_bytes = w->signed_i8 ? w->K : w->K / (8 / w->bits);
-    const uint32_t scale_stride = (w->K + w->group_size - 1) / w->group_size;
-    const uintptr_t qa = reinterpret_cast<uintptr_t>(w->qbytes);
-    const bool i8_ok = scale_stride == 1 && row_bytes % G4A_LI8_UNIT_BYTES == 0 && w->K % 64 == 0 &&
-                       uint64_t(w->K / 64) * 1024 <= LINEAR_LDS_BYTES && (qa & 15) == 0;
-    const uint64_t weight_bytes = uint64_t(w->N) * row_bytes;
-    if (i8_ok && (ctx->linear_i8_use == 1 || (ctx->linear_i8_use < 0 && weight_bytes >= LINEAR_I8_MIN_BYTES)))
-        return false;
-    const uint64_t vpw = 32 / w->bits, words_per_row = uint64_t(w->K) * w->bits / 32;
-    const uint64_t kpad = (words_per_row + 63) / 64 * 64 * vpw;
-    if ((uint64_t(w->K) * w->bits) % 32 != 0 || scale_stride != 1 || (qa & 3) != 0 || kpad * 4 > LINEAR_LDS_BYTES)
-        return false;
-    if (uint64_t(w->N) >= uint64_t(std::max(ctx->cu_count, 1)) * 64) return false;  // the (1, 8) form
-    return !(w->bits == 2 && words_per_row % 64 == 32);                            // 32 lanes per row
+bool projection_on_short_words(const g4a_ctx* ctx, const g4a_qweight* w, const float* x) {
+    const LinearChoice c = choose_linear(ctx, 0, w, nullptr, x, 1);
+    return c.kind == LinearChoice::WORDS && c.variant == 0 && !c.half;
 }
 
 }  // namespace
@@ -1495,7 +1562,7 @@ int g4a_attention_linear_q(g4a_ctx* ctx, const g4a_attn_args* a, const g4a_qweig
     const bool fuse = ctx->fuse_projection && a->T == 1 && (pl.kernel == G4A_KERNEL_DECODE || pl.kernel == G4A_KERNEL_DECODE_SHORT) &&
                       pl.splits >= 2 && pl.splits <= G4A_FUSE_MAX_SPLITS && pl.splits <= COMBINE_ROW_SPLITS &&
                       a->Hq <= G4A_FUSE_MAX_HEADS && (a->Dh == 256 || a->Dh == 512) && a->Dv == a->Dh &&
-                      (reinterpret_cast<uintptr_t>(a->out) & 15) == 0 && projection_on_short_words(ctx, w);
+                      (reinterpret_cast<uintptr_t>(a->out) & 15) == 0 && projection_on_short_words(ctx, w, a->out);
     if (int rc = attention_run(ctx, a, an, !fuse)) return rc;
     if (!fuse) return linear_q_launch(ctx, 0, w, nullptr, a->out, nullptr, 0, 0, y, a->T);
     G4aLinearParams p{};
@@ -1709,6 +1776,12 @@ int g4a_capture_begin(g4a_ctx* ctx) {
     if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
     if (ctx->capturing) return fail(ctx, G4A_E_ARG, "a capture is already open on this context");
     if (ctx->timing) return fail(ctx, G4A_E_ARG, "per-kernel timing is on: turn it off before capturing");
+    // a graph is where g4a_attention_noalloc is most used, and looking the static
+    // scratch array up may load it, which is no stream work: do it before the capture
+    if (!ctx->scratch) {
+        HIP_TRY(ctx, hipSetDevice(ctx->device));
+        if (int rc = scratch_setup(ctx)) return rc;
+    }
     HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
     ctx->capturing = true;
     ctx->capture_code = 0;

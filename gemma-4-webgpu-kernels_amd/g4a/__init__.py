@@ -30,6 +30,13 @@ _u32p = ctypes.POINTER(ctypes.c_uint32)
 _f32p = ctypes.c_void_p
 
 
+class Options(ctypes.Structure):
+    """g4a_options (include/g4a.h): a context's kernel-selection options."""
+    _fields_ = [("size", ctypes.c_uint32), ("short_decode", ctypes.c_int32), ("short_max_wgs", ctypes.c_uint32),
+                ("batch_kernel", ctypes.c_int32), ("batch_keys_per_split", ctypes.c_uint32),
+                ("linear_i8", ctypes.c_int32), ("fuse_projection", ctypes.c_int32)]
+
+
 class AttnArgs(ctypes.Structure):
     _fields_ = [
         ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("out", ctypes.c_void_p),
@@ -96,6 +103,8 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
     ctxp = ctypes.c_void_p
     sig = {
         "g4a_create": (c_int, [c_int, ctypes.c_char_p, ctypes.POINTER(ctxp)]),
+        "g4a_create_with": (c_int, [c_int, ctypes.c_char_p, ctypes.POINTER(Options), ctypes.POINTER(ctxp)]),
+        "g4a_default_options": (None, [ctypes.POINTER(Options)]),
         "g4a_destroy": (None, [ctxp]),
         "g4a_last_error": (ctypes.c_char_p, [ctxp]),
         "g4a_malloc": (c_int, [ctxp, sz, ctypes.POINTER(vp)]),
@@ -238,13 +247,21 @@ class Graph:
 
 
 class Context:
-    """One g4a context: a device, its gfx950 module, one stream."""
+    """One g4a context: a device, its gfx950 module, one stream. `options`
+    (a dict of g4a_options fields, e.g. {"fuse_projection": 1}) overrides the
+    library's defaults for this context."""
 
-    def __init__(self, device: int = 0, hsaco: Optional[Path] = None):
+    def __init__(self, device: int = 0, hsaco: Optional[Path] = None, options: Optional[dict] = None):
         self.lib = load_library()
         h = ctypes.c_void_p()
         path = str(hsaco).encode() if hsaco else None
-        rc = self.lib.g4a_create(device, path, ctypes.byref(h))
+        opts = Options()
+        self.lib.g4a_default_options(ctypes.byref(opts))
+        for k, v in (options or {}).items():
+            if k not in dict(Options._fields_) or k == "size":
+                raise ValueError(f"unknown g4a option {k!r}")
+            setattr(opts, k, v)
+        rc = self.lib.g4a_create_with(device, path, ctypes.byref(opts), ctypes.byref(h))
         if rc != G4A_OK:
             raise G4aError(rc, self.lib.g4a_last_error(None).decode())
         self.handle = h

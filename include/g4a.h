@@ -47,6 +47,28 @@ typedef enum g4a_status {
  * device acquisition (rust/src/device.rs:25-66). `hsaco_path` NULL loads
  * g4a_kernels.hsaco from the directory of libg4a.so. */
 int g4a_create(int device, const char *hsaco_path, g4a_ctx **out);
+
+/* Kernel-selection options of a context, fixed at creation. g4a_create uses
+ * the defaults (g4a_default_options); the others exist to compare kernels and
+ * to opt into behaviour that is off by default. No counterpart in the
+ * reference (its backend has no such choices). */
+typedef struct g4a_options {
+    uint32_t size;            /* sizeof(g4a_options), set by g4a_default_options */
+    int32_t short_decode;     /* 1 (default): decode splits that fit the CUs with 32 keys run the
+                                 short-context kernel; 0: always the streaming kernel */
+    uint32_t short_max_wgs;   /* 4 (default), 2 or 1: workgroups sharing one short-kernel split */
+    int32_t batch_kernel;     /* g4a_attention_decode_batch: 0 (default) automatic, 1 short, 2 streaming */
+    uint32_t batch_keys_per_split; /* streaming batch launches: 0 (default) automatic */
+    int32_t linear_i8;        /* -1 (default): the int8 matrix-core projection for M <= 2 weights of
+                                 16 MB and more; 1: for every eligible weight; 0: never */
+    int32_t fuse_projection;  /* 0 (default); 1: g4a_attention_linear_q merges a decode step's
+                                 split partials inside its projection (2..16 splits, short-weight
+                                 projections): bit-identical, measured slower on MI355X */
+} g4a_options;
+void g4a_default_options(g4a_options *opts);
+/* g4a_create with options (NULL: the defaults); fails with G4A_E_ARG on an
+ * options struct of another size or an option out of range. */
+int g4a_create_with(int device, const char *hsaco_path, const g4a_options *opts, g4a_ctx **out);
 void g4a_destroy(g4a_ctx *ctx);
 /* Message of the last failed call on this context ("" if none). With a NULL
  * ctx: the message of the last failed g4a_create in this process. */
@@ -117,7 +139,9 @@ int g4a_attention(g4a_ctx *ctx, const g4a_attn_args *args);
  * call's split partials and pre-split K/V live in a static scratch array of
  * G4A_NOALLOC_SCRATCH_BYTES compiled into libg4a.so instead of the context's
  * workspace, and that it calls no allocator. Each GPU holds its own copy of the
- * array, set up by g4a_create on that GPU and held until the process ends.
+ * array, looked up (and so loaded onto the GPU) by the first no-alloc call or
+ * graph capture on that GPU, and held until the process ends: a process that
+ * does neither does not hold it.
  * Fails with G4A_E_UNSUPPORTED, enqueueing nothing, when the call needs more
  * scratch than the array holds (decode: T*Hq*splits*(Dh+2)*4 bytes for more
  * than one split; prefill: about 2*keys*Hkv*Dh*4 bytes plus the partials of
@@ -179,6 +203,8 @@ typedef struct g4a_attn_plan {
     size_t workspace_bytes;
 } g4a_attn_plan;
 
+/* The host dispatch's decisions for a call, without GPU work (a query: a
+ * failure here does not discard an open graph capture). */
 int g4a_attention_plan(g4a_ctx *ctx, const g4a_attn_args *args, g4a_attn_plan *plan);
 
 /* ---- KV cache writes -----------------------------------------------------
@@ -334,7 +360,7 @@ int g4a_linear_q_gelu_mul_cols(g4a_ctx *ctx, const g4a_qweight *w, const float *
  * (Gemma4Model::attention, rust/src/model.rs:287-303: o_proj(attention(q, k, v))):
  * the results of g4a_attention(args) then g4a_linear_q(w, args->out, y, T),
  * with w->K = Hq * Dv; args->out receives the attention rows as usual. On a
- * context created with G4A_FUSE_PROJECTION=1 in the environment, a decode
+ * context created with g4a_options::fuse_projection = 1, a decode
  * step (T = 1) that runs 2 .. 16 splits, with a projection the short-weight
  * word kernel takes (N below 64 per CU, one scale per row, a weight under the
  * int8 kernel's size threshold) and a 16-byte aligned args->out, launches no
@@ -367,9 +393,12 @@ int g4a_embed_rows_q(g4a_ctx *ctx, const g4a_qweight *table, const uint32_t *ids
  * (explicit position arrays, embedding ids), a larger workspace or a new RoPE
  * table, and g4a_h2d / g4a_d2h / g4a_zero / g4a_sync / the timers, fail with
  * G4A_E_ARG while a capture is open: run such calls once before capturing.
- * After any failure inside a capture, still call g4a_capture_end, which then
- * returns that first failure's code and no graph (the recording would lack the
- * refused call). Rows without visible keys are cleared by a fill kernel, not a
+ * After any failing call that enqueues work inside a capture, still call
+ * g4a_capture_end, which then returns that first failure's code and no graph
+ * (the recording would lack the refused call); a failing query
+ * (g4a_attention_plan) enqueues nothing and leaves the capture usable. The
+ * first g4a_capture_begin on a GPU also sets up g4a_attention_noalloc's
+ * static scratch array there, so no-alloc calls record without allocating. Rows without visible keys are cleared by a fill kernel, not a
  * memset, so a replay clears them too. A graph replays with the workspace it
  * was captured with: a later eager call that needs a larger workspace gets a
  * new one and the old one is kept until the context's last graph is

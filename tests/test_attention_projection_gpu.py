@@ -1,6 +1,6 @@
 """GPU parity of g4a_attention_linear_q: an attention call followed by its
 quantised output projection (Gemma4Model::attention's `o_proj(attention(..))`,
-rust/src/model.rs:287-303). On a context created with G4A_FUSE_PROJECTION=1, a
+rust/src/model.rs:287-303). On a context created with the fuse_projection option, a
 decode step with 2..16 splits and a projection on the short-weight word kernel
 launches no LSE combine: the projection merges the split partials while it
 stages its activation row, in the combine kernel's order. A default context
@@ -14,7 +14,6 @@ runs the combine and the projection separately. Bars:
 Covers fused steps (sliding window on a ring, global at a short context, two kv
 heads, 2/4/8-bit and I8 weights, 2..16 splits) and calls that must not fuse
 (one split, more than 16 splits, several queries, an unaligned output)."""
-import os
 
 import numpy as np
 import pytest
@@ -34,15 +33,7 @@ def step(msg):
 @pytest.fixture(scope="module")
 def fctx():
     """A context whose g4a_attention_linear_q merges eligible decode steps in the projection."""
-    old = os.environ.get("G4A_FUSE_PROJECTION")
-    os.environ["G4A_FUSE_PROJECTION"] = "1"
-    try:
-        c = g4a.Context(0)
-    finally:
-        if old is None:
-            del os.environ["G4A_FUSE_PROJECTION"]
-        else:
-            os.environ["G4A_FUSE_PROJECTION"] = old
+    c = g4a.Context(0, options={"fuse_projection": 1})
     yield c
     c.close()
 

@@ -16,10 +16,9 @@ Bars, written per test:
     general;
   - an activation row holding an inf or NaN: bit-identical to the oracle (that
     row is computed in the CPU's order), NaN where the oracle has NaN.
-Contexts here set G4A_LINEAR_I8=1, which sends every eligible projection to
+Contexts here set the linear_i8 option to 1, which sends every eligible projection to
 this kernel; the default context sends weights of 16 MB and more.
 """
-import os
 
 import numpy as np
 import pytest
@@ -39,15 +38,7 @@ def step(msg):
 @pytest.fixture(scope="module")
 def ictx():
     """A context that runs every eligible M <= 2 projection on the int8 kernel."""
-    old = os.environ.get("G4A_LINEAR_I8")
-    os.environ["G4A_LINEAR_I8"] = "1"
-    try:
-        c = g4a.Context(0)
-    finally:
-        if old is None:
-            del os.environ["G4A_LINEAR_I8"]
-        else:
-            os.environ["G4A_LINEAR_I8"] = old
+    c = g4a.Context(0, options={"linear_i8": 1})
     yield c
     c.close()
 
@@ -150,7 +141,7 @@ def test_int8_kernel_nonfinite_rows(ictx):
 
 
 def test_default_context_takes_large_weights(ctx):
-    """The default context (no G4A_LINEAR_I8) sends a 2-bit weight of 16 MB or
+    """The default context (linear_i8 -1) sends a 2-bit weight of 16 MB or
     more at M = 1 to the int8 kernel: [49152, 1536] is 18.9 MB."""
     N, K = 49152, 1536
     w = _qw(12, N, K, 2)

@@ -110,3 +110,115 @@ def test_noalloc_refuses_what_needs_an_allocation(ctx):
     finally:
         for d in dev + [out]:
             d.free()
+
+
+def test_noalloc_records_into_a_graph_on_a_fresh_context():
+    """The no-allocation property itself: on a fresh context (no workspace yet), a HIP graph
+    capture refuses any workspace growth, so g4a_attention cannot record a 256-split decode
+    or a head_dim 512 prefill there, while g4a_attention_noalloc records both. The graph's
+    replays (outputs overwritten in between, other eager work between them) match eager
+    g4a_attention runs of the same calls bit for bit."""
+    fresh = g4a.Context(0)
+    decode = synth.gemma_inputs(T=1, S=32768, Dh=512, seed=11)
+    prefill = synth.gemma_inputs(T=1024, S=1024, Dh=512, seed=12, q_pos=np.arange(1024))
+    bufs, graph = [], None
+    try:
+        calls = []
+        for ins, label in ((decode, "decode hd512 @32768"), (prefill, "prefill hd512 T1024")):
+            T, Hq, Dh = ins.q.shape
+            dq, dk, dv = (fresh.upload(x) for x in (ins.q, ins.k, ins.v))
+            out = fresh.empty((T, Hq * Dh))
+            bufs += [dq, dk, dv, out]
+            kw = dict(T=T, S=ins.k.shape[0], Hq=Hq, Hkv=1, Dh=Dh, Dv=Dh, q_pos0=int(ins.q_pos[0]), k_pos0=0)
+            calls.append((label, dq, dk, dv, out, kw))
+        for label, dq, dk, dv, out, kw in calls:
+            step(f"g4a_attention under a capture on a fresh context, {label}: refused (its workspace would grow)")
+            fresh.capture_begin()
+            try:
+                with pytest.raises(g4a.G4aError, match="workspace must grow"):
+                    fresh.attention(dq.ptr, dk.ptr, dv.ptr, out.ptr, **kw)
+            finally:
+                with pytest.raises(g4a.G4aError):
+                    fresh.capture_end()
+        step("g4a_attention_noalloc under a capture on the same fresh context: recorded")
+        fresh.capture_begin()
+        try:
+            for label, dq, dk, dv, out, kw in calls:
+                fresh.attention_noalloc(dq.ptr, dk.ptr, dv.ptr, out.ptr, **kw)
+        except Exception:
+            try:
+                fresh.capture_end().free()
+            except g4a.G4aError:
+                pass
+            raise
+        graph = fresh.capture_end()
+        # eager reference results through g4a_attention (which may now grow its workspace)
+        want = []
+        for label, dq, dk, dv, out, kw in calls:
+            fresh.attention(dq.ptr, dk.ptr, dv.ptr, out.ptr, **kw)
+            want.append(out.to_host())
+        rng = np.random.default_rng(5)
+        for rep in range(3):
+            step(f"graph replay {rep}")
+            for label, dq, dk, dv, out, kw in calls:
+                fresh.h2d(out.ptr, rng.standard_normal(out.shape).astype(np.float32))
+            graph.launch()
+            fresh.sync()
+            for (label, *_rest), w in zip(calls, want):
+                got = _rest[3].to_host()
+                assert np.array_equal(got, w), f"replay {rep}, {label}: differs from eager g4a_attention"
+            # eager work between replays
+            label, dq, dk, dv, out, kw = calls[0]
+            fresh.attention(dq.ptr, dk.ptr, dv.ptr, out.ptr, **kw)
+            fresh.sync()
+        print("  both calls recorded without an allocation; replays bit-identical to eager runs", flush=True)
+    finally:
+        if graph is not None:
+            graph.free()
+        for d in bufs:
+            d.free()
+        fresh.close()
+
+
+_LAZY_SCRIPT = r"""
+import ctypes, sys
+sys.path.insert(0, sys.argv[1])
+import numpy as np
+import g4a
+hip = ctypes.CDLL("libamdhip64.so")
+def free_bytes():
+    f, t = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(f), ctypes.byref(t)) == 0
+    return f.value
+ctx = g4a.Context(0)
+q, k, v, out = ctx.empty((1, 8, 256)), ctx.empty((512, 1, 256)), ctx.empty((512, 1, 256)), ctx.empty((1, 2048))
+for b in (q, k, v):
+    ctx.zero(b.ptr, b.nbytes)
+ctx.sync()
+before = free_bytes()
+ctx.attention_noalloc(q.ptr, k.ptr, v.ptr, out.ptr, T=1, S=512, Hq=8, Hkv=1, Dh=256, Dv=256, q_pos0=511, k_pos0=0,
+                      window=512)
+ctx.sync()
+after = free_bytes()
+print(f"FREE_BEFORE {before} FREE_AFTER {after}", flush=True)
+ctx.close()
+"""
+
+
+def test_noalloc_scratch_is_taken_at_first_use():
+    """A process that creates a context holds no scratch array until its first no-alloc call
+    (the array is looked up, and so loaded onto the GPU, there): the device's free memory
+    drops by the array's size at that call, not at g4a_create."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    pkg = str(Path(g4a.__file__).resolve().parents[1])
+    r = subprocess.run([sys.executable, "-c", _LAZY_SCRIPT, pkg], capture_output=True, text=True, timeout=100)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
+    line = [x for x in r.stdout.splitlines() if x.startswith("FREE_BEFORE")][-1].split()
+    before, after = int(line[1]), int(line[3])
+    taken = before - after
+    print(f"  free device memory dropped by {taken / 2**20:.1f} MiB at the first no-alloc call "
+          f"(array {g4a.NOALLOC_SCRATCH_BYTES / 2**20:.0f} MiB)", flush=True)
+    assert taken >= g4a.NOALLOC_SCRATCH_BYTES, "the scratch array was not taken at the first no-alloc call"
