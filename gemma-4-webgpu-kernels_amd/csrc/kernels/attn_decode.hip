@@ -57,12 +57,14 @@ __device__ __forceinline__ float score_epilogue(float dot, float scale, float so
 typedef float f4v __attribute__((ext_vector_type(4)));  // MFMA accumulator (4 VGPRs)
 
 // Split partials: the acc value of row ih (= query * Hq + head), split s, dim d
-// sits at ((ih * (DH/16) + d/16) * nsplit + s) * 16 + d%16, so the combine
-// block of 16 dims reads one contiguous run over all splits. The (m, l) pairs
-// follow all acc values: [ih][s][2].
+// sits at (ih * nsplit + s) * DH + d: a split's row of a head is one contiguous
+// run of DH floats, so the decode kernels' final stores are whole 2 KiB rows
+// (at hd512 @32K the workgroups' scattered 64-byte stores had cost ~0.25 us
+// more at the end of the launch); the combine reads split s of a head at stride
+// DH. The (m, l) pairs follow all acc values: [ih][s][2].
 template <int DH>
 __device__ __forceinline__ size_t part_index(size_t ih, uint32_t nsplit, uint32_t s, uint32_t d) {
-    return ((ih * (DH / 16) + d / 16) * nsplit + s) * 16 + (d & 15);
+    return (ih * nsplit + s) * DH + d;
 }
 
 // Sixteen dims (16B .. 16B+15 of a 64-dim stage) of the exact dots of the two
@@ -1269,8 +1271,8 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
 // out = sum_s acc_s * e^(m_s - M) / sum_s l_s * e^(m_s - M), M = max_s m_s; 0 when the
 // denominator is 0 (the semantics of rust/src/kernels/attention_combine.wgsl:1-28).
 // One block per (16 output dims, head, query): wide enough that a decode
-// step's partials are read by the whole GPU; the block's acc values are one
-// contiguous run (part_index). The split weights e^(m_s - M) are
+// step's partials are read by the whole GPU; the block reads 64 bytes of each
+// split's row (part_index). The split weights e^(m_s - M) are
 // computed once per block into LDS; thread (group g, dim i) then sums splits
 // s = g, g + 16, ... in split order, and the 16 groups reduce through LDS. The
 // first COMBINE_EARLY splits of each thread (all of them up to 256 splits) are
@@ -1306,7 +1308,7 @@ __device__ __forceinline__ void combine(const G4aCombineParams& p, uint32_t qi) 
 #pragma unroll
     for (int u = 0; u < COMBINE_EARLY; ++u) {
         const uint32_t s = grp + 16 * u;
-        x0[u] = acc[(size_t)(s < ns ? s : ns - 1) * 16];
+        x0[u] = acc[(size_t)(s < ns ? s : ns - 1) * DH];
     }
     float M = NEG_INF;
 #pragma unroll
@@ -1340,11 +1342,11 @@ __device__ __forceinline__ void combine(const G4aCombineParams& p, uint32_t qi) 
     for (; s + 16 * (U - 1) < ns; s += 16 * U) {
         float x[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) x[u] = acc[(size_t)(s + 16 * u) * 16];
+        for (int u = 0; u < U; ++u) x[u] = acc[(size_t)(s + 16 * u) * DH];
 #pragma unroll
         for (int u = 0; u < U; ++u) A += x[u] * wgt[s + 16 * u];
     }
-    for (; s < ns; s += 16) A += acc[(size_t)s * 16] * wgt[s];
+    for (; s < ns; s += 16) A += acc[(size_t)s * DH] * wgt[s];
     red[grp][i] = A;
     __syncthreads();
     if (tid < 16) {
@@ -1382,7 +1384,7 @@ __device__ __forceinline__ void combine_rows(const G4aCombineParams& p, uint32_t
         const float* __restrict__ acc = p.part + part_index<DH>(ih, ns, 0, 256 * e + tid);
 #pragma unroll
         for (uint32_t u = 0; u < COMBINE_ROW_EARLY; ++u)  // ns >= 1: the clamped loads stay in the split range
-            x0[e][u] = acc[(size_t)(u < early ? u : early - 1) * 16];
+            x0[e][u] = acc[(size_t)(u < early ? u : early - 1) * DH];
     }
     if (tid < 64) {
         const float M = wave_max(mls.x);
@@ -1396,7 +1398,7 @@ __device__ __forceinline__ void combine_rows(const G4aCombineParams& p, uint32_t
 #pragma unroll
     for (int e = 0; e < DH / 256; ++e) {
         const uint32_t d = 256 * e + tid;
-        const float* __restrict__ acc = p.part + part_index<DH>(ih, ns, 0, d);  // split s at acc[16 s]
+        const float* __restrict__ acc = p.part + part_index<DH>(ih, ns, 0, d);  // split s at acc[DH s]
         float A = 0.0f;
 #pragma unroll
         for (uint32_t u = 0; u < COMBINE_ROW_EARLY; ++u)
@@ -1405,11 +1407,11 @@ __device__ __forceinline__ void combine_rows(const G4aCombineParams& p, uint32_t
         for (; s + 8 <= ns; s += 8) {
             float x[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) x[u] = acc[(size_t)(s + u) * 16];
+            for (int u = 0; u < 8; ++u) x[u] = acc[(size_t)(s + u) * DH];
 #pragma unroll
             for (int u = 0; u < 8; ++u) A += x[u] * wgt[s + u];
         }
-        for (; s < ns; ++s) A += acc[(size_t)s * 16] * wgt[s];
+        for (; s < ns; ++s) A += acc[(size_t)s * DH] * wgt[s];
         p.out[ih * DH + d] = L > 0.0f ? A / L : 0.0f;
     }
 }
@@ -1439,10 +1441,10 @@ __device__ __forceinline__ void combine_row_stage(const float* __restrict__ part
     auto issue = [&](int g, uint32_t k) {
         const uint32_t kk = k < K ? k : K - 4;
         const uint32_t h = kk / DH, d = kk - h * DH;
-        const float* __restrict__ acc = part + part_index<DH>(h, ns, 0, d);  // split s at acc[16 s]
+        const float* __restrict__ acc = part + part_index<DH>(h, ns, 0, d);  // split s at acc[DH s]
 #pragma unroll
         for (int s = 0; s < FS; ++s)  // ns >= 1: the clamped loads stay in the split range
-            x[g][s] = *reinterpret_cast<const float4*>(acc + (size_t)((uint32_t)s < ns ? s : ns - 1) * 16);
+            x[g][s] = *reinterpret_cast<const float4*>(acc + (size_t)((uint32_t)s < ns ? s : ns - 1) * DH);
     };
     issue(0, 4 * tid);
     issue(1, 1024 + 4 * tid);
