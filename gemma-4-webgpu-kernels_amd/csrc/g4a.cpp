@@ -40,6 +40,9 @@ constexpr float PREFILL_TAU_LOGN = 2.0f;
 constexpr uint32_t MAX_SPLITS = 1024;
 // Split counts merged by the one-block-per-head combine kernel (combine_rows).
 constexpr uint32_t COMBINE_ROW_SPLITS = 16;
+// Output dims and threads per block of the wide combine kernel (combine).
+constexpr uint32_t kCombineDims = 32;
+constexpr uint32_t kCombineThreads = 512;
 // Keys per 4-wave workgroup of the short-context decode kernel (two 16-key tiles).
 constexpr uint32_t SHORT_KEYS = 32;
 // Most visible keys of a batched decode step (1024 splits of the short kernel).
@@ -938,8 +941,8 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
         if (pl.splits <= COMBINE_ROW_SPLITS) {
             if (int rc = launch(ctx, ctx->combine_rows[d512], dim3(a->Hq, a->T, 1), dim3(256, 1, 1), cp, "combine"))
                 return rc;
-        } else if (int rc = launch(ctx, ctx->combine[d512], dim3(a->Dh / 16, a->Hq, a->T), dim3(256, 1, 1), cp,
-                                   "combine")) {
+        } else if (int rc = launch(ctx, ctx->combine[d512], dim3(a->Dh / kCombineDims, a->Hq, a->T),
+                                   dim3(kCombineThreads, 1, 1), cp, "combine")) {
             return rc;
         }
     }
@@ -1119,8 +1122,8 @@ int g4a_attention_decode_batch(g4a_ctx* ctx, const g4a_attn_args* args, uint32_t
                                 "batched combine", true))
                 return rc;
         if (L.wide)
-            if (int rc = launch(ctx, ctx->combine_batch[d512], dim3(ref->Dh / 16, bp.Hq, L.count), dim3(256, 1, 1), bp,
-                                "batched combine", true))
+            if (int rc = launch(ctx, ctx->combine_batch[d512], dim3(ref->Dh / kCombineDims, bp.Hq, L.count),
+                                dim3(kCombineThreads, 1, 1), bp, "batched combine", true))
                 return rc;
     }
     // the rest, one call at a time
@@ -1866,8 +1869,14 @@ int g4a_kernel_timing(g4a_ctx* ctx, int enable) {
     if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
     if (int rc = refuse_in_capture(ctx, "g4a_kernel_timing")) return rc;
     if (enable && ctx->kev.empty()) {
+        // Timing-only events: without a system-scope fence the timed dispatch ends
+        // with the same device-scope release as an untimed one. With the fence, the
+        // stop event bound to the kernel makes it write its dirty L2 lines back to
+        // memory first (a decode step's 4 MiB of split partials: ~1 us more than the
+        // profiler's duration of the same kernel). Results are read only after a
+        // stream synchronize, which does not rely on these events.
         ctx->kev.resize(2 * kMaxTimed, nullptr);
-        for (auto& ev : ctx->kev) HIP_TRY(ctx, hipEventCreate(&ev));
+        for (auto& ev : ctx->kev) HIP_TRY(ctx, hipEventCreateWithFlags(&ev, hipEventDisableSystemFence));
     }
     if (ctx->kev_used) HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     ctx->timing = enable != 0;

@@ -1270,38 +1270,45 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
 
 // out = sum_s acc_s * e^(m_s - M) / sum_s l_s * e^(m_s - M), M = max_s m_s; 0 when the
 // denominator is 0 (the semantics of rust/src/kernels/attention_combine.wgsl:1-28).
-// One block per (16 output dims, head, query): wide enough that a decode
-// step's partials are read by the whole GPU; the block reads 64 bytes of each
-// split's row (part_index). The split weights e^(m_s - M) are
-// computed once per block into LDS; thread (group g, dim i) then sums splits
-// s = g, g + 16, ... in split order, and the 16 groups reduce through LDS. The
-// first COMBINE_EARLY splits of each thread (all of them up to 256 splits) are
-// loaded together with the (m, l) pairs, before the weights are known, so a
-// step pays one memory round trip for them instead of two.
+// One block of COMBINE_THREADS per (32 output dims, head, query): the block
+// reads one whole 128-byte piece of each split's row (part_index), so every
+// fetched line is used by the block that fetched it (blocks of 16 dims each
+// used half of every line, and the other half came in again on another XCD).
+// Every wave computes the maximum M and the weighted sum of l itself from all
+// (m, l) pairs and keeps its own copy of the split weights e^(m_s - M) in LDS,
+// so no barrier stands between the loads and the sums. Thread (group g, dim i)
+// sums splits s = g, g + 16, ... in split order, and the 16 groups reduce
+// through LDS. The first COMBINE_EARLY splits of each thread (all of them up
+// to 256 splits) are loaded together with the (m, l) pairs, before the weights
+// are known, so a step pays one memory round trip for them instead of two.
 constexpr int COMBINE_MAX_SPLITS = 1024;
 constexpr int COMBINE_EARLY = 16;
+constexpr int COMBINE_DIMS = 32;
+constexpr int COMBINE_THREADS = 512;
 
 template <int DH>
 __device__ __forceinline__ void combine(const G4aCombineParams& p, uint32_t qi) {
-    __shared__ float wgt[COMBINE_MAX_SPLITS];
-    __shared__ float red[16][17];
-    __shared__ float redm[4], redl[4];
+    static_assert(DH % COMBINE_DIMS == 0, "whole blocks of dims");
+    __shared__ float wgt[COMBINE_THREADS / 64][COMBINE_MAX_SPLITS];  // one copy per wave
+    __shared__ float red[16][COMBINE_DIMS + 1];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
-    const int i = tid & 15, grp = tid >> 4;
+    const int i = tid & (COMBINE_DIMS - 1), grp = tid / COMBINE_DIMS;  // 16 groups
     const size_t ih = (size_t)qi * p.Hq + blockIdx.y;
-    const uint32_t d = blockIdx.x * 16 + i;
-    const float* __restrict__ ml = p.part + (size_t)p.T * p.Hq * p.nsplit * DH + ih * p.nsplit * 2;
-    // this block's 16 dims: a contiguous [split][16] run
-    const float* __restrict__ acc = p.part + part_index<DH>(ih, p.nsplit, 0, blockIdx.x * 16) + i;
+    const uint32_t d = blockIdx.x * COMBINE_DIMS + i;
+    const float2* __restrict__ ml =
+        reinterpret_cast<const float2*>(p.part + (size_t)p.T * p.Hq * p.nsplit * DH + ih * p.nsplit * 2);
+    // this block's 32 dims: a 128-byte run in each split's row, DH floats apart
+    const float* __restrict__ acc = p.part + part_index<DH>(ih, p.nsplit, 0, blockIdx.x * COMBINE_DIMS) + i;
     const uint32_t ns = p.nsplit;
-    // (m, l) of splits tid, tid + 256, ... first (their wait then leaves the partials in flight)
-    float2 mls[COMBINE_MAX_SPLITS / 256];
+    float* const wg = wgt[w];
+    // (m, l) of splits lane, lane + 64, ... first (their wait then leaves the partials in flight)
+    float2 mls[COMBINE_MAX_SPLITS / 64];
 #pragma unroll
-    for (int r = 0; r < COMBINE_MAX_SPLITS / 256; ++r) {
-        const uint32_t s = tid + 256 * r;
-        mls[r] = s < ns ? reinterpret_cast<const float2*>(ml)[s] : make_float2(NEG_INF, 0.0f);
+    for (int r = 0; r < COMBINE_MAX_SPLITS / 64; ++r) {
+        const uint32_t s = lane + 64 * r;
+        mls[r] = s < ns ? ml[s] : make_float2(NEG_INF, 0.0f);
     }
     // splits grp + 16 u, u < COMBINE_EARLY (clamped: loads past the last split repeat it and are not summed)
     float x0[COMBINE_EARLY];
@@ -1312,30 +1319,30 @@ __device__ __forceinline__ void combine(const G4aCombineParams& p, uint32_t qi) 
     }
     float M = NEG_INF;
 #pragma unroll
-    for (int r = 0; r < COMBINE_MAX_SPLITS / 256; ++r) M = fmaxf(M, mls[r].x);
+    for (int r = 0; r < COMBINE_MAX_SPLITS / 64; ++r) M = fmaxf(M, mls[r].x);
     M = wave_max(M);
-    if (lane == 0) redm[w] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
     float L = 0.0f;
 #pragma unroll
-    for (int r = 0; r < COMBINE_MAX_SPLITS / 256; ++r) {
-        const uint32_t s = tid + 256 * r;
+    for (int r = 0; r < COMBINE_MAX_SPLITS / 64; ++r) {
+        const uint32_t s = lane + 64 * r;
         if (s < ns) {
             const float e = (mls[r].x == NEG_INF) ? 0.0f : expf(mls[r].x - M);
-            wgt[s] = e;
+            wg[s] = e;
             L += mls[r].y * e;
         }
     }
     L = wave_sum(L);
-    if (lane == 0) redl[w] = L;
-    __syncthreads();
-    L = redl[0] + redl[1] + redl[2] + redl[3];
+    // the wave's own LDS writes above are read below by other lanes of the same
+    // wave: a wave's LDS instructions execute in order, so only the compiler
+    // must keep them in place
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     float A = 0.0f;
 #pragma unroll
     for (int u = 0; u < COMBINE_EARLY; ++u) {
         const uint32_t s = grp + 16 * u;
-        if (s < ns) A += x0[u] * wgt[s];
+        if (s < ns) A += x0[u] * wg[s];
     }
     constexpr int U = 8;
     uint32_t s = grp + 16 * COMBINE_EARLY;
@@ -1344,12 +1351,12 @@ __device__ __forceinline__ void combine(const G4aCombineParams& p, uint32_t qi) 
 #pragma unroll
         for (int u = 0; u < U; ++u) x[u] = acc[(size_t)(s + 16 * u) * DH];
 #pragma unroll
-        for (int u = 0; u < U; ++u) A += x[u] * wgt[s + 16 * u];
+        for (int u = 0; u < U; ++u) A += x[u] * wg[s + 16 * u];
     }
-    for (; s < ns; s += 16) A += acc[(size_t)s * DH] * wgt[s];
+    for (; s < ns; s += 16) A += acc[(size_t)s * DH] * wg[s];
     red[grp][i] = A;
     __syncthreads();
-    if (tid < 16) {
+    if (tid < COMBINE_DIMS) {
         A = 0.0f;
 #pragma unroll
         for (int g = 0; g < 16; ++g) A += red[g][tid];
@@ -1540,7 +1547,7 @@ __device__ __forceinline__ void decode_wave_batch(const G4aBatchParams& b) {
 
 // The LSE combines of a batched decode, each sequence merged by the kernel a
 // single call with its split count uses: more than COMBINE_ROW_SPLITS splits
-// here, grid (DH/16, Hq, sequences) ...
+// here, grid (DH/COMBINE_DIMS, Hq, sequences) of COMBINE_THREADS ...
 template <int DH>
 __device__ __forceinline__ void combine_batch(const G4aBatchParams& b) {
     G4aDecodeParams p;
@@ -1667,8 +1674,8 @@ __global__ __launch_bounds__(512) void g4a_decode_wave_batch_kpos_d256(G4aBatchP
 __global__ __launch_bounds__(512) void g4a_decode_wave_batch_kpos_d512(G4aBatchParams b) {
     decode_wave_batch<512, true>(b);
 }
-__global__ __launch_bounds__(256) void g4a_combine_batch_d256(G4aBatchParams b) { combine_batch<256>(b); }
-__global__ __launch_bounds__(256) void g4a_combine_batch_d512(G4aBatchParams b) { combine_batch<512>(b); }
+__global__ __launch_bounds__(COMBINE_THREADS) void g4a_combine_batch_d256(G4aBatchParams b) { combine_batch<256>(b); }
+__global__ __launch_bounds__(COMBINE_THREADS) void g4a_combine_batch_d512(G4aBatchParams b) { combine_batch<512>(b); }
 __global__ __launch_bounds__(256) void g4a_combine_rows_batch_d256(G4aBatchParams b) { combine_rows_batch<256>(b); }
 __global__ __launch_bounds__(256) void g4a_combine_rows_batch_d512(G4aBatchParams b) { combine_rows_batch<512>(b); }
 __global__ __launch_bounds__(256) void g4a_combine_rows_d256(G4aCombineParams p) {
@@ -1677,7 +1684,7 @@ __global__ __launch_bounds__(256) void g4a_combine_rows_d256(G4aCombineParams p)
 __global__ __launch_bounds__(256) void g4a_combine_rows_d512(G4aCombineParams p) {
     combine_rows<512>(p, blockIdx.x, blockIdx.y);
 }
-__global__ __launch_bounds__(256) void g4a_combine_d256(G4aCombineParams p) { combine<256>(p, blockIdx.z); }
-__global__ __launch_bounds__(256) void g4a_combine_d512(G4aCombineParams p) { combine<512>(p, blockIdx.z); }
+__global__ __launch_bounds__(COMBINE_THREADS) void g4a_combine_d256(G4aCombineParams p) { combine<256>(p, blockIdx.z); }
+__global__ __launch_bounds__(COMBINE_THREADS) void g4a_combine_d512(G4aCombineParams p) { combine<512>(p, blockIdx.z); }
 __global__ __launch_bounds__(64) void g4a_generic_attention(G4aGenericParams p) { generic_attention(p); }
 }
