@@ -46,6 +46,14 @@ namespace {
 // hi/lo split) instead of its subnormals, whose absolute steps would add up
 // over many small weights. O and l carry the same scale, so O / l is unchanged.
 constexpr float PF_RESCALE = 4.0f;
+// Bound of the wait for a pair partner's half of the end-of-kernel dots (each
+// try sleeps ~64 cycles: ~1.7 ms in all, against a few microseconds expected).
+// Built with G4A_PF_PAIR_SPIN=0, every wave computes every dot itself (the path
+// a wave takes once a wait has run out), for testing that path.
+#ifndef G4A_PF_PAIR_SPIN
+#define G4A_PF_PAIR_SPIN (1 << 16)
+#endif
+constexpr int PF_PAIR_SPIN = G4A_PF_PAIR_SPIN;
 constexpr float PF_PSCALE = 1024.0f;
 
 // e^x for the in-loop probabilities: the hardware 2^x of x log2(e). The rounded
@@ -768,7 +776,7 @@ struct DsplitCfg {
     static constexpr int CAP = 256;                   // candidate entries per wave
     static constexpr int XS = 8 * 64 * 4;             // partial-score exchange [wave][lane][4]
     static constexpr int STAGE = (64 + 16) * 36;      // per-wave staging floats at the end (in the tile buffers)
-    static constexpr int SMEM = 2 * TILE + XS + 8 * 2 * CAP + 8 * 16;
+    static constexpr int SMEM = 2 * TILE + XS + 8 * 2 * CAP + 8 * 16 + 8;  // ..., pair flags
     static constexpr int PART_WAVE = NCH * 16 * 64 + 2 * 16;  // a wave's partial: O, then l and m of its rows
     static_assert(8 * STAGE <= 2 * TILE, "the end-of-kernel staging areas fit in the tile buffers");
     static_assert(BK * NPR == 8 * 4, "a tile is 64 pieces of 1 KiB: 8 per wave");
@@ -803,6 +811,12 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
     uint32_t* const my_keys = reinterpret_cast<uint32_t*>(smem + 2 * C::TILE + C::XS + w * 2 * CAP);
     float* const my_s = smem + 2 * C::TILE + C::XS + w * 2 * CAP + CAP;
     float* const my_m = smem + 2 * C::TILE + C::XS + 8 * 2 * CAP + w * 16;
+    // end-of-kernel exchange of the pair's dots: flags (one per wave) in their own
+    // slots, set to 0 before the first barrier; the dots over the partial-score
+    // exchange area, which the tile loop no longer uses by then
+    uint32_t* const pair_flags = reinterpret_cast<uint32_t*>(smem + 2 * C::TILE + C::XS + 8 * 2 * CAP + 8 * 16);
+    if (lane == 0) pair_flags[w] = 0u;
+    float* const pair_dots = smem + 2 * C::TILE + (w & 3) * 128;  // [2 batch parities][64]
 
     auto key_hi = [&](int64_t i) -> int32_t {
         const int64_t lim = (int64_t)p.q_pos0 + i - (int64_t)p.k_pos0 + 1;
@@ -1005,64 +1019,113 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
         }
         cnt = 0;
     };
-    // End-of-kernel correction: 32-dim segments of the wave's 16 q rows and of 64
-    // candidates' k rows are staged in its LDS area with coalesced reads (two
-    // segments in flight), each lane runs its candidate's sequential dot from LDS.
-    auto flush_staged = [&](float* stage) {
+    // End-of-kernel correction. The two waves of a pair hold the same candidate
+    // list, so each computes the exact dots of one half of every batch of 64
+    // (wave dhf: candidates base + 32 dhf + j, lane j) and the halves meet in LDS:
+    // 32-dim segments of the wave's 16 q rows and of its 32 candidates' k rows are
+    // staged in its LDS area with coalesced reads (two segments in flight), each
+    // lane runs its candidate's sequential dot from LDS, and the dots go to the
+    // pair's exchange slots (double-buffered by batch parity) with a flag. Every
+    // dot is the same sequence of operations whichever wave computes it. The wait
+    // for the partner's flag is bounded: past the bound the wave computes the
+    // partner's half itself, so a wave never waits on a flag forever.
+    auto flush_staged = [&](float* stage, float* xch, uint32_t* flags) {
         constexpr int SR = 36;
         constexpr int NSEG = DH / 32;
-        float* const kst = stage;              // [64 candidates][SR]
-        float* const qst = stage + 64 * SR;    // [16 rows][SR]
+        constexpr int NC = 32;                 // candidates per wave and batch
+        float* const kst = stage;              // [NC candidates][SR]
+        float* const qst = stage + NC * SR;    // [16 rows][SR]
         const int seg = lane >> 3, part = lane & 7;
         const float* const q0 = p.q + ((size_t)min(qw, p.T - 1) * p.Hq + h0 + seg) * DH + 4 * part;
         const float* const q1 = p.q + ((size_t)min(qw + 1, p.T - 1) * p.Hq + h0 + seg) * DH + 4 * part;
-        for (int base = 0; base < cnt; base += 64) {
+        uint32_t* const my_flag = flags + w;
+        const uint32_t* const other_flag = flags + (w ^ 4);
+        uint32_t batch = 0;
+        bool solo = false;
+        for (int base = 0; base < cnt; base += 64, ++batch) {
             const int e = base + lane;
             const bool has = e < cnt;
             const uint32_t pk = has ? my_keys[e] : 0u;
             const uint32_t rho = pk >> 28, kap = has ? (pk & 0x0fffffffu) : (uint32_t)wg_lo;
-            const float* krow[8];
+            // exact dots of candidates base + NC * hs + (lane % NC), read back from the lanes that hold them
+            auto dots_of_half = [&](int hs) -> float {
+                const float* krow[4];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t ki = (uint32_t)__shfl((int)kap, 8 * i + seg, 64);
-                krow[i] = kbase + prow(ki) * row_stride + 4 * part;
-            }
-            float4 kA[8], qA[2], kB[8], qB[2];
-            auto load_seg = [&](int sg, float4 (&kk)[8], float4 (&qq)[2]) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) kk[i] = ld4(krow[i] + 32 * sg);
-                qq[0] = ld4(q0 + 32 * sg);
-                qq[1] = ld4(q1 + 32 * sg);
-            };
-            float dot = 0.0f;
-            auto consume = [&](int sg, float4 (&kk)[8], float4 (&qq)[2]) {
-                wave_sync();  // the previous segment's reads are done
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    *reinterpret_cast<float4*>(kst + (8 * i + seg) * SR + 4 * part) = kk[i];
-                *reinterpret_cast<float4*>(qst + seg * SR + 4 * part) = qq[0];
-                *reinterpret_cast<float4*>(qst + (8 + seg) * SR + 4 * part) = qq[1];
-                if (sg + 2 < NSEG) load_seg(sg + 2, kk, qq);
-                wave_sync();
-                const float* kr = kst + lane * SR;
-                const float* qv = qst + rho * SR;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * u);
-                    const float4 q4 = *reinterpret_cast<const float4*>(qv + 4 * u);
-                    dot = dot + q4.x * k4.x;
-                    dot = dot + q4.y * k4.y;
-                    dot = dot + q4.z * k4.z;
-                    dot = dot + q4.w * k4.w;
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t ki = (uint32_t)__shfl((int)kap, NC * hs + 8 * i + seg, 64);
+                    krow[i] = kbase + prow(ki) * row_stride + 4 * part;
                 }
-            };
-            static_assert(NSEG % 2 == 0, "segments are consumed in pairs");
-            load_seg(0, kA, qA);
-            load_seg(1, kB, qB);
+                const uint32_t rc = (uint32_t)__shfl((int)rho, NC * hs + (lane & (NC - 1)), 64);
+                float4 kA[4], qA[2], kB[4], qB[2];
+                auto load_seg = [&](int sg, float4 (&kk)[4], float4 (&qq)[2]) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) kk[i] = ld4(krow[i] + 32 * sg);
+                    qq[0] = ld4(q0 + 32 * sg);
+                    qq[1] = ld4(q1 + 32 * sg);
+                };
+                float dot = 0.0f;
+                // prefetch (a constant at every call site) reloads kk, qq with segment sg + 2
+                auto consume = [&](int sg, float4 (&kk)[4], float4 (&qq)[2], bool prefetch) {
+                    wave_sync();  // the previous segment's reads are done
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        *reinterpret_cast<float4*>(kst + (8 * i + seg) * SR + 4 * part) = kk[i];
+                    *reinterpret_cast<float4*>(qst + seg * SR + 4 * part) = qq[0];
+                    *reinterpret_cast<float4*>(qst + (8 + seg) * SR + 4 * part) = qq[1];
+                    if (prefetch) load_seg(sg + 2, kk, qq);
+                    wave_sync();
+                    const float* kr = kst + (lane & (NC - 1)) * SR;  // lanes NC.. repeat lanes 0 .. NC-1
+                    const float* qv = qst + rc * SR;
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * u);
+                        const float4 q4 = *reinterpret_cast<const float4*>(qv + 4 * u);
+                        dot = dot + q4.x * k4.x;
+                        dot = dot + q4.y * k4.y;
+                        dot = dot + q4.z * k4.z;
+                        dot = dot + q4.w * k4.w;
+                    }
+                };
+                static_assert(NSEG % 2 == 0 && NSEG >= 4, "segments are consumed in pairs");
+                load_seg(0, kA, qA);
+                load_seg(1, kB, qB);
+                // the last pair is peeled off so the loop's loads are unconditional: the
+                // waits before each store then count only the older segment's loads
 #pragma unroll 1
-            for (int sg = 0; sg < NSEG; sg += 2) {
-                consume(sg, kA, qA);
-                consume(sg + 1, kB, qB);
+                for (int sg = 0; sg < NSEG - 2; sg += 2) {
+                    consume(sg, kA, qA, true);
+                    consume(sg + 1, kB, qB, true);
+                }
+                consume(NSEG - 2, kA, qA, false);
+                consume(NSEG - 1, kB, qB, false);
+                return dot;
+            };
+            float* const slot = xch + (batch & 1u) * 64;
+            const float mine = dots_of_half(dhf);
+            bool seen = false;
+            if (!solo) {
+                if (lane < NC) slot[NC * dhf + lane] = mine;
+                // publish this batch's half (the exchange writes above are ordered before the flag)
+                __hip_atomic_store(my_flag, batch + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                for (int spin = 0; spin < PF_PAIR_SPIN; ++spin) {
+                    if (__hip_atomic_load(other_flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= batch + 1u) {
+                        seen = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+            float dot;
+            if (seen) {
+                dot = slot[lane];
+            } else {
+                // no half from the partner in time: this wave computes both from here on and
+                // leaves the exchange slots alone (the partner may still read its last half)
+                solo = true;
+                const float theirs = dots_of_half(dhf ^ 1);
+                const float a = __shfl(mine, lane & (NC - 1), 64);
+                const float b = __shfl(theirs, lane & (NC - 1), 64);
+                dot = (lane >> 5) == dhf ? a : b;
             }
             const float delta = delta_and_l(base, has, rho, dot, e);
             correct_o(base, delta, rho, kap);
@@ -1214,7 +1277,7 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
         publish_m(m_run);
         compact();
         publish_m(m_ref);
-        flush_staged(smem + w * C::STAGE);
+        flush_staged(smem + w * C::STAGE, pair_dots, pair_flags);
     }
     float l = l_part;
     l = g4a_col_sum4(l);
