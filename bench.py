@@ -771,10 +771,10 @@ def main(argv=None):
     if args.only:
         out = {}
         if args.only == "decode":
-            out.update(decode_configs(ctx, args.steps, args.warmup))
+            out.update(decode_configs(ctx, args.steps, args.warmup, cpu=not args.no_cpu))
         elif args.only == "prefill":
             for name, T, Dh, W in PREFILL_CONFIGS:
-                out[name] = prefill(ctx, T, Dh, W, steps=args.steps, warmup=args.warmup)
+                out[name] = prefill(ctx, T, Dh, W, steps=args.steps, warmup=args.warmup, cpu=not args.no_cpu)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         elif args.only == "linear":
             for name, op, N, K, bits, M in LINEAR_CONFIGS:
@@ -785,7 +785,7 @@ def main(argv=None):
                 out[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=args.steps, warmup=args.warmup, holes=holes)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         elif args.only == "reference":
-            out["reference bench --kernels cases"] = reference_bench(ctx, args.steps, args.warmup)
+            out["reference bench --kernels cases"] = reference_bench(ctx, args.steps, args.warmup, cpu=not args.no_cpu)
         elif args.only == "oproj":
             out["configs[4] token + o_proj @32768"] = schedule_with_projection(ctx, steps=args.steps,
                                                                                warmup=args.warmup)
@@ -794,7 +794,8 @@ def main(argv=None):
                 out[name] = producer(ctx, T, Dh, theta, rot, pos0, cap, steps=args.steps)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         else:
-            out["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=args.steps, warmup=args.warmup)
+            out["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=args.steps, warmup=args.warmup,
+                                                                            cpu=not args.no_cpu)
         ctx.close()
         print(json.dumps({"only": args.only, "results": out}))
         return 0
