@@ -229,7 +229,42 @@ def oracle_module():
     return oracle
 
 
-def schedule_35_layers(ctx, steps, warmup, cpu=True):
+def _schedule_graph(ctx, token, steps, warmup, algo):
+    """The schedule's calls captured once into a HIP graph, replayed back to back:
+    µs per token, median of REGIONS regions of `steps` replays."""
+    ctx.capture_begin()
+    try:
+        ctx.attention_batch(token)
+    except g4a.G4aError:
+        try:  # close the capture; it reports the same failure and makes no graph
+            ctx.capture_end().free()
+        except g4a.G4aError:
+            pass
+        raise
+    graph = ctx.capture_end()
+    try:
+        for _ in range(max(warmup, 1)):
+            graph.launch()
+        ctx.sync()
+
+        def replay():
+            for _ in range(steps):
+                graph.launch()
+            ctx.sync()
+        warm_up(replay)
+        times = []
+        for _ in range(REGIONS):
+            ctx.timer_start()
+            for _ in range(steps):
+                graph.launch()
+            times.append(ctx.timer_stop() / steps)
+    finally:
+        graph.free()
+    ms_graph = float(np.median(times))
+    return {"us_per_token_graph": ms_graph * 1e3, "GB_s_graph": algo / (ms_graph * 1e-3) / 1e9}
+
+
+def schedule_35_layers(ctx, steps, warmup, cpu=True, graph=True):
     """one token of the 35-layer Gemma-4-E2B attention schedule at 32768 context.
     Layers 4,9,...,34 are global (hd512, full context); the rest local (hd256, 512-slot ring).
     Layers 15..34 reuse the KV of layer 14 (global) or 13 (local) (rust/src/config.rs:152-159),
@@ -265,37 +300,13 @@ def schedule_35_layers(ctx, steps, warmup, cpu=True):
         res.update(cpu_us=us, cpu_threads=oracle.thread_count(HQ), cpu_sample=f"{n} whole tokens (35 calls), median")
     # the same token's 35 calls captured once into a HIP graph and replayed
     # (reported beside the eager figure; a capture error is reported, not fatal)
-    try:
-        ctx.capture_begin()
+    if not graph:
+        res["graph"] = "not measured (--no-graph)"
+    else:
         try:
-            ctx.attention_batch(token)
-        except g4a.G4aError:
-            try:  # close the capture; it reports the same failure and makes no graph
-                ctx.capture_end().free()
-            except g4a.G4aError:
-                pass
-            raise
-        graph = ctx.capture_end()
-        for _ in range(max(warmup, 1)):
-            graph.launch()
-        ctx.sync()
-
-        def replay():
-            for _ in range(steps):
-                graph.launch()
-            ctx.sync()
-        warm_up(replay)
-        times = []
-        for _ in range(REGIONS):
-            ctx.timer_start()
-            for _ in range(steps):
-                graph.launch()
-            times.append(ctx.timer_stop() / steps)
-        ms_graph = float(np.median(times))
-        graph.free()
-        res.update(us_per_token_graph=ms_graph * 1e3, GB_s_graph=algo / (ms_graph * 1e-3) / 1e9)
-    except g4a.G4aError as e:
-        res["graph_error"] = str(e)
+            res.update(_schedule_graph(ctx, token, steps, warmup, algo))
+        except g4a.G4aError as e:
+            res["graph_error"] = str(e)
     for a in list(qs) + list(outs) + [x for kv in caches.values() for x in kv]:
         a.free()
     return res
@@ -741,6 +752,9 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="headline decode only (no extras, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="leave out the configs[4] HIP-graph replay figure (rocprofv3's kernel trace "
+                         "crashed in the replay's graph launch on this image)")
     ap.add_argument("--only", choices=["decode", "prefill", "schedule", "producer", "batch", "linear", "oproj",
                                        "reference"],
                     default=None,
@@ -795,7 +809,8 @@ def main(argv=None):
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         else:
             out["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=args.steps, warmup=args.warmup,
-                                                                            cpu=not args.no_cpu)
+                                                                            cpu=not args.no_cpu,
+                                                                            graph=not args.no_graph)
         ctx.close()
         print(json.dumps({"only": args.only, "results": out}))
         return 0
@@ -876,7 +891,8 @@ def main(argv=None):
         for name, n, L, Dh, W, cap, holes in BATCH_CONFIGS:
             extras[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=50, warmup=10, holes=holes)
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
-        extras["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=20, warmup=3, cpu=cpu)
+        extras["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=20, warmup=3, cpu=cpu,
+                                                                          graph=not args.no_graph)
         print(f"[bench] schedule: {extras['configs[4] 35-layer schedule @32768']}", file=sys.stderr, flush=True)
         extras["configs[4] token + o_proj @32768"] = schedule_with_projection(ctx, steps=20, warmup=3)
         print(f"[bench] token + o_proj: {extras['configs[4] token + o_proj @32768']}", file=sys.stderr, flush=True)
