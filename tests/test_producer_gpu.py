@@ -5,7 +5,7 @@ the fused per-layer producer g4a_attn_producer (rust/src/model.rs:256-281 with
 the KV append of rust/src/kvcache.rs:49-62) writing into linear and ring
 caches. Bar: bit-identical to the oracle (and so within max-abs 1e-5,
 mean-abs 1e-6): the kernel sums the squares in the reference's order and takes
-sin/cos from libm tables built on the host.""" 
+sin/cos from libm tables built on the host."""
 import numpy as np
 import pytest
 
@@ -20,7 +20,8 @@ MAX_ABS = 1e-5
 MEAN_ABS = 1e-6
 
 
-def assert_parity(got, want, label):
+def assert_parity(got, want, label, exact=True):
+    """max-abs / mean-abs bar, and with `exact` (every producer output) bit-identity."""
     got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
     d = np.abs(got.astype(np.float64) - want.astype(np.float64))
     mx, mean = float(d.max()), float(d.mean())
@@ -30,7 +31,8 @@ def assert_parity(got, want, label):
     assert mx <= MAX_ABS and mean <= MEAN_ABS, f"{label}: max-abs {mx:.3e} mean-abs {mean:.3e}"
     # the producer does every op in the reference's order (sequential sum of squares, libm sin/cos
     # tables), so its rows are the CPU backend's bit for bit
-    assert ndiff == 0, f"{label}: {ndiff} values differ from the oracle's"
+    if exact:
+        assert ndiff == 0, f"{label}: {ndiff} values differ from the oracle's"
 
 
 def step(msg):
@@ -209,7 +211,8 @@ def test_producer_feeds_the_decode_kernel(ctx):
         order = [(p % cap) for p in range(P - cap + 1, P + 1)]
         want = oracle.attention(q_gpu, rk[order], rv[order], pos, np.arange(P - cap + 1, P + 1, dtype=np.uint32),
                                 window=512)
-        assert_parity(out.to_host(), want, "producer -> attention")
+        # the attention itself sums its splits in another order than the CPU: the tolerance only
+        assert_parity(out.to_host(), want, "producer -> attention", exact=False)
     finally:
         for b in bufs + [qo_d, out]:
             b.free()
