@@ -43,8 +43,9 @@ HQ = 8
 # streams from HBM. Warm figures use one copy, read step after step.
 COLD_REUSE_BYTES = 512 << 20
 # Timing protocol of every figure: the --warmup steps, then the same workload
-# run back to back for at least WARM_MS of wall time, then REGIONS timed
-# regions of exactly --steps steps each; the median region is reported.
+# run back to back for at least WARM_MS of wall time, then one round of regions
+# that is discarded, then REGIONS timed regions of exactly --steps steps each
+# (the extras' regions grown to EXTRA_REGION_MS); the median region is reported.
 WARM_MS = 50.0
 REGIONS = 3
 EXTRA_REGION_MS = 2.0  # the extra workloads' regions hold at least this much GPU time
@@ -131,12 +132,15 @@ def time_steps(ctx, calls, steps, warmup, regions=REGIONS, min_region_ms=0.0):
     (ms/step), then the same steps again with the main kernel of every call
     carrying dispatch-attached start/stop events (its average duration). The
     per-dispatch events add a few microseconds between launches, so they stay
-    out of the region that gives ms/step. The medians over the rounds are
-    returned (single regions vary by several per cent between runs). With
-    min_region_ms > 0 (the extra workloads; the headline times exactly
-    --steps), a region grows past `steps` steps until it holds about that much
-    GPU time, estimated from the warm-up: 20 steps of a 7 µs call are too
-    short a region to repeat within 2 %.
+    out of the region that gives ms/step. One more round runs first and is
+    discarded (its step region read 3-7 % slower than the later ones on the
+    short workloads, after the warm-up's synchronised batches); the medians over
+    the kept rounds are returned (single regions vary by several per cent
+    between runs). With min_region_ms > 0 (the extra workloads; the headline
+    times exactly --steps), a region grows past `steps` steps until it holds
+    about that much GPU time, estimated from one batch before the warm-up
+    (which then runs the grown batch): 20 steps of a 7 µs call are too short a
+    region to repeat within 2 %.
     Returns (ms/step, main-kernel ms/launch, per-round ms/step list)."""
     def batch(n):
         return [kw for i in range(n) for kw in calls[i % len(calls)]]
@@ -148,7 +152,6 @@ def time_steps(ctx, calls, steps, warmup, regions=REGIONS, min_region_ms=0.0):
     def one_batch():
         ctx.attention_batch(timed)
         ctx.sync()
-    warm_up(one_batch)
     if min_region_ms > 0:
         t0 = time.perf_counter()
         one_batch()
@@ -157,9 +160,10 @@ def time_steps(ctx, calls, steps, warmup, regions=REGIONS, min_region_ms=0.0):
         if grown > steps:
             steps = grown
             timed = ctx.prepare_batch(batch(steps))
-            one_batch()
+    # the warm-up runs the batch the regions time (after any growth)
+    warm_up(one_batch)
     step_ms, kernel_ms = [], []
-    for _ in range(regions):
+    for _ in range(regions + 1):
         ctx.timer_start()
         ctx.attention_batch(timed)
         step_ms.append(ctx.timer_stop() / steps)
@@ -169,6 +173,7 @@ def time_steps(ctx, calls, steps, warmup, regions=REGIONS, min_region_ms=0.0):
         kms, n = ctx.kernel_timing_read()
         ctx.kernel_timing(False)
         kernel_ms.append(kms / n if n else float("nan"))
+    step_ms, kernel_ms = step_ms[1:], kernel_ms[1:]  # the first round is discarded
     return float(np.median(step_ms)), float(np.median(kernel_ms)), step_ms
 
 
@@ -837,8 +842,8 @@ def main(argv=None):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "timing": f"--warmup steps, then >= {WARM_MS:.0f} ms of the same steps back to back, then {REGIONS} timed "
-                  f"regions of exactly --steps steps; ms_per_step is the median region",
+        "timing": f"--warmup steps, then >= {WARM_MS:.0f} ms of the same steps back to back, then one discarded "
+                  f"round, then {REGIONS} timed regions of exactly --steps steps; ms_per_step is the median region",
         "regions_us_per_step": [round(x * 1e3, 3) for x in head_regions],
         "ms_per_step": ms,
         "us_per_step": ms * 1e3,
