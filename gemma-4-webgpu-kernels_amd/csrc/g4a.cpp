@@ -123,6 +123,7 @@ struct g4a_ctx {
     hipFunction_t linear_f32_words[3] = {};  // f32 weights: (MT, RU) = (1, 2), (1, 8), (4, 4)
     hipFunction_t linear_f32_elem = nullptr;
     hipFunction_t ew = nullptr;              // elementwise ops
+    hipFunction_t u32_add = nullptr;         // device counters (positions of replayed decode steps)
     hipFunction_t slice_cols = nullptr;
     hipFunction_t rms_rows = nullptr;        // (residual +) RMSNorm (* scalar) over rows of any width
     hipFunction_t embed_f32 = nullptr;
@@ -636,6 +637,7 @@ int g4a_create_with(int device, const char* hsaco_path, const g4a_options* opts,
             if (int rc = get_fn(ctx, &ctx->linear_f32_words[v], f32_words[v])) return bail(rc);
         if (int rc = get_fn(ctx, &ctx->linear_f32_elem, "g4a_linear_f32_elem")) return bail(rc);
         if (int rc = get_fn(ctx, &ctx->ew, "g4a_ew")) return bail(rc);
+        if (int rc = get_fn(ctx, &ctx->u32_add, "g4a_u32_add")) return bail(rc);
         if (int rc = get_fn(ctx, &ctx->slice_cols, "g4a_slice_cols")) return bail(rc);
         if (int rc = get_fn(ctx, &ctx->rms_rows, "g4a_rms_rows")) return bail(rc);
         if (int rc = get_fn(ctx, &ctx->embed_f32, "g4a_embed_rows_f32")) return bail(rc);
@@ -790,7 +792,8 @@ int stage_positions(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bo
 // Enqueues an analysed attention call. With combine == false a multi-split
 // decode leaves its partials in the workspace (the caller merges them). With
 // noalloc the call allocates nothing: its scratch is the static array.
-int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool combine, bool noalloc = false) {
+int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool combine, bool noalloc = false,
+                  const uint32_t* dpos = nullptr) {
     const g4a_attn_plan& pl = an.plan;
     if (a->T == 0) return G4A_OK;
     const size_t out_bytes = size_t(a->T) * a->Hq * a->Dv * sizeof(float);
@@ -922,6 +925,7 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
     dp.window = a->sliding_window;
     dp.scale = a->scale;
     dp.softcap = a->attn_softcap;
+    dp.dpos = dpos;
     const int d512 = a->Dh == 512 ? 1 : 0;
     const int g8 = group == 8 ? 1 : 0;
     if (pl.kernel == G4A_KERNEL_DECODE_SHORT) {
@@ -972,6 +976,34 @@ int g4a_attention_noalloc(g4a_ctx* ctx, const g4a_attn_args* a) {
     Analysis an;
     if (int rc = analyse(ctx, a, &an, true)) return rc;
     return attention_run(ctx, a, an, true, /*noalloc=*/true);
+}
+
+int g4a_attention_devpos(g4a_ctx* ctx, const g4a_attn_args* a, const uint32_t* pos) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (!a || !pos) return fail(ctx, G4A_E_ARG, "null args / device position");
+    if (a->T != 1) return fail(ctx, G4A_E_UNSUPPORTED, "a device-position decode step has one query (T = %u)", a->T);
+    if (a->q_pos || a->k_pos)
+        return fail(ctx, G4A_E_ARG, "a device-position decode step takes contiguous positions (q_pos, k_pos NULL)");
+    if (a->S == 0) return fail(ctx, G4A_E_ARG, "S (the most keys a replay sees) must be at least 1");
+    if (uint64_t(a->k_pos0) + a->S - 1 >= (uint64_t(1) << 32))
+        return fail(ctx, G4A_E_ARG, "k_pos0 %u + S %u passes 2^32", a->k_pos0, a->S);
+    // planned for the largest key range: the query at the last of the S keys
+    g4a_attn_args m = *a;
+    m.q_pos0 = a->k_pos0 + a->S - 1;
+    Analysis an;
+    if (int rc = analyse(ctx, &m, &an, true)) return rc;
+    if (an.plan.kernel != G4A_KERNEL_DECODE && an.plan.kernel != G4A_KERNEL_DECODE_SHORT)
+        return fail(ctx, G4A_E_UNSUPPORTED, "a device-position decode step runs on the decode kernels (groups of 4 "
+                    "or 8 heads, head_dim 256 or 512); this shape plans kernel %u", an.plan.kernel);
+    return attention_run(ctx, &m, an, true, false, pos);
+}
+
+int g4a_u32_add(g4a_ctx* ctx, uint32_t* counters, uint32_t n, uint32_t inc) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (n == 0) return G4A_OK;
+    if (!counters) return fail(ctx, G4A_E_ARG, "null counters");
+    G4aCounterParams p{counters, n, inc};
+    return launch(ctx, ctx->u32_add, dim3((n + 255) / 256, 1, 1), dim3(256, 1, 1), p, "counter add");
 }
 
 int g4a_attention_batch(g4a_ctx* ctx, const g4a_attn_args* args, uint32_t n) {
@@ -1242,7 +1274,7 @@ int sincos_table(g4a_ctx* ctx, float theta, uint32_t rot, const float* freq_host
 // One g4a_norm_rope launch over up to three row segments.
 int norm_rope_launch(g4a_ctx* ctx, G4aNormRopeSeg* segs, uint32_t nseg, uint32_t T, uint32_t Dh, uint32_t rot,
                      const uint32_t* positions, uint32_t pos0, float theta, float eps, uint32_t cache_row,
-                     uint32_t ring_cap) {
+                     uint32_t ring_cap, const uint32_t* dpos = nullptr, uint32_t dpos_max = 0) {
     if (Dh == 0 || Dh % 4 != 0 || Dh > 1024)
         return fail(ctx, G4A_E_UNSUPPORTED, "head_dim %u: RMSNorm/RoPE rows need head_dim %% 4 == 0 and <= 1024", Dh);
     if (rot % 2 != 0 || rot > Dh) return fail(ctx, G4A_E_ARG, "rotary_dim %u must be even and <= head_dim %u", rot, Dh);
@@ -1264,6 +1296,8 @@ int norm_rope_launch(g4a_ctx* ctx, G4aNormRopeSeg* segs, uint32_t nseg, uint32_t
     p.cache_row = cache_row;
     p.ring_cap = ring_cap;
     p.pos0 = pos0;
+    p.dpos = dpos;
+    p.max_pos = dpos_max;
     bool needs_rope = false;
     for (uint32_t i = 0; i < nseg; ++i) {
         needs_rope |= segs[i].rope != 0;
@@ -1271,7 +1305,7 @@ int norm_rope_launch(g4a_ctx* ctx, G4aNormRopeSeg* segs, uint32_t nseg, uint32_t
     }
     if (needs_rope && rot) {
         if (int rc = freq_table(ctx, theta, rot, &p.freq)) return rc;
-        uint32_t max_pos = pos0 + (T ? T - 1 : 0);
+        uint32_t max_pos = dpos ? dpos_max : pos0 + (T ? T - 1 : 0);
         if (positions) {
             bool contig = true;
             max_pos = 0;
@@ -1748,7 +1782,9 @@ int g4a_rope(g4a_ctx* ctx, const float* x, float* y, uint32_t T, uint32_t heads,
     return norm_rope_launch(ctx, &seg, 1, T, head_dim, rotary_dim, positions, pos0, theta, 0.0f, 0, 0);
 }
 
-int g4a_attn_producer(g4a_ctx* ctx, const g4a_producer_args* a) {
+namespace {
+
+int producer_run(g4a_ctx* ctx, const g4a_producer_args* a, const uint32_t* dpos, uint32_t dpos_max) {
     if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
     if (!a) return fail(ctx, G4A_E_ARG, "null args");
     if (!a->q || !a->q_out) return fail(ctx, G4A_E_ARG, "null q / q_out");
@@ -1766,7 +1802,19 @@ int g4a_attn_producer(g4a_ctx* ctx, const g4a_producer_args* a) {
         segs[n++] = G4aNormRopeSeg{a->v, nullptr, a->v_cache, a->Hkv, 1u, 0u, 1u, first};
     }
     return norm_rope_launch(ctx, segs, n, a->T, a->Dh, a->rotary_dim, a->positions, a->pos0, a->theta, a->eps,
-                            a->cache_row, a->kv_ring_cap);
+                            a->cache_row, a->kv_ring_cap, dpos, dpos_max);
+}
+
+}  // namespace
+
+int g4a_attn_producer(g4a_ctx* ctx, const g4a_producer_args* a) { return producer_run(ctx, a, nullptr, 0); }
+
+int g4a_attn_producer_devpos(g4a_ctx* ctx, const g4a_producer_args* a, const uint32_t* pos, uint32_t max_pos) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (!a || !pos) return fail(ctx, G4A_E_ARG, "null args / device position");
+    if (a->T != 1) return fail(ctx, G4A_E_UNSUPPORTED, "a device-position producer step has one token (T = %u)", a->T);
+    if (a->positions) return fail(ctx, G4A_E_ARG, "a device-position producer step takes its position from `pos`");
+    return producer_run(ctx, a, pos, max_pos);
 }
 
 struct g4a_graph {

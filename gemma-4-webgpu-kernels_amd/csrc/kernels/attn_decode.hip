@@ -56,6 +56,24 @@ __device__ __forceinline__ float score_epilogue(float dot, float scale, float so
 
 typedef float f4v __attribute__((ext_vector_type(4)));  // MFMA accumulator (4 VGPRs)
 
+// A decode step whose query position lives in device memory (G4aDecodeParams::dpos,
+// g4a_attention_devpos): the position is read at run time and the key range follows
+// from it (keys k_pos0 .. qpos, the last `window` of them), so a captured step
+// replays at whatever position the counter holds. The planned k_end bounds the
+// range: a counter past the plan reads no key beyond it.
+__device__ __forceinline__ G4aDecodeParams at_device_pos(const G4aDecodeParams& p) {
+    G4aDecodeParams r = p;
+    if (p.dpos) {
+        const uint32_t qp = __builtin_amdgcn_readfirstlane(*p.dpos);
+        const uint32_t n = qp >= p.k_pos0 ? qp - p.k_pos0 + 1u : 0u;  // keys at or before the query
+        const uint32_t lo = (p.window && n > p.window) ? n - p.window : 0u;
+        r.q_pos0 = qp;
+        r.k_end = min(n, p.k_end);
+        r.k_start = min(lo, r.k_end);
+    }
+    return r;
+}
+
 // Split partials: the acc value of row ih (= query * Hq + head), split s, dim d
 // sits at (ih * nsplit + s) * DH + d: a split's row of a head is one contiguous
 // run of DH floats, so the decode kernels' final stores are whole 2 KiB rows
@@ -1628,14 +1646,19 @@ __device__ __forceinline__ void generic_attention(const G4aGenericParams& p) {
 }  // namespace
 
 extern "C" {
+// the contiguous-position single-call kernels also take a device position (at_device_pos)
 __global__ __launch_bounds__(512) void g4a_decode_d256_g8(G4aDecodeParams p) {
-    decode_wave<256, false>(p, blockIdx.x, blockIdx.y);
+    decode_wave<256, false>(at_device_pos(p), blockIdx.x, blockIdx.y);
 }
 __global__ __launch_bounds__(512) void g4a_decode_d512_g8(G4aDecodeParams p) {
-    decode_wave<512, false>(p, blockIdx.x, blockIdx.y);
+    decode_wave<512, false>(at_device_pos(p), blockIdx.x, blockIdx.y);
 }
-__global__ __launch_bounds__(512) void g4a_decode_d256_g4(G4aDecodeParams p) { decode_split<256, 4, false>(p); }
-__global__ __launch_bounds__(512) void g4a_decode_d512_g4(G4aDecodeParams p) { decode_split<512, 4, false>(p); }
+__global__ __launch_bounds__(512) void g4a_decode_d256_g4(G4aDecodeParams p) {
+    decode_split<256, 4, false>(at_device_pos(p));
+}
+__global__ __launch_bounds__(512) void g4a_decode_d512_g4(G4aDecodeParams p) {
+    decode_split<512, 4, false>(at_device_pos(p));
+}
 __global__ __launch_bounds__(512) void g4a_decode_d256_g8_kpos(G4aDecodeParams p) {
     decode_wave<256, true>(p, blockIdx.x, blockIdx.y);
 }
@@ -1645,23 +1668,23 @@ __global__ __launch_bounds__(512) void g4a_decode_d512_g8_kpos(G4aDecodeParams p
 __global__ __launch_bounds__(512) void g4a_decode_d256_g4_kpos(G4aDecodeParams p) { decode_split<256, 4, true>(p); }
 __global__ __launch_bounds__(512) void g4a_decode_d512_g4_kpos(G4aDecodeParams p) { decode_split<512, 4, true>(p); }
 __global__ __launch_bounds__(256) void g4a_decode_short_d256(G4aDecodeParams p) {
-    decode_short<256>(p, blockIdx.x, blockIdx.y);
+    decode_short<256>(at_device_pos(p), blockIdx.x, blockIdx.y);
 }
 __global__ __launch_bounds__(256) void g4a_decode_short_d512(G4aDecodeParams p) {
-    decode_short<512>(p, blockIdx.x, blockIdx.y);
+    decode_short<512>(at_device_pos(p), blockIdx.x, blockIdx.y);
 }
 // DS workgroups per split (grid x = DS * splits): workgroup DS s + dh owns output dims part dh
 __global__ __launch_bounds__(256) void g4a_decode_short2_d256(G4aDecodeParams p) {
-    decode_short<256, 2>(p, blockIdx.x >> 1, blockIdx.y, blockIdx.x & 1u);
+    decode_short<256, 2>(at_device_pos(p), blockIdx.x >> 1, blockIdx.y, blockIdx.x & 1u);
 }
 __global__ __launch_bounds__(256) void g4a_decode_short2_d512(G4aDecodeParams p) {
-    decode_short<512, 2>(p, blockIdx.x >> 1, blockIdx.y, blockIdx.x & 1u);
+    decode_short<512, 2>(at_device_pos(p), blockIdx.x >> 1, blockIdx.y, blockIdx.x & 1u);
 }
 __global__ __launch_bounds__(256) void g4a_decode_short4_d256(G4aDecodeParams p) {
-    decode_short<256, 4>(p, blockIdx.x >> 2, blockIdx.y, blockIdx.x & 3u);
+    decode_short<256, 4>(at_device_pos(p), blockIdx.x >> 2, blockIdx.y, blockIdx.x & 3u);
 }
 __global__ __launch_bounds__(256) void g4a_decode_short4_d512(G4aDecodeParams p) {
-    decode_short<512, 4>(p, blockIdx.x >> 2, blockIdx.y, blockIdx.x & 3u);
+    decode_short<512, 4>(at_device_pos(p), blockIdx.x >> 2, blockIdx.y, blockIdx.x & 3u);
 }
 __global__ __launch_bounds__(256) void g4a_decode_short_batch_d256(G4aBatchParams b) { decode_short_batch<256>(b); }
 __global__ __launch_bounds__(256) void g4a_decode_short_batch_d512(G4aBatchParams b) { decode_short_batch<512>(b); }

@@ -88,9 +88,16 @@ __device__ __forceinline__ void embed_rows_f32(const G4aEmbedF32Params& p) {
     }
 }
 
+// counters[i] += inc (u32, wrapping): one thread per counter, vector loads and stores
+__device__ __forceinline__ void u32_add(const G4aCounterParams& p) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < p.n) p.c[i] = p.c[i] + p.inc;
+}
+
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(256) void g4a_ew(G4aEwParams p) { ew(p); }
+extern "C" __global__ __launch_bounds__(256) void g4a_u32_add(G4aCounterParams p) { u32_add(p); }
 extern "C" __global__ __launch_bounds__(256) void g4a_slice_cols(G4aSliceColsParams p) { slice_cols(p); }
 extern "C" __global__ __launch_bounds__(256) void g4a_rms_rows(G4aRmsRowsParams p) { rms_rows(p); }
 extern "C" __global__ __launch_bounds__(256) void g4a_embed_rows_f32(G4aEmbedF32Params p) { embed_rows_f32(p); }

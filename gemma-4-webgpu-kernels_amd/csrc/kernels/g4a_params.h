@@ -29,6 +29,11 @@ struct G4aDecodeParams {
     uint32_t ring_cap;
     uint32_t window;
     float scale, softcap;
+    // Device position (g4a_attention_devpos), or null. When set (T = 1, contiguous
+    // positions), the query's position is read from it at run time and the key
+    // range follows: keys k_pos0 .. qpos (the last `window` of them), k_end never
+    // past the planned k_end; q_pos0, k_start and k_end above are then the plan's.
+    const uint32_t* dpos;
 };
 
 // One sequence of a batched decode launch (g4a_decode_*_batch_*,
@@ -184,6 +189,11 @@ struct G4aNormRopeParams {
     uint32_t nseg, total_rows;
     uint32_t cache_row, ring_cap;
     float eps;
+    // Device position (g4a_attn_producer_devpos), or null. When set (T = 1): the
+    // token's position and its logical cache row are *dpos, read at run time; a
+    // position past max_pos (the table's and the cache's bound) writes nothing.
+    const uint32_t* dpos;
+    uint32_t max_pos;
 };
 
 // The int8 matrix-core projection (M <= 2): threads per workgroup, and the row
@@ -257,6 +267,14 @@ struct G4aEwParams {
     size_t n;
     float s;
     uint32_t op;
+};
+
+// counters[i] += inc for i < n (u32, wrapping): advances device positions between
+// replays of a captured decode step (g4a_u32_add).
+struct G4aCounterParams {
+    uint32_t* c;
+    uint32_t n;
+    uint32_t inc;
 };
 
 struct G4aSliceColsParams {

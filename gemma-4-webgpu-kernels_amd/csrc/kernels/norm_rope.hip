@@ -55,6 +55,14 @@ __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
     const uint32_t row = blockIdx.x * NR_WAVES + w;
+    // a device position (T = 1) is read at run time; past max_pos the launch writes nothing
+    // (every thread of the grid leaves here, before any barrier)
+    uint32_t pos0 = p.pos0, cache_row = p.cache_row;
+    if (p.dpos) {
+        pos0 = __builtin_amdgcn_readfirstlane(*p.dpos);
+        if (pos0 > p.max_pos) return;
+        cache_row = pos0;
+    }
     // no early return: every wave reaches the workgroup barriers of the norm
     bool live = row < p.total_rows;
     // segment of this row (rows are segment-major: seg s covers T * heads_s rows)
@@ -143,7 +151,7 @@ __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
         __builtin_amdgcn_wave_barrier();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const uint32_t rot = p.rotary_dim, half = rot / 2;
-        const uint32_t ipos = p.pos ? p.pos[t] : p.pos0 + t;
+        const uint32_t ipos = p.pos ? p.pos[t] : pos0 + t;
         const float pos = (float)ipos;
         const bool tab = ipos < p.sc_rows;
         const float2* const sc_row = p.sc + (size_t)(tab ? ipos : 0u) * half;
@@ -173,7 +181,7 @@ __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
     }
     size_t orow = (size_t)t;
     if (S.cache) {
-        const uint64_t lr = (uint64_t)p.cache_row + t;
+        const uint64_t lr = (uint64_t)cache_row + t;
         orow = p.ring_cap ? (size_t)(lr % p.ring_cap) : (size_t)lr;
     }
     float* const yr = S.y + (orow * S.heads + h) * Dh;

@@ -116,6 +116,9 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "g4a_sync": (c_int, [ctxp]),
         "g4a_attention": (c_int, [ctxp, ctypes.POINTER(AttnArgs)]),
         "g4a_attention_noalloc": (c_int, [ctxp, ctypes.POINTER(AttnArgs)]),
+        "g4a_attention_devpos": (c_int, [ctxp, ctypes.POINTER(AttnArgs), vp]),
+        "g4a_attn_producer_devpos": (c_int, [ctxp, ctypes.POINTER(ProducerArgs), vp, ctypes.c_uint32]),
+        "g4a_u32_add": (c_int, [ctxp, vp, ctypes.c_uint32, ctypes.c_uint32]),
         "g4a_attention_batch": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.c_uint32]),
         "g4a_attention_decode_batch": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.c_uint32, _u32p]),
         "g4a_attention_plan": (c_int, [ctxp, ctypes.POINTER(AttnArgs), ctypes.POINTER(AttnPlan)]),
@@ -328,6 +331,16 @@ class Context:
         a, keep = make_args(q, k, v, out, **kw)
         self._check(self.lib.g4a_attention_noalloc(self.handle, ctypes.byref(a)))
 
+    def attention_devpos(self, q: int, k: int, v: int, out: int, pos: int, **kw) -> None:
+        """g4a_attention_devpos: one decode query at the position held by the device u32
+        at `pos`; S (in kw) is the most keys any replay sees."""
+        a, keep = make_args(q, k, v, out, **kw)
+        self._check(self.lib.g4a_attention_devpos(self.handle, ctypes.byref(a), pos))
+
+    def u32_add(self, counters: int, n: int, inc: int) -> None:
+        """g4a_u32_add: n device u32 counters += inc, by a kernel (records into a graph)."""
+        self._check(self.lib.g4a_u32_add(self.handle, counters, n, inc))
+
     @staticmethod
     def prepare_batch(calls: list[dict]) -> tuple:
         """Marshal a list of attention() keyword sets into a g4a_attn_args array
@@ -377,6 +390,14 @@ class Context:
         a = ProducerArgs(q, k or None, v or None, q_norm or None, k_norm or None, q_out, k_cache or None,
                          v_cache or None, T, Hq, Hkv, Dh, rotary_dim, pp, pos0, cache_row, ring_cap, theta, eps)
         self._check(self.lib.g4a_attn_producer(self.handle, ctypes.byref(a)))
+
+    def attn_producer_devpos(self, *, pos, max_pos, q, k=0, v=0, q_norm=0, k_norm=0, q_out, k_cache=0, v_cache=0,
+                             Hq, Hkv, Dh, rotary_dim, ring_cap=0, theta, eps) -> None:
+        """g4a_attn_producer_devpos: one token at the position held by the device u32 at
+        `pos` (written to cache row *pos); positions past max_pos write nothing."""
+        a = ProducerArgs(q, k or None, v or None, q_norm or None, k_norm or None, q_out, k_cache or None,
+                         v_cache or None, 1, Hq, Hkv, Dh, rotary_dim, None, 0, 0, ring_cap, theta, eps)
+        self._check(self.lib.g4a_attn_producer_devpos(self.handle, ctypes.byref(a), pos, max_pos))
 
     # ---- the rest of the backend trait (device pointers) ----
     def ew(self, op: str, a: int, y: int, n: int, b: int = 0, s: float = 0.0) -> None:

@@ -410,6 +410,41 @@ int g4a_capture_end(g4a_ctx *ctx, g4a_graph **graph);
 int g4a_graph_launch(g4a_ctx *ctx, g4a_graph *graph);
 int g4a_graph_destroy(g4a_graph *graph);
 
+/* ---- decode steps at a device position (a captured decode loop) ----------
+ * No counterpart in the reference (it records no graphs). A graph replays the
+ * arguments it captured, so a decode step captured with host positions replays
+ * the same token. These entry points take the token's position from a u32 in
+ * device memory instead, read when the kernels run: a decode step captured
+ * once replays token after token when the graph ends with g4a_u32_add on that
+ * position.
+ *
+ * g4a_attention_devpos: g4a_attention for one query (T = 1, contiguous
+ * positions: q_pos and k_pos NULL) at position *pos over keys at positions
+ * k_pos0, k_pos0 + 1, ... (logical rows 0, 1, ..., of a linear cache or ring):
+ * the visible keys are those at or before *pos, the last sliding_window of
+ * them when it is set. args->S is the most keys any replay sees (the query at
+ * position k_pos0 + S - 1 at most); the split plan and workspace are those of
+ * that largest step, q_pos0 is ignored, and a position past it sees only the
+ * first S keys. Results match g4a_attention on the same step, bit for bit
+ * where both run the same kernels with the same split count (a sliding
+ * window's short-kernel step; or g4a_attention with args->splits set to the
+ * largest step's count); the splits past the step's keys are empty and merge
+ * as zeros. Refused (G4A_E_UNSUPPORTED) for shapes that do not run on the
+ * decode kernels.
+ *
+ * g4a_attn_producer_devpos: g4a_attn_producer for one token (T = 1,
+ * positions NULL) at position *pos, written to logical cache row *pos (pos0
+ * and cache_row are ignored). max_pos bounds the position: the RoPE tables
+ * are built up to it by this call (so a capture of it needs no table growth),
+ * and a position past it writes nothing. For a linear cache, max_pos must be
+ * a row the cache holds.
+ *
+ * g4a_u32_add: counters[i] += inc (wrapping) for i < n, by a kernel (so it
+ * records into a graph). */
+int g4a_attention_devpos(g4a_ctx *ctx, const g4a_attn_args *args, const uint32_t *pos);
+int g4a_attn_producer_devpos(g4a_ctx *ctx, const g4a_producer_args *args, const uint32_t *pos, uint32_t max_pos);
+int g4a_u32_add(g4a_ctx *ctx, uint32_t *counters, uint32_t n, uint32_t inc);
+
 /* ---- timing (HIP events on the context's stream) ----------------------- */
 int g4a_timer_start(g4a_ctx *ctx);
 /* Records the stop event, waits for it and returns the elapsed milliseconds. */

@@ -5,7 +5,8 @@
 //     explicit position arrays and forced splits (the key-range trim of
 //     rust/src/backend_wgpu.rs:924-936, the split choice, workspace sizing),
 //     checking the plan's invariants;
-//   - argument errors, g4a_create without a device, and option validation;
+//   - argument errors (also of the device-position entry points), g4a_create
+//     without a device, and option validation;
 //   - the oracle's attention, rms_norm, rope, projections and embeddings on
 //     small inputs, including empty ones.
 // Any sanitizer report aborts the process (halt_on_error); exit status 0 = clean.
@@ -129,6 +130,17 @@ void error_paths() {
         check(ctx == nullptr, "a failed create returns no context");
     }
     check(g4a_create(0, nullptr, nullptr) != G4A_OK, "null out refused");
+    // the device-position entry points refuse a missing context or arguments before any device work
+    g4a_attn_args d{};
+    d.T = 1;
+    d.S = 100;
+    d.Hq = 8;
+    d.Hkv = 1;
+    d.Dh = d.Dv = 256;
+    check(g4a_attention_devpos(nullptr, &d, nullptr) != G4A_OK, "devpos attention without a context refused");
+    g4a_producer_args pa{};
+    check(g4a_attn_producer_devpos(nullptr, &pa, nullptr, 0) != G4A_OK, "devpos producer without a context refused");
+    check(g4a_u32_add(nullptr, nullptr, 1, 1) != G4A_OK, "counter add without a context refused");
 }
 
 void oracle_paths() {
