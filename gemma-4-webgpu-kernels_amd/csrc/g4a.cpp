@@ -895,7 +895,8 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
                             dim3(512, 1, 1), pp, "prefill", true))
             return rc;
         if (pp.nbig == 0) return G4A_OK;
-        return launch(ctx, ctx->prefill_merge, dim3(pp.nbig, a->Hkv, 1), dim3(512, 1, 1), pp, "prefill merge");
+        // one 4-wave workgroup per (split block, dim half, kv head)
+        return launch(ctx, ctx->prefill_merge, dim3(2 * pp.nbig, a->Hkv, 1), dim3(256, 1, 1), pp, "prefill merge");
     }
     // split-K flash-decode (+ combine)
     const uint32_t *qd = nullptr, *kd = nullptr;

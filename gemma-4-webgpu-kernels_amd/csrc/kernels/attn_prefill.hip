@@ -1315,35 +1315,54 @@ __device__ __forceinline__ void prefill_dsplit(const G4aPrefillParams& p) {
 }
 
 // Merge of the two halves of each split query block of prefill_dsplit:
-// workgroup = (split block, kv head), wave w = the producing waves' (row block,
-// dim half); out = (O0 e^{m0-M} + O1 e^{m1-M}) / (l0 e^{m0-M} + l1 e^{m1-M}).
+// workgroup = (split block, dim half, kv head), wave w = the producing waves'
+// (row block w, dim half); out = (O0 e^{m0-M} + O1 e^{m1-M}) / (l0 e^{m0-M} + l1 e^{m1-M}).
+// Every load of a thread is issued before the first use (the stores to `out`
+// would otherwise keep the compiler from moving later loads above them: one
+// memory round trip per 8 loads).
 template <int DH>
 __device__ __forceinline__ void prefill_merge(const G4aPrefillParams& p) {
     using C = DsplitCfg<DH>;
     constexpr int HD = C::HD, NCH = C::NCH;
     const int tid = threadIdx.x, lane = tid & 63;
-    const int w = tid >> 6;
-    const int rb = w & 3, dhf = w >> 2;
+    const int rb = tid >> 6, dhf = blockIdx.x & 1;
+    const int w = rb + 4 * dhf;  // the producing wave
     const int g = lane >> 4, rl = lane & 15;
     const uint32_t kvh = blockIdx.y;
     const uint32_t NB = (p.T + 7) / 8;
-    const uint32_t blk = NB - p.nbig + blockIdx.x;
+    const uint32_t sb = blockIdx.x >> 1;
+    const uint32_t blk = NB - p.nbig + sb;
     const uint32_t qw = blk * 8 + 2 * rb;
     const uint32_t h0 = kvh * 8;
-    const uint32_t bi = kvh * p.nbig + blockIdx.x;
-    const float* const p0 = p.part + ((size_t)(bi * 2 + 0) * 8 + w) * C::PART_WAVE;
-    const float* const p1 = p.part + ((size_t)(bi * 2 + 1) * 8 + w) * C::PART_WAVE;
+    const uint32_t bi = kvh * p.nbig + sb;
+    const float* __restrict__ const p0 = p.part + ((size_t)(bi * 2 + 0) * 8 + w) * C::PART_WAVE;
+    const float* __restrict__ const p1 = p.part + ((size_t)(bi * 2 + 1) * 8 + w) * C::PART_WAVE;
+    float x0[4][NCH][4], x1[4][NCH][4], l0[4], m0[4], l1[4], m1[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = 4 * g + r;
+        l0[r] = p0[NCH * 16 * 64 + row];
+        m0[r] = p0[NCH * 16 * 64 + 16 + row];
+        l1[r] = p1[NCH * 16 * 64 + row];
+        m1[r] = p1[NCH * 16 * 64 + 16 + row];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int idx = ((c * 4 + e) * 4 + r) * 64 + lane;
+                x0[r][c][e] = p0[idx];
+                x1[r][c][e] = p1[idx];
+            }
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int row = 4 * g + r;
         const uint32_t qi = qw + (row >> 3);
         if (qi >= p.T) continue;
-        const float l0 = p0[NCH * 16 * 64 + row], m0 = p0[NCH * 16 * 64 + 16 + row];
-        const float l1 = p1[NCH * 16 * 64 + row], m1 = p1[NCH * 16 * 64 + 16 + row];
-        const float M = fmaxf(m0, m1);
-        const float e0 = (m0 == NEG_INF) ? 0.0f : expf(m0 - M);
-        const float e1 = (m1 == NEG_INF) ? 0.0f : expf(m1 - M);
-        const float L = l0 * e0 + l1 * e1;
+        const float M = fmaxf(m0[r], m1[r]);
+        const float e0 = (m0[r] == NEG_INF) ? 0.0f : expf(m0[r] - M);
+        const float e1 = (m1[r] == NEG_INF) ? 0.0f : expf(m1[r] - M);
+        const float L = l0[r] * e0 + l1[r] * e1;
         const float inv = L > 0.0f ? 1.0f / L : 0.0f;
         const float a0 = e0 * inv, a1 = e1 * inv;
         float* orow = p.out + ((size_t)qi * p.Hq + h0 + (row & 7)) * DH + HD * dhf + 4 * rl;
@@ -1351,10 +1370,7 @@ __device__ __forceinline__ void prefill_merge(const G4aPrefillParams& p) {
         for (int c = 0; c < NCH; ++c) {
             float o[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int idx = ((c * 4 + e) * 4 + r) * 64 + lane;
-                o[e] = p0[idx] * a0 + p1[idx] * a1;
-            }
+            for (int e = 0; e < 4; ++e) o[e] = x0[r][c][e] * a0 + x1[r][c][e] * a1;
             *reinterpret_cast<float4*>(orow + 64 * c) = make_float4(o[0], o[1], o[2], o[3]);
         }
     }
@@ -1365,6 +1381,6 @@ __device__ __forceinline__ void prefill_merge(const G4aPrefillParams& p) {
 extern "C" {
 __global__ __launch_bounds__(512) void g4a_prefill2_d256(G4aPrefillParams p) { prefill_pair<256>(p); }
 __global__ __launch_bounds__(512) void g4a_prefill2_d512(G4aPrefillParams p) { prefill_dsplit<512>(p); }
-__global__ __launch_bounds__(512) void g4a_prefill_merge_d512(G4aPrefillParams p) { prefill_merge<512>(p); }
+__global__ __launch_bounds__(256) void g4a_prefill_merge_d512(G4aPrefillParams p) { prefill_merge<512>(p); }
 __global__ __launch_bounds__(256) void g4a_split_kv(G4aSplitParams p) { split_kv(p); }
 }
