@@ -234,12 +234,14 @@ def oracle_module():
     return oracle
 
 
-def _schedule_graph(ctx, token, steps, warmup, algo):
-    """The schedule's calls captured once into a HIP graph, replayed back to back:
-    µs per token, median of REGIONS regions of `steps` replays."""
+def _graph_ms(ctx, record, steps, warmup, reset=None):
+    """`record()` (the calls of one token) captured once into a HIP graph and replayed
+    back to back: ms per replay, median of REGIONS regions of `steps` replays after
+    the --warmup replays and the time-based warm-up. `reset()`, when given, runs
+    (eagerly) before every batch of replays (it rewinds a device position)."""
     ctx.capture_begin()
     try:
-        ctx.attention_batch(token)
+        record()
     except g4a.G4aError:
         try:  # close the capture; it reports the same failure and makes no graph
             ctx.capture_end().free()
@@ -248,25 +250,31 @@ def _schedule_graph(ctx, token, steps, warmup, algo):
         raise
     graph = ctx.capture_end()
     try:
+        if reset:
+            reset()
         for _ in range(max(warmup, 1)):
             graph.launch()
         ctx.sync()
 
         def replay():
+            if reset:
+                reset()
             for _ in range(steps):
                 graph.launch()
             ctx.sync()
         warm_up(replay)
         times = []
         for _ in range(REGIONS):
+            if reset:
+                reset()
+                ctx.sync()
             ctx.timer_start()
             for _ in range(steps):
                 graph.launch()
             times.append(ctx.timer_stop() / steps)
     finally:
         graph.free()
-    ms_graph = float(np.median(times))
-    return {"us_per_token_graph": ms_graph * 1e3, "GB_s_graph": algo / (ms_graph * 1e-3) / 1e9}
+    return float(np.median(times))
 
 
 def schedule_35_layers(ctx, steps, warmup, cpu=True, graph=True):
@@ -309,9 +317,34 @@ def schedule_35_layers(ctx, steps, warmup, cpu=True, graph=True):
         res["graph"] = "not measured (--no-graph)"
     else:
         try:
-            res.update(_schedule_graph(ctx, token, steps, warmup, algo))
+            ms_graph = _graph_ms(ctx, lambda: ctx.attention_batch(token), steps, warmup)
+            res.update(us_per_token_graph=ms_graph * 1e3, GB_s_graph=algo / (ms_graph * 1e-3) / 1e9)
         except g4a.G4aError as e:
             res["graph_error"] = str(e)
+        # the decode loop a server replays: the token captured once with its position in device
+        # memory (g4a_attention_devpos, planned for S keys) and the position's increment; each
+        # region rewinds the position so its replays run at positions S - steps .. S - 1
+        pos = ctx.empty((1,), np.uint32)
+        try:
+            def record_loop():
+                for kw in token:
+                    kw2 = dict(kw)
+                    q, k, v, out = kw2.pop("q"), kw2.pop("k"), kw2.pop("v"), kw2.pop("out")
+                    ctx.attention_devpos(q, k, v, out, pos.ptr, **kw2)
+                ctx.u32_add(pos.ptr, 1, 1)
+
+            def rewind():
+                ctx.h2d(pos.ptr, np.array([S - steps], np.uint32))
+            rewind()
+            record_loop()  # once eagerly: the plans' workspace exists before the capture
+            ms_loop = _graph_ms(ctx, record_loop, steps, warmup, reset=rewind)
+            res.update(us_per_token_loop=ms_loop * 1e3,
+                       loop="the token captured once with device positions (g4a_attention_devpos + "
+                            "g4a_u32_add), replayed at advancing positions")
+        except g4a.G4aError as e:
+            res["loop_error"] = str(e)
+        finally:
+            pos.free()
     for a in list(qs) + list(outs) + [x for kv in caches.values() for x in kv]:
         a.free()
     return res
