@@ -277,6 +277,16 @@ def _graph_ms(ctx, record, steps, warmup, reset=None):
     return float(np.median(times))
 
 
+def graph_call_us(ctx, call, n):
+    """µs per call of call(0) .. call(n-1) run back to back: the n calls captured once
+    into a HIP graph (no host work between them) and replayed, the median of REGIONS
+    regions of 5 replays after the time-based warm-up. The launch-bound extras report
+    this beside their per-dispatch event time, which, with the calls issued one by
+    one from Python, includes each dispatch's own launch latency and varies by up
+    to 2x between runs."""
+    return _graph_ms(ctx, lambda: [call(i) for i in range(n)], 5, 1) * 1e3 / n
+
+
 def schedule_35_layers(ctx, steps, warmup, cpu=True, graph=True):
     """one token of the 35-layer Gemma-4-E2B attention schedule at 32768 context.
     Layers 4,9,...,34 are global (hd512, full context); the rest local (hd256, 512-slot ring).
@@ -450,10 +460,11 @@ PRODUCER_CONFIGS = [
 ]
 
 
-def producer(ctx, T, Dh, theta, rot, pos0, ring_cap, steps, cpu_reps=3):
+def producer(ctx, T, Dh, theta, rot, pos0, ring_cap, steps, cpu_reps=3, graph=True):
     """The attention producer of one layer (per-head q/k RMSNorm + partial RoPE, v norm,
-    K/V rows into the cache): kernel time per call from dispatch-attached events (a
-    Python loop issues the calls, so host time is not what is measured), and the CPU
+    K/V rows into the cache): µs per call with `steps` calls back to back, replayed
+    from a captured graph (the rates come from it); the kernel time per dispatch from
+    events attached to calls issued one by one from Python beside it; and the CPU
     oracle's composition of the same ops on the host."""
     sys.path.insert(0, str(REPO / "oracle"))
     import oracle
@@ -473,6 +484,12 @@ def producer(ctx, T, Dh, theta, rot, pos0, ring_cap, steps, cpu_reps=3):
         ctx.sync()
     warm_up(run)
     kms = kernel_regions(ctx, run)
+    call_us = None
+    if graph:
+        try:
+            call_us = graph_call_us(ctx, lambda i: ctx.attn_producer(**kw), steps)
+        except g4a.G4aError:
+            pass
     for a in (q, k, v, w, qo, kc, vc):
         a.free()
     pos = np.arange(pos0, pos0 + T, dtype=np.uint32)
@@ -481,10 +498,13 @@ def producer(ctx, T, Dh, theta, rot, pos0, ring_cap, steps, cpu_reps=3):
         t0 = time.perf_counter()
         oracle.producer(q_h, k_h, v_h, w_h, w_h, pos, theta, rot, 1e-6)
         times.append(time.perf_counter() - t0)
-    us = kms * 1e3
     b = producer_bytes(T, Dh)
-    return {"kernel_us": us, "GB_s": b / (us * 1e-6) / 1e9, "frac_hbm_peak": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-            "bytes": b, "cpu_oracle_us": float(np.median(times)) * 1e6, "cpu_threads": 1}
+    us = call_us if call_us is not None else kms * 1e3
+    return {"us_per_call": call_us, "kernel_dispatch_us": kms * 1e3, "GB_s": b / (us * 1e-6) / 1e9,
+            "frac_hbm_peak": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "bytes": b,
+            "timing": "us_per_call: calls back to back, replayed from a captured graph (rates from it); "
+                      "kernel_dispatch_us: one event pair per dispatch issued from Python",
+            "cpu_oracle_us": float(np.median(times)) * 1e6, "cpu_threads": 1}
 
 
 PREFILL_CONFIGS = [("configs[3a] prefill hd256 T2048 window512", 2048, 256, 512),
@@ -621,10 +641,11 @@ def linear_bytes(op, N, K, bits, M):
     return nw * (N * K * bits // 8 + 4 * N) + 4 * M * K + 4 * M * N
 
 
-def linear_bench(ctx, op, N, K, bits, M, steps, cpu=True):
-    """Kernel µs per call from dispatch-attached events over `steps` calls, the
-    weights rotated over enough copies to pass the 256 MB MALL; and the CPU
-    oracle on the same call (1 thread)."""
+def linear_bench(ctx, op, N, K, bits, M, steps, cpu=True, graph=True):
+    """µs per call with max(`steps`, copies) calls back to back, replayed from a captured
+    graph (the rates come from it), the weights rotated over enough copies to pass the
+    256 MB MALL; the kernel time per dispatch from events on calls issued one by one from
+    Python beside it; and the CPU oracle on the same call (1 thread)."""
     sys.path.insert(0, str(REPO / "oracle"))
     import oracle
     nw = 2 if op == "geglu" else 1
@@ -652,12 +673,21 @@ def linear_bench(ctx, op, N, K, bits, M, steps, cpu=True):
             ctx.linear_q_geglu(pair[0], pair[1], x.ptr, y.ptr, M)
         else:
             ctx.linear_q(pair[0], x.ptr, y.ptr, M)
+    # every pass walks all the copies, so a pass's working set is past the MALL too
+    ncalls = max(steps, copies)
+
     def run():
-        for i in range(steps):
+        for i in range(ncalls):
             call(i)
         ctx.sync()
     warm_up(run)
     kms = kernel_regions(ctx, run)
+    call_us = None
+    if graph:
+        try:
+            call_us = graph_call_us(ctx, call, ncalls)
+        except g4a.G4aError:
+            pass
     for pair in ws:
         for w in pair:
             ctx.free(w.args.qbytes)
@@ -665,10 +695,12 @@ def linear_bench(ctx, op, N, K, bits, M, steps, cpu=True):
         w.free()
     x.free()
     y.free()
-    us = kms * 1e3
+    us = call_us if call_us is not None else kms * 1e3
     b = linear_bytes(op, N, K, bits, M)
-    res = {"kernel_us": us, "GB_s": b / (us * 1e-6) / 1e9, "frac_hbm_peak": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-           "bytes": b, "weight_copies_rotated": copies}
+    res = {"us_per_call": call_us, "kernel_dispatch_us": kms * 1e3, "GB_s": b / (us * 1e-6) / 1e9,
+           "frac_hbm_peak": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "bytes": b, "weight_copies_rotated": copies,
+           "timing": "us_per_call: calls back to back, replayed from a captured graph (rates from it); "
+                     "kernel_dispatch_us: one event pair per dispatch issued from Python"}
     if M >= 16:
         # 2 flops per multiply-add of the projection(s), against the dense bf16 matrix peak
         # (the kernel issues three bf16 MFMAs per multiply-add: x split into three exact parts)
@@ -791,8 +823,9 @@ def main(argv=None):
     ap.add_argument("--quick", action="store_true", help="headline decode only (no extras, no CPU baseline)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
-                    help="leave out the configs[4] HIP-graph replay figure (rocprofv3's kernel trace "
-                         "crashed in the replay's graph launch on this image)")
+                    help="leave out the HIP-graph replay figures (configs[4]'s replayed token, the producer's "
+                         "and the projections' back-to-back calls): rocprofv3's kernel trace crashed in the "
+                         "replay's graph launch on this image")
     ap.add_argument("--only", choices=["decode", "prefill", "schedule", "producer", "batch", "linear", "oproj",
                                        "reference"],
                     default=None,
@@ -830,7 +863,8 @@ def main(argv=None):
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         elif args.only == "linear":
             for name, op, N, K, bits, M in LINEAR_CONFIGS:
-                out[name] = linear_bench(ctx, op, N, K, bits, M, steps=args.steps)
+                out[name] = linear_bench(ctx, op, N, K, bits, M, steps=args.steps, cpu=not args.no_cpu,
+                                         graph=not args.no_graph)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         elif args.only == "batch":
             for name, n, L, Dh, W, cap, holes in BATCH_CONFIGS:
@@ -843,7 +877,7 @@ def main(argv=None):
                                                                                warmup=args.warmup)
         elif args.only == "producer":
             for name, T, Dh, theta, rot, pos0, cap in PRODUCER_CONFIGS:
-                out[name] = producer(ctx, T, Dh, theta, rot, pos0, cap, steps=args.steps)
+                out[name] = producer(ctx, T, Dh, theta, rot, pos0, cap, steps=args.steps, graph=not args.no_graph)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         else:
             out["configs[4] 35-layer schedule @32768"] = schedule_35_layers(ctx, steps=args.steps, warmup=args.warmup,
@@ -921,10 +955,10 @@ def main(argv=None):
             extras[name] = prefill(ctx, T, Dh, W, steps=5, warmup=2, cpu=cpu)
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
         for name, T, Dh, theta, rot, pos0, cap in PRODUCER_CONFIGS:
-            extras[name] = producer(ctx, T, Dh, theta, rot, pos0, cap, steps=50)
+            extras[name] = producer(ctx, T, Dh, theta, rot, pos0, cap, steps=50, graph=not args.no_graph)
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
         for name, op, N, K, bits, M in LINEAR_CONFIGS:
-            extras[name] = linear_bench(ctx, op, N, K, bits, M, steps=100)
+            extras[name] = linear_bench(ctx, op, N, K, bits, M, steps=100, graph=not args.no_graph)
             print(f"[bench] {name}: {extras[name]}", file=sys.stderr, flush=True)
         for name, n, L, Dh, W, cap, holes in BATCH_CONFIGS:
             extras[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=50, warmup=10, holes=holes)
