@@ -1583,14 +1583,23 @@ __device__ __forceinline__ void combine_rows_batch(const G4aBatchParams& b) {
     combine_rows<DH>(cp, blockIdx.x, 0u);
 }
 
-// Generic masked online-softmax attention, one wave per (query, head), for any
-// head dims (Dh <= 1024, Dv <= 1024) and group sizes. Same exact score
-// arithmetic as the fast path; the semantics of rust/src/kernels/attention.wgsl
-// plus the soft-cap of rust/src/backend_cpu.rs:303-305.
+// Generic masked attention, one wave per (query, head) row, for any head dims
+// (Dh <= 1024, Dv <= 1024) and group sizes: the shapes the fast kernels do not
+// take. It follows the CPU backend's row in its order (rust/src/backend_cpu.rs:
+// 286-331) rather than an online softmax, so that nothing but expf / tanhf
+// separates it from the reference: (1) the row maximum of the scores, (2) e_j =
+// exp(s_j - max) and their sum in key order, inv = 1 / sum (0 when the sum is
+// 0), (3) out += (e_j * inv) * v_j in key order, multiply and add rounded
+// separately, weights of 0 skipped. The scores (the exact sequential dot, the
+// scale, the soft-cap of rust/src/backend_cpu.rs:303-305) are recomputed in
+// each pass instead of being stored, so any key count runs without a buffer;
+// the key-order sum and accumulation are dependent chains over the row's keys.
+// The reference GPU's fallback (rust/src/kernels/attention.wgsl) has the same
+// masking semantics with an online softmax.
 __device__ __forceinline__ void generic_attention(const G4aGenericParams& p) {
     constexpr int MAXV = 16;  // Dv <= 64 * MAXV
     __shared__ float qs[1024];
-    __shared__ float pb[64];
+    __shared__ float eb[64];
     const int lane = threadIdx.x;
     const uint32_t h = blockIdx.x, qi = blockIdx.y;
     const uint32_t group = p.Hq / p.Hkv;
@@ -1599,12 +1608,10 @@ __device__ __forceinline__ void generic_attention(const G4aGenericParams& p) {
     const float* __restrict__ qr = p.q + ((size_t)qi * p.Hq + h) * p.Dh;
     for (uint32_t d = lane; d < p.Dh; d += 64) qs[d] = qr[d];
     __syncthreads();
-    float m = NEG_INF, l = 0.0f;
-    float acc[MAXV];
-#pragma unroll
-    for (int e = 0; e < MAXV; ++e) acc[e] = 0.0f;
-    for (uint32_t t0 = p.k_start; t0 < p.k_end; t0 += 64) {
-        const uint32_t nk = min(64u, p.k_end - t0);
+
+    // the score of this lane's key of the 64-key tile at t0 (NEG_INF when masked
+    // or past the tile's nk keys)
+    auto score = [&](uint32_t t0, uint32_t nk) -> float {
         const bool inr = (uint32_t)lane < nk;
         const uint32_t j = inr ? t0 + lane : t0;
         const float* __restrict__ kr = p.k + ((size_t)phys_row(j, p.ring_cap) * p.Hkv + kvh) * p.Dh;
@@ -1612,34 +1619,52 @@ __device__ __forceinline__ void generic_attention(const G4aGenericParams& p) {
         for (uint32_t d = 0; d < p.Dh; ++d) dot = dot + qs[d] * kr[d];
         const uint32_t kp = p.k_pos ? p.k_pos[j] : p.k_pos0 + j;
         const bool vis = inr && kp <= qpos && (p.window == 0 || qpos - kp < p.window);
-        const float sc = vis ? score_epilogue(dot, p.scale, p.softcap) : NEG_INF;
-        const float mn = fmaxf(m, wave_max(sc));
-        const float corr = (m == NEG_INF) ? 0.0f : expf(m - mn);
-        const float pr = (sc == NEG_INF) ? 0.0f : expf(sc - mn);
-        l = l * corr + pr;
-        m = mn;
-#pragma unroll
-        for (int e = 0; e < MAXV; ++e) acc[e] *= corr;
-        pb[lane] = pr;
+        return vis ? score_epilogue(dot, p.scale, p.softcap) : NEG_INF;
+    };
+    // e_j of this lane's key into eb (0 for a masked key: it adds nothing to the sum)
+    auto weights = [&](uint32_t t0, uint32_t nk, float maxv) {
+        const float s = score(t0, nk);
+        eb[lane] = s == NEG_INF ? 0.0f : expf(s - maxv);
         __syncthreads();
+    };
+
+    // 1: the row maximum (the order of a maximum does not matter)
+    float maxv = NEG_INF;
+    for (uint32_t t0 = p.k_start; t0 < p.k_end; t0 += 64)
+        maxv = fmaxf(maxv, wave_max(score(t0, min(64u, p.k_end - t0))));
+    // 2: the sum of the e_j in key order (every lane runs the same chain)
+    float sum = 0.0f;
+    for (uint32_t t0 = p.k_start; t0 < p.k_end; t0 += 64) {
+        const uint32_t nk = min(64u, p.k_end - t0);
+        weights(t0, nk, maxv);
+        for (uint32_t jj = 0; jj < nk; ++jj) sum = sum + eb[jj];
+        __syncthreads();
+    }
+    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    // 3: out += (e_j * inv) * v_j in key order; lane l owns dims l, l + 64, ...
+    float acc[MAXV];
+#pragma unroll
+    for (int e = 0; e < MAXV; ++e) acc[e] = 0.0f;
+    for (uint32_t t0 = p.k_start; t0 < p.k_end; t0 += 64) {
+        const uint32_t nk = min(64u, p.k_end - t0);
+        weights(t0, nk, maxv);
         for (uint32_t jj = 0; jj < nk; ++jj) {
-            const float pj = pb[jj];
+            const float w = eb[jj] * inv;
+            if (w == 0.0f) continue;  // the same for every lane
             const float* __restrict__ vr = p.v + ((size_t)phys_row(t0 + jj, p.ring_cap) * p.Hkv + kvh) * p.Dv;
 #pragma unroll
             for (int e = 0; e < MAXV; ++e) {
                 const uint32_t d = lane + 64 * e;
-                if (d < p.Dv) acc[e] = __builtin_fmaf(pj, vr[d], acc[e]);
+                if (d < p.Dv) acc[e] = acc[e] + w * vr[d];
             }
         }
         __syncthreads();
     }
-    l = wave_sum(l);
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     float* o = p.out + ((size_t)qi * p.Hq + h) * p.Dv;
 #pragma unroll
     for (int e = 0; e < MAXV; ++e) {
         const uint32_t d = lane + 64 * e;
-        if (d < p.Dv) o[d] = acc[e] * inv;
+        if (d < p.Dv) o[d] = acc[e];
     }
 }
 
