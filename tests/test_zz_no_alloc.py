@@ -81,6 +81,47 @@ def test_noalloc_matches_attention_twice(ctx, first, second):
             print(f"  {label}: bit-identical", flush=True)
 
 
+def _draw_noalloc_case(rng, i):
+    Hkv = int(rng.choice([1, 1, 2]))
+    Hq = Hkv * int(rng.choice([8, 8, 8, 4, 2]))
+    Dh = int(rng.choice([256, 256, 512, 512, 64]))
+    T = int(rng.choice([1, 1, 2, 5, 16, 40, 300]))
+    S = int(rng.integers(T, 8000))
+    window = int(rng.choice([0, 0, 512, int(rng.integers(1, 2000))]))
+    softcap = float(rng.choice([0.0, 0.0, 30.0]))
+    scale = float(rng.choice([1.0, 0.0625]))
+    k0 = int(rng.choice([0, int(rng.integers(1, 1000))]))
+    return dict(i=i, T=T, S=S, Hq=Hq, Hkv=Hkv, Dh=Dh, window=window, softcap=softcap, scale=scale, k0=k0)
+
+
+RANDOM_CASES = [_draw_noalloc_case(np.random.default_rng(9100 + i), i) for i in range(16)]
+
+
+@pytest.mark.parametrize("c", RANDOM_CASES, ids=[f"case{c['i']}" for c in RANDOM_CASES])
+def test_noalloc_random_shapes_match_attention(ctx, c):
+    """Seeded random shapes (head groups, head dims, windows, soft-cap, scale, query
+    counts, caches from a non-zero position), one after another on the shared
+    array: g4a_attention_noalloc gives g4a_attention's bits, or, where the call's
+    scratch would pass the array, refuses it and writes nothing."""
+    T, S, k0 = c["T"], c["S"], c["k0"]
+    ins = synth.gemma_inputs(T=T, S=S, Dh=c["Dh"], seed=9200 + c["i"], Hq=c["Hq"], Hkv=c["Hkv"],
+                             q_pos=np.arange(k0 + S - T, k0 + S))
+    ins = synth.AttnInputs(ins.q, ins.k, ins.v, np.arange(k0 + S - T, k0 + S, dtype=np.uint32),
+                           np.arange(k0, k0 + S, dtype=np.uint32))
+    kw = dict(window=c["window"], softcap=c["softcap"], scale=c["scale"])
+    label = (f"random case {c['i']}: T={T} S={S} Hq={c['Hq']} Hkv={c['Hkv']} Dh={c['Dh']} window={c['window']} "
+             f"softcap={c['softcap']} scale={c['scale']} k_pos0={k0}")
+    plan = ctx.plan(T=T, S=S, Hq=c["Hq"], Hkv=c["Hkv"], Dh=c["Dh"], Dv=c["Dh"], q_pos0=k0 + S - T, k_pos0=k0, **kw)
+    if plan.workspace_bytes > g4a.NOALLOC_SCRATCH_BYTES:
+        step(f"{label}: {plan.workspace_bytes} bytes of scratch, past the array: refused")
+        with pytest.raises(g4a.G4aError, match="bytes of scratch"):
+            _run_both(ctx, ins, label, **kw)
+        return
+    got, got_na, _ = _run_both(ctx, ins, label, **kw)
+    assert np.array_equal(got_na, got), f"{label}: noalloc differs from g4a_attention"
+    print(f"  {label}: bit-identical", flush=True)
+
+
 def test_noalloc_refuses_what_needs_an_allocation(ctx):
     ins = synth.gemma_inputs(T=1, S=300, Dh=256, seed=9)
     k_pos = np.arange(300, dtype=np.uint32)
