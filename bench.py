@@ -763,6 +763,51 @@ def decode_configs(ctx, steps_arg, warmup_arg, cpu=True):
     return extras
 
 
+CONTEXT_SWEEP = [1024, 2048, 4096, 8192, 16384, 32768, 65536, 131072, 262144, 524288, 1048576]
+CONTEXT_BASE_KEYS = 131072  # seeded keys generated on the host; longer caches repeat them on the device
+
+
+def context_sweep(ctx, steps, warmup):
+    """hd512 global decode (8 heads over one kv head) across context lengths, cold:
+    µs per step (decode + combine back to back), the decode kernel's dispatch-event
+    time, and their HBM rates. Past Gemma-4-E2B's 131072 keys the cache repeats its
+    first 131072 seeded rows (device copies; the time depends on the bytes only)."""
+    res = {}
+    for S in CONTEXT_SWEEP:
+        base = min(S, CONTEXT_BASE_KEYS)
+        ins = synth.gemma_inputs(T=1, S=base, Dh=512, seed=11)
+        q = ctx.upload(ins.q)
+        out = ctx.empty((1, HQ * 512))
+        row_bytes = 512 * 4
+        kv = []
+        for _ in range(cold_copies(2 * S * row_bytes)):
+            pair = []
+            for src in (ins.k, ins.v):
+                d = ctx.malloc(S * row_bytes)
+                for r0 in range(0, S, base):
+                    n = min(base, S - r0)
+                    ctx.h2d(d + r0 * row_bytes, src[:n])
+                pair.append(d)
+            kv.append(pair)
+        ctx.sync()
+        kw = dict(T=1, S=S, Hq=HQ, Hkv=1, Dh=512, Dv=512, q_pos0=S - 1, k_pos0=0)
+        calls = [[dict(q=q.ptr, k=k, v=v, out=out.ptr, **kw)] for k, v in kv]
+        ms, kms, regions = time_steps(ctx, calls, steps, warmup, min_region_ms=EXTRA_REGION_MS)
+        pl = ctx.plan(**kw)
+        b = decode_bytes(S, 512)
+        res[str(S)] = {"us_per_step": round(ms * 1e3, 2), "kernel_dispatch_us": round(kms * 1e3, 2),
+                       "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
+                       "frac_hbm_peak_kernel": round(b / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3),
+                       "kernel": g4a.KERNEL_NAMES[pl.kernel], "splits": pl.splits, "kv_copies_rotated": len(kv)}
+        print(f"[bench] context {S}: {res[str(S)]}", file=sys.stderr, flush=True)
+        for pair in kv:
+            for d in pair:
+                ctx.free(d)
+        q.free()
+        out.free()
+    return res
+
+
 # The reference's own attention timings (Apple M4, wgpu/Metal, ms per op, wall
 # clock around 60 back-to-back ops: rust/README.md:136-140, rust/src/main.rs:574-587)
 # for the cases of its `bench --kernels` (rust/src/main.rs:544-560) it publishes.
@@ -826,7 +871,7 @@ def main(argv=None):
                          "and the projections' back-to-back calls): rocprofv3's kernel trace crashed in the "
                          "replay's graph launch on this image")
     ap.add_argument("--only", choices=["decode", "prefill", "schedule", "producer", "batch", "linear", "oproj",
-                                       "reference"],
+                                       "reference", "context"],
                     default=None,
                     help="run only these extra workloads (for profiling) and print their JSON line")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
@@ -869,6 +914,8 @@ def main(argv=None):
             for name, n, L, Dh, W, cap, holes in BATCH_CONFIGS:
                 out[name] = batched_decode(ctx, n, L, Dh, W, cap, steps=args.steps, warmup=args.warmup, holes=holes)
                 print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
+        elif args.only == "context":
+            out["hd512 decode across context lengths"] = context_sweep(ctx, args.steps, args.warmup)
         elif args.only == "reference":
             out["reference bench --kernels cases"] = reference_bench(ctx, args.steps, args.warmup, cpu=not args.no_cpu)
         elif args.only == "oproj":
