@@ -48,7 +48,10 @@ constexpr uint32_t SHORT_KEYS = 32;
 // Most visible keys of a batched decode step (1024 splits of the short kernel).
 constexpr uint32_t BATCH_MAX_KEYS = SHORT_KEYS * MAX_SPLITS;
 
-std::string g_create_error;
+// The message of the last failure that had no context (g4a_create, or a call
+// given a NULL context), per thread: two threads that fail at once each read
+// their own.
+thread_local std::string g_create_error;
 
 // Bytes of the static scratch array a call that allocates nothing may use.
 constexpr size_t NOALLOC_SCRATCH_BYTES = G4A_NOALLOC_SCRATCH_BYTES;

@@ -71,7 +71,8 @@ void g4a_default_options(g4a_options *opts);
 int g4a_create_with(int device, const char *hsaco_path, const g4a_options *opts, g4a_ctx **out);
 void g4a_destroy(g4a_ctx *ctx);
 /* Message of the last failed call on this context ("" if none). With a NULL
- * ctx: the message of the last failed g4a_create in this process. */
+ * ctx: the message of the calling thread's last failure that had no context
+ * (a g4a_create, or a call given a NULL context such as a plan query). */
 const char *g4a_last_error(const g4a_ctx *ctx);
 
 /* Device buffers. Replace raw_buf / alloc_in (rust/src/backend_wgpu.rs:371-402)

@@ -100,6 +100,36 @@ def test_argument_errors_are_reported_not_crashed():
     assert "ring" in g4a.load_library().g4a_last_error(None).decode()
 
 
+def test_context_free_errors_are_per_thread():
+    """g4a_last_error(NULL) is the calling thread's own last context-free failure:
+    two threads failing plan queries at once, each with its own error, each read
+    their own message (rust/src/backend_wgpu.rs:283 reports construction errors
+    as a String per call; the C-ABI keeps one per thread)."""
+    import threading
+    lib = g4a.load_library()
+    bad = {"heads": dict(Hq=6, Hkv=4), "ring": dict(S=2048, q_pos0=2047, window=0, ring_cap=512)}
+    seen = {k: [] for k in bad}
+    start = threading.Barrier(2)
+
+    def worker(kind):
+        start.wait()
+        for _ in range(300):
+            kw = dict(T=1, S=300, Hq=8, Hkv=1, Dh=256, Dv=256, q_pos0=299)
+            kw.update(bad[kind])
+            a, keep = g4a.make_args(0, 0, 0, 0, **kw)
+            p = g4a.AttnPlan()
+            rc = lib.g4a_attention_plan(None, ctypes.byref(a), ctypes.byref(p))
+            seen[kind].append((rc, lib.g4a_last_error(None).decode()))
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in bad]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert all(rc == -3 and "multiple of Hkv" in msg for rc, msg in seen["heads"]), seen["heads"][:3]
+    assert all(rc == -3 and "ring" in msg for rc, msg in seen["ring"]), seen["ring"][:3]
+
+
 def test_ring_plan_accepts_window_inside_ring():
     p = _plan(S=40000, q_pos0=39999, window=512, ring_cap=512)
     assert (p.k_start, p.k_end) == (40000 - 512, 40000)
