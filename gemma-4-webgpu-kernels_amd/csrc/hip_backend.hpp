@@ -1,7 +1,7 @@
 // C++ mirror of the reference's backend-agnostic op surface for the attention
 // path (rust/src/backend.rs:59-180), implemented over the C-ABI of libg4a.so.
-// It is what a Rust `HipBackend` does through FFI (INTEGRATION.md shows that
-// binding): same op names, same argument meaning, same conventions:
+// It does what a Rust `HipBackend` would do over the same calls through FFI:
+// same op names, same argument meaning, same conventions:
 //   - ops are infallible: a failing g4a call throws std::runtime_error (the
 //     Rust backend panics, rust/src/backend_wgpu.rs:1077-1078); only
 //     construction reports failure as a value to handle (here: create() throws

@@ -4,8 +4,8 @@
  * This is the drop-in boundary for the attention ops of the reference's
  * backend-agnostic op trait (rust/src/backend.rs:88-180). A Rust `HipBackend`
  * implements `Backend::attention` / `Backend::kv_append` over these calls
- * (see the FFI binding in INTEGRATION.md); the C++ mirror of the trait lives in
- * gemma-4-webgpu-kernels_amd/csrc/hip_backend.hpp.
+ * through an FFI crate that declares them as `extern "C"`; the C++ mirror of
+ * the trait lives in gemma-4-webgpu-kernels_amd/csrc/hip_backend.hpp.
  *
  * Conventions
  *   - Every call returns G4A_OK (0) or a negative g4a_status; the message of
