@@ -745,6 +745,13 @@ int g4a_sync(g4a_ctx* ctx) {
     return G4A_OK;
 }
 
+int g4a_stream(g4a_ctx* ctx, void** stream) {
+    if (!ctx) return fail(ctx, G4A_E_ARG, "null ctx");
+    if (!stream) return fail(ctx, G4A_E_ARG, "null stream out");
+    *stream = static_cast<void*>(ctx->stream);
+    return G4A_OK;
+}
+
 int g4a_attention_plan(g4a_ctx* ctx, const g4a_attn_args* a, g4a_attn_plan* plan) {
     // a query: its failures do not discard an open graph capture
     struct Query {

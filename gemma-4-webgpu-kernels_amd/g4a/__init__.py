@@ -107,6 +107,7 @@ def load_library(path: Path = LIB_PATH) -> ctypes.CDLL:
         "g4a_default_options": (None, [ctypes.POINTER(Options)]),
         "g4a_destroy": (None, [ctxp]),
         "g4a_last_error": (ctypes.c_char_p, [ctxp]),
+        "g4a_stream": (c_int, [ctxp, ctypes.POINTER(vp)]),
         "g4a_malloc": (c_int, [ctxp, sz, ctypes.POINTER(vp)]),
         "g4a_free": (c_int, [ctxp, vp]),
         "g4a_h2d": (c_int, [ctxp, vp, vp, sz]),
@@ -306,6 +307,12 @@ class Context:
 
     def zero(self, dst: int, nbytes: int) -> None:
         self._check(self.lib.g4a_zero(self.handle, dst, nbytes))
+
+    def stream(self) -> int:
+        """The context's HIP stream handle (g4a_stream), e.g. for torch.cuda.ExternalStream."""
+        s = ctypes.c_void_p()
+        self._check(self.lib.g4a_stream(self.handle, ctypes.byref(s)))
+        return s.value
 
     def sync(self) -> None:
         self._check(self.lib.g4a_sync(self.handle))

@@ -91,6 +91,12 @@ int g4a_d2d(g4a_ctx *ctx, void *dst, const void *src, size_t bytes);
 int g4a_zero(g4a_ctx *ctx, void *dst, size_t bytes);
 /* Wait for all work on the context's stream (Backend::flush + device poll). */
 int g4a_sync(g4a_ctx *ctx);
+/* The context's HIP stream (a hipStream_t), for callers that order their own
+ * work against the context's by stream order or events instead of g4a_sync
+ * (e.g. torch.cuda.ExternalStream). No counterpart in the reference, whose
+ * backend hides its queue. The stream stays the context's: do not destroy it,
+ * and do not use it after g4a_destroy. */
+int g4a_stream(g4a_ctx *ctx, void **stream);
 
 /* ---- attention -----------------------------------------------------------
  * Backend::attention (rust/src/backend.rs:119-120) with AttnOpts

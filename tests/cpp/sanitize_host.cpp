@@ -141,6 +141,8 @@ void error_paths() {
     g4a_producer_args pa{};
     check(g4a_attn_producer_devpos(nullptr, &pa, nullptr, 0) != G4A_OK, "devpos producer without a context refused");
     check(g4a_u32_add(nullptr, nullptr, 1, 1) != G4A_OK, "counter add without a context refused");
+    void* stream = nullptr;
+    check(g4a_stream(nullptr, &stream) != G4A_OK && stream == nullptr, "stream query without a context refused");
 }
 
 void oracle_paths() {

@@ -4,6 +4,9 @@ in directly. A g4a context runs on its own stream; work is ordered against
 torch's stream by synchronizing on each side (torch.cuda.synchronize() before,
 Context.sync() after). The results must equal the same calls on buffers the
 library allocated, bit for bit, and the oracle's within the north star's bar.
+A caller may also share the context's stream (g4a_stream, wrapped as
+torch.cuda.ExternalStream) and interleave its own kernels with the library's
+calls in stream order, with no synchronization between them.
 
 The check runs in a child process. The PyTorch wheel carries its own HIP
 runtime under the same soname as /opt/rocm's (libamdhip64.so.7), and the one
@@ -62,6 +65,19 @@ x_d, y_d = ctx.upload(x_h), ctx.empty((1, N))
 ctx.linear_q(own, x_d.ptr, y_d.ptr, 1)
 assert np.array_equal(ty.cpu().numpy(), y_d.to_host()), "projection on torch tensors differs"
 own.free(); x_d.free(); y_d.free()
+
+# the context's stream shared with torch (g4a_stream): torch kernels and library
+# calls in one stream order, with no synchronization between them
+s = torch.cuda.ExternalStream(ctx.stream())
+with torch.cuda.stream(s):
+    q3 = (q * 2.0) * 0.5  # torch kernels on the context's stream: q again, bit for bit
+    out3 = torch.full_like(out, float("nan"))
+    ctx.attention(q3.data_ptr(), k.data_ptr(), v.data_ptr(), out3.data_ptr(), T=1, S=5000, Hq=8, Hkv=1, Dh=512,
+                  Dv=512, q_pos0=4999, k_pos0=0)
+    res3 = out3 + 0.0  # a torch kernel reading the library's output in stream order
+s.synchronize()
+assert np.array_equal(res3.cpu().numpy(), got), "the shared-stream sequence differs"
+print("SHARED STREAM torch -> g4a -> torch in stream order: bit-identical", flush=True)
 ctx.close()
 print("PROJECTION bit-identical to library-owned buffers", flush=True)
 print("INTEROP OK", flush=True)
