@@ -45,6 +45,8 @@ constexpr uint32_t kCombineDims = 32;
 constexpr uint32_t kCombineThreads = 512;
 // Keys per 4-wave workgroup of the short-context decode kernel (two 16-key tiles).
 constexpr uint32_t SHORT_KEYS = 32;
+// splits x head_dim from which a short call's workgroups of one split share an XCD
+constexpr uint64_t SHORT_GROUP_MIN_SPLIT_DIMS = 16384;
 // Most visible keys of a batched decode step (1024 splits of the short kernel).
 constexpr uint32_t BATCH_MAX_KEYS = SHORT_KEYS * MAX_SPLITS;
 
@@ -945,6 +947,10 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
         const uint64_t wg = uint64_t(pl.splits) * a->T * a->Hkv, cus = uint64_t(std::max(ctx->cu_count, 1));
         const uint32_t ds = ctx->short_ds >= 4 && 4 * wg <= cus ? 4u : ctx->short_ds >= 2 && 2 * wg <= cus ? 2u : 1u;
         hipFunction_t fn = ds == 4 ? ctx->decode_short4[d512] : ds == 2 ? ctx->decode_short2[d512] : ctx->decode_short[d512];
+        // the ds workgroups of a split on one XCD once their repeated K reads reach
+        // 2 MiB over the call (splits x 32 keys x Dh x 4 bytes): hd512 from 32 splits,
+        // hd256 from 64; below that, spreading them over the XCDs is as fast or faster
+        dp.xcd_group = ds > 1 && pl.splits % 8 == 0 && uint64_t(pl.splits) * a->Dh >= SHORT_GROUP_MIN_SPLIT_DIMS;
         if (int rc = launch(ctx, fn, dim3(pl.splits * ds, a->T, a->Hkv), dim3(256, 1, 1), dp, "short decode", true))
             return rc;
     } else if (int rc = launch(ctx, ctx->decode[d512][g8][kd ? 1 : 0], dim3(pl.splits, a->T, a->Hkv),
