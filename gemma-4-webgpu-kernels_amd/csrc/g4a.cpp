@@ -45,8 +45,6 @@ constexpr uint32_t kCombineDims = 32;
 constexpr uint32_t kCombineThreads = 512;
 // Keys per 4-wave workgroup of the short-context decode kernel (two 16-key tiles).
 constexpr uint32_t SHORT_KEYS = 32;
-// splits x head_dim from which a short call's workgroups of one split share an XCD
-constexpr uint64_t SHORT_GROUP_MIN_SPLIT_DIMS = 16384;
 // Most visible keys of a batched decode step (1024 splits of the short kernel).
 constexpr uint32_t BATCH_MAX_KEYS = SHORT_KEYS * MAX_SPLITS;
 
@@ -96,6 +94,8 @@ struct g4a_ctx {
     hipFunction_t decode_short[2] = {nullptr, nullptr};  // [dh512]
     hipFunction_t decode_short2[2] = {nullptr, nullptr};  // [dh512] two workgroups per split (output dim halves)
     hipFunction_t decode_short4[2] = {nullptr, nullptr};  // [dh512] four workgroups per split (quarters)
+    hipFunction_t decode_short2x[2] = {nullptr, nullptr};  // the same two / four with a split's
+    hipFunction_t decode_short4x[2] = {nullptr, nullptr};  // workgroups on one XCD
     hipFunction_t decode_batch[2] = {nullptr, nullptr};   // [dh512] short decode over many sequences
     hipFunction_t decode_wave_batch[2] = {nullptr, nullptr};  // [dh512] streaming decode over many sequences
     hipFunction_t decode_wave_batch_kpos[2] = {nullptr, nullptr};  // [dh512] the same, explicit key positions
@@ -580,6 +580,10 @@ int g4a_create_with(int device, const char* hsaco_path, const g4a_options* opts,
     if (int rc = get_fn(ctx, &ctx->decode_short2[1], "g4a_decode_short2_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_short4[0], "g4a_decode_short4_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_short4[1], "g4a_decode_short4_d512")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->decode_short2x[0], "g4a_decode_short2x_d256")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->decode_short2x[1], "g4a_decode_short2x_d512")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->decode_short4x[0], "g4a_decode_short4x_d256")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->decode_short4x[1], "g4a_decode_short4x_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_batch[0], "g4a_decode_short_batch_d256")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_batch[1], "g4a_decode_short_batch_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->decode_wave_batch[0], "g4a_decode_wave_batch_d256")) return bail(rc);
@@ -946,11 +950,12 @@ int attention_run(g4a_ctx* ctx, const g4a_attn_args* a, const Analysis& an, bool
         // fit the CUs: a shorter P.V and merge per workgroup, bit-identical results
         const uint64_t wg = uint64_t(pl.splits) * a->T * a->Hkv, cus = uint64_t(std::max(ctx->cu_count, 1));
         const uint32_t ds = ctx->short_ds >= 4 && 4 * wg <= cus ? 4u : ctx->short_ds >= 2 && 2 * wg <= cus ? 2u : 1u;
-        hipFunction_t fn = ds == 4 ? ctx->decode_short4[d512] : ds == 2 ? ctx->decode_short2[d512] : ctx->decode_short[d512];
-        // the ds workgroups of a split on one XCD once their repeated K reads reach
-        // 2 MiB over the call (splits x 32 keys x Dh x 4 bytes): hd512 from 32 splits,
-        // hd256 from 64; below that, spreading them over the XCDs is as fast or faster
-        dp.xcd_group = ds > 1 && pl.splits % 8 == 0 && uint64_t(pl.splits) * a->Dh >= SHORT_GROUP_MIN_SPLIT_DIMS;
+        // the ds workgroups of a split on one XCD (one L2 fill of its K rows for all
+        // of them) when the split count is a multiple of 8, which the mapping needs
+        const bool grouped = ds > 1 && pl.splits % 8 == 0;
+        hipFunction_t fn = ds == 4 ? (grouped ? ctx->decode_short4x[d512] : ctx->decode_short4[d512])
+                           : ds == 2 ? (grouped ? ctx->decode_short2x[d512] : ctx->decode_short2[d512])
+                                     : ctx->decode_short[d512];
         if (int rc = launch(ctx, fn, dim3(pl.splits * ds, a->T, a->Hkv), dim3(256, 1, 1), dp, "short decode", true))
             return rc;
     } else if (int rc = launch(ctx, ctx->decode[d512][g8][kd ? 1 : 0], dim3(pl.splits, a->T, a->Hkv),

@@ -1668,24 +1668,6 @@ __device__ __forceinline__ void generic_attention(const G4aGenericParams& p) {
     }
 }
 
-// Workgroup x of a short-kernel launch with ds workgroups per split -> (split,
-// part of the output dims). Workgroups are dealt to the XCDs round-robin by
-// index, so with xcd_group set (the host sets it only when the split count is a
-// multiple of 8) the ds workgroups of a split share x mod 8, i.e. one XCD: they
-// all read the split's K rows, which one L2 fill then serves instead of one
-// fill per XCD. Placement only: the results do not depend on it.
-__device__ __forceinline__ void short_split_part(uint32_t bx, uint32_t ds, const G4aDecodeParams& p,
-                                                 uint32_t& split, uint32_t& part) {
-    if (p.xcd_group) {
-        const uint32_t r = bx >> 3;
-        part = r % ds;
-        split = (bx & 7u) + 8u * (r / ds);
-    } else {
-        split = bx / ds;
-        part = bx % ds;
-    }
-}
-
 }  // namespace
 
 extern "C" {
@@ -1718,24 +1700,34 @@ __global__ __launch_bounds__(256) void g4a_decode_short_d512(G4aDecodeParams p) 
 }
 // DS workgroups per split (grid x = DS * splits): workgroup DS s + dh owns output dims part dh
 __global__ __launch_bounds__(256) void g4a_decode_short2_d256(G4aDecodeParams p) {
-    uint32_t split, part;
-    short_split_part(blockIdx.x, 2u, p, split, part);
-    decode_short<256, 2>(at_device_pos(p), split, blockIdx.y, part);
+    decode_short<256, 2>(at_device_pos(p), blockIdx.x >> 1, blockIdx.y, blockIdx.x & 1u);
 }
 __global__ __launch_bounds__(256) void g4a_decode_short2_d512(G4aDecodeParams p) {
-    uint32_t split, part;
-    short_split_part(blockIdx.x, 2u, p, split, part);
-    decode_short<512, 2>(at_device_pos(p), split, blockIdx.y, part);
+    decode_short<512, 2>(at_device_pos(p), blockIdx.x >> 1, blockIdx.y, blockIdx.x & 1u);
 }
 __global__ __launch_bounds__(256) void g4a_decode_short4_d256(G4aDecodeParams p) {
-    uint32_t split, part;
-    short_split_part(blockIdx.x, 4u, p, split, part);
-    decode_short<256, 4>(at_device_pos(p), split, blockIdx.y, part);
+    decode_short<256, 4>(at_device_pos(p), blockIdx.x >> 2, blockIdx.y, blockIdx.x & 3u);
 }
 __global__ __launch_bounds__(256) void g4a_decode_short4_d512(G4aDecodeParams p) {
-    uint32_t split, part;
-    short_split_part(blockIdx.x, 4u, p, split, part);
-    decode_short<512, 4>(at_device_pos(p), split, blockIdx.y, part);
+    decode_short<512, 4>(at_device_pos(p), blockIdx.x >> 2, blockIdx.y, blockIdx.x & 3u);
+}
+// The same with a split's DS workgroups on one XCD: workgroups are dealt to the
+// XCDs round-robin by index, and x = (split mod 8) + 8 (DS (split div 8) + part)
+// gives the DS workgroups of a split the same x mod 8, so one L2 fill of the
+// split's K rows (which all of them read) serves them all. The host launches
+// these only with a split count that is a multiple of 8. Placement only: the
+// results are the split-major kernels' bit for bit.
+__global__ __launch_bounds__(256) void g4a_decode_short2x_d256(G4aDecodeParams p) {
+    decode_short<256, 2>(at_device_pos(p), (blockIdx.x & 7u) + 8u * (blockIdx.x >> 4), blockIdx.y, (blockIdx.x >> 3) & 1u);
+}
+__global__ __launch_bounds__(256) void g4a_decode_short2x_d512(G4aDecodeParams p) {
+    decode_short<512, 2>(at_device_pos(p), (blockIdx.x & 7u) + 8u * (blockIdx.x >> 4), blockIdx.y, (blockIdx.x >> 3) & 1u);
+}
+__global__ __launch_bounds__(256) void g4a_decode_short4x_d256(G4aDecodeParams p) {
+    decode_short<256, 4>(at_device_pos(p), (blockIdx.x & 7u) + 8u * (blockIdx.x >> 5), blockIdx.y, (blockIdx.x >> 3) & 3u);
+}
+__global__ __launch_bounds__(256) void g4a_decode_short4x_d512(G4aDecodeParams p) {
+    decode_short<512, 4>(at_device_pos(p), (blockIdx.x & 7u) + 8u * (blockIdx.x >> 5), blockIdx.y, (blockIdx.x >> 3) & 3u);
 }
 __global__ __launch_bounds__(256) void g4a_decode_short_batch_d256(G4aBatchParams b) { decode_short_batch<256>(b); }
 __global__ __launch_bounds__(256) void g4a_decode_short_batch_d512(G4aBatchParams b) { decode_short_batch<512>(b); }

@@ -34,9 +34,6 @@ struct G4aDecodeParams {
     // range follows: keys k_pos0 .. qpos (the last `window` of them), k_end never
     // past the planned k_end; q_pos0, k_start and k_end above are then the plan's.
     const uint32_t* dpos;
-    // Short kernel with 2 or 4 workgroups per split: 1 places a split's workgroups
-    // on one XCD (they share its K rows), 0 deals them in split order.
-    uint32_t xcd_group;
 };
 
 // One sequence of a batched decode launch (g4a_decode_*_batch_*,
