@@ -1075,10 +1075,16 @@ __device__ __forceinline__ void decode_short(const G4aDecodeParams& p, uint32_t 
     if (active) {
         const float* const kb = p.k + (size_t)kvh * DH;
         const float* const vb = p.v + (size_t)kvh * DH;
+        // one modulo per wave: the host sends a ring here only when it holds at least
+        // 64 rows, so base + (offset < KEYS) passes the ring's end at most once
+        const uint32_t base = phys_row(t0, p.ring_cap);
         uint32_t rows[KEYS / 2];
 #pragma unroll
-        for (int i = 0; i < KEYS / 2; ++i)
-            rows[i] = phys_row(t0 + min((uint32_t)(8 * half + i), nk - 1), p.ring_cap);
+        for (int i = 0; i < KEYS / 2; ++i) {
+            uint32_t x = base + min((uint32_t)(8 * half + i), nk - 1);
+            if (p.ring_cap && x >= p.ring_cap) x -= p.ring_cap;
+            rows[i] = x;
+        }
 #pragma unroll
         for (int i = 0; i < KEYS / 2; ++i)
 #pragma unroll
