@@ -1388,62 +1388,45 @@ __device__ __forceinline__ void combine(const G4aCombineParams& p, uint32_t qi) 
     }
 }
 
-// The same merge for up to COMBINE_ROW_SPLITS splits, one block per (head,
-// query): wave 0 computes the split weights into LDS, then thread t sums dims
-// t (+256) over the splits in split order, 8 loads in flight. A block per 16
-// dims would leave most of its threads idle at these split counts. The first
-// COMBINE_ROW_EARLY splits' partials are loaded before the weights are known,
-// so a short decode's merge pays one memory round trip, not two.
+// The same merge for up to COMBINE_ROW_SPLITS splits (the host sends no more),
+// one block per (head, query); thread t sums dims t (+256) over the splits in
+// split order. Every wave loads the (m, l) pairs beside its partial loads and
+// computes the split weights itself (lane s holds split s's), taking split s's
+// by a readlane: the wave reductions end in readlanes, so each wave's weights
+// and sum have the same bits, and no LDS hand-off or barrier sits between the
+// loads' one memory round trip and the sums.
 constexpr uint32_t COMBINE_ROW_SPLITS = 16;
-constexpr uint32_t COMBINE_ROW_EARLY = 16;
 
 template <int DH>
 __device__ __forceinline__ void combine_rows(const G4aCombineParams& p, uint32_t h, uint32_t qi) {
-    __shared__ float wgt[COMBINE_ROW_SPLITS];
-    __shared__ float lsum;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
     const size_t ih = (size_t)qi * p.Hq + h;
-    const uint32_t ns = p.nsplit;
-    const uint32_t early = ns < COMBINE_ROW_EARLY ? ns : COMBINE_ROW_EARLY;
-    // wave 0's (m, l) loads go first: the wait for them then leaves the early partials in flight
-    const bool on = (uint32_t)tid < ns && tid < 64;
-    float2 mls = make_float2(NEG_INF, 0.0f);
-    if (on) mls = reinterpret_cast<const float2*>(p.part + (size_t)p.T * p.Hq * ns * DH + ih * ns * 2)[tid];
-    float x0[DH / 256][COMBINE_ROW_EARLY];
+    const uint32_t ns = p.nsplit;  // 1 .. COMBINE_ROW_SPLITS: the clamped loads stay in the split range
+    const bool on = (uint32_t)lane < ns;
+    const float2 ml = reinterpret_cast<const float2*>(p.part + (size_t)p.T * p.Hq * ns * DH +
+                                                      ih * ns * 2)[min((uint32_t)lane, ns - 1)];
+    float x[DH / 256][COMBINE_ROW_SPLITS];
 #pragma unroll
     for (int e = 0; e < DH / 256; ++e) {
-        const float* __restrict__ acc = p.part + part_index<DH>(ih, ns, 0, 256 * e + tid);
+        const float* __restrict__ acc = p.part + part_index<DH>(ih, ns, 0, 256 * e + tid);  // split s at acc[DH s]
 #pragma unroll
-        for (uint32_t u = 0; u < COMBINE_ROW_EARLY; ++u)  // ns >= 1: the clamped loads stay in the split range
-            x0[e][u] = acc[(size_t)(u < early ? u : early - 1) * DH];
+        for (uint32_t u = 0; u < COMBINE_ROW_SPLITS; ++u)
+            x[e][u] = acc[(size_t)(u < ns ? u : ns - 1) * DH];
     }
-    if (tid < 64) {
-        const float M = wave_max(mls.x);
-        const float e = (mls.x == NEG_INF) ? 0.0f : expf(mls.x - M);
-        if (on) wgt[tid] = e;
-        const float L = wave_sum(on ? mls.y * e : 0.0f);
-        if (tid == 0) lsum = L;
-    }
-    __syncthreads();
-    const float L = lsum;
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the weights' arithmetic
+    const float mx = on ? ml.x : NEG_INF;
+    const float M = wave_max(mx);
+    const float wt = (mx == NEG_INF) ? 0.0f : expf(mx - M);
+    const float L = wave_sum(on ? ml.y * wt : 0.0f);
 #pragma unroll
     for (int e = 0; e < DH / 256; ++e) {
-        const uint32_t d = 256 * e + tid;
-        const float* __restrict__ acc = p.part + part_index<DH>(ih, ns, 0, d);  // split s at acc[DH s]
         float A = 0.0f;
 #pragma unroll
-        for (uint32_t u = 0; u < COMBINE_ROW_EARLY; ++u)
-            if (u < early) A += x0[e][u] * wgt[u];
-        uint32_t s = early;
-        for (; s + 8 <= ns; s += 8) {
-            float x[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) x[u] = acc[(size_t)(s + u) * DH];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) A += x[u] * wgt[s + u];
+        for (uint32_t u = 0; u < COMBINE_ROW_SPLITS; ++u) {  // a select, not a branch: a branch would
+            const float t = A + x[e][u] * g4a_lane(wt, u);  // take each load into it, one round trip each
+            A = u < ns ? t : A;
         }
-        for (; s < ns; ++s) A += acc[(size_t)s * DH] * wgt[s];
-        p.out[ih * DH + d] = L > 0.0f ? A / L : 0.0f;
+        p.out[ih * DH + 256 * e + tid] = L > 0.0f ? A / L : 0.0f;
     }
 }
 
@@ -1452,7 +1435,7 @@ __device__ __forceinline__ void combine_rows(const G4aCombineParams& p, uint32_t
 // merged attention row (the activation row of the output projection that
 // follows), zeros from Hq * DH up to KP; xout, if set, receives the row too.
 // Each wave computes the split weights of heads wave, wave + 4, ... exactly as
-// combine_rows' wave 0 does; each dim then sums its splits in order from 0,
+// each wave of combine_rows does; each dim then sums its splits in order from 0,
 // multiplies and adds rounded separately, so every value has combine_rows'
 // bits. Thread t merges four adjacent dims (one float4 of a split's 16-dim
 // row) in each 1024-dim group; the loads of two groups (every split) are in
