@@ -71,6 +71,29 @@ def test_short_decode_cases(ctx):
         assert_parity(got, want, label)
 
 
+def test_every_split_count_of_the_small_combine(ctx):
+    """Split counts 2..16 merge on the one-block-per-head combine (combine_rows),
+    in which every wave takes the split weights from lanes 0..ns-1 and loads each
+    split's partial at an index clamped into the split range. Every count, both
+    head dims, one and two queries (the combine's second grid row), a ragged
+    last split; the counts that are multiples of 8 also run the decode kernels
+    that place a split's workgroups on one XCD."""
+    c = ctx
+    for Dh in (256, 512):
+        for ns in range(2, 17):
+            for T in (1, 2):
+                S = 32 * (ns - 1) + 1 + (7 * ns + 3 * T) % 32  # in (32 (ns - 1), 32 ns]: ns splits
+                label = f"{ns} splits: T={T} S={S} Dh={Dh}"
+                kw = dict(T=T, S=S, Hq=8, Hkv=1, Dh=Dh, Dv=Dh, q_pos0=S - T, k_pos0=0)
+                _check_plan(c, **kw)
+                assert c.plan(**kw).splits == ns, label
+                step(label)
+                ins = synth.gemma_inputs(T=T, S=S, Dh=Dh, seed=1000 + 40 * ns + 2 * T + Dh // 256)
+                want = oracle.attention(ins.q, ins.k, ins.v, ins.q_pos, ins.k_pos)
+                got = g4a.attention_host(c, ins.q, ins.k, ins.v)
+                assert_parity(got, want, label)
+
+
 def test_back_to_back_calls(ctx):
     """Calls with different split counts, query counts and head dims queued in
     one stream without a sync between them (they share the context's partial
