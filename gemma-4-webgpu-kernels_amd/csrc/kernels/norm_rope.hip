@@ -53,7 +53,10 @@ __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
     __shared__ __attribute__((aligned(16))) float stage[NR_WAVES][NR_STRIDE];
     __shared__ float row_ss[NR_WAVES];
     const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
+    // wave-uniform (readfirstlane): the row, its segment and the segment's fields then
+    // stay in scalar registers, read from the kernel arguments by scalar loads; a
+    // per-lane row index made every field a vector load with a wait at each use
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t row = blockIdx.x * NR_WAVES + w;
     // a device position (T = 1) is read at run time; past max_pos the launch writes nothing
     // (every thread of the grid leaves here, before any barrier)
@@ -72,7 +75,7 @@ __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
         r -= p.T * p.seg[si].heads;
         ++si;
     }
-    const G4aNormRopeSeg& S = p.seg[si];
+    const G4aNormRopeSeg S = p.seg[si];
     const uint32_t t = r / S.heads, h = r % S.heads;
     live = live && t >= S.first_t;  // else its ring slot is taken by a later token of this call
     const uint32_t Dh = p.Dh;
