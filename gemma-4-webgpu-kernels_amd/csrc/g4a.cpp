@@ -110,7 +110,8 @@ struct g4a_ctx {
     hipFunction_t generic = nullptr;
     hipFunction_t prefill[2] = {nullptr, nullptr};                          // [dh512]
     hipFunction_t split_kv = nullptr;  // K/V pre-split for the head_dim 256 prefill
-    hipFunction_t norm_rope = nullptr;  // the attention producer (RMSNorm + RoPE + KV write)
+    hipFunction_t norm_rope = nullptr;        // the attention producer (RMSNorm + RoPE + KV write)
+    hipFunction_t norm_rope_short = nullptr;  // the same with its loads issued together (<= 1 workgroup per CU)
     hipFunction_t linear_words[3][3][3] = {};  // [bits 2/4/8][(MT, RU) = (1, 2), (1, 8), (4, 4)][mode]
     hipFunction_t linear_elem[3] = {};         // [mode]
     hipFunction_t linear_mfma[3][2][3] = {};   // [bits 2/4/8][64 / 128 weight rows per tile][mode]: M >= 16
@@ -604,6 +605,7 @@ int g4a_create_with(int device, const char* hsaco_path, const g4a_options* opts,
     if (int rc = get_fn(ctx, &ctx->prefill_merge, "g4a_prefill_merge_d512")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->split_kv, "g4a_split_kv")) return bail(rc);
     if (int rc = get_fn(ctx, &ctx->norm_rope, "g4a_norm_rope")) return bail(rc);
+    if (int rc = get_fn(ctx, &ctx->norm_rope_short, "g4a_norm_rope_short")) return bail(rc);
     {
         static const int bits[3] = {2, 4, 8};
         static const int mt_ru[3][2] = {{1, 2}, {1, 8}, {4, 4}};
@@ -1346,7 +1348,11 @@ int norm_rope_launch(g4a_ctx* ctx, G4aNormRopeSeg* segs, uint32_t nseg, uint32_t
         if (int rc = sincos_table(ctx, theta, rot, freq_host, max_pos, &p.sc, &p.sc_rows)) return rc;
     }
     const uint32_t blocks = uint32_t((rows + 3) / 4);
-    return launch(ctx, ctx->norm_rope, dim3(blocks, 1, 1), dim3(256, 1, 1), p, "norm/rope rows", true);
+    // launches of at most one workgroup per CU (decode steps) wait on latency: their
+    // kernel issues the norm weights and sin/cos together; longer ones keep registers
+    // free for occupancy (the same rows either way)
+    hipFunction_t fn = blocks <= uint32_t(std::max(ctx->cu_count, 1)) ? ctx->norm_rope_short : ctx->norm_rope;
+    return launch(ctx, fn, dim3(blocks, 1, 1), dim3(256, 1, 1), p, "norm/rope rows", true);
 }
 
 // ---- quantised projections -------------------------------------------------

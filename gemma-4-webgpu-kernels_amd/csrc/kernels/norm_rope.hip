@@ -49,6 +49,13 @@ constexpr int NR_MAXE = 4;     // float4 groups per lane: Dh <= 1024
 // sequential sums (lane r reads row r) on different banks.
 constexpr int NR_STRIDE = NR_MAXE * 256 + 4;
 
+// HOIST (the short form, for launches of at most one workgroup per CU: decode
+// steps) issues the norm weights and the rotation's sin/cos together right after
+// the norm's barriers, at indices clamped into range; the long form (prefill)
+// loads each where it is used, which keeps registers free for occupancy (the
+// short form's loads made a 2048-token prefill 14 % slower). The operations and
+// their order are the same in both, so the rows are bit-identical.
+template <bool HOIST>
 __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
     __shared__ __attribute__((aligned(16))) float stage[NR_WAVES][NR_STRIDE];
     __shared__ float row_ss[NR_WAVES];
@@ -124,6 +131,37 @@ __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
         __syncthreads();
     }
     if (!live) return;
+    // short form: every load the rest of the row needs goes out here, before the first
+    // use, at indices clamped into range and under wave-uniform tests only (loads under
+    // the per-dim bounds tests below wait one at a time: the norm weights per 256 dims,
+    // the sin/cos per dim)
+    const uint32_t rot = p.rotary_dim, half = rot / 2;
+    const bool rope = S.rope && rot;
+    float4 wv[NR_MAXE];
+    if (HOIST && S.norm && S.w) {
+#pragma unroll
+        for (int e = 0; e < NR_MAXE; ++e)
+            if (256u * e < Dh) wv[e] = *reinterpret_cast<const float4*>(S.w + min(4u * lane + 256u * e, Dh - 4));
+    }
+    uint32_t ipos = 0;
+    bool tab = false;
+    float2 scv[NR_MAXE][4];
+    if (rope) {
+        ipos = p.pos ? p.pos[t] : pos0 + t;
+        tab = ipos < p.sc_rows;
+        if (HOIST && tab) {
+            const float2* const sc_row = p.sc + (size_t)ipos * half;
+#pragma unroll
+            for (int e = 0; e < NR_MAXE; ++e)
+                if (256u * e < rot) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t d = min(4u * lane + 256u * e + i, rot - 1);
+                        scv[e][i] = sc_row[d < half ? d : d - half];
+                    }
+                }
+        }
+    }
     if (S.norm) {
         const float ss = row_ss[w];
         const float inv = 1.0f / sqrtf(ss / (float)Dh + p.eps);
@@ -136,15 +174,15 @@ __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
             v[e].z = v[e].z * inv;
             v[e].w = v[e].w * inv;
             if (S.w) {
-                const float4 wv = *reinterpret_cast<const float4*>(S.w + d);
-                v[e].x = v[e].x * wv.x;
-                v[e].y = v[e].y * wv.y;
-                v[e].z = v[e].z * wv.z;
-                v[e].w = v[e].w * wv.w;
+                const float4 ww = HOIST ? wv[e] : *reinterpret_cast<const float4*>(S.w + d);
+                v[e].x = v[e].x * ww.x;
+                v[e].y = v[e].y * ww.y;
+                v[e].z = v[e].z * ww.z;
+                v[e].w = v[e].w * ww.w;
             }
         }
     }
-    if (S.rope && p.rotary_dim) {
+    if (rope) {
         float* const ys = stage[w];
 #pragma unroll
         for (int e = 0; e < NR_MAXE; ++e) {
@@ -153,10 +191,7 @@ __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
         }
         __builtin_amdgcn_wave_barrier();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        const uint32_t rot = p.rotary_dim, half = rot / 2;
-        const uint32_t ipos = p.pos ? p.pos[t] : pos0 + t;
         const float pos = (float)ipos;
-        const bool tab = ipos < p.sc_rows;
         const float2* const sc_row = p.sc + (size_t)(tab ? ipos : 0u) * half;
 #pragma unroll
         for (int e = 0; e < NR_MAXE; ++e) {
@@ -171,7 +206,7 @@ __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
                 const float a = ys[j], b = ys[j + half];
                 float sn, cs;
                 if (tab) {
-                    const float2 v2 = sc_row[j];
+                    const float2 v2 = HOIST ? scv[e][i] : sc_row[j];
                     sn = v2.x;
                     cs = v2.y;
                 } else {
@@ -197,4 +232,7 @@ __device__ __forceinline__ void norm_rope_rows(const G4aNormRopeParams& p) {
 
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256) void g4a_norm_rope(G4aNormRopeParams p) { norm_rope_rows(p); }
+extern "C" __global__ __launch_bounds__(256) void g4a_norm_rope(G4aNormRopeParams p) { norm_rope_rows<false>(p); }
+extern "C" __global__ __launch_bounds__(256) void g4a_norm_rope_short(G4aNormRopeParams p) {
+    norm_rope_rows<true>(p);
+}
