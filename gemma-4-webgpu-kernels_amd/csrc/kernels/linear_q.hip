@@ -446,7 +446,29 @@ __device__ __forceinline__ void linear_q_mfma(const G4aLinearParams& p) {
         if (st + 1 < nsteps) stage_x(buf ^ 1);
     }
 
-    // lane (g, rl) of blocks (ab, tb) holds weight rows 16 AB wv + 16 ab + 4 g + i, token 16 tb + rl
+    // lane (g, rl) of blocks (ab, tb) holds weight rows 16 AB wv + 16 ab + 4 g + i, token 16 tb + rl.
+    // Every scale (and b value) is loaded before the first store, at indices clamped
+    // into range: y may alias them as far as the compiler knows, so a load after a
+    // store waited for it, one memory round trip per output.
+    float sc[AB][4], sc2[AB][4], bv[AB][4][4];
+#pragma unroll
+    for (int ab = 0; ab < AB; ++ab)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t n = min(n0 + 16 * AB * wv + 16 * ab + 4 * g + i, N - 1);
+            sc[ab][i] = p.s[n];
+            if (MODE == 1) sc2[ab][i] = p.s2[n];
+            if (MODE == 2) {
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb) {
+                    const uint32_t m = min(m0 + 16 * tb + rl, M - 1);
+                    bv[ab][tb][i] = p.b[(size_t)m * p.b_stride + p.b_off + n];
+                }
+            }
+        }
+    // all of them in (s_waitcnt vmcnt(0)): with no load left pending, the compiler
+    // puts no wait among the stores below, which vmcnt also counts on this GPU
+    __builtin_amdgcn_s_waitcnt(0x0F70);
 #pragma unroll
     for (int ab = 0; ab < AB; ++ab)
 #pragma unroll
@@ -457,10 +479,10 @@ __device__ __forceinline__ void linear_q_mfma(const G4aLinearParams& p) {
             for (int i = 0; i < 4; ++i) {
                 const uint32_t n = n0 + 16 * AB * wv + 16 * ab + 4 * g + i;
                 if (n >= N) continue;
-                const float v = acc[ab][tb][i] * (p.s[n] * F::INV_F);
+                const float v = acc[ab][tb][i] * (sc[ab][i] * F::INV_F);
                 float o = v;
-                if (MODE == 1) o = gelu_tanh(v) * (acc2[ab][tb][i] * (p.s2[n] * F::INV_F));
-                if (MODE == 2) o = gelu_tanh(v) * p.b[(size_t)m * p.b_stride + p.b_off + n];
+                if (MODE == 1) o = gelu_tanh(v) * (acc2[ab][tb][i] * (sc2[ab][i] * F::INV_F));
+                if (MODE == 2) o = gelu_tanh(v) * bv[ab][tb][i];
                 p.y[(size_t)m * N + n] = o;
             }
         }
