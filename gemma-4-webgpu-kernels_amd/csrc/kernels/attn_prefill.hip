@@ -159,21 +159,25 @@ __device__ __forceinline__ void split_kv(const G4aSplitParams& p) {
         __shared__ float redmax[4];
         const uint32_t tile = blockIdx.x / p.Hkv, h = blockIdx.x % p.Hkv;
         const uint32_t nitems = 16 * nbk;
+        // every row is loaded whatever `seen` says (row_of keeps each inside the cache)
+        // and an unseen one is replaced by zeros where it is used: a load under the test,
+        // or zeros written over its registers, waited for the load on the spot
         float4 x0[MAXI], x1[MAXI];
-        float mx = 0.0f;
+        bool ok[MAXI];
 #pragma unroll
         for (int u = 0; u < MAXI; ++u) {
             const uint32_t it = threadIdx.x + 256 * u;
-            x0[u] = x1[u] = zero4;
-            if (it < nitems) {
-                const size_t jj = (size_t)tile * 16 + it / nbk;
-                if (seen(jj)) {
-                    const float* src = p.k + (row_of(jj) * p.Hkv + h) * p.Dh + 8 * (it % nbk);
-                    x0[u] = ld4(src);
-                    x1[u] = ld4(src + 4);
-                }
-                mx = fmaxf(mx, absmax8(x0[u], x1[u]));
-            }
+            const size_t jj = (size_t)tile * 16 + it / nbk;
+            const float* src = p.k + (row_of(jj) * p.Hkv + h) * p.Dh + 8 * (it % nbk);
+            x0[u] = ld4(src);
+            x1[u] = ld4(src + 4);
+            ok[u] = it < nitems && seen(jj);
+        }
+        float mx = 0.0f;  // unseen rows count as zeros, which cannot raise it
+#pragma unroll
+        for (int u = 0; u < MAXI; ++u) {
+            const float m8 = absmax8(x0[u], x1[u]);
+            mx = ok[u] ? fmaxf(mx, m8) : mx;
         }
         mx = g4a_wave_max(mx);
         if ((threadIdx.x & 63) == 0) redmax[threadIdx.x >> 6] = mx;
@@ -186,7 +190,7 @@ __device__ __forceinline__ void split_kv(const G4aSplitParams& p) {
             if (it < nitems) {
                 const size_t jj = (size_t)tile * 16 + it / nbk;
                 h8v hi, lo;
-                split8h(x0[u], x1[u], a, hi, lo);
+                split8h(ok[u] ? x0[u] : zero4, ok[u] ? x1[u] : zero4, a, hi, lo);
                 float* dst = p.kout + (jj * p.Hkv + h) * p.Dh + 8 * (it % nbk);
                 *reinterpret_cast<h8v*>(dst) = hi;
                 *reinterpret_cast<h8v*>(dst + 4) = lo;
@@ -204,9 +208,12 @@ __device__ __forceinline__ void split_kv(const G4aSplitParams& p) {
     const uint32_t h = (uint32_t)(t % p.Hkv);
     const size_t qd = t / p.Hkv;
     float4 x[4];
+    bool ok[4];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-        x[kk] = seen(4 * qd + kk) ? ld4(p.v + (row_of(4 * qd + kk) * p.Hkv + h) * p.Dh + 64 * c + 4 * n) : zero4;
+    for (int kk = 0; kk < 4; ++kk) {  // all four rows in flight at once; an unseen one is zeros where used
+        x[kk] = ld4(p.v + (row_of(4 * qd + kk) * p.Hkv + h) * p.Dh + 64 * c + 4 * n);
+        ok[kk] = seen(4 * qd + kk);
+    }
     float* const blk = p.vout + (qd * p.Hkv + h) * 4 * p.Dh;
     bool bad = false;
 #pragma unroll
@@ -214,7 +221,8 @@ __device__ __forceinline__ void split_kv(const G4aSplitParams& p) {
         h4v hi, lo;
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            const float xv = e == 0 ? x[kk].x : (e == 1 ? x[kk].y : (e == 2 ? x[kk].z : x[kk].w));
+            const float xl = e == 0 ? x[kk].x : (e == 1 ? x[kk].y : (e == 2 ? x[kk].z : x[kk].w));
+            const float xv = ok[kk] ? xl : 0.0f;
             bad |= !(fabsf(xv) <= 32768.0f);
             split16(xv, hi, lo, kk);
         }
