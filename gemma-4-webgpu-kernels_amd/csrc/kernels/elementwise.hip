@@ -58,8 +58,20 @@ __device__ __forceinline__ void rms_rows(const G4aRmsRowsParams& p) {
     __shared__ float part[256];
     const uint32_t row = blockIdx.x, tid = threadIdx.x;
     const float* __restrict__ xr = p.x + (size_t)row * p.D;
+    // RU chunks of 256 at a time: their loads go out together (indices clamped into
+    // the row), then the chunk's terms are added in the same order as one by one
+    constexpr uint32_t RU = 8;
     float ss = 0.0f;
-    for (uint32_t d = tid; d < p.D; d += 256) ss += xr[d] * xr[d];
+    for (uint32_t d0 = tid; d0 < p.D; d0 += RU * 256) {
+        float xv[RU];
+#pragma unroll
+        for (uint32_t u = 0; u < RU; ++u) xv[u] = xr[min(d0 + 256 * u, p.D - 1)];
+#pragma unroll
+        for (uint32_t u = 0; u < RU; ++u) {
+            const float t = ss + xv[u] * xv[u];
+            ss = d0 + 256 * u < p.D ? t : ss;
+        }
+    }
     part[tid] = ss;
     __syncthreads();
     for (uint32_t st = 128; st > 0; st >>= 1) {
@@ -70,12 +82,28 @@ __device__ __forceinline__ void rms_rows(const G4aRmsRowsParams& p) {
     const float sc = p.scale_by ? p.scale_by[0] : 1.0f;
     float* __restrict__ yr = p.y + (size_t)row * p.D;
     const float* __restrict__ rr = p.res ? p.res + (size_t)row * p.D : nullptr;
-    for (uint32_t d = tid; d < p.D; d += 256) {
-        float n = xr[d] * inv;
-        if (p.w) n = n * p.w[d];
-        if (rr) n = rr[d] + n;
-        if (p.scale_by) n = n * sc;
-        yr[d] = n;
+    const float* __restrict__ wr = p.w;
+    // the chunk's loads all go out before its stores: a load after a store to y
+    // (which may alias x, w or the residual as far as the compiler knows) waited
+    for (uint32_t d0 = tid; d0 < p.D; d0 += RU * 256) {
+        float xv[RU], wv[RU], rv[RU];
+#pragma unroll
+        for (uint32_t u = 0; u < RU; ++u) {
+            const uint32_t d = min(d0 + 256 * u, p.D - 1);
+            xv[u] = xr[d];
+            if (wr) wv[u] = wr[d];
+            if (rr) rv[u] = rr[d];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < RU; ++u) {
+            const uint32_t d = d0 + 256 * u;
+            if (d >= p.D) break;
+            float n = xv[u] * inv;
+            if (wr) n = n * wv[u];
+            if (rr) n = rv[u] + n;
+            if (p.scale_by) n = n * sc;
+            yr[d] = n;
+        }
     }
 }
 
